@@ -1,0 +1,295 @@
+#!/usr/bin/env python
+"""Benchmark of the batch-invariant kernels on one MI355X.
+
+Default workload: 4-bit affine quantized matmul at
+the Llama-3-8B MLP shape, x bf16 [M, 4096] @ W[14336, 4096]^T with W packed
+4-bit, group 64, bf16 scales/biases; the headline is the decode GEMV, M = 1.
+A step is one call of the op on one batch. Weights are rotated over >= 512 MB
+of distinct copies so every step streams them from HBM (the 256 MB Infinity
+Cache would otherwise hold them). Time is measured with HIP events on the
+stream the kernels run on.
+
+    python bench.py [--steps K] [--warmup W] [--op qmm4|qmm8|linear|rmsnorm|decode|prefill|gemm|all]
+
+Prints one JSON line per op (the default op only, unless --op is given).
+`value` is the achieved fraction of the op's roofline in percent (HBM 8 TB/s,
+or dense bf16 MFMA 2.5 PFLOP/s for the MFMA-bound ops), computed from the
+algorithmic bytes/flops of one call over the measured call time.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "mlx-batch-invariant_amd"):
+    sys.path.insert(0, str(p))
+
+PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
+PEAK_BF16 = 2.5e15         # FLOP/s, dense bf16 MFMA
+METRIC = "% of HBM/MFMA roofline per op at batch 1–256, with bitwise batch invariance"
+ROTATE_BYTES = 512 << 20
+
+
+def _sync():
+    import torch
+    torch.cuda.synchronize()
+
+
+def _time_calls(fn, n, warmup, rotate):
+    """Per-call durations (s) of fn(i) from HIP events on the current stream."""
+    import torch
+    for i in range(warmup):
+        fn(i % rotate)
+    _sync()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for i in range(n):
+        evs[i][0].record()
+        fn((warmup + i) % rotate)
+        evs[i][1].record()
+    _sync()
+    return [a.elapsed_time(b) * 1e-3 for a, b in evs]
+
+
+def _bits(t):
+    import torch
+    return t.contiguous().view(torch.uint8).cpu().numpy().tobytes()
+
+
+# ---- workloads ------------------------------------------------------------------
+
+def qmm_bytes(M, N, K, bits, gs):
+    return N * K * bits // 8 + 2 * 2 * N * (K // gs) + 2 * M * K + 2 * M * N
+
+
+def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
+    import torch
+    import mlx_batch_invariant_amd as bi
+    N, K = 14336, 4096
+    g = torch.Generator().manual_seed(0)
+    W = 0.02 * torch.randn((N, K), generator=g)
+    wq, s, b = bi.quantize(W, group_size=gs, bits=bits, dtype=torch.bfloat16)
+    del W
+    per = qmm_bytes(1, N, K, bits, gs)
+    ncopy = max(1, math.ceil(ROTATE_BYTES / per))
+    copies = [(wq.cuda(), s.cuda(), b.cuda())]
+    for _ in range(ncopy - 1):
+        copies.append(tuple(t.clone() for t in copies[0]))
+    xs = (torch.randn((max(Ms), K), generator=g)).to(torch.bfloat16).cuda()
+
+    def call(M):
+        return lambda i: bi.batch_invariant_quantized_matmul(xs[:M], *copies[i], group_size=gs, bits=bits)
+
+    table = {}
+    for M in Ms:
+        t = statistics.median(_time_calls(call(M), args.steps, args.warmup, ncopy))
+        by = qmm_bytes(M, N, K, bits, gs)
+        table[M] = {"us": round(t * 1e6, 3), "GBps": round(by / t / 1e9, 1),
+                    "frac_hbm": round(by / t / PEAK_HBM, 4)}
+    # headline M = 1 over exactly `steps` timed calls
+    _sync()
+    t0 = time.perf_counter()
+    durs = _time_calls(call(1), args.steps, args.warmup, ncopy)
+    wall = time.perf_counter() - t0
+    # bitwise invariance in the same run: row 0 at M = 1 vs inside M = 64
+    inv = all(_bits(call(1)(0)[0]) == _bits(call(M)(0)[0]) for M in Ms)
+    # stock, non-invariant baselines: dequantize + hipBLASLt, and bf16 GEMV on the
+    # pre-dequantized weight
+    Wd = bi.dequantize(copies[0][0], copies[0][1], copies[0][2], gs, bits, dtype=torch.bfloat16)
+    stock_deq = statistics.median(_time_calls(
+        lambda i: torch.matmul(xs[:1], bi.dequantize(*copies[i], gs, bits, dtype=torch.bfloat16).t()), 5, 2, ncopy))
+    stock_bf16 = statistics.median(_time_calls(lambda i: torch.matmul(xs[:1], Wd.t()), args.steps, args.warmup, 1))
+    t_med = statistics.median(durs)
+    by1 = qmm_bytes(1, N, K, bits, gs)
+    achieved = by1 / t_med
+    cpu = None if args.no_cpu else cpu_baseline_qmm(bits, gs)
+    return {
+        "metric": METRIC,
+        "value": round(100 * achieved / PEAK_HBM, 2),
+        "unit": "% of HBM roofline (4-bit g64 qmatmul, M=1)" if bits == 4 else f"% of HBM roofline ({bits}-bit g{gs} qmatmul, M=1)",
+        "ms_per_step": round(sum(durs) / len(durs) * 1e3, 5),
+        "wall_s_timed": round(wall, 4),
+        "dtype": "bf16",
+        "config": {"workload": f"qmatmul {bits}-bit g{gs} affine, x[M,4096] @ W[14336,4096]^T, Llama-3-8B MLP shape",
+                   "M": 1, "M_sweep": list(Ms), "weights_rotated_MB": round(ncopy * per / 2**20)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                     "algorithmic_bytes": by1, "kernel": "bi_quantized_matmul (gemm_direct split + fold_groups)"},
+        "per_m": table,
+        "bitwise_invariant_M1_vs_all": inv,
+        "stock_gpu": {"dequant_plus_matmul_us": round(stock_deq * 1e6, 2),
+                      "bf16_hipblaslt_gemv_us": round(stock_bf16 * 1e6, 2),
+                      "note": "non-invariant torch paths, reported only"},
+        "cpu_baseline": cpu,
+    }
+
+
+def cpu_baseline_qmm(bits, gs, budget_s=10.0):
+    """The oracle (numpy port of the same arithmetic) on a bounded sample of
+    the M = 1 workload: as many 512-row slices of W as fit in ~budget_s."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import bi_oracle as ora
+    N, K, rows = 14336, 4096, 512
+    rng = np.random.default_rng(0)
+    x = ora.round_to(rng.standard_normal((1, K)).astype(np.float32), "bf16")
+    done_bytes, t_used, slices = 0, 0.0, 0
+    with threadpool_limits(limits=1):
+        while t_used < budget_s and slices * rows < N:
+            codes = rng.integers(0, 1 << bits, size=(rows, K))
+            w = ora.pack(codes, bits)
+            sc = ora.round_to(rng.uniform(1e-3, 1e-2, size=(rows, K // gs)).astype(np.float32), "bf16")
+            bs = ora.round_to(rng.uniform(-0.05, 0.05, size=(rows, K // gs)).astype(np.float32), "bf16")
+            t0 = time.perf_counter()
+            Wd = ora.dequantize(w, sc, bs, gs, bits, "bf16")
+            ora.matmul(x, Wd, "bf16")
+            t_used += time.perf_counter() - t0
+            slices += 1
+            done_bytes += qmm_bytes(1, rows, K, bits, gs)
+    return {"value": round(done_bytes / t_used / 1e9, 4), "unit": "GB/s (algorithmic bytes)", "cores": 1,
+            "kind": "port", "sample": f"M=1, {slices} x {rows} of the 14336 weight rows, K=4096, "
+                                      f"{bits}-bit g{gs}; numpy oracle, 1 BLAS thread, {t_used:.1f} s"}
+
+
+def bench_linear(args):
+    """RMSNorm then linear, Qwen2-0.5B shape."""
+    import torch
+    import mlx_batch_invariant_amd as bi
+    g = torch.Generator().manual_seed(0)
+    N, K = 4864, 896
+    per = N * K * 2
+    ncopy = math.ceil(ROTATE_BYTES / per)
+    Ws = [(0.02 * torch.randn((N, K), generator=g)).to(torch.bfloat16).cuda()]
+    Ws += [Ws[0].clone() for _ in range(ncopy - 1)]
+    gam = (1 + 0.1 * torch.randn(K, generator=g)).to(torch.bfloat16).cuda()
+    out = {}
+    for M in (1, 4, 16, 64, 256):
+        x = torch.randn((M, K), generator=g).to(torch.bfloat16).cuda()
+        tn = statistics.median(_time_calls(lambda i: bi.batch_invariant_rms_norm(x, gam, 1e-6), args.steps, args.warmup, 1))
+        h = bi.batch_invariant_rms_norm(x, gam, 1e-6)
+        tl = statistics.median(_time_calls(lambda i: bi.batch_invariant_matmul(h, Ws[i].t()), args.steps, args.warmup, ncopy))
+        ts = statistics.median(_time_calls(lambda i: torch.nn.functional.linear(h, Ws[i]), args.steps, args.warmup, ncopy))
+        by_l = per + 2 * M * (K + N)
+        by_n = 4 * M * K + 2 * K
+        out[M] = {"rmsnorm_us": round(tn * 1e6, 2), "rmsnorm_GBps": round(by_n / tn / 1e9, 1),
+                  "linear_us": round(tl * 1e6, 2), "linear_GBps": round(by_l / tl / 1e9, 1),
+                  "linear_frac_hbm": round(by_l / tl / PEAK_HBM, 4), "stock_linear_us": round(ts * 1e6, 2)}
+    return {"metric": METRIC, "op": "rmsnorm+linear (config 1)", "per_m": out}
+
+
+def bench_decode(args):
+    """split-KV decode, GQA 32/8, D 128, ragged lengths."""
+    import numpy as np
+    import torch
+    import mlx_batch_invariant_amd as bi
+    g = torch.Generator().manual_seed(0)
+    res = {}
+    for B in (1, 16, 64, 256):
+        rng = np.random.default_rng(B)
+        lens = rng.integers(1, 8193, size=B)
+        L = 8192
+        k = torch.randn((B, 8, L, 128), generator=g).to(torch.bfloat16).cuda()
+        v = torch.randn((B, 8, L, 128), generator=g).to(torch.bfloat16).cuda()
+        q = torch.randn((B, 32, 1, 128), generator=g).to(torch.bfloat16).cuda()
+        kl = torch.tensor(lens, dtype=torch.int32).cuda()
+        t = statistics.median(_time_calls(lambda i: bi.batch_invariant_decode_attention(
+            q, k, v, scale=128 ** -0.5, kv_lens=kl), args.steps, args.warmup, 1))
+        by = 4096 * int(lens.sum()) + 16384 * B
+        res[B] = {"us": round(t * 1e6, 2), "GBps": round(by / t / 1e9, 1), "frac_hbm": round(by / t / PEAK_HBM, 4),
+                  "sum_len": int(lens.sum())}
+        del k, v
+    return {"metric": METRIC, "op": "decode attention (config 3)", "per_b": res}
+
+
+def bench_prefill(args):
+    """causal prefill T=2048, GQA 32/8, D 128."""
+    import torch
+    import mlx_batch_invariant_amd as bi
+    g = torch.Generator().manual_seed(0)
+    res = {}
+    T = 2048
+    for B in (1, 4, 16):
+        q = torch.randn((B, 32, T, 128), generator=g).to(torch.bfloat16).cuda()
+        k = torch.randn((B, 8, T, 128), generator=g).to(torch.bfloat16).cuda()
+        v = torch.randn((B, 8, T, 128), generator=g).to(torch.bfloat16).cuda()
+        t = statistics.median(_time_calls(lambda i: bi.batch_invariant_prefill_attention(
+            q, k, v, scale=128 ** -0.5, causal=True), max(3, args.steps // 4), 2, 1))
+        ts = statistics.median(_time_calls(lambda i: torch.nn.functional.scaled_dot_product_attention(
+            q, k, v, is_causal=True, enable_gqa=True), max(3, args.steps // 4), 2, 1))
+        fl = 4 * B * 32 * 128 * T * (T + 1) / 2
+        res[B] = {"ms": round(t * 1e3, 3), "TFLOPs": round(fl / t / 1e12, 1), "frac_mfma": round(fl / t / PEAK_BF16, 4),
+                  "stock_sdpa_ms": round(ts * 1e3, 3)}
+    return {"metric": METRIC, "op": "prefill attention (config 4)", "per_b": res}
+
+
+def bench_gemm(args):
+    """Large-M bf16 GEMM (config 5 prefill shape): [M,4096] x [14336,4096]^T."""
+    import torch
+    import mlx_batch_invariant_amd as bi
+    g = torch.Generator().manual_seed(0)
+    N, K = 14336, 4096
+    W = (0.02 * torch.randn((N, K), generator=g)).to(torch.bfloat16).cuda()
+    res = {}
+    for M in (256, 4096):
+        x = torch.randn((M, K), generator=g).to(torch.bfloat16).cuda()
+        t = statistics.median(_time_calls(lambda i: bi.batch_invariant_matmul(x, W.t()), max(3, args.steps // 2), 2, 1))
+        ts = statistics.median(_time_calls(lambda i: torch.matmul(x, W.t()), max(3, args.steps // 2), 2, 1))
+        fl = 2 * M * N * K
+        res[M] = {"ms": round(t * 1e3, 3), "TFLOPs": round(fl / t / 1e12, 1), "frac_mfma": round(fl / t / PEAK_BF16, 4),
+                  "stock_ms": round(ts * 1e3, 3), "stock_TFLOPs": round(fl / ts / 1e12, 1)}
+    return {"metric": METRIC, "op": "bf16 GEMM (large M)", "per_m": res}
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--op", default="qmm4", choices=["qmm4", "qmm8", "linear", "rmsnorm", "decode", "prefill", "gemm", "all"])
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    a = p.parse_args(argv)
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: every kernel here is single-GPU and no multi-GPU "
+              "path exists in this build (see DESIGN.md for how it would shard).", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    import mlx_batch_invariant_amd as bi
+    bi._lib.load()
+    ops = ["qmm4", "qmm8", "linear", "decode", "prefill", "gemm"] if a.op == "all" else [a.op]
+    for op in ops:
+        if op == "qmm4":
+            r = bench_qmm(a, 4, 64)
+        elif op == "qmm8":
+            r = bench_qmm(a, 8, 128)
+        elif op in ("linear", "rmsnorm"):
+            r = bench_linear(a)
+        elif op == "decode":
+            r = bench_decode(a)
+        elif op == "prefill":
+            r = bench_prefill(a)
+        else:
+            r = bench_gemm(a)
+        r.setdefault("n_gpus", 1)
+        r.setdefault("steps", a.steps)
+        r.setdefault("warmup", a.warmup)
+        r.setdefault("higher_is_better", True)
+        r.setdefault("scaling", "weak")
+        r.setdefault("vs_baseline", None)
+        r.setdefault("data", "synthetic (seeded torch.Generator, random-init weights)")
+        r.setdefault("gpu", torch.cuda.get_device_name(0))
+        print(json.dumps(r), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

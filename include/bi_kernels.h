@@ -1,0 +1,136 @@
+/*
+ * bi_kernels.h — C ABI of the MI355X (gfx950) batch-invariant kernel library.
+ *
+ * Every entry point is asynchronous on the caller's HIP stream (`stream` is a
+ * hipStream_t passed as a plain pointer; NULL means the default stream), never
+ * allocates, frees or synchronises, and validates its arguments before it
+ * launches anything.
+ *
+ * Return codes: 0 = ok; BI_E_INVALID_ARG / BI_E_UNSUPPORTED / BI_E_WORKSPACE
+ * (negative) = rejected before launch, nothing was enqueued; >0 = the
+ * hipError_t of a failed launch. bi_last_error() returns a thread-local
+ * message describing the last non-zero return on the calling thread.
+ *
+ * Buffers are device pointers owned by the caller. Element type is chosen by
+ * `dtype` (BI_F32 / BI_F16 / BI_BF16) and is the same for every floating-point
+ * operand of a call; accumulation is always fp32.
+ *
+ * The reference ("mlx-batch-invariant") has no native ABI: its kernels are Metal
+ * source strings launched through mx.fast.metal_kernel from Python. Each entry
+ * point below replaces one of those Python launchers; the citation names it.
+ */
+#ifndef BI_KERNELS_H
+#define BI_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BI_ABI_VERSION 1
+
+enum bi_dtype { BI_F32 = 0, BI_F16 = 1, BI_BF16 = 2 };
+
+enum bi_status {
+  BI_OK = 0,
+  BI_E_INVALID_ARG = -1, /* shapes, strides, alignment or pointers are wrong */
+  BI_E_UNSUPPORTED = -2, /* valid request this library has no kernel for    */
+  BI_E_WORKSPACE = -3    /* workspace missing or smaller than required      */
+};
+
+/* Contract constants. They fix the reduction order, so changing either one
+ * changes result bits. Reference: kernels/matmul.py:46 (GROUP_K = 256),
+ * kernels/attention.py:38 (SPLIT_SIZE = 256). */
+#define BI_GROUP_K 256
+#define BI_SPLIT_KEYS 256
+
+int bi_abi_version(void);
+const char* bi_last_error(void);
+/* Threshold of the launch-shape policy: GEMMs with M <= this many rows run one
+ * workgroup per (tile, K group) plus an ordered fold kernel. Launch shape only;
+ * it never changes bits. Reference: kernels/matmul.py:47 (SPLIT_M_MAX). */
+int bi_split_m_max(void);
+
+/* ---- RMSNorm --------------------------------------------------------------
+ * out[r, :] = T( (float(x[r, :]) * inv_r) * float(w) ),
+ * inv_r = 1 / sqrt( ss_r / D + eps ), ss_r reduced in a fixed order that
+ * depends on D only. w may be NULL (all ones). x rows are `x_row_stride`
+ * elements apart; out is contiguous [rows, D].
+ * Replaces: kernels/rmsnorm.py:64-79 (batch_invariant_rms_norm) and its
+ * kernel kernels/rmsnorm.py:19-47. */
+int bi_rms_norm(const void* x, int64_t x_row_stride, const void* w, void* out,
+                int64_t rows, int64_t D, float eps, int dtype, void* stream);
+
+/* ---- Dense matmul ---------------------------------------------------------
+ * out[M, N] = a[M, K] @ b[K, N], with b given transposed: element b[k, n] is at
+ * bt[n * ldb + k] (the k-contiguous nn.Linear weight layout). a rows are lda
+ * elements apart; out is contiguous [M, N]. Requires K % 8 == 0, lda % 8 == 0,
+ * ldb % 8 == 0 and 16-byte aligned a/bt (the Python layer pads or copies
+ * otherwise, which does not change bits).
+ * The workspace holds fp32 group partials for small-M launches; query its
+ * size with bi_matmul_workspace_bytes (0 means none needed).
+ * Replaces: kernels/matmul.py:279-314 (launch_tiled) + :317-340
+ * (batch_invariant_matmul), kernels :81-234. */
+size_t bi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out,
+              int64_t M, int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes,
+              void* stream);
+
+/* ---- Affine quantized matmul (MLX packed format) ---------------------------
+ * out[M, N] = x[M, K] @ W^T with W[n, k] = T(fmaf(code(n,k), scale, bias)),
+ * code(n, k) = (w[n, k*bits/32] >> (bits * (k % (32/bits)))) & (2^bits - 1),
+ * scale/bias = scales/biases[n, k / group_size] (element type = dtype).
+ * w is contiguous uint32 [N, K*bits/32]; scales, biases contiguous
+ * [N, K/group_size]. bits in {4, 8}, group_size in {32, 64, 128},
+ * K % group_size == 0. x rows are ldx elements apart (ldx % 8 == 0).
+ * Replaces: kernels/quantized.py:106-125 (batch_invariant_quantized_matmul),
+ * kernels :33-67 (dequant-on-stage). */
+size_t bi_quantized_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                        const void* biases, void* out, int64_t M, int64_t N, int64_t K,
+                        int bits, int group_size, int dtype, void* ws, size_t ws_bytes,
+                        void* stream);
+
+/* ---- Split-KV decode attention (one query token per sequence) -------------
+ * q [B, Hq, D], k/v [B, Hkv, L, D] addressed through element strides
+ *   strides[0..1] = q  (batch, head)
+ *   strides[2..4] = k  (batch, head, position)
+ *   strides[5..7] = v  (batch, head, position)
+ * with d contiguous. out contiguous [B, Hq, D]. kv_lens (device int32[B], may
+ * be NULL = all L) gives each sequence's own key count, 1 <= len <= L; a
+ * sequence's output depends only on its own first len keys. Hq % Hkv == 0,
+ * D in {64, 128}. Keys go in fixed splits of BI_SPLIT_KEYS; the workspace
+ * holds per-split (m, l, acc) partials (bi_attn_decode_workspace_bytes).
+ * Replaces: kernels/attention.py:326-365 (batch_invariant_decode_attention),
+ * kernels :47-171; kv_lens is an extension the reference lacks. */
+size_t bi_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t L, int64_t D);
+int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                   void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                   const int64_t* strides, float scale, int dtype, void* ws,
+                   size_t ws_bytes, void* stream);
+
+/* ---- Prefill attention (any number of query tokens) ------------------------
+ * q [B, Hq, Tq, D], k/v [B, Hkv, L, D] through element strides
+ *   strides[0..2] = q (batch, head, token)
+ *   strides[3..5] = k (batch, head, position)
+ *   strides[6..8] = v (batch, head, position)
+ * out contiguous [B, Hq, Tq, D]. With causal != 0, query t of sequence b sees
+ * keys [0, len_b - Tq + t + 1) (bottom-right aligned, so a later chunk of a
+ * prompt run against the whole cache is a valid prefill); otherwise all len_b.
+ * len_b = kv_lens[b] (device int32[B], may be NULL = L), Tq <= len_b <= L when
+ * causal. Same split order and per-key update as bi_attn_decode, so a token's
+ * output equals a later decode step's and chunked equals one-shot prefill.
+ * Replaces: kernels/attention.py:368-390 (batch_invariant_prefill_attention),
+ * kernels :173-254. */
+int bi_attn_prefill(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                    void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
+                    int64_t D, const int64_t* strides, int causal, float scale, int dtype,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BI_KERNELS_H */

@@ -1,0 +1,95 @@
+"""Build the gfx950 kernel library ``libbi_kernels.so`` in-tree.
+
+    python mlx-batch-invariant_amd/csrc/build.py [--jobs N] [--verbose]
+
+Every ``*.hip`` file in this directory is compiled with hipcc for gfx950 and
+linked into ``mlx_batch_invariant_amd/libbi_kernels.so`` next to the Python
+package. The library links the HIP runtime by its SONAME (libamdhip64.so.7),
+so inside a process that has imported torch it binds to the runtime torch
+already loaded and shares torch's streams and allocations.
+
+Numerics flags are part of the batch-invariance contract and must not be
+changed per file: no fp contraction (every fma is explicit), no fast math,
+IEEE division and sqrt, denormals kept, and no packed-fp32 instructions.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+PKG = HERE.parent / "mlx_batch_invariant_amd"
+OUT = PKG / "libbi_kernels.so"
+OBJ = HERE / "_build"
+
+ARCH = "gfx950"
+CFLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fno-fast-math",
+    "-fno-gpu-flush-denormals-to-zero",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-mcode-object-version=5",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build the kernel library)")
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature; harmless.
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    cc = hipcc()
+    OBJ.mkdir(exist_ok=True)
+    srcs = sorted(HERE.glob("*.hip"))
+    objs = [OBJ / (s.stem + ".o") for s in srcs]
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [ex.submit(_run, [cc, *CFLAGS, "-c", str(s), "-o", str(o)], verbose)
+                for s, o in zip(srcs, objs)]
+        for f in futs:
+            f.result()
+    tmp = OUT.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--jobs", type=int, default=None)
+    p.add_argument("--verbose", action="store_true")
+    a = p.parse_args(argv)
+    out = build(a.jobs, a.verbose)
+    print(f"built {out}")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

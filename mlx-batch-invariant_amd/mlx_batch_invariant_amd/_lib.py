@@ -1,0 +1,122 @@
+"""ctypes binding of the gfx950 kernel library (``libbi_kernels.so``).
+
+The library is the only compute path: there is no CPU or PyTorch fallback
+inside the ``batch_invariant_*`` functions. If the library is missing on a
+machine with a GPU, every call raises. Unsupported *inputs* (CPU tensors,
+unsupported dtypes, masks, ...) are a separate matter handled by ``ops.py``,
+which counts them as fallbacks to the stock torch op, or raises in strict mode,
+as the reference does (mlx_batch_invariant/ops.py:36-39).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_NAME = "libbi_kernels.so"
+LIB_PATH = Path(os.environ.get("BI_KERNELS_LIB", Path(__file__).resolve().parent / LIB_NAME))
+
+BI_F32, BI_F16, BI_BF16 = 0, 1, 2
+DTYPE_CODE = {torch.float32: BI_F32, torch.float16: BI_F16, torch.bfloat16: BI_BF16}
+FLOAT_DTYPES = tuple(DTYPE_CODE)
+
+GROUP_K = 256      # fixed K group of the matmul fold (contract constant)
+SPLIT_KEYS = 256   # fixed attention split size (contract constant)
+
+_c_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+
+# name -> (restype, argtypes); must match include/bi_kernels.h
+_SIGNATURES = {
+    "bi_abi_version": (ctypes.c_int, []),
+    "bi_last_error": (ctypes.c_char_p, []),
+    "bi_split_m_max": (ctypes.c_int, []),
+    "bi_rms_norm": (ctypes.c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, ctypes.c_float, ctypes.c_int, _vp]),
+    "bi_matmul_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
+    "bi_matmul": (ctypes.c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
+                                 _vp, ctypes.c_size_t, _vp]),
+    "bi_quantized_matmul_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
+    "bi_quantized_matmul": (ctypes.c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64,
+                                           ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t, _vp]),
+    "bi_attn_decode_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64, _c_i64]),
+    "bi_attn_decode": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                      ctypes.POINTER(_c_i64), ctypes.c_float, ctypes.c_int, _vp,
+                                      ctypes.c_size_t, _vp]),
+    "bi_attn_prefill": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                       _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_float,
+                                       ctypes.c_int, _vp]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class KernelLibraryError(RuntimeError):
+    """The kernel library is missing, stale, or a call into it failed."""
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once (after torch, so the HIP runtime is shared)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise KernelLibraryError(
+                f"{LIB_PATH} not found: build it with `python mlx-batch-invariant_amd/csrc/build.py` "
+                "(or __graft_entry__.build())")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.bi_abi_version() != 1:
+            raise KernelLibraryError(f"{LIB_PATH}: ABI version {lib.bi_abi_version()} != 1")
+        _lib = lib
+        return lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_SIGNATURES)
+
+
+def gpu_available() -> bool:
+    return torch.cuda.is_available()
+
+
+def is_gpu_tensor(t) -> bool:
+    return isinstance(t, torch.Tensor) and t.is_cuda
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().bi_last_error().decode(errors="replace")
+        kind = {-1: ValueError, -2: NotImplementedError, -3: ValueError}.get(rc, KernelLibraryError)
+        raise kind(f"{what} failed (code {rc}): {msg}")
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def workspace(nbytes: int, device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def require_gpu(what: str, *tensors) -> None:
+    for t in tensors:
+        if t is not None and not is_gpu_tensor(t):
+            raise ValueError(f"{what}: the batch-invariant kernels run on the GPU; got a tensor on {t.device}")
+    load()

@@ -1,0 +1,34 @@
+"""Batch-invariant gfx950 kernels (hand-written HIP, C ABI in include/bi_kernels.h).
+
+Every kernel obeys one rule (reference: mlx_batch_invariant/kernels/__init__.py:1-17):
+the floating-point reduction order of an output element never depends on how many
+*other* rows or sequences share the launch.
+
+* matmul / quantized matmul: fixed 256-wide K groups, one MFMA instruction and one
+  k-slot map for every tile shape, group partials folded left to right in fp32;
+* rmsnorm: one workgroup per row, fixed-stride partials, fixed-shape wave/LDS tree;
+* attention: fixed 256-key splits folded in index order, one shared per-key update.
+
+Only the launch shape adapts to the batch. Division and sqrt are correctly
+rounded, expf is the full-precision device expf, every fma is explicit and the
+build forbids fp contraction and fast math, so compiler choices cannot make two
+kernels disagree.
+"""
+
+from .matmul import batch_invariant_matmul
+from .rmsnorm import batch_invariant_rms_norm
+from .quantized import batch_invariant_quantized_matmul
+from .attention import (
+    batch_invariant_attention,
+    batch_invariant_decode_attention,
+    batch_invariant_prefill_attention,
+)
+
+__all__ = [
+    "batch_invariant_matmul",
+    "batch_invariant_rms_norm",
+    "batch_invariant_quantized_matmul",
+    "batch_invariant_decode_attention",
+    "batch_invariant_prefill_attention",
+    "batch_invariant_attention",
+]

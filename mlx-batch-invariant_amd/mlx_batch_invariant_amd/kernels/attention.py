@@ -1,0 +1,168 @@
+"""Batch-invariant split-KV attention on gfx950.
+
+Canonical order per (sequence, head, query) (reference:
+mlx_batch_invariant/kernels/attention.py:1-32):
+
+* keys are processed in fixed splits of ``SPLIT_SIZE`` = 256 in index order;
+  key ``j`` always lands in split ``j // 256`` at the same position;
+* the score is ``fp32(dot(q, k_j) * scale)`` with the dot taken by a fixed
+  chain of ``v_mfma_f32_16x16x32`` steps over the head dimension;
+* inside a split the online softmax runs key by key:
+  ``m' = max(m, s); corr = exp(m - m'); p = exp(s - m'); l = fma(l, corr, p);
+  acc = fma(acc, corr, p * v)`` from exact zeros;
+* splits are merged left to right with ``c_old = exp(M - M'); c_new = exp(m - M');
+  L = fma(L, c_old, l * c_new); A = fma(A, c_old, acc * c_new)``, and the
+  output is ``T(A / L)``.
+
+Decode (T_q == 1) writes per-split partials and folds them in a combine
+kernel; prefill folds in registers. Both kernels include the same per-key
+update and merge source, so a token's output from prefill equals the output
+of a later decode step for that position, and chunked prefill equals one-shot
+prefill. Causal masking is bottom-right aligned (query t of a T_q-token chunk
+sees ``len - T_q + t + 1`` keys), as in MLX.
+
+``kv_lens`` (int32 [B], optional) is an extension the reference does not have:
+sequence b uses only its first ``kv_lens[b]`` keys, and its output is bit-for-bit
+what it would be alone with K/V cut to that length.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+SPLIT_SIZE = _lib.SPLIT_KEYS
+SUPPORTED_HEAD_DIMS = (64, 128)
+
+
+def supports(q, k, v, mask, sinks=None) -> bool:
+    """Reference predicate kernels/attention.py:299-310 (mask None or "causal")."""
+    try:
+        return bool(
+            q.ndim == 4 and k.ndim == 4 and v.ndim == 4
+            and (mask is None or (isinstance(mask, str) and mask == "causal"))
+            and sinks is None
+            and q.shape[1] % k.shape[1] == 0
+            and k.shape == v.shape
+            and q.shape[-1] == k.shape[-1]
+            and q.shape[-1] in SUPPORTED_HEAD_DIMS
+            and q.shape[0] == k.shape[0]
+            and (mask is None or q.shape[2] <= k.shape[2])
+            and q.dtype in _lib.FLOAT_DTYPES
+            and all(_lib.is_gpu_tensor(t) for t in (q, k, v))
+        )
+    except (AttributeError, TypeError):
+        return False
+
+
+def _prep(q, k, v):
+    dt = q.dtype
+    if dt not in _lib.FLOAT_DTYPES:
+        raise ValueError(f"attention: unsupported dtype {dt}")
+    if k.dtype != dt:
+        k = k.to(dt)
+    if v.dtype != dt:
+        v = v.to(dt)
+    return dt, k, v
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    es = t.element_size()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all((t.stride(i) * es) % 16 == 0 and t.stride(i) >= 0 for i in range(t.ndim - 1)))
+
+
+def _fix(t: torch.Tensor) -> torch.Tensor:
+    return t if _aligned(t) else t.contiguous()
+
+
+def _lens(kv_lens, B: int, L: int, device) -> torch.Tensor | None:
+    if kv_lens is None:
+        return None
+    kl = torch.as_tensor(kv_lens, dtype=torch.int32, device=device).reshape(-1).contiguous()
+    if kl.numel() != B:
+        raise ValueError(f"kv_lens has {kl.numel()} entries for batch {B}")
+    return kl
+
+
+def _check_split(split_size: int) -> None:
+    if split_size != SPLIT_SIZE:
+        raise ValueError(f"split_size is a contract constant ({SPLIT_SIZE}); got {split_size}")
+
+
+def batch_invariant_decode_attention(q, k, v, *, scale: float, split_size: int = SPLIT_SIZE,
+                                     kv_lens=None) -> torch.Tensor:
+    """T_q == 1. Per-split partials (the GU query heads of a kv head share each
+    K/V row), then an ordered combine (reference: kernels/attention.py:326-365)."""
+    _check_split(split_size)
+    B, Hq, Tq, D = q.shape
+    _, Hkv, L, _ = k.shape
+    if Tq != 1:
+        raise ValueError(f"decode attention needs T_q == 1, got {Tq}")
+    if D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
+        raise ValueError(f"decode attention: unsupported shape q {tuple(q.shape)} k {tuple(k.shape)}")
+    dt, k, v = _prep(q, k, v)
+    _lib.require_gpu("batch_invariant_decode_attention", q, k, v)
+    q3 = _fix(q[:, :, 0, :])
+    k = _fix(k)
+    v = _fix(v)
+    kl = _lens(kv_lens, B, L, q.device)
+    out = torch.empty((B, Hq, 1, D), dtype=dt, device=q.device)
+    if B == 0:
+        return out
+    lib = _lib.load()
+    ws_bytes = lib.bi_attn_decode_workspace_bytes(B, Hq, L, D)
+    ws = _lib.workspace(ws_bytes, q.device)
+    strides = (_lib._c_i64 * 8)(q3.stride(0), q3.stride(1), k.stride(0), k.stride(1), k.stride(2),
+                                v.stride(0), v.stride(1), v.stride(2))
+    rc = lib.bi_attn_decode(q3.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
+                            B, Hq, Hkv, L, D, strides, float(scale), _lib.DTYPE_CODE[dt],
+                            _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
+    _lib.check(rc, "bi_attn_decode")
+    return out
+
+
+def batch_invariant_prefill_attention(q, k, v, *, scale: float, causal: bool,
+                                      split_size: int = SPLIT_SIZE, kv_lens=None) -> torch.Tensor:
+    """Any T_q. Blocks of 16 (token, head) rows share each K/V row; same split
+    loop and merge as decode (reference: kernels/attention.py:368-390)."""
+    _check_split(split_size)
+    B, Hq, Tq, D = q.shape
+    _, Hkv, L, _ = k.shape
+    if D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
+        raise ValueError(f"prefill attention: unsupported shape q {tuple(q.shape)} k {tuple(k.shape)}")
+    if causal and Tq > L:
+        raise ValueError(f"causal prefill needs T_q <= L (T_q={Tq}, L={L})")
+    dt, k, v = _prep(q, k, v)
+    _lib.require_gpu("batch_invariant_prefill_attention", q, k, v)
+    q = _fix(q)
+    k = _fix(k)
+    v = _fix(v)
+    kl = _lens(kv_lens, B, L, q.device)
+    out = torch.empty((B, Hq, Tq, D), dtype=dt, device=q.device)
+    if B == 0 or Tq == 0:
+        return out
+    lib = _lib.load()
+    strides = (_lib._c_i64 * 9)(q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1),
+                                k.stride(2), v.stride(0), v.stride(1), v.stride(2))
+    rc = lib.bi_attn_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
+                             B, Hq, Hkv, Tq, L, D, strides, 1 if causal else 0, float(scale),
+                             _lib.DTYPE_CODE[dt], _lib.stream_of(q))
+    _lib.check(rc, "bi_attn_prefill")
+    return out
+
+
+def batch_invariant_attention(q, k, v, *, scale: float | None = None, mask=None, kv_lens=None) -> torch.Tensor:
+    """Dispatch: decode path for T_q == 1, prefill otherwise (reference:
+    kernels/attention.py:393-397). ``mask`` is None or "causal"."""
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    if mask is not None and mask != "causal":
+        raise ValueError("batch_invariant_attention: mask must be None or 'causal'")
+    if q.shape[2] == 1:
+        return batch_invariant_decode_attention(q, k, v, scale=scale, kv_lens=kv_lens)
+    return batch_invariant_prefill_attention(q, k, v, scale=scale, causal=(mask == "causal"),
+                                             kv_lens=kv_lens)

@@ -1,0 +1,99 @@
+"""Batch-invariant matmul: C[M, N] = A[M, K] @ B[K, N] on gfx950.
+
+Canonical reduction order (reference: mlx_batch_invariant/kernels/matmul.py:1-38):
+
+* K is cut into fixed groups of ``GROUP_K`` = 256; group ``g`` covers
+  ``k in [256 g, 256 g + 256)`` whatever M, N or the launch shape.
+* Inside a group, eight ``v_mfma_f32_16x16x32`` steps (operands in the input
+  dtype, fp32 accumulator starting from exact zero) walk the group with the
+  fixed k-slot map ``k = 256 g + 64 q + 8 s + e`` (lane quarter q, step s,
+  element e). fp32 inputs use a chain of ``v_mfma_f32_16x16x4_f32``.
+* The output is the left fold ``((0 + p_0) + p_1) + ...`` of group partials
+  as plain fp32 adds, rounded once to the output dtype.
+
+Launch shapes that only change who computes an element: M <= ``SPLIT_M_MAX``
+with more than one group writes fp32 group partials and folds them in a
+second kernel; larger M folds in registers. The choice never changes bits.
+
+B is consumed transposed (``bt[n, k]``, k contiguous), which is how
+``nn.Linear`` stores its weight, so ``x @ W.T`` needs no copy. Other layouts
+and odd K are copied / zero-padded first; neither changes the arithmetic.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+GROUP_K = _lib.GROUP_K
+SPLIT_M_MAX = 32
+
+
+def _kcontig(t: torch.Tensor) -> bool:
+    """Rows k-contiguous with 16-byte aligned row starts (what the kernel reads)."""
+    es = t.element_size()
+    return (t.stride(-1) == 1 and (t.stride(0) * es) % 16 == 0 and t.data_ptr() % 16 == 0
+            and t.stride(0) >= t.shape[-1])
+
+
+def _prep_rows(t: torch.Tensor, K8: int) -> torch.Tensor:
+    """[R, K] -> [R, K8] k-contiguous, 16-byte aligned rows, zero-padded to K8."""
+    K = t.shape[1]
+    if K8 == K and _kcontig(t):
+        return t
+    out = torch.zeros((t.shape[0], K8), dtype=t.dtype, device=t.device)
+    out[:, :K] = t
+    return out
+
+
+def matmul_bt(a2: torch.Tensor, bt: torch.Tensor) -> torch.Tensor:
+    """out[M, N] = a2[M, K] @ bt[N, K].T, both already the output dtype, on the GPU."""
+    M, K = a2.shape
+    N = bt.shape[0]
+    out = torch.empty((M, N), dtype=a2.dtype, device=a2.device)
+    if M == 0:
+        return out
+    if N == 0 or K == 0:
+        return out.zero_()
+    K8 = (K + 7) // 8 * 8
+    a2 = _prep_rows(a2, K8)
+    bt = _prep_rows(bt, K8)
+    lib = _lib.load()
+    ws_bytes = lib.bi_matmul_workspace_bytes(M, N, K8)
+    ws = _lib.workspace(ws_bytes, a2.device)
+    rc = lib.bi_matmul(a2.data_ptr(), a2.stride(0), bt.data_ptr(), bt.stride(0), out.data_ptr(),
+                       M, N, K8, _lib.DTYPE_CODE[a2.dtype], _lib.ptr(ws), ws_bytes,
+                       _lib.stream_of(a2))
+    _lib.check(rc, "bi_matmul")
+    return out
+
+
+def batch_invariant_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a @ b`` for 2-D ``b`` with a batch-invariant reduction order.
+
+    ``a`` may have leading dims; they are flattened into M. ``b`` must be 2-D
+    (a transposed view such as ``W.T`` is consumed in place). Accumulation is
+    fp32; the output dtype is the promoted input dtype
+    (reference: kernels/matmul.py:317-340).
+    """
+    if b.ndim != 2:
+        raise ValueError("batch_invariant_matmul: b must be 2-D")
+    if a.ndim < 1:
+        raise ValueError("batch_invariant_matmul: a must have at least one dim")
+    K = a.shape[-1]
+    if K != b.shape[0]:
+        raise ValueError(f"shape mismatch {tuple(a.shape)} @ {tuple(b.shape)}")
+    out_dtype = torch.result_type(a, b)
+    if out_dtype not in _lib.FLOAT_DTYPES:
+        raise ValueError(f"batch_invariant_matmul: unsupported dtype {out_dtype}")
+    _lib.require_gpu("batch_invariant_matmul", a, b)
+    lead = a.shape[:-1]
+    N = b.shape[1]
+    a2 = a.reshape(-1, K)
+    if a2.dtype != out_dtype:
+        a2 = a2.to(out_dtype)
+    if b.dtype != out_dtype:
+        b = b.to(out_dtype)
+    out = matmul_bt(a2, b.t())
+    return out.reshape(*lead, N)

@@ -1,0 +1,206 @@
+"""Functional entry points with explicit fallback accounting.
+
+Torch counterpart of mlx_batch_invariant/ops.py:1-104. Each op has the
+signature of the stock torch op it stands in for and returns the
+batch-invariant result when a kernel supports the inputs; otherwise it calls
+the stock op (captured at import, so patching never recurses) and records a
+fallback under ``"op:reason"``, or raises ``RuntimeError`` when the mode is
+strict. "Deterministic" with ten silent fallbacks is not deterministic, so the
+counters are public through ``stats()``.
+
+Counter keys (same as the reference): handled ``matmul``, ``addmm``,
+``quantized_matmul``, ``rms_norm``, ``sdpa_decode``, ``sdpa_prefill``;
+fallbacks ``matmul:non-2d-rhs-or-non-float``, ``addmm:non-2d-rhs-or-non-float``,
+``quantized_matmul:{mode}-{bits}bit-g{gs}-{T|N}``, ``rms_norm:non-float``,
+``sdpa:array-mask``, ``sdpa:sinks-or-shape``. One reason is new: inputs
+that are not GPU tensors fall back as ``{op}:non-gpu-tensor``.
+"""
+
+from __future__ import annotations
+
+import math
+from collections import Counter
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .kernels import (
+    batch_invariant_attention,
+    batch_invariant_matmul,
+    batch_invariant_quantized_matmul,
+    batch_invariant_rms_norm,
+)
+from .kernels import attention as _attn
+from .kernels import quantized as _quant
+
+# Stock implementations, captured at import so patching never recurses.
+_orig_matmul = torch.matmul
+_orig_mm = torch.mm
+_orig_addmm = torch.addmm
+_orig_tensor_matmul = torch.Tensor.__matmul__
+_orig_linear = F.linear
+_orig_rms_norm = F.rms_norm
+_orig_sdpa = F.scaled_dot_product_attention
+
+handled: Counter = Counter()
+fallbacks: Counter = Counter()
+strict: bool = False
+
+
+def _fallback(op: str, reason: str):
+    fallbacks[f"{op}:{reason}"] += 1
+    if strict:
+        raise RuntimeError(f"batch-invariant mode: no kernel for {op} ({reason})")
+
+
+def _is_float(x) -> bool:
+    return isinstance(x, torch.Tensor) and x.dtype in _lib.FLOAT_DTYPES
+
+
+def _on_gpu(*ts) -> bool:
+    return all(_lib.is_gpu_tensor(t) for t in ts if t is not None)
+
+
+def _mm_reason(a, b) -> str | None:
+    """None if the dense kernel takes (a, b); else the fallback reason."""
+    if not (_is_float(a) and _is_float(b) and b.ndim == 2 and a.ndim >= 1):
+        return "non-2d-rhs-or-non-float"
+    if not _on_gpu(a, b) or a.device != b.device:
+        return "non-gpu-tensor"
+    return None
+
+
+def matmul(a, b, *, out=None):
+    reason = "out-argument" if out is not None else _mm_reason(a, b)
+    if reason is None:
+        handled["matmul"] += 1
+        return batch_invariant_matmul(a, b)
+    _fallback("matmul", reason)
+    return _orig_matmul(a, b) if out is None else _orig_matmul(a, b, out=out)
+
+
+def mm(a, b, *, out=None):
+    reason = "out-argument" if out is not None else _mm_reason(a, b)
+    if reason is None and a.ndim == 2:
+        handled["matmul"] += 1
+        return batch_invariant_matmul(a, b)
+    _fallback("matmul", reason or "non-2d-rhs-or-non-float")
+    return _orig_mm(a, b) if out is None else _orig_mm(a, b, out=out)
+
+
+def tensor_matmul(self, other):
+    reason = _mm_reason(self, other)
+    if reason is None:
+        handled["matmul"] += 1
+        return batch_invariant_matmul(self, other)
+    _fallback("matmul", reason)
+    return _orig_tensor_matmul(self, other)
+
+
+def addmm(c, a, b, *, beta=1, alpha=1, out=None):
+    reason = "out-argument" if out is not None else _mm_reason(a, b)
+    if reason is None and a.ndim != 2:
+        reason = "non-2d-rhs-or-non-float"
+    if reason is None and isinstance(c, torch.Tensor) and not _on_gpu(c):
+        reason = "non-gpu-tensor"
+    if reason is None:
+        handled["addmm"] += 1
+        prod = batch_invariant_matmul(a, b)
+        if alpha != 1:
+            prod = prod * alpha
+        return prod + (c if beta == 1 else c * beta)
+    _fallback("addmm", reason)
+    kw = {"beta": beta, "alpha": alpha}
+    return _orig_addmm(c, a, b, **kw) if out is None else _orig_addmm(c, a, b, out=out, **kw)
+
+
+def linear(input, weight, bias=None):
+    """``F.linear``: ``input @ weight.T (+ bias)``. Counted as ``matmul`` without
+    bias and ``addmm`` with bias, like MLX's nn.Linear (x @ W.T / mx.addmm)."""
+    op = "matmul" if bias is None else "addmm"
+    reason = _mm_reason(input, weight.t() if isinstance(weight, torch.Tensor) and weight.ndim == 2 else weight)
+    if reason is None and bias is not None and not _on_gpu(bias):
+        reason = "non-gpu-tensor"
+    if reason is None:
+        handled[op] += 1
+        prod = batch_invariant_matmul(input, weight.t())
+        return prod if bias is None else prod + bias
+    _fallback(op, reason)
+    return _orig_linear(input, weight, bias)
+
+
+def quantized_matmul(x, w, scales, biases=None, transpose: bool = True, group_size=None,
+                     bits=None, mode: str = "affine"):
+    """Signature of mx.quantized_matmul (reference ops.py:65-77). There is no
+    stock torch op for the MLX affine format; the stock path is dequantize +
+    torch.matmul."""
+    gs = 64 if group_size is None else group_size
+    b = 4 if bits is None else bits
+    if _quant.supports(x, w, scales, biases, transpose, gs, b, mode):
+        handled["quantized_matmul"] += 1
+        return batch_invariant_quantized_matmul(x, w, scales, biases, group_size=gs, bits=b)
+    _fallback("quantized_matmul", f"{mode}-{b}bit-g{gs}-{'T' if transpose else 'N'}")
+    if mode != "affine" or biases is None:
+        raise NotImplementedError(f"quantized_matmul: no stock path for mode={mode!r} without biases")
+    W = _quant.dequantize(w, scales, biases, gs, b, dtype=x.dtype)
+    return _orig_matmul(x, W.t() if transpose else W)
+
+
+def rms_norm(input, normalized_shape, weight=None, eps=None):
+    if isinstance(normalized_shape, int):
+        normalized_shape = (normalized_shape,)
+    shape_ok = (isinstance(input, torch.Tensor)
+                and tuple(input.shape[input.ndim - len(normalized_shape):]) == tuple(normalized_shape))
+    if _is_float(input) and shape_ok and (weight is None or _is_float(weight)):
+        if _on_gpu(input, weight):
+            handled["rms_norm"] += 1
+            D = math.prod(normalized_shape)
+            e = torch.finfo(input.dtype).eps if eps is None else eps
+            x2 = input.reshape(*input.shape[:input.ndim - len(normalized_shape)], D)
+            w2 = None if weight is None else weight.reshape(D)
+            return batch_invariant_rms_norm(x2, w2, e).reshape(input.shape)
+        _fallback("rms_norm", "non-gpu-tensor")
+    else:
+        _fallback("rms_norm", "non-float")
+    return _orig_rms_norm(input, normalized_shape, weight, eps)
+
+
+def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.0,
+                                 is_causal=False, scale=None, enable_gqa=False, **kwargs):
+    """``F.scaled_dot_product_attention``. ``is_causal`` follows torch's
+    top-left alignment; for T_q <= L that equals the kernel's bottom-right
+    causal mask on the first T_q keys, so that is what is run."""
+    q, k, v = query, key, value
+    ok = (attn_mask is None and dropout_p == 0.0 and not kwargs
+          and isinstance(q, torch.Tensor) and q.ndim == 4 and k.ndim == 4
+          and (q.shape[1] == k.shape[1] or enable_gqa)
+          and not (is_causal and q.shape[2] > k.shape[2]))
+    if ok:
+        if is_causal and q.shape[2] < k.shape[2]:
+            k = k[:, :, : q.shape[2]]
+            v = v[:, :, : q.shape[2]]
+        mask = "causal" if is_causal else None
+        if _attn.supports(q, k, v, mask):
+            handled["sdpa_decode" if q.shape[2] == 1 else "sdpa_prefill"] += 1
+            sc = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+            return batch_invariant_attention(q, k, v, scale=sc, mask=mask)
+    if isinstance(attn_mask, torch.Tensor):
+        reason = "array-mask"
+    elif ok and not _on_gpu(q, k, v):
+        reason = "non-gpu-tensor"
+    else:
+        reason = "sinks-or-shape"
+    _fallback("sdpa", reason)
+    extra = {"enable_gqa": enable_gqa} if enable_gqa else {}
+    return _orig_sdpa(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
+                      is_causal=is_causal, scale=scale, **extra, **kwargs)
+
+
+def reset_stats():
+    handled.clear()
+    fallbacks.clear()
+
+
+def stats() -> dict:
+    return {"handled": dict(handled), "fallbacks": dict(fallbacks)}

@@ -1,0 +1,347 @@
+"""CPU oracle: numpy restatement of the batch-invariant kernels' arithmetic.
+
+TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s ``cpu_baseline`` leg may import this module, and only as the
+checker (or the timed CPU baseline). The product path never calls it.
+
+Each function restates one canonical reduction order of the reference,
+mlx-batch-invariant (files cited per function), in the concrete form the
+gfx950 kernels commit to. All arithmetic is float32 unless stated;
+``fma(a, b, c)`` is emulated as one float64 evaluation rounded once to
+float32, which is exact whenever ``a * b`` fits 53 bits and the sum does not
+straddle a float32 rounding tie (always true for the bf16/fp16 products used
+here; otherwise it can differ from a hardware fma in the last float32 bit).
+
+Pinning (how each function is checked, tests/test_oracle.py):
+
+* ``rms_norm``          float64 closed form (tolerance), permutation/scale
+                        invariants, bit-exact squares-sum cases.
+* ``unpack`` /
+  ``dequantize``        hand-packed known-answer words (tests/golden), brute
+                        force over all 16/256 codes, closed form with Fraction.
+* ``matmul``            integer known-answer tests (every order is exact),
+                        identity operand, float64 GEMM within the fp32 bound,
+                        a planted fold-order mistake that the checks catch.
+* ``attention``         single key -> V, equal scores -> mean of V, one-hot V,
+                        float64 softmax closed form, split-boundary lengths.
+
+Parity of the hardware MFMA's internal summation is modelled, not pinned:
+``matmul`` and the attention scores assume each 32-wide MFMA step adds the
+exact sum of its products to the accumulator with one fp32 rounding. The GPU
+tests therefore compare matmul/attention at a stated tolerance (1 ulp of the
+output type plus an fp32 accumulation bound), and bit-exactly only where the
+arithmetic is exactly specified (RMSNorm, dequantization, integer KATs).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+GROUP_K = 256
+STEPS = 8
+SPLIT = 256
+TG = 256
+VEC = 8
+
+
+# ---------------------------------------------------------------------------
+# Storage types
+# ---------------------------------------------------------------------------
+
+def f32_to_bf16_bits(x) -> np.ndarray:
+    """float32 -> bf16 bit pattern, round to nearest even; NaN -> quiet NaN."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(x)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r = np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+    return r.astype(np.uint16)
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    b = np.ascontiguousarray(b, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_to(x, dtype: str) -> np.ndarray:
+    """Round float32 values to the storage type (RNE) and return them as float32."""
+    x = np.asarray(x, dtype=np.float32)
+    if dtype == "bf16":
+        return bf16_bits_to_f32(f32_to_bf16_bits(x)).reshape(x.shape)
+    if dtype == "f16":
+        return x.astype(np.float16).astype(np.float32)
+    if dtype == "f32":
+        return x.copy()
+    raise ValueError(dtype)
+
+
+def fma32(a, b, c) -> np.ndarray:
+    """fmaf emulated through float64 (see the module docstring for exactness)."""
+    return (np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)).astype(np.float32)
+
+
+def ulp(x, dtype: str) -> np.ndarray:
+    """Spacing of the storage type at |x| (subnormal spacing near zero)."""
+    mant = {"bf16": 7, "f16": 10, "f32": 23}[dtype]
+    emin = {"bf16": -126, "f16": -14, "f32": -126}[dtype]
+    ax = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.where(ax > 0, ax, 1.0)))
+    e = np.maximum(e, emin)
+    return np.exp2(e - mant)
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm — reference kernels/rmsnorm.py:19-47 (fixed-stride partials, fixed
+# tree, precise rsqrt, out = T((x * inv) * w)); gfx950 order: 8-element chunks,
+# thread t owns chunks t, t+256, ...; wave64 xor butterfly 32..1; waves folded
+# left to right; inv = 1 / sqrt(ss / D + eps).
+# ---------------------------------------------------------------------------
+
+def _butterfly64(v: np.ndarray) -> np.ndarray:
+    """v[..., 64] -> lane-0 value of the xor butterfly over offsets 32..1."""
+    idx = np.arange(64)
+    for off in (32, 16, 8, 4, 2, 1):
+        v = (v + v[..., idx ^ off]).astype(np.float32)
+    return v[..., 0]
+
+
+def rms_norm(x, w, eps: float, dtype: str) -> np.ndarray:
+    """x [rows, D] float32 values representable in ``dtype``; w [D] or None."""
+    x = np.asarray(x, np.float32)
+    rows, D = x.shape
+    nchunks = -(-D // VEC)
+    nc = max(1, -(-nchunks // TG))
+    pad = np.zeros((rows, nc * TG * VEC), np.float32)
+    pad[:, :D] = x
+    chunks = pad.reshape(rows, nc, TG, VEC)
+    ss = np.zeros((rows, TG), np.float32)
+    for c in range(nc):
+        for e in range(VEC):
+            v = chunks[:, c, :, e]
+            ss = fma32(v, v, ss)
+    waves = ss.reshape(rows, TG // 64, 64)
+    sums = _butterfly64(waves)                        # [rows, 4]
+    total = sums[:, 0]
+    for i in range(1, TG // 64):
+        total = (total + sums[:, i]).astype(np.float32)
+    mean = (total / np.float32(D)).astype(np.float32)
+    inv = (np.float32(1.0) / np.sqrt((mean + np.float32(eps)).astype(np.float32))).astype(np.float32)
+    wv = np.ones(D, np.float32) if w is None else np.asarray(w, np.float32)
+    out = ((x * inv[:, None]).astype(np.float32) * wv[None, :]).astype(np.float32)
+    return round_to(out, dtype)
+
+
+# ---------------------------------------------------------------------------
+# MLX affine quantization — reference kernels/quantized.py:1-22 (format),
+# :44-67 (dequant-on-stage: fma(float(code), scale, bias) rounded once to T).
+# ---------------------------------------------------------------------------
+
+def unpack(w_u32, bits: int) -> np.ndarray:
+    """uint32 [N, W] -> codes [N, W * 32/bits], code i of a word at bits [bits*i, bits*(i+1))."""
+    w = np.asarray(w_u32).astype(np.uint32).astype(np.uint64)
+    per = 32 // bits
+    shifts = (np.arange(per, dtype=np.uint64) * bits)
+    codes = (w[..., None] >> shifts) & np.uint64((1 << bits) - 1)
+    return codes.reshape(w.shape[0], -1).astype(np.int64)
+
+
+def pack(codes, bits: int) -> np.ndarray:
+    codes = np.asarray(codes, np.uint64)
+    per = 32 // bits
+    N, K = codes.shape
+    c = codes.reshape(N, K // per, per)
+    shifts = (np.arange(per, dtype=np.uint64) * bits)
+    return (c << shifts).sum(-1).astype(np.uint32)
+
+
+def dequantize(w_u32, scales, biases, group_size: int, bits: int, dtype: str) -> np.ndarray:
+    """W[n, k] = T(fmaf(code, scale[n, k//gs], bias[n, k//gs])) as float32."""
+    codes = unpack(w_u32, bits).astype(np.float64)
+    s = np.repeat(np.asarray(scales, np.float64), group_size, axis=1)
+    b = np.repeat(np.asarray(biases, np.float64), group_size, axis=1)
+    return round_to((codes * s + b).astype(np.float32), dtype)
+
+
+# ---------------------------------------------------------------------------
+# Matmul — reference kernels/matmul.py:1-38, :81-190 (fixed 256 K groups, MMA
+# steps from a zero accumulator, group partials folded left to right with
+# plain fp32 adds, :174-176 and the combine :226-234).
+# gfx950 k-slot map: group g, step s, lane quarter q, element e ->
+#   k = 256 g + 64 q + 8 s + e.
+# ---------------------------------------------------------------------------
+
+def step_indices(g: int, s: int) -> np.ndarray:
+    return np.array([GROUP_K * g + 64 * q + 8 * s + e for q in range(4) for e in range(8)])
+
+
+def matmul(a, bt, dtype: str) -> np.ndarray:
+    """out[M, N] = a[M, K] @ bt[N, K].T in the kernels' order.
+
+    16-bit types: one MFMA step adds the exact sum of its 32 products to the
+    accumulator with one fp32 rounding. fp32: the step is a chain of four-
+    product MFMAs (k = 256 g + 64 q + 8 s + e for q = 0..3, one e at a time).
+    """
+    a = np.asarray(a, np.float32)
+    bt = np.asarray(bt, np.float32)
+    M, K = a.shape
+    N = bt.shape[0]
+    G = -(-K // GROUP_K)
+    Kp = G * GROUP_K
+    ap = np.zeros((M, Kp), np.float64)
+    bp = np.zeros((N, Kp), np.float64)
+    ap[:, :K] = a
+    bp[:, :K] = bt
+    total = np.zeros((M, N), np.float32)
+    for g in range(G):
+        acc = np.zeros((M, N), np.float32)
+        for s in range(STEPS):
+            idx = step_indices(g, s)
+            if dtype == "f32":
+                for e in range(8):
+                    sub = idx[e::8]
+                    acc = (acc + ap[:, sub] @ bp[:, sub].T).astype(np.float32)
+            else:
+                acc = (acc + ap[:, idx] @ bp[:, idx].T).astype(np.float32)
+        total = (total + acc).astype(np.float32)
+    return round_to(total, dtype)
+
+
+def matmul_error_bound(a, bt) -> np.ndarray:
+    """A bound on how far two fp32 summation orders of the same products can
+    disagree: 2 * K * 2^-24 * sum_k |a||b|  (per element)."""
+    a = np.abs(np.asarray(a, np.float64))
+    bt = np.abs(np.asarray(bt, np.float64))
+    K = a.shape[1]
+    return 2.0 * K * 2.0 ** -24 * (a @ bt.T)
+
+
+# ---------------------------------------------------------------------------
+# Attention — reference kernels/attention.py:1-32 (canonical order), :47-75
+# (_KEY_UPDATE), :77-85 / :149-171 (_MERGE, combine + precise divide),
+# :173-254 (prefill, nkeys = L - Tq + t + 1 for causal).
+# ---------------------------------------------------------------------------
+
+def _scores(qrows, krows, scale: float) -> np.ndarray:
+    """qrows [R, D], krows [L, D] -> s [R, L] with the MFMA step model over D
+    (step s covers d in [32 s, 32 s + 32)) and an fp32 scale multiply."""
+    R, D = qrows.shape
+    dot = np.zeros((R, krows.shape[0]), np.float32)
+    q64 = qrows.astype(np.float64)
+    k64 = krows.astype(np.float64)
+    for s in range(D // 32):
+        sl = slice(32 * s, 32 * s + 32)
+        dot = (dot + q64[:, sl] @ k64[:, sl].T).astype(np.float32)
+    return (dot * np.float32(scale)).astype(np.float32)
+
+
+def attention(q, k, v, scale: float, causal: bool, dtype: str, kv_lens=None) -> np.ndarray:
+    """q [B, Hq, Tq, D], k/v [B, Hkv, L, D] (float32 values in ``dtype``)."""
+    q = np.asarray(q, np.float32)
+    k = np.asarray(k, np.float32)
+    v = np.asarray(v, np.float32)
+    B, Hq, Tq, D = q.shape
+    Hkv, L = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    out = np.zeros((B, Hq, Tq, D), np.float32)
+    for b in range(B):
+        n_len = L if kv_lens is None else int(kv_lens[b])
+        for hk in range(Hkv):
+            heads = list(range(hk * G, hk * G + G))
+            qrows = q[b, heads].reshape(G * Tq, D)                       # row = (head, token)
+            tok = np.tile(np.arange(Tq), G)
+            nkeys = (n_len - Tq + tok + 1) if causal else np.full(G * Tq, n_len)
+            s_all = _scores(qrows, k[b, hk, :n_len], scale)              # [R, n_len]
+            R = qrows.shape[0]
+            Mx = np.full(R, -np.inf, np.float32)
+            Ls = np.zeros(R, np.float32)
+            A = np.zeros((R, D), np.float32)
+            nsplit = -(-int(nkeys.max()) // SPLIT)
+            for sp in range(nsplit):
+                j0 = sp * SPLIT
+                m = np.full(R, -np.inf, np.float32)
+                l = np.zeros(R, np.float32)
+                acc = np.zeros((R, D), np.float32)
+                for j in range(j0, min(j0 + SPLIT, int(nkeys.max()))):
+                    act = j < nkeys
+                    sj = s_all[:, j]
+                    with np.errstate(invalid="ignore", over="ignore"):
+                        m_new = np.maximum(m, sj)
+                        corr = np.exp((m - m_new).astype(np.float32)).astype(np.float32)
+                        p = np.exp((sj - m_new).astype(np.float32)).astype(np.float32)
+                    l_new = fma32(l, corr, p)
+                    pv = (p[:, None] * v[b, hk, j][None, :]).astype(np.float32)
+                    acc_new = fma32(acc, corr[:, None], pv)
+                    m = np.where(act, m_new, m)
+                    l = np.where(act, l_new, l)
+                    acc = np.where(act[:, None], acc_new, acc)
+                touched = j0 < nkeys
+                with np.errstate(invalid="ignore", over="ignore"):
+                    M_new = np.maximum(Mx, m)
+                    c_old = np.exp((Mx - M_new).astype(np.float32)).astype(np.float32)
+                    c_new = np.exp((m - M_new).astype(np.float32)).astype(np.float32)
+                L_new = fma32(Ls, c_old, (l * c_new).astype(np.float32))
+                A_new = fma32(A, c_old[:, None], (acc * c_new[:, None]).astype(np.float32))
+                Mx = np.where(touched, M_new, Mx)
+                Ls = np.where(touched, L_new, Ls)
+                A = np.where(touched[:, None], A_new, A)
+            with np.errstate(invalid="ignore", divide="ignore"):
+                o = (A / Ls[:, None]).astype(np.float32)
+            out[b, heads] = o.reshape(G, Tq, D)
+    return round_to(out, dtype)
+
+
+def attention_float64(q, k, v, scale: float, causal: bool, kv_lens=None) -> np.ndarray:
+    """Textbook softmax(q k^T * scale) v in float64 (closed form, no splits)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    B, Hq, Tq, D = q.shape
+    Hkv, L = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    out = np.zeros((B, Hq, Tq, D))
+    for b in range(B):
+        n_len = L if kv_lens is None else int(kv_lens[b])
+        for h in range(Hq):
+            kk = k[b, h // G, :n_len]
+            vv = v[b, h // G, :n_len]
+            s = (q[b, h] @ kk.T) * scale
+            if causal:
+                t = np.arange(Tq)[:, None]
+                j = np.arange(n_len)[None, :]
+                s = np.where(j < n_len - Tq + t + 1, s, -np.inf)
+            s = s - s.max(-1, keepdims=True)
+            p = np.exp(s)
+            out[b, h] = (p / p.sum(-1, keepdims=True)) @ vv
+    return out
+
+
+def rms_norm_float64(x, w, eps: float) -> np.ndarray:
+    x = np.asarray(x, np.float64)
+    wv = 1.0 if w is None else np.asarray(w, np.float64)
+    return x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * wv
+
+
+# ---------------------------------------------------------------------------
+# Comparison helpers used by the tests
+# ---------------------------------------------------------------------------
+
+def max_ulp_excess(got, want, dtype: str, atol=0.0) -> float:
+    """max over elements of (|got - want| - atol) / ulp(want); <= 1 means every
+    element is within one storage ulp (after the absolute allowance)."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    d = np.abs(got - want) - atol
+    return float(np.max(d / ulp(want, dtype))) if d.size else 0.0
+
+
+def isclose_report(got, want) -> str:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    i = int(np.argmax(np.abs(got - want)))
+    return f"max|diff|={np.abs(got - want).max():.3e} at flat {i}: got {got.flat[i]!r} want {want.flat[i]!r}"
+
+
+def sqrt_scale(D: int) -> float:
+    return 1.0 / math.sqrt(D)

@@ -1,0 +1,74 @@
+"""The C-ABI library on a host without a GPU: it loads, exports every symbol
+include/bi_kernels.h declares, and rejects bad arguments before launching."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mlx_batch_invariant_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "bi_kernels.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(bi_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared()
+    assert len(names) >= 11
+    for n in names:
+        assert hasattr(lib, n), n
+    assert sorted(_lib.exported_symbols()) == names
+    assert lib.bi_abi_version() == 1
+    assert lib.bi_split_m_max() == 32
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    assert lib.bi_matmul_workspace_bytes(1, 14336, 4096) == 16 * 1 * 14336 * 4
+    assert lib.bi_matmul_workspace_bytes(32, 100, 896) == 4 * 32 * 100 * 4
+    assert lib.bi_matmul_workspace_bytes(33, 100, 896) == 0          # fused
+    assert lib.bi_matmul_workspace_bytes(8, 100, 256) == 0           # one group
+    assert lib.bi_quantized_matmul_workspace_bytes(4, 14336, 4096) == 16 * 4 * 14336 * 4
+    ns = (8192 + 255) // 256
+    bh = 256 * 32 * ns
+    assert lib.bi_attn_decode_workspace_bytes(256, 32, 8192, 128) == (2 * ((bh + 3) // 4 * 4) + bh * 128) * 4
+
+
+def _err(lib):
+    return lib.bi_last_error().decode()
+
+
+def test_invalid_arguments_are_rejected_before_launch():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    # K not a multiple of 8
+    assert lib.bi_matmul(p, 12, p, 12, p, 2, 4, 12, 2, None, 0, None) == -1
+    assert "multiples of 8" in _err(lib)
+    # missing workspace for a split launch
+    assert lib.bi_matmul(p, 512, p, 512, p, 2, 4, 512, 2, None, 0, None) == -3
+    # unsupported quantization
+    assert lib.bi_quantized_matmul(p, 64, p, p, p, p, 2, 4, 64, 3, 64, 2, None, 0, None) == -2
+    assert lib.bi_quantized_matmul(p, 96, p, p, p, p, 2, 4, 96, 4, 64, 2, None, 0, None) == -1
+    # unknown dtype, bad shapes
+    assert lib.bi_rms_norm(p, 8, None, p, 2, 8, 1e-6, 7, None) == -2
+    assert lib.bi_rms_norm(p, 4, None, p, 2, 8, 1e-6, 2, None) == -1
+    assert lib.bi_rms_norm(p, 8, None, p, 0, 8, 1e-6, 2, None) == 0     # nothing to do
+    strides = (ctypes.c_int64 * 9)(*([128] * 9))
+    assert lib.bi_attn_decode(p, p, p, None, p, 1, 4, 4, 10, 96, strides, 1.0, 2, p, 1 << 20, None) == -2
+    assert lib.bi_attn_decode(p, p, p, None, p, 1, 6, 4, 10, 128, strides, 1.0, 2, p, 1 << 20, None) == -1
+    assert lib.bi_attn_decode(p, p, p, None, p, 1, 4, 4, 10, 128, strides, 1.0, 2, None, 0, None) == -3
+    assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 20, 10, 128, strides, 1, 1.0, 2, None) == -1
+    bad = (ctypes.c_int64 * 9)(*([3] * 9))
+    assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 5, 10, 128, bad, 0, 1.0, 2, None) == -1
+
+
+@pytest.mark.parametrize("name", ["matmul", "rmsnorm", "quantized", "attention"])
+def test_product_modules_do_not_import_the_oracle(name):
+    src = (Path(_lib.__file__).parent / "kernels" / f"{name}.py").read_text()
+    assert "oracle" not in src.replace("oracle)", "")

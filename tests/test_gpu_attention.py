@@ -1,0 +1,177 @@
+"""Attention on the GPU: parity with the oracle and the float64 closed form,
+known answers, batch invariance (also with ragged kv_lens), chunked prefill ==
+one-shot prefill, decode == prefill for the same position."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import DT, bits, gen, randn, to_np
+from oracle import bi_oracle as ora
+from sweep import sweep
+
+pytestmark = pytest.mark.gpu
+
+
+def _bi():
+    import mlx_batch_invariant_amd as bi
+    return bi
+
+
+def _qkv(B, Hq, Hkv, Tq, L, D, dt, seed):
+    g = gen(seed)
+    return (randn((B, Hq, Tq, D), DT[dt], g), randn((B, Hkv, L, D), DT[dt], g),
+            randn((B, Hkv, L, D), DT[dt], g))
+
+
+def _tol_check(got, want, dt):
+    # outputs are convex combinations of V rows (|v| ~ 1): one ulp of the
+    # output type plus a small absolute allowance for fp32 order differences.
+    atol = 2e-6 if dt == "f32" else 1e-6
+    assert ora.max_ulp_excess(got, want, dt, atol=atol) <= 1.0, ora.isclose_report(got, want)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("Hq,Hkv,L,D", [(8, 2, 1000, 128), (4, 4, 300, 64), (32, 8, 513, 128), (8, 1, 256, 128)])
+def test_decode_matches_oracle(dt, Hq, Hkv, L, D):
+    q, k, v = _qkv(2, Hq, Hkv, 1, L, D, dt, seed=L + D)
+    sc = 1 / math.sqrt(D)
+    got = to_np(_bi().batch_invariant_decode_attention(q, k, v, scale=sc))
+    want = ora.attention(to_np(q), to_np(k), to_np(v), sc, False, dt)
+    _tol_check(got, want, dt)
+    ref64 = ora.attention_float64(to_np(q), to_np(k), to_np(v), sc, False)
+    assert np.abs(got - ref64).max() < (2e-2 if dt == "bf16" else 4e-3)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_matches_oracle(dt, causal):
+    q, k, v = _qkv(2, 8, 2, 37, 300, 64, dt, seed=3)
+    got = to_np(_bi().batch_invariant_prefill_attention(q, k, v, scale=0.125, causal=causal))
+    want = ora.attention(to_np(q), to_np(k), to_np(v), 0.125, causal, dt)
+    _tol_check(got, want, dt)
+
+
+def test_prefill_matches_float64_closed_form():
+    """Reference test_prefill_matches_stock_causal_with_cache, against float64."""
+    q, k, v = _qkv(2, 8, 2, 37, 150, 64, "f32", seed=3)
+    for causal in (True, False):
+        got = to_np(_bi().batch_invariant_prefill_attention(q, k, v, scale=0.125, causal=causal))
+        ref = ora.attention_float64(to_np(q), to_np(k), to_np(v), 0.125, causal)
+        assert np.abs(got - ref).max() / np.abs(ref).max() < 1e-4
+
+
+def test_single_key_returns_v_exactly():
+    q, k, v = _qkv(3, 8, 2, 1, 1, 128, "bf16", seed=4)
+    got = _bi().batch_invariant_decode_attention(q, k, v, scale=0.1)
+    want = v[:, :, 0:1, :].repeat_interleave(4, dim=1)
+    assert bits(got) == bits(want)
+
+
+def test_equal_scores_give_mean_of_v():
+    """scale = 0 makes every score 0: out = mean of V (exact for a power-of-2 count
+    of V rows that are small integers)."""
+    g = gen(5)
+    L = 256
+    q = randn((1, 4, 1, 128), torch.bfloat16, g)
+    k = randn((1, 4, L, 128), torch.bfloat16, g)
+    v = torch.randint(-4, 5, (1, 4, L, 128), generator=g).to(torch.bfloat16).cuda()
+    got = _bi().batch_invariant_decode_attention(q, k, v, scale=0.0)
+    want = v.float().mean(dim=2, keepdim=True)
+    np.testing.assert_allclose(to_np(got), to_np(want), rtol=0, atol=to_np(want).__abs__().max() * 2 ** -7)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_decode_batch_invariant(dt):
+    Hq, Hkv, L, D = 8, 2, 1000, 128
+    q0, k0, v0 = _qkv(1, Hq, Hkv, 1, L, D, dt, seed=0)
+    filler = lambda n, g: (randn((n, Hq, 1, D), DT[dt], g), randn((n, Hkv, L, D), DT[dt], g),
+                           randn((n, Hkv, L, D), DT[dt], g))
+    run = lambda t: _bi().batch_invariant_decode_attention(t[0], t[1], t[2], scale=D ** -0.5)
+    fails = sweep((q0, k0, v0), filler, run, batches=[1, 2, 3, 4, 8, 16, 32, 64])
+    assert not fails, fails
+
+
+def test_decode_ragged_kv_lens_equal_alone():
+    """per-sequence lengths in one batch; each sequence's
+    output equals running it alone with K/V cut to its own length."""
+    Hq, Hkv, D, L = 32, 8, 128, 2100
+    rng = np.random.default_rng(0)
+    B = 12
+    lens = rng.integers(1, L + 1, size=B)
+    lens[0], lens[1], lens[2], lens[3] = 1, 256, 257, L
+    q, k, v = _qkv(B, Hq, Hkv, 1, L, D, "bf16", seed=8)
+    kl = torch.tensor(lens, dtype=torch.int32).cuda()
+    out = _bi().batch_invariant_decode_attention(q, k, v, scale=D ** -0.5, kv_lens=kl)
+    for b in range(B):
+        n = int(lens[b])
+        alone = _bi().batch_invariant_decode_attention(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n],
+                                                       scale=D ** -0.5)
+        assert bits(out[b:b + 1]) == bits(alone), (b, n)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_chunked_prefill_and_decode_equivalence(dt):
+    """Reference attention_structure_checks (harness/sweep.py:188-207): T=600,
+    chunk at T1=257 (off the 256 split), decode(last) == prefill(last)."""
+    Hq, Hkv, D, T, T1 = 8, 2, 128, 600, 257
+    q, k, v = _qkv(2, Hq, Hkv, T, T, D, dt, seed=0)
+    sc = D ** -0.5
+    att = _bi().batch_invariant_attention
+    full = att(q, k, v, scale=sc, mask="causal")
+    part1 = att(q[:, :, :T1], k[:, :, :T1], v[:, :, :T1], scale=sc, mask="causal")
+    part2 = att(q[:, :, T1:], k, v, scale=sc, mask="causal")
+    assert bits(torch.cat([part1, part2], 2)) == bits(full)
+    dec = att(q[:, :, T - 1:T], k, v, scale=sc)
+    assert bits(dec) == bits(full[:, :, T - 1:T])
+    for t in (0, 1, 255, 256, 300, 511, 512, 599):
+        d = att(q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1], scale=sc)
+        assert bits(d) == bits(full[:, :, t:t + 1]), t
+
+
+def test_prefill_chunks_128_512_llama_gqa():
+    """BASELINE config 4 shape (GQA 32/8, D=128) at T=2048: chunks of 128 and
+    512 against the cache equal one-shot prefill."""
+    Hq, Hkv, D, T = 32, 8, 128, 2048
+    q, k, v = _qkv(1, Hq, Hkv, T, T, D, "bf16", seed=2)
+    sc = D ** -0.5
+    att = _bi().batch_invariant_prefill_attention
+    full = att(q, k, v, scale=sc, causal=True)
+    for C in (128, 512):
+        parts = [att(q[:, :, s:s + C], k[:, :, :s + C], v[:, :, :s + C], scale=sc, causal=True)
+                 for s in range(0, T, C)]
+        assert bits(torch.cat(parts, 2)) == bits(full), C
+
+
+def test_prefill_batch_invariant():
+    Hq, Hkv, Tq, L, D = 8, 2, 48, 300, 128
+    q0, k0, v0 = _qkv(1, Hq, Hkv, Tq, L, D, "bf16", seed=0)
+    filler = lambda n, g: (randn((n, Hq, Tq, D), torch.bfloat16, g), randn((n, Hkv, L, D), torch.bfloat16, g),
+                           randn((n, Hkv, L, D), torch.bfloat16, g))
+    run = lambda t: _bi().batch_invariant_prefill_attention(t[0], t[1], t[2], scale=D ** -0.5, causal=True)
+    fails = sweep((q0, k0, v0), filler, run, batches=[1, 2, 3, 8, 16])
+    assert not fails, fails
+
+
+def test_prefill_kv_lens_equal_alone():
+    Hq, Hkv, D, L, Tq = 8, 2, 64, 700, 40
+    q, k, v = _qkv(3, Hq, Hkv, Tq, L, D, "bf16", seed=9)
+    lens = [40, 511, 700]
+    out = _bi().batch_invariant_prefill_attention(q, k, v, scale=0.125, causal=True,
+                                                  kv_lens=torch.tensor(lens, dtype=torch.int32).cuda())
+    for b, n in enumerate(lens):
+        alone = _bi().batch_invariant_prefill_attention(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n],
+                                                        scale=0.125, causal=True)
+        assert bits(out[b:b + 1]) == bits(alone), b
+
+
+def test_strided_kv_cache_view():
+    """K/V read through strides: a cache preallocated for 1024 positions and
+    viewed at 600 gives the same bits as a compact copy."""
+    Hq, Hkv, D = 8, 2, 128
+    q, k, v = _qkv(2, Hq, Hkv, 1, 1024, D, "bf16", seed=10)
+    a = _bi().batch_invariant_decode_attention(q, k[:, :, :600], v[:, :, :600], scale=0.1)
+    b = _bi().batch_invariant_decode_attention(q, k[:, :, :600].contiguous(), v[:, :, :600].contiguous(), scale=0.1)
+    assert bits(a) == bits(b)

@@ -1,0 +1,136 @@
+"""Dense matmul on the GPU: integer known answers (exact), identity, parity
+with the oracle at the stated tolerance, batch invariance across the
+split/fused and tile-height boundaries, MFMA row independence."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import DT, bits, gen, randn, to_np
+from oracle import bi_oracle as ora
+from sweep import sweep
+
+pytestmark = pytest.mark.gpu
+
+
+def _bi():
+    import mlx_batch_invariant_amd as bi
+    return bi
+
+
+def _mm(a, b):
+    return _bi().batch_invariant_matmul(a, b)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("M,N,K", [(1, 64, 256), (5, 100, 896), (33, 48, 1000), (100, 130, 512), (17, 16, 8), (300, 70, 264)])
+def test_matmul_integer_known_answer(dt, M, N, K):
+    """Small integers: every partial sum is an integer < 2^24, so every order is
+    exact and the result must equal the int64 product bit for bit."""
+    rng = np.random.default_rng(M * 1000 + N + K)
+    a = rng.integers(-3, 4, size=(M, K))
+    bt = rng.integers(-3, 4, size=(N, K))
+    want = a @ bt.T
+    assert np.abs(want).max() < 2 ** 24  # the fp32 total is the exact integer
+    A = torch.tensor(a, dtype=DT[dt]).cuda()
+    Bt = torch.tensor(bt, dtype=DT[dt]).cuda()
+    got = _mm(A, Bt.t())
+    np.testing.assert_array_equal(to_np(got), ora.round_to(want.astype(np.float32), dt))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_matmul_identity(dt):
+    g = gen(3)
+    K = 640
+    Bt = randn((96, K), DT[dt], g)
+    eye = torch.eye(K, dtype=DT[dt]).cuda()
+    got = _mm(eye, Bt.t())                  # row k of the result is column k of B
+    assert bits(got) == bits(Bt.t().contiguous())
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("M,N,K", [(1, 4864, 896), (16, 256, 4096), (32, 200, 896), (64, 300, 1024), (257, 130, 520)])
+def test_matmul_matches_oracle(dt, M, N, K):
+    g = gen(M + N + K)
+    a = randn((M, K), DT[dt], g)
+    bt = randn((N, K), DT[dt], g, scale=0.02)
+    got = to_np(_mm(a, bt.t()))
+    want = ora.matmul(to_np(a), to_np(bt), dt)
+    atol = ora.matmul_error_bound(to_np(a), to_np(bt))
+    excess = ora.max_ulp_excess(got, want, dt, atol=atol)
+    assert excess <= 1.0, ora.isclose_report(got, want)
+
+
+def test_matmul_rounding_model_report(capsys):
+    """How often the GPU matches the oracle's MFMA model exactly (fp32 partial
+    sums observed through fp32 outputs). Reported, asserted only loosely."""
+    g = gen(11)
+    a = randn((16, 4096), torch.float32, g).to(torch.bfloat16).to(torch.float32)
+    bt = randn((512, 4096), torch.float32, g).to(torch.bfloat16).to(torch.float32)
+    a16, b16 = a.to(torch.bfloat16), bt.to(torch.bfloat16)
+    # bf16 operands, fp32 result: use the fp32 kernel on bf16-valued data and the bf16 kernel
+    got16 = to_np(_mm(a16, b16.t()))
+    want16 = ora.matmul(to_np(a16), to_np(b16), "bf16")
+    frac = float(np.mean(got16 == want16))
+    print(f"bf16 matmul exact-match fraction vs MFMA model: {frac:.6f}")
+    assert frac > 0.9
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("N,K", [(4864, 896), (4096, 4096)])
+def test_matmul_batch_invariant(dt, N, K):
+    g = gen(0)
+    W = randn((N, K), DT[dt], g, scale=0.02)
+    probe = randn((1, K), DT[dt], g)
+    fails = sweep(probe, lambda n, gg: randn((n, K), DT[dt], gg), lambda x: _mm(x, W.t()))
+    assert not fails, fails
+
+
+def test_matmul_row_position_independence():
+    """The probe row at every position of 16- and 64-row batches: MFMA rows are
+    computed independently of the other rows of the tile."""
+    g = gen(5)
+    K, N = 1024, 256
+    W = randn((N, K), torch.bfloat16, g, scale=0.02)
+    probe = randn((1, K), torch.bfloat16, g)
+    fails = sweep(probe, lambda n, gg: randn((n, K), torch.bfloat16, gg), lambda x: _mm(x, W.t()),
+                  batches=[16, 64, 48], positions=lambda B: range(B))
+    assert not fails, fails
+
+
+def test_matmul_split_equals_fused():
+    g = gen(6)
+    K, N = 4096, 512
+    W = randn((N, K), torch.bfloat16, g, scale=0.02)
+    x = randn((33, K), torch.bfloat16, g)
+    fused = _mm(x, W.t())                    # M = 33: in-register fold
+    split = _mm(x[:32], W.t())               # M = 32: partials + fold kernel
+    one = _mm(x[:1], W.t())
+    assert bits(fused[:32]) == bits(split)
+    assert bits(fused[:1]) == bits(one)
+
+
+def test_matmul_layouts_and_leading_dims():
+    g = gen(7)
+    a = randn((2, 3, 200), torch.bfloat16, g)
+    b_row = randn((200, 72), torch.bfloat16, g)      # row-major [K, N]: copied to k-major
+    out = _mm(a, b_row)
+    ref = _mm(a.reshape(6, 200), b_row.t().contiguous().t())
+    assert out.shape == (2, 3, 72)
+    assert bits(out.reshape(6, 72)) == bits(ref)
+    v = randn((200,), torch.bfloat16, g)             # 1-D lhs
+    assert _mm(v, b_row).shape == (72,)
+    odd = randn((3, 13), torch.float16, g)           # K % 8 != 0 -> zero-padded copy
+    w13 = randn((13, 5), torch.float16, g)
+    want = ora.matmul(to_np(odd), to_np(w13).T, "f16")
+    assert ora.max_ulp_excess(to_np(_mm(odd, w13)), want, "f16") <= 1
+
+
+def test_matmul_errors():
+    bi = _bi()
+    a = torch.zeros((2, 8), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        bi.batch_invariant_matmul(a, torch.zeros((9, 4), dtype=torch.bfloat16, device="cuda"))
+    with pytest.raises(ValueError):
+        bi.batch_invariant_matmul(a, torch.zeros((2, 8, 4), dtype=torch.bfloat16, device="cuda"))
+    assert bi.batch_invariant_matmul(a[:0], torch.zeros((8, 4), dtype=torch.bfloat16, device="cuda")).shape == (0, 4)

@@ -1,0 +1,95 @@
+"""Affine quantized matmul on the GPU: bit-exact unpack + dequantization
+(identity probe), parity with the oracle, batch invariance at the Llama-3-8B
+MLP shape, agreement with the dense kernel on the dequantized weight."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import DT, bits, gen, randn, to_np
+from oracle import bi_oracle as ora
+from sweep import sweep
+
+pytestmark = pytest.mark.gpu
+
+CASES = [(4, 32), (4, 64), (4, 128), (8, 32), (8, 64), (8, 128)]
+
+
+def _bi():
+    import mlx_batch_invariant_amd as bi
+    return bi
+
+
+def _qweights(N, K, bits_, gs, dt, seed, scale=0.02):
+    g = gen(seed)
+    W = torch.randn((N, K), generator=g) * scale
+    return _bi().quantize(W, group_size=gs, bits=bits_, dtype=DT[dt])
+
+
+@pytest.mark.parametrize("bits_,gs", CASES)
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_dequantization_bit_exact(bits_, gs, dt):
+    """x = I_K makes row k of the output exactly W[:, k] as dequantized by the
+    kernel (one non-zero product per sum), so unpacking, group indexing and the
+    fmaf + rounding are compared bit for bit with the closed form."""
+    N, K = 96, 512
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 1000 + gs)
+    eye = torch.eye(K, dtype=DT[dt])
+    got = _bi().batch_invariant_quantized_matmul(eye.cuda(), wq.cuda(), s.cuda(), b.cuda(),
+                                                  group_size=gs, bits=bits_)
+    want = ora.dequantize(wq.view(torch.int32).numpy().view(np.uint32), to_np(s), to_np(b), gs, bits_, dt)
+    np.testing.assert_array_equal(to_np(got), want.T)
+
+
+@pytest.mark.parametrize("bits_,gs", CASES)
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("M", [1, 9, 40])
+def test_quantized_matches_oracle(bits_, gs, dt, M):
+    N, K = 200, 1024
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=M + bits_ + gs)
+    x = randn((M, K), DT[dt], gen(M))
+    got = to_np(_bi().batch_invariant_quantized_matmul(x, wq.cuda(), s.cuda(), b.cuda(),
+                                                       group_size=gs, bits=bits_))
+    W = ora.dequantize(wq.view(torch.int32).numpy().view(np.uint32), to_np(s), to_np(b), gs, bits_, dt)
+    want = ora.matmul(to_np(x), W, dt)
+    atol = ora.matmul_error_bound(to_np(x), W)
+    assert ora.max_ulp_excess(got, want, dt, atol=atol) <= 1.0, ora.isclose_report(got, want)
+
+
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128)])
+def test_quantized_equals_dense_on_dequantized_weight(bits_, gs):
+    """Same tile body: the quantized kernel and the dense kernel on the
+    dequantized bf16 weight give identical bits."""
+    N, K = 512, 2048
+    wq, s, b = _qweights(N, K, bits_, gs, "bf16", seed=9)
+    W = torch.tensor(ora.dequantize(wq.view(torch.int32).numpy().view(np.uint32), to_np(s), to_np(b),
+                                    gs, bits_, "bf16")).to(torch.bfloat16).cuda()
+    for M in (1, 7, 32, 33, 100):
+        x = randn((M, K), torch.bfloat16, gen(M))
+        q = _bi().batch_invariant_quantized_matmul(x, wq.cuda(), s.cuda(), b.cuda(), group_size=gs, bits=bits_)
+        d = _bi().batch_invariant_matmul(x, W.t())
+        assert bits(q) == bits(d), M
+
+
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
+def test_quantized_batch_invariant_llama_mlp(bits_, gs):
+    """W [14336, 4096], x [M, 4096], M in 1..64 (and beyond)."""
+    N, K = 14336, 4096
+    wq, s, b = _qweights(N, K, bits_, gs, "bf16", seed=0)
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    probe = randn((1, K), torch.bfloat16, gen(1))
+    run = lambda x: _bi().batch_invariant_quantized_matmul(x, wq, s, b, group_size=gs, bits=bits_)
+    fails = sweep(probe, lambda n, gg: randn((n, K), torch.bfloat16, gg), run,
+                  batches=[1, 2, 4, 8, 16, 32, 64, 128, 256])
+    assert not fails, fails
+
+
+def test_quantized_errors():
+    bi = _bi()
+    x = torch.zeros((2, 64), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((8, 8), dtype=torch.uint32, device="cuda")
+    s = torch.zeros((8, 1), dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError):
+        bi.batch_invariant_quantized_matmul(x, w, s, s, group_size=64, bits=3)
+    with pytest.raises(ValueError):
+        bi.batch_invariant_quantized_matmul(x[:, :32], w, s, s, group_size=64, bits=4)

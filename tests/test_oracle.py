@@ -1,0 +1,210 @@
+"""Pin the CPU oracle (CPU only): every oracle function is checked against
+known answers, closed forms or invariants that a plausible mistake (dropped
+term, wrong index, transposed operand, wrong fold) would break."""
+
+import json
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import bi_oracle as ora
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+# ---- storage types ------------------------------------------------------------
+
+def test_bf16_round_to_nearest_even_known_answers():
+    vals = np.array([1.0, -2.5, 0.0, -0.0, 3.0e38, 1e-40], np.float32)
+    want = [0x3F80, 0xC020, 0x0000, 0x8000, 0x7F62, 0x0001]
+    assert ora.f32_to_bf16_bits(vals).tolist() == want
+    # ties: 0x3F808000 is halfway between 0x3F80 and 0x3F81 -> even 0x3F80;
+    # 0x3F818000 halfway between 0x3F81 and 0x3F82 -> even 0x3F82
+    ties = np.array([0x3F808000, 0x3F818000, 0x3F808001, 0x7FC00000], np.uint32).view(np.float32)
+    got = ora.f32_to_bf16_bits(ties)
+    assert got[:3].tolist() == [0x3F80, 0x3F82, 0x3F81]
+    assert np.isnan(ora.bf16_bits_to_f32(got[3:]))[0]
+
+
+def test_round_to_f16_matches_numpy_half():
+    x = np.random.default_rng(0).standard_normal(1000).astype(np.float32)
+    assert np.array_equal(ora.round_to(x, "f16"), x.astype(np.float16).astype(np.float32))
+
+
+# ---- quantized format -----------------------------------------------------------
+
+def test_unpack_golden_words():
+    """Hand-packed words of the MLX affine layout (codes low-to-high)."""
+    kat = json.loads((GOLDEN / "quant_kat.json").read_text())
+    for case in kat["unpack"]:
+        w = np.array([case["words"]], np.uint32)
+        assert ora.unpack(w, case["bits"]).tolist() == [case["codes"]]
+        assert ora.pack(np.array([case["codes"]]), case["bits"]).tolist() == [case["words"]]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_unpack_brute_force_every_code_every_slot(bits):
+    per = 32 // bits
+    for slot in range(per):
+        for code in range(1 << bits):
+            w = np.array([[code << (bits * slot)]], np.uint64).astype(np.uint32)
+            c = ora.unpack(w, bits)[0]
+            assert c[slot] == code and c.sum() == code
+
+
+def test_pack_unpack_roundtrip_random():
+    rng = np.random.default_rng(1)
+    for bits in (4, 8):
+        w = rng.integers(0, 2 ** 32, size=(7, 24), dtype=np.uint64).astype(np.uint32)
+        assert np.array_equal(ora.pack(ora.unpack(w, bits), bits), w)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_dequantize_matches_exact_rational_closed_form(dtype):
+    """T(fmaf(code, scale, bias)): exact rational code*scale+bias, rounded once
+    to fp32 (Fraction -> float is correctly rounded in double, and every value
+    here is a double that rounds to float32 without a tie), then to T."""
+    rng = np.random.default_rng(2)
+    N, gs, bits = 6, 32, 4
+    K = 4 * gs
+    codes = rng.integers(0, 16, size=(N, K))
+    scales = ora.round_to(rng.uniform(1e-3, 5e-2, size=(N, K // gs)).astype(np.float32), dtype)
+    biases = ora.round_to(rng.uniform(-0.2, 0.2, size=(N, K // gs)).astype(np.float32), dtype)
+    got = ora.dequantize(ora.pack(codes, bits), scales, biases, gs, bits, dtype)
+    for n in range(N):
+        for k in range(0, K, 7):
+            exact = Fraction(int(codes[n, k])) * Fraction(float(scales[n, k // gs])) + Fraction(float(biases[n, k // gs]))
+            f32 = np.float32(float(exact))
+            assert got[n, k] == ora.round_to(np.array([f32]), dtype)[0]
+
+
+# ---- RMSNorm ------------------------------------------------------------------
+
+@pytest.mark.parametrize("D", [1, 7, 896, 4096, 9000])
+def test_rms_norm_close_to_float64_closed_form(D):
+    rng = np.random.default_rng(D)
+    x = ora.round_to(rng.standard_normal((5, D)).astype(np.float32), "bf16")
+    w = ora.round_to((1 + 0.1 * rng.standard_normal(D)).astype(np.float32), "bf16")
+    for eps in (1e-6, 0.5):           # a dropped or misplaced eps fails at eps = 0.5
+        got = ora.rms_norm(x, w, eps, "f32")
+        ref = ora.rms_norm_float64(x, w, eps)
+        assert np.max(np.abs(got - ref) / (np.abs(ref) + 1e-30)) < 1e-5
+
+
+def test_rms_norm_known_answer_constant_row():
+    """x = c everywhere: ss = D c^2 exactly (powers of two), so
+    out = c / sqrt(c^2 + eps) rounded, times w."""
+    D, c, eps = 512, 0.5, 0.25
+    x = np.full((1, D), c, np.float32)
+    got = ora.rms_norm(x, None, eps, "f32")
+    inv = np.float32(1) / np.sqrt(np.float32(c * c + eps))
+    assert np.all(got == np.float32(c) * inv)
+
+
+def test_rms_norm_weight_none_is_ones_and_rows_independent():
+    rng = np.random.default_rng(3)
+    x = ora.round_to(rng.standard_normal((9, 300)).astype(np.float32), "bf16")
+    a = ora.rms_norm(x, None, 1e-6, "bf16")
+    b = ora.rms_norm(x, np.ones(300, np.float32), 1e-6, "bf16")
+    assert np.array_equal(a, b)
+    assert np.array_equal(ora.rms_norm(x[4:5], None, 1e-6, "bf16"), a[4:5])
+
+
+# ---- matmul -------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,N,K", [(3, 5, 256), (7, 9, 1000), (1, 33, 8)])
+def test_matmul_integer_known_answer(M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    a = rng.integers(-3, 4, size=(M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, size=(N, K)).astype(np.float32)
+    assert np.array_equal(ora.matmul(a, b, "f32"), (a.astype(np.int64) @ b.T.astype(np.int64)).astype(np.float32))
+
+
+def test_matmul_k_slot_map_covers_each_k_once():
+    for g in range(3):
+        ks = np.concatenate([ora.step_indices(g, s) for s in range(ora.STEPS)])
+        assert sorted(ks.tolist()) == list(range(256 * g, 256 * g + 256))
+
+
+def test_matmul_identity_and_transpose():
+    rng = np.random.default_rng(4)
+    B = ora.round_to(rng.standard_normal((40, 300)).astype(np.float32), "bf16")
+    eye = np.eye(300, dtype=np.float32)
+    assert np.array_equal(ora.matmul(eye, B, "bf16"), B.T)     # a transposed operand would fail
+    assert np.array_equal(ora.matmul(B, eye, "bf16"), B)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+def test_matmul_close_to_float64(dtype):
+    rng = np.random.default_rng(5)
+    a = ora.round_to(rng.standard_normal((8, 1536)).astype(np.float32), dtype)
+    b = ora.round_to(rng.standard_normal((12, 1536)).astype(np.float32), dtype)
+    ref = a.astype(np.float64) @ b.T.astype(np.float64)
+    got = ora.matmul(a, b, "f32")
+    assert np.all(np.abs(got - ref) <= ora.matmul_error_bound(a, b))
+
+
+def test_matmul_group_fold_order_is_observable():
+    """The fp32 fold of group partials is ((0 + p0) + p1) + p2: choose groups
+    whose partials are 2^24, 1, 1 -> 2^24 (each +1 rounds away); a fold that
+    summed p1 + p2 first would give 2^24 + 2."""
+    K = 768
+    a = np.zeros((1, K), np.float32)
+    b = np.zeros((1, K), np.float32)
+    a[0, 0], b[0, 0] = 4096.0, 4096.0          # group 0: 2^24
+    a[0, 256], b[0, 256] = 1.0, 1.0            # group 1: 1
+    a[0, 512], b[0, 512] = 1.0, 1.0            # group 2: 1
+    assert ora.matmul(a, b, "f32")[0, 0] == np.float32(2 ** 24)
+
+
+# ---- attention ------------------------------------------------------------------
+
+def _qkv(B, Hq, Hkv, Tq, L, D, seed):
+    rng = np.random.default_rng(seed)
+    r = lambda *s: ora.round_to(rng.standard_normal(s).astype(np.float32), "bf16")
+    return r(B, Hq, Tq, D), r(B, Hkv, L, D), r(B, Hkv, L, D)
+
+
+def test_attention_single_key_is_v():
+    q, k, v = _qkv(2, 4, 2, 1, 1, 64, 0)
+    out = ora.attention(q, k, v, 0.3, False, "f32")
+    assert np.array_equal(out, np.repeat(v, 2, axis=1))
+
+
+def test_attention_zero_scale_is_mean_of_v():
+    q, k, _ = _qkv(1, 2, 1, 1, 512, 32, 1)
+    v = np.random.default_rng(1).integers(-4, 5, size=(1, 1, 512, 32)).astype(np.float32)
+    out = ora.attention(q, k, v, 0.0, False, "f32")
+    assert np.array_equal(out[0, 0, 0], v[0, 0].sum(0) / np.float32(512))
+
+
+@pytest.mark.parametrize("L", [1, 255, 256, 257, 513, 1000])
+def test_attention_close_to_float64_softmax(L):
+    q, k, v = _qkv(1, 4, 2, 3, L, 64, L)
+    for causal in ((False, True) if L >= 3 else (False,)):   # causal needs T_q <= L
+        got = ora.attention(q, k, v, 0.125, causal, "f32")
+        ref = ora.attention_float64(q, k, v, 0.125, causal)
+        assert np.abs(got - ref).max() < 2e-5, (L, causal)
+
+
+def test_attention_one_hot_v_gives_softmax_probabilities():
+    q, k, _ = _qkv(1, 1, 1, 1, 40, 64, 7)
+    v = np.zeros((1, 1, 40, 64), np.float32)
+    v[0, 0, np.arange(40), np.arange(40)] = 1.0
+    got = ora.attention(q, k, v, 0.2, False, "f32")[0, 0, 0, :40]
+    s = (q[0, 0, 0].astype(np.float64) @ k[0, 0].T.astype(np.float64)) * 0.2
+    p = np.exp(s - s.max())
+    assert np.abs(got - p / p.sum()).max() < 1e-6
+
+
+def test_attention_kv_lens_and_causal_structure():
+    q, k, v = _qkv(2, 4, 2, 5, 300, 64, 9)
+    lens = [300, 120]
+    full = ora.attention(q, k, v, 0.1, True, "bf16", kv_lens=lens)
+    alone = ora.attention(q[1:], k[1:, :, :120], v[1:, :, :120], 0.1, True, "bf16")
+    assert np.array_equal(full[1:], alone)
+    # bottom-right causal: the last token sees every key (== non-causal)
+    nc = ora.attention(q[:, :, -1:], k, v, 0.1, False, "bf16", kv_lens=lens)
+    assert np.array_equal(full[:, :, -1:], nc)
