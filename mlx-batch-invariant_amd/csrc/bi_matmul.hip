@@ -1,12 +1,17 @@
 // bi_matmul.hip — batch-invariant dense and affine-quantized matmul for gfx950.
 //
-// Kernels (all run the tile body of bi_gemm_tile.h):
-//   gemm_direct<..., SPLIT=true>   one workgroup per (column tile, K group);
-//                                  writes the raw fp32 group partial
-//                                  part[g, m, n]  (small M, several groups)
-//   bi_fold_groups                 out = T(((0 + part[0]) + part[1]) + ...)
-//   gemm_direct<..., SPLIT=false>  folds all groups in registers and writes T
-// Reference launchers: kernels/matmul.py:279-314 (launch_tiled; split for
+// Kernels (all run the arithmetic of bi_gemm_tile.h):
+//   gemm_direct  M <= 32. Each wave owns 16 columns x MT 16-row tiles; its A
+//                and B fragments go straight from global memory into
+//                registers (quantized B is dequantized in registers). With
+//                more than one K group it runs one workgroup per (column
+//                tile, group) and writes the raw fp32 group partial.
+//   fold_groups  out = T(((0 + part[0]) + part[1]) + ...), the split fold.
+//   gemm_lds     M > 32. A BM x BN tile per 256-thread workgroup, K staged
+//                64 at a time through double-buffered LDS (quantized B is
+//                dequantized while it is staged), all groups folded in
+//                registers.
+// Reference launchers: kernels/matmul.py:279-314 (launch_tiled: split for
 // M <= SPLIT_M_MAX and more than one group, fused otherwise), the combine
 // kernel kernels/matmul.py:226-234, and kernels/quantized.py:106-125.
 #include "bi_gemm_tile.h"
@@ -15,85 +20,75 @@ namespace bi {
 
 constexpr int kSplitMMax = 32;
 
-// MT m-tiles x NT n-tiles of 16x16 per wave, WAVES waves per workgroup along n.
-template <typename T, class BSrc, int MT, int NT, int WAVES, bool SPLIT>
-__global__ __launch_bounds__(kWave* WAVES) void gemm_direct(const T* __restrict__ a,
-                                                            int64_t lda, BSrc bsrc,
-                                                            T* __restrict__ out,
+// ---------------------------------------------------------------------------
+// gemm_direct: MT m-tiles x 1 n-tile per wave, WAVES waves per workgroup
+// along n. SPLIT: one group per workgroup (blockIdx.z), raw partial out.
+// ---------------------------------------------------------------------------
+template <typename T, class BSrc, int MT, int WAVES, bool SPLIT>
+__global__ __launch_bounds__(kWave* WAVES) void gemm_direct(const T* __restrict__ a, int64_t lda,
+                                                            BSrc bsrc, T* __restrict__ out,
                                                             float* __restrict__ part, int M,
                                                             int N, int K, int G) {
   typedef typename Frag<T>::type F;
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int r = lane % 16, q = lane / 16;
-  const int n_base = (blockIdx.x * WAVES + wave) * 16 * NT;
+  const int n_base = (blockIdx.x * WAVES + wave) * 16;
   const int m_base = blockIdx.y * 16 * MT;
   if (n_base >= N) return;  // wave-uniform; the kernel has no block barrier
   const int g0 = SPLIT ? (int)blockIdx.z : 0;
   const int g1 = SPLIT ? g0 + 1 : G;
 
-  f32x4 total[MT][NT];
+  f32x4 total[MT];
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) total[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < MT; ++i) total[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int g = g0; g < g1; ++g) {
-    typename BSrc::Raw braw[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j) bsrc.load(braw[j], n_base + 16 * j + r, g, q);
-    f32x4 acc[MT][NT];
+    // Load phase: every fragment of the group is requested before any is used.
+    typename BSrc::Raw braw;
+    bsrc.load(braw, n_base + r, g, q);
+    F af[MT][kSteps];
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < kSteps; ++s) af[i][s] = load_a_frag(a, lda, m_base + 16 * i + r, M, K, g, q, s);
+    // Compute phase.
+    f32x4 acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      F af[MT];
+      const F bf = bsrc.frag(braw, s);
 #pragma unroll
-      for (int i = 0; i < MT; ++i) af[i] = load_a_frag(a, lda, m_base + 16 * i + r, M, K, g, q, s);
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const F bf = bsrc.frag(braw[j], s);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) acc[i][j] = mfma_step(af[i], bf, acc[i][j]);
-      }
+      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
     }
     if constexpr (SPLIT) {
+      const int n = n_base + r;
 #pragma unroll
       for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const int n = n_base + 16 * j + r;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int m = m_base + 16 * i + 4 * q + e;
-            if (m < M && n < N) part[((int64_t)g * M + m) * N + n] = acc[i][j][e];
-          }
-        }
-    } else {
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < NT; ++j) total[i][j] = total[i][j] + acc[i][j];
-    }
-  }
-  if constexpr (!SPLIT) {
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const int n = n_base + 16 * j + r;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int m = m_base + 16 * i + 4 * q + e;
-          if (m < M && n < N) out[(int64_t)m * N + n] = to_store<T>(total[i][j][e]);
+          if (m < M && n < N) part[((int64_t)g * M + m) * N + n] = acc[i][e];
         }
+    } else {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) total[i] = total[i] + acc[i];
+    }
+  }
+  if constexpr (!SPLIT) {
+    const int n = n_base + r;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m_base + 16 * i + 4 * q + e;
+        if (m < M && n < N) out[(int64_t)m * N + n] = to_store<T>(total[i][e]);
       }
   }
 }
 
-// Left fold of the group partials, exactly the fused kernel's fold:
+// Left fold of the group partials, exactly the fused kernels' fold:
 // total = 0; total = total + part[g] for g = 0 .. G-1; out = T(total).
 template <typename T>
 __global__ __launch_bounds__(256) void fold_groups(const float* __restrict__ part,
@@ -105,46 +100,261 @@ __global__ __launch_bounds__(256) void fold_groups(const float* __restrict__ par
   out[idx] = to_store<T>(total);
 }
 
+// ---------------------------------------------------------------------------
+// gemm_lds: BM x BN tile, 4 waves in 2 x 2, each wave (BM/2) x (BN/2).
+// K stage = 64 (two MFMA steps); group g = stages 4g .. 4g+3.
+// ---------------------------------------------------------------------------
+constexpr int kStageK = 64;
+constexpr int kLdsPad = 8;                      // elements; rows 16 B apart in banks
+constexpr int kLdsRow = kStageK + kLdsPad;      // LDS row length (elements)
+
+// Stages one BM x 64 slab of A (rows m0 .., k0 ..) into LDS, 8-element chunks.
+template <typename T, int ROWS>
+struct StageA {
+  static constexpr int kChunks = ROWS * (kStageK / 8) / 256;  // per thread
+  typedef typename Frag<T>::type F;
+  F v[kChunks];
+  __device__ __forceinline__ void load(const T* a, int64_t lda, int M, int K, int m0, int k0) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int row = c / 8, kc = c % 8;
+      const int m = m0 + row, k = k0 + 8 * kc;
+      const bool ok = m < M && k < K;
+      const F x = frag_load(a + (ok ? (int64_t)m * lda + k : 0));
+      v[i] = ok ? x : frag_zero<F>();
+    }
+  }
+  __device__ __forceinline__ void store(T* lds) const {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int row = c / 8, kc = c % 8;
+      *reinterpret_cast<F*>(lds + row * kLdsRow + 8 * kc) = v[i];
+    }
+  }
+};
+
+// B stage for dense operands: same chunking as A over bt rows (columns n).
+template <typename T, int ROWS>
+struct StageDenseB {
+  StageA<T, ROWS> s;
+  __device__ __forceinline__ void load(const DenseB<T>& b, int n0, int k0) {
+    s.load(b.bt, b.ldb, b.N, b.K, n0, k0);
+  }
+  __device__ __forceinline__ void store(T* lds) const { s.store(lds); }
+};
+
+// B stage for quantized operands: each chunk is 8 consecutive codes of one
+// row, dequantized with the row's scale/bias for that k and rounded to T.
+template <typename T, int BITS, int GS, int ROWS>
+struct StageQuantB {
+  static constexpr int kChunks = ROWS * (kStageK / 8) / 256;
+  static constexpr int kWords = BITS / 4;
+  typedef typename Frag<T>::type F;
+  uint32_t w[kChunks][kWords];
+  float sc[kChunks], bs[kChunks];
+  bool ok[kChunks];
+  __device__ __forceinline__ void load(const QuantB<T, BITS, GS>& b, int n0, int k0) {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int row = c / 8, kc = c % 8;
+      const int n = n0 + row, k = k0 + 8 * kc;
+      const bool good = n < b.N && k < b.K;
+      const int64_t nn = good ? n : 0;
+      const int kk = good ? k : 0;
+      const uint32_t* wp = b.w + nn * b.words_per_row + (int64_t)kk * BITS / 32;
+      if constexpr (BITS == 4) {
+        w[i][0] = wp[0];
+      } else {
+        const uint2 x = *reinterpret_cast<const uint2*>(wp);
+        w[i][0] = x.x;
+        w[i][1] = x.y;
+      }
+      const int64_t si = nn * b.groups_per_row + kk / GS;
+      sc[i] = to_f32(b.scales[si]);
+      bs[i] = to_f32(b.biases[si]);
+      ok[i] = good;
+    }
+  }
+  __device__ __forceinline__ void store(T* lds) const {
+#pragma unroll
+    for (int i = 0; i < kChunks; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      const int row = c / 8, kc = c % 8;
+      float d[8];
+      if constexpr (BITS == 4) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d[e] = __builtin_fmaf((float)((w[i][0] >> (4 * e)) & 0xFu), sc[i], bs[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          d[e] = __builtin_fmaf((float)((w[i][0] >> (8 * e)) & 0xFFu), sc[i], bs[i]);
+          d[4 + e] = __builtin_fmaf((float)((w[i][1] >> (8 * e)) & 0xFFu), sc[i], bs[i]);
+        }
+      }
+      F f;
+      if constexpr (sizeof(T) == 2) {
+        typedef T vec8 __attribute__((ext_vector_type(8)));
+        vec8 rr;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rr[e] = to_store<T>(d[e]);
+        f = __builtin_bit_cast(F, rr);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f.lo[e] = d[e];
+          f.hi[e] = d[4 + e];
+        }
+      }
+      *reinterpret_cast<F*>(lds + row * kLdsRow + 8 * kc) = ok[i] ? f : frag_zero<F>();
+    }
+  }
+};
+
+template <class BSrc, typename T, int ROWS> struct StageFor;
+template <typename T, int ROWS> struct StageFor<DenseB<T>, T, ROWS> { typedef StageDenseB<T, ROWS> type; };
+template <typename T, int BITS, int GS, int ROWS> struct StageFor<QuantB<T, BITS, GS>, T, ROWS> {
+  typedef StageQuantB<T, BITS, GS, ROWS> type;
+};
+
+template <typename T, class BSrc, int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_lds(const T* __restrict__ a, int64_t lda, BSrc bsrc,
+                                                T* __restrict__ out, int M, int N, int K, int G,
+                                                int tiles_n, int tiles_total) {
+  typedef typename Frag<T>::type F;
+  constexpr int TM = BM / 32, TN = BN / 32;  // 16x16 tiles per wave along m and n
+  __shared__ __attribute__((aligned(16))) T As[2][BM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) T Bs[2][BN * kLdsRow];
+
+  // XCD-aware tile order: consecutive workgroup ids are dealt round-robin to
+  // the 8 XCDs; give each XCD a contiguous run of tiles so neighbouring tiles
+  // share that XCD's L2. Launch order only.
+  const int bid = blockIdx.x;
+  const int per_xcd = (tiles_total + 7) / 8;
+  const int tile = (bid % 8) * per_xcd + bid / 8;
+  if (tile >= tiles_total) return;  // uniform per workgroup, before any barrier
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  const int r = lane % 16, q = lane / 16;
+
+  f32x4 total[TM][TN], acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      total[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc[i][j] = total[i][j];
+    }
+
+  StageA<T, BM> sa;
+  typename StageFor<BSrc, T, BN>::type sb;
+  const int nstages = 4 * G;
+  sa.load(a, lda, M, K, m0, 0);
+  sb.load(bsrc, n0, 0);
+  sa.store(As[0]);
+  sb.store(Bs[0]);
+  __syncthreads();
+
+  for (int st = 0; st < nstages; ++st) {
+    const int buf = st & 1;
+    if (st + 1 < nstages) {
+      sa.load(a, lda, M, K, m0, (st + 1) * kStageK);
+      sb.load(bsrc, n0, (st + 1) * kStageK);
+    }
+    const T* Ab = As[buf] + (wm * TM * 16 + r) * kLdsRow + 8 * q;
+    const T* Bb = Bs[buf] + (wn * TN * 16 + r) * kLdsRow + 8 * q;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      F af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const F*>(Ab + 16 * i * kLdsRow + 32 * s2);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const F*>(Bb + 16 * j * kLdsRow + 32 * s2);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_step(af[i], bf[j], acc[i][j]);
+    }
+    if ((st & 3) == 3) {  // end of a 256-k group: fold and restart from zero
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          total[i][j] = total[i][j] + acc[i][j];
+          acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    if (st + 1 < nstages) {
+      sa.store(As[buf ^ 1]);
+      sb.store(Bs[buf ^ 1]);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * TN * 16 + 16 * j + r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + wm * TM * 16 + 16 * i + 4 * q + e;
+        if (m < M && n < N) out[(int64_t)m * N + n] = to_store<T>(total[i][j][e]);
+      }
+    }
+}
+
 static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 
 // Launch-shape policy (kernels/matmul.py:279-314): M <= 32 with more than one
 // group -> split partials + fold; otherwise fused. Bits never depend on it.
 static inline bool use_split(int64_t M, int G) { return M <= kSplitMMax && G > 1; }
 
+template <typename T, class BSrc, int BM, int BN>
+static void launch_lds(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K,
+                       int G, hipStream_t st) {
+  const int tn = ceil_div(N, BN), tmm = ceil_div(M, BM);
+  const int total = tn * tmm;
+  const int grid = ((total + 7) / 8) * 8;
+  gemm_lds<T, BSrc, BM, BN><<<grid, 256, 0, st>>>(a, lda, bsrc, out, M, N, K, G, tn, total);
+}
+
 template <typename T, class BSrc>
 static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K,
                     float* ws, hipStream_t st, const char* what) {
   const int G = ceil_div(K, kGroupK);
   constexpr int WAVES = 4;
-  if (use_split(M, G)) {
+  if (M <= kSplitMMax) {
+    const bool split = use_split(M, G);
+    dim3 grid(ceil_div(N, 16 * WAVES), 1, split ? G : 1);
     if (M <= 16) {
-      dim3 grid(ceil_div(N, 16 * WAVES), 1, G);
-      gemm_direct<T, BSrc, 1, 1, WAVES, true><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws,
-                                                                          M, N, K, G);
+      if (split) gemm_direct<T, BSrc, 1, WAVES, true><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G);
+      else gemm_direct<T, BSrc, 1, WAVES, false><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G);
     } else {
-      dim3 grid(ceil_div(N, 16 * WAVES), 1, G);
-      gemm_direct<T, BSrc, 2, 1, WAVES, true><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws,
-                                                                          M, N, K, G);
+      if (split) gemm_direct<T, BSrc, 2, WAVES, true><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G);
+      else gemm_direct<T, BSrc, 2, WAVES, false><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G);
     }
     int rc = bi_host::launch_status(what);
-    if (rc) return rc;
+    if (rc || !split) return rc;
     const int64_t MN = (int64_t)M * N;
     fold_groups<T><<<(unsigned)((MN + 255) / 256), 256, 0, st>>>(ws, out, MN, G);
     return bi_host::launch_status(what);
   }
-  if (M <= 16) {
-    dim3 grid(ceil_div(N, 16 * WAVES), 1, 1);
-    gemm_direct<T, BSrc, 1, 1, WAVES, false><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out,
-                                                                         nullptr, M, N, K, G);
-  } else if (M <= 32) {
-    dim3 grid(ceil_div(N, 16 * WAVES), 1, 1);
-    gemm_direct<T, BSrc, 2, 1, WAVES, false><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out,
-                                                                         nullptr, M, N, K, G);
+  // M > 32: LDS-tiled; the largest tile that still gives the chip >= 256 tiles.
+  auto tiles = [&](int bm, int bn) { return (int64_t)ceil_div(M, bm) * ceil_div(N, bn); };
+  if constexpr (sizeof(T) == 4) {
+    if (tiles(64, 128) >= 256) launch_lds<T, BSrc, 64, 128>(a, lda, bsrc, out, M, N, K, G, st);
+    else launch_lds<T, BSrc, 64, 64>(a, lda, bsrc, out, M, N, K, G, st);
   } else {
-    constexpr int MT = sizeof(T) == 4 ? 2 : 4;
-    dim3 grid(ceil_div(N, 16 * WAVES), ceil_div(M, 16 * MT), 1);
-    gemm_direct<T, BSrc, MT, 1, WAVES, false><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out,
-                                                                          nullptr, M, N, K, G);
+    if (tiles(128, 128) >= 256) launch_lds<T, BSrc, 128, 128>(a, lda, bsrc, out, M, N, K, G, st);
+    else if (tiles(64, 128) >= 256) launch_lds<T, BSrc, 64, 128>(a, lda, bsrc, out, M, N, K, G, st);
+    else launch_lds<T, BSrc, 64, 64>(a, lda, bsrc, out, M, N, K, G, st);
   }
   return bi_host::launch_status(what);
 }
@@ -168,7 +378,8 @@ int check_common(const char* what, int64_t M, int64_t N, int64_t K, void* out, v
   if (M < 0 || N <= 0 || K <= 0)
     return fail(BI_E_INVALID_ARG, "%s: bad shape M=%lld N=%lld K=%lld", what, (long long)M,
                 (long long)N, (long long)K);
-  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL || M * N > ((int64_t)1 << 46))
+  if (M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL || M * N > ((int64_t)1 << 46) ||
+      ((M + 63) / 64) * ((N + 63) / 64) > 0x7fffffffLL - 8)
     return fail(BI_E_UNSUPPORTED, "%s: shape too large", what);
   if (M > 0 && !out) return fail(BI_E_INVALID_ARG, "%s: null out", what);
   const size_t need = split_ws_bytes(M, N, K);

@@ -169,11 +169,37 @@ def dequantize(w_u32, scales, biases, group_size: int, bits: int, dtype: str) ->
 # steps from a zero accumulator, group partials folded left to right with
 # plain fp32 adds, :174-176 and the combine :226-234).
 # gfx950 k-slot map: group g, step s, lane quarter q, element e ->
-#   k = 256 g + 64 q + 8 s + e.
+#   k = 256 g + 32 s + 8 q + e   (step s covers k in [256 g + 32 s, +32)).
 # ---------------------------------------------------------------------------
 
 def step_indices(g: int, s: int) -> np.ndarray:
-    return np.array([GROUP_K * g + 64 * q + 8 * s + e for q in range(4) for e in range(8)])
+    return np.array([GROUP_K * g + 32 * s + 8 * q + e for q in range(4) for e in range(8)])
+
+
+def group_partials(a, bt, dtype: str) -> np.ndarray:
+    """acc_g[M, N] for every K group (fp32), the values the split launch writes."""
+    a = np.asarray(a, np.float32)
+    bt = np.asarray(bt, np.float32)
+    M, K = a.shape
+    N = bt.shape[0]
+    G = -(-K // GROUP_K)
+    ap = np.zeros((M, G * GROUP_K), np.float64)
+    bp = np.zeros((N, G * GROUP_K), np.float64)
+    ap[:, :K] = a
+    bp[:, :K] = bt
+    out = np.zeros((G, M, N), np.float32)
+    for g in range(G):
+        acc = np.zeros((M, N), np.float32)
+        for s in range(STEPS):
+            idx = step_indices(g, s)
+            if dtype == "f32":
+                for e in range(8):
+                    sub = idx[e::8]
+                    acc = (acc + ap[:, sub] @ bp[:, sub].T).astype(np.float32)
+            else:
+                acc = (acc + ap[:, idx] @ bp[:, idx].T).astype(np.float32)
+        out[g] = acc
+    return out
 
 
 def matmul(a, bt, dtype: str) -> np.ndarray:
@@ -181,7 +207,7 @@ def matmul(a, bt, dtype: str) -> np.ndarray:
 
     16-bit types: one MFMA step adds the exact sum of its 32 products to the
     accumulator with one fp32 rounding. fp32: the step is a chain of four-
-    product MFMAs (k = 256 g + 64 q + 8 s + e for q = 0..3, one e at a time).
+    product MFMAs (k = 256 g + 32 s + 8 q + e for q = 0..3, one e at a time).
     """
     a = np.asarray(a, np.float32)
     bt = np.asarray(bt, np.float32)

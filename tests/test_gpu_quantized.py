@@ -56,6 +56,21 @@ def test_quantized_matches_oracle(bits_, gs, dt, M):
     assert ora.max_ulp_excess(got, want, dt, atol=atol) <= 1.0, ora.isclose_report(got, want)
 
 
+@pytest.mark.parametrize("bits_,gs,K", [(4, 64, 1088), (4, 32, 1056), (8, 128, 1152), (8, 32, 288)])
+@pytest.mark.parametrize("M", [1, 20, 40])
+def test_quantized_partial_last_group(bits_, gs, K, M):
+    """K not a multiple of 256: the last K group is cut short (zero padding)."""
+    N = 136
+    wq, s, b = _qweights(N, K, bits_, gs, "bf16", seed=K + M)
+    x = randn((M, K), torch.bfloat16, gen(K))
+    got = to_np(_bi().batch_invariant_quantized_matmul(x, wq.cuda(), s.cuda(), b.cuda(), group_size=gs, bits=bits_))
+    W = ora.dequantize(wq.view(torch.int32).numpy().view(np.uint32), to_np(s), to_np(b), gs, bits_, "bf16")
+    want = ora.matmul(to_np(x), W, "bf16")
+    assert ora.max_ulp_excess(got, want, "bf16", atol=ora.matmul_error_bound(to_np(x), W)) <= 1.0
+    one = _bi().batch_invariant_quantized_matmul(x[:1], wq.cuda(), s.cuda(), b.cuda(), group_size=gs, bits=bits_)
+    assert bits(one) == bits(torch.tensor(got[:1]).to(torch.bfloat16).cuda())
+
+
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128)])
 def test_quantized_equals_dense_on_dequantized_weight(bits_, gs):
     """Same tile body: the quantized kernel and the dense kernel on the
