@@ -43,12 +43,41 @@ def _sync():
     torch.cuda.synchronize()
 
 
-def _time_calls(fn, n, warmup, rotate):
-    """Per-call durations (s) of fn(i) from HIP events on the current stream."""
+def _time_calls(fn, n, warmup, rotate, graph=True, replays=3):
+    """Per-call device time (s) of fn(i), i cycling over `rotate` weight copies.
+
+    graph=True: the n calls are captured into one HIP graph (so the host's
+    per-call launch cost cannot leave the GPU idle between kernels), the graph
+    is replayed, and each replay is bracketed by HIP events on the stream the
+    kernels run on; the result is replay time / n, once per replay.
+    graph=False: events around each eagerly launched call."""
     import torch
     for i in range(warmup):
         fn(i % rotate)
     _sync()
+    if graph:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn(0)                         # allocator warm-up on the capture stream
+        torch.cuda.current_stream().wait_stream(s)
+        _sync()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fn(i % rotate)
+        g.replay()
+        _sync()
+        out = []
+        for _ in range(replays):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            g.replay()
+            b.record()
+            _sync()
+            out.append(a.elapsed_time(b) * 1e-3 / n)
+        del g
+        return out
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
     for i in range(n):
         evs[i][0].record()
@@ -93,18 +122,20 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
         by = qmm_bytes(M, N, K, bits, gs)
         table[M] = {"us": round(t * 1e6, 3), "GBps": round(by / t / 1e9, 1),
                     "frac_hbm": round(by / t / PEAK_HBM, 4)}
-    # headline M = 1 over exactly `steps` timed calls
+    # headline M = 1: exactly `steps` timed calls, captured in one graph
     _sync()
     t0 = time.perf_counter()
-    durs = _time_calls(call(1), args.steps, args.warmup, ncopy)
+    durs = _time_calls(call(1), args.steps, args.warmup, ncopy, replays=1)
     wall = time.perf_counter() - t0
+    eager = statistics.median(_time_calls(call(1), args.steps, args.warmup, ncopy, graph=False))
     # bitwise invariance in the same run: row 0 at M = 1 vs inside M = 64
     inv = all(_bits(call(1)(0)[0]) == _bits(call(M)(0)[0]) for M in Ms)
     # stock, non-invariant baselines: dequantize + hipBLASLt, and bf16 GEMV on the
     # pre-dequantized weight
     Wd = bi.dequantize(copies[0][0], copies[0][1], copies[0][2], gs, bits, dtype=torch.bfloat16)
     stock_deq = statistics.median(_time_calls(
-        lambda i: torch.matmul(xs[:1], bi.dequantize(*copies[i], gs, bits, dtype=torch.bfloat16).t()), 5, 2, ncopy))
+        lambda i: torch.matmul(xs[:1], bi.dequantize(*copies[i], gs, bits, dtype=torch.bfloat16).t()), 5, 2, ncopy,
+        graph=False))
     stock_bf16 = statistics.median(_time_calls(lambda i: torch.matmul(xs[:1], Wd.t()), args.steps, args.warmup, 1))
     t_med = statistics.median(durs)
     by1 = qmm_bytes(1, N, K, bits, gs)
@@ -115,6 +146,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
         "value": round(100 * achieved / PEAK_HBM, 2),
         "unit": "% of HBM roofline (4-bit g64 qmatmul, M=1)" if bits == 4 else f"% of HBM roofline ({bits}-bit g{gs} qmatmul, M=1)",
         "ms_per_step": round(sum(durs) / len(durs) * 1e3, 5),
+        "eager_us_per_call": round(eager * 1e6, 2),
         "wall_s_timed": round(wall, 4),
         "dtype": "bf16",
         "config": {"workload": f"qmatmul {bits}-bit g{gs} affine, x[M,4096] @ W[14336,4096]^T, Llama-3-8B MLP shape",

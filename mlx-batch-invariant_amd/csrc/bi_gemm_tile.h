@@ -28,9 +28,13 @@
 // operand r is the row, for B the column; both hold the 8 k of quarter q.
 // Result register i of lane l is element (row 4 (l/16) + i, column l % 16).
 //
-// Every global load below is issued unconditionally from a clamped, in-bounds
-// address and masked afterwards with a select, so the compiler can put all of
-// a group's loads in flight at once instead of branching around each one.
+// Every global load below is issued unconditionally from an in-bounds address,
+// so the compiler can put all of a group's loads in flight at once instead of
+// branching around each one. Rows of A past M and columns of B past N are
+// clamped to the last valid row/column rather than masked: an MFMA output
+// element depends only on its own row and column, and the results of those
+// padding rows/columns are never stored. Only k past K, in a last group cut
+// short, is masked to exact zero on both operands (the FULL = false path).
 #pragma once
 
 #include "bi_common.h"
@@ -50,18 +54,23 @@ struct DenseB {
   int64_t ldb;
   int N, K;
 
+  // n must already be clamped into [0, N). FULL: the whole group lies inside K.
+  template <bool FULL>
   __device__ __forceinline__ void load(Raw& raw, int n, int g, int q) const {
-    const bool col_ok = n < N;
-    const T* p = bt + (int64_t)(col_ok ? n : 0) * ldb;
+    const T* p = bt + (int64_t)n * ldb + g * kGroupK + 8 * q;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      const int k0 = g * kGroupK + 32 * s + 8 * q;
-      const bool ok = col_ok && k0 < K;
-      const F v = frag_load(p + (ok ? k0 : 0));
-      raw.f[s] = ok ? v : frag_zero<F>();
+      if constexpr (FULL) {
+        raw.f[s] = frag_load(p + 32 * s);
+      } else {
+        const bool ok = g * kGroupK + 32 * s + 8 * q < K;
+        const F v = frag_load(ok ? p + 32 * s : bt);
+        raw.f[s] = ok ? v : frag_zero<F>();
+      }
     }
   }
-  __device__ __forceinline__ F frag(const Raw& raw, int s) const { return raw.f[s]; }
+  template <bool FULL>
+  __device__ __forceinline__ F frag(const Raw& raw, int s, int /*kg*/) const { return raw.f[s]; }
 };
 
 // ---------------------------------------------------------------------------
@@ -83,7 +92,6 @@ struct QuantB {
     uint32_t w[kSteps][kWordsPerStep];
     float scale[kGroupsPerK];
     float bias[kGroupsPerK];
-    int kg;  // first k of the group
   };
   const uint32_t* w;
   const T* scales;
@@ -91,47 +99,52 @@ struct QuantB {
   int N, K;
   int64_t words_per_row, groups_per_row;
 
+  // n must already be clamped into [0, N). FULL: the whole group lies inside K
+  // (then its kGroupsPerK scales are contiguous and, with K % 256 == 0, aligned).
+  template <bool FULL>
   __device__ __forceinline__ void load(Raw& raw, int n, int g, int q) const {
     const int kg = g * kGroupK;
-    raw.kg = kg;
-    const bool col_ok = n < N;
-    const int64_t nn = col_ok ? n : 0;
-    const uint32_t* wp = w + nn * words_per_row;
+    const uint32_t* wp = w + (int64_t)n * words_per_row + (int64_t)(kg + 8 * q) * BITS / 32;
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      const int k0 = kg + 32 * s + 8 * q;                  // K % 32 == 0: whole step in or out
-      const bool ok = col_ok && kg + 32 * s < K;
-      const int64_t wi = ok ? (int64_t)k0 * BITS / 32 : 0;
+      // word offset of step s: 32 s codes further along the row
+      const bool ok = FULL || kg + 32 * s < K;             // K % 32 == 0: whole step in or out
+      const uint32_t* p = ok ? wp + s * (32 * BITS / 32) : w;
       if constexpr (BITS == 4) {
-        raw.w[s][0] = wp[wi];
+        raw.w[s][0] = *p;
       } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(wp + wi);
+        const uint2 v = *reinterpret_cast<const uint2*>(p);
         raw.w[s][0] = v.x;
         raw.w[s][1] = v.y;
       }
     }
-    // Scales/biases of the group: up to kGroupsPerK consecutive entries of row
-    // n (fewer in a last group cut short by K; those read entry 0 and are
-    // never used, since their steps are masked).
+    const int64_t s0 = (int64_t)n * groups_per_row + kg / GS;
 #pragma unroll
     for (int i = 0; i < kGroupsPerK; ++i) {
-      const bool ok = col_ok && kg + i * GS < K;
-      const int64_t si = ok ? nn * groups_per_row + kg / GS + i : 0;
-      raw.scale[i] = to_f32(scales[si]);
-      raw.bias[i] = to_f32(biases[si]);
+      const bool ok = FULL || kg + i * GS < K;
+      raw.scale[i] = to_f32(scales[ok ? s0 + i : 0]);
+      raw.bias[i] = to_f32(biases[ok ? s0 + i : 0]);
     }
   }
 
-  __device__ __forceinline__ F frag(const Raw& raw, int s) const {
+  template <bool FULL>
+  __device__ __forceinline__ F frag(const Raw& raw, int s, int kg) const {
     const int gi = (32 * s) / GS;
     const float sc = raw.scale[gi];
     const float bs = raw.bias[gi];
-    const bool valid = raw.kg + 32 * s < K;
     float d[8];
     if constexpr (BITS == 4) {
-      const uint32_t word = raw.w[s][0];
+      // Split the word's nibbles into two registers of four bytes each; the
+      // empty asm hides the masks from the optimizer so each code converts
+      // with one v_cvt_f32_ubyteN.
+      uint32_t lo = raw.w[s][0] & 0x0F0F0F0Fu;
+      uint32_t hi = (raw.w[s][0] >> 4) & 0x0F0F0F0Fu;
+      asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d[e] = __builtin_fmaf((float)((word >> (4 * e)) & 0xFu), sc, bs);
+      for (int j = 0; j < 4; ++j) {
+        d[2 * j] = __builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), sc, bs);
+        d[2 * j + 1] = __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), sc, bs);
+      }
     } else {
       const uint32_t w0 = raw.w[s][0], w1 = raw.w[s][1];
 #pragma unroll
@@ -140,35 +153,42 @@ struct QuantB {
         d[4 + e] = __builtin_fmaf((float)((w1 >> (8 * e)) & 0xFFu), sc, bs);
       }
     }
+    F f;
     if constexpr (sizeof(T) == 2) {
       typedef T vec8 __attribute__((ext_vector_type(8)));
       vec8 r;
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = to_store<T>(d[e]);
-      const F f = __builtin_bit_cast(F, r);
-      return valid ? f : frag_zero<F>();
+      f = __builtin_bit_cast(F, r);
     } else {
-      f32x8 r;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        r.lo[e] = d[e];
-        r.hi[e] = d[4 + e];
+        f.lo[e] = d[e];
+        f.hi[e] = d[4 + e];
       }
-      return valid ? r : frag_zero<f32x8>();
+    }
+    if constexpr (FULL) {
+      return f;
+    } else {
+      return kg + 32 * s < K ? f : frag_zero<F>();
     }
   }
 };
 
-// A fragment straight from global memory: row m, group g, quarter q, step s.
-template <typename T>
+// A fragment straight from global memory: row m (already clamped into
+// [0, M)), group g, quarter q, step s. FULL: the group lies inside K.
+template <typename T, bool FULL>
 __device__ __forceinline__ typename Frag<T>::type load_a_frag(const T* a, int64_t lda, int m,
-                                                             int M, int K, int g, int q,
-                                                             int s) {
+                                                             int K, int g, int q, int s) {
   typedef typename Frag<T>::type F;
   const int k0 = g * kGroupK + 32 * s + 8 * q;
-  const bool ok = m < M && k0 < K;
-  const F v = frag_load(a + (ok ? (int64_t)m * lda + k0 : 0));
-  return ok ? v : frag_zero<F>();
+  if constexpr (FULL) {
+    return frag_load(a + (int64_t)m * lda + k0);
+  } else {
+    const bool ok = k0 < K;
+    const F v = frag_load(a + (ok ? (int64_t)m * lda + k0 : 0));
+    return ok ? v : frag_zero<F>();
+  }
 }
 
 }  // namespace bi

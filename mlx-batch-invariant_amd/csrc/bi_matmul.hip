@@ -24,18 +24,45 @@ constexpr int kSplitMMax = 32;
 // gemm_direct: MT m-tiles x 1 n-tile per wave, WAVES waves per workgroup
 // along n. SPLIT: one group per workgroup (blockIdx.z), raw partial out.
 // ---------------------------------------------------------------------------
+template <typename T, class BSrc, int MT, bool FULL>
+__device__ __forceinline__ void direct_group(const T* a, int64_t lda, const BSrc& bsrc, int n,
+                                             const int (&rows)[MT], int K, int g, int q,
+                                             f32x4 (&acc)[MT]) {
+  typedef typename Frag<T>::type F;
+  // Load phase: every fragment of the group is requested before any is used.
+  typename BSrc::Raw braw;
+  bsrc.template load<FULL>(braw, n, g, q);
+  F af[MT][kSteps];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) af[i][s] = load_a_frag<T, FULL>(a, lda, rows[i], K, g, q, s);
+  // Compute phase.
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const F bf = bsrc.template frag<FULL>(braw, s, g * kGroupK);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
+  }
+}
+
 template <typename T, class BSrc, int MT, int WAVES, bool SPLIT>
 __global__ __launch_bounds__(kWave* WAVES) void gemm_direct(const T* __restrict__ a, int64_t lda,
                                                             BSrc bsrc, T* __restrict__ out,
                                                             float* __restrict__ part, int M,
                                                             int N, int K, int G) {
-  typedef typename Frag<T>::type F;
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int r = lane % 16, q = lane / 16;
   const int n_base = (blockIdx.x * WAVES + wave) * 16;
   const int m_base = blockIdx.y * 16 * MT;
   if (n_base >= N) return;  // wave-uniform; the kernel has no block barrier
+  const int n = min(n_base + r, N - 1);          // clamped: padding columns are not stored
+  int rows[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) rows[i] = min(m_base + 16 * i + r, M - 1);
   const int g0 = SPLIT ? (int)blockIdx.z : 0;
   const int g1 = SPLIT ? g0 + 1 : G;
 
@@ -44,32 +71,16 @@ __global__ __launch_bounds__(kWave* WAVES) void gemm_direct(const T* __restrict_
   for (int i = 0; i < MT; ++i) total[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int g = g0; g < g1; ++g) {
-    // Load phase: every fragment of the group is requested before any is used.
-    typename BSrc::Raw braw;
-    bsrc.load(braw, n_base + r, g, q);
-    F af[MT][kSteps];
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) af[i][s] = load_a_frag(a, lda, m_base + 16 * i + r, M, K, g, q, s);
-    // Compute phase.
     f32x4 acc[MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const F bf = bsrc.frag(braw, s);
-#pragma unroll
-      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
-    }
+    if ((g + 1) * kGroupK <= K) direct_group<T, BSrc, MT, true>(a, lda, bsrc, n, rows, K, g, q, acc);
+    else direct_group<T, BSrc, MT, false>(a, lda, bsrc, n, rows, K, g, q, acc);
     if constexpr (SPLIT) {
-      const int n = n_base + r;
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int m = m_base + 16 * i + 4 * q + e;
-          if (m < M && n < N) part[((int64_t)g * M + m) * N + n] = acc[i][e];
+          if (m < M && n_base + r < N) part[((int64_t)g * M + m) * N + n] = acc[i][e];
         }
     } else {
 #pragma unroll
@@ -77,26 +88,34 @@ __global__ __launch_bounds__(kWave* WAVES) void gemm_direct(const T* __restrict_
     }
   }
   if constexpr (!SPLIT) {
-    const int n = n_base + r;
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m_base + 16 * i + 4 * q + e;
-        if (m < M && n < N) out[(int64_t)m * N + n] = to_store<T>(total[i][e]);
+        if (m < M && n_base + r < N) out[(int64_t)m * N + n] = to_store<T>(total[i][e]);
       }
   }
 }
 
 // Left fold of the group partials, exactly the fused kernels' fold:
 // total = 0; total = total + part[g] for g = 0 .. G-1; out = T(total).
+// Loads are issued eight groups at a time; the adds stay in group order.
 template <typename T>
 __global__ __launch_bounds__(256) void fold_groups(const float* __restrict__ part,
                                                    T* __restrict__ out, int64_t MN, int G) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= MN) return;
   float total = 0.0f;
-  for (int g = 0; g < G; ++g) total = total + part[(int64_t)g * MN + idx];
+  int g = 0;
+  for (; g + 8 <= G; g += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = part[(int64_t)(g + j) * MN + idx];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) total = total + v[j];
+  }
+  for (; g < G; ++g) total = total + part[(int64_t)g * MN + idx];
   out[idx] = to_store<T>(total);
 }
 
