@@ -98,6 +98,95 @@ __global__ __launch_bounds__(kWave* WAVES) void gemm_direct(const T* __restrict_
   }
 }
 
+// ---------------------------------------------------------------------------
+// gemv_wg: M <= 32, the decode-shaped launch. One workgroup per 16 columns
+// covers every K group: wave w computes groups w, w + W, w + 2W, ... (the
+// loads of its next group are in flight while it computes the current one)
+// and writes each raw fp32 group partial to LDS; after a barrier the
+// workgroup folds the partials in group order, ((0 + p0) + p1) + ..., exactly
+// the fold of the other launches. Concurrent waves of a workgroup read
+// neighbouring 256-k stretches of the same 16 weight rows.
+// Dynamic LDS: G * MT * 64 f32x4 (1 KB per group and m-tile).
+// ---------------------------------------------------------------------------
+template <typename T, class BSrc, int MT>
+struct GroupLoads {
+  typedef typename Frag<T>::type F;
+  typename BSrc::Raw b;
+  F a[MT][kSteps];
+  __device__ __forceinline__ void load(const T* a_, int64_t lda, const BSrc& bsrc, int n,
+                                       const int (&rows)[MT], int K, int g, int q) {
+    bsrc.template load<true>(b, n, g, q);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) a[i][s] = load_a_frag<T, true>(a_, lda, rows[i], K, g, q, s);
+  }
+  __device__ __forceinline__ void compute(const BSrc& bsrc, int g, f32x4 (&acc)[MT]) const {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const F bf = bsrc.template frag<true>(b, s, g * kGroupK);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(a[i][s], bf, acc[i]);
+    }
+  }
+};
+
+template <typename T, class BSrc, int MT, int W>
+__global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int64_t lda,
+                                                    BSrc bsrc, T* __restrict__ out, int M, int N,
+                                                    int K, int G) {
+  extern __shared__ __attribute__((aligned(16))) f32x4 part[];  // [G][MT][64]
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int r = lane % 16, q = lane / 16;
+  const int n_base = blockIdx.x * 16;
+  const int m_base = blockIdx.y * 16 * MT;
+  const int n = min(n_base + r, N - 1);          // clamped: padding columns are not stored
+  int rows[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) rows[i] = min(m_base + 16 * i + r, M - 1);
+
+  const int gfull = K / kGroupK;                 // groups lying entirely inside K
+  // Full groups, software-pipelined two deep.
+  int g = wave;
+  if (g < gfull) {
+    GroupLoads<T, BSrc, MT> cur;
+    cur.load(a, lda, bsrc, n, rows, K, g, q);
+    for (; g < gfull; g += W) {
+      GroupLoads<T, BSrc, MT> nxt;
+      const bool more = g + W < gfull;
+      if (more) nxt.load(a, lda, bsrc, n, rows, K, g + W, q);
+      f32x4 acc[MT];
+      cur.compute(bsrc, g, acc);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) part[(g * MT + i) * kWave + lane] = acc[i];
+      if (more) cur = nxt;
+    }
+  }
+  // A last group cut short by K (zero-padded past K).
+  if (gfull < G && wave == gfull % W) {
+    f32x4 acc[MT];
+    direct_group<T, BSrc, MT, false>(a, lda, bsrc, n, rows, K, gfull, q, acc);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) part[(gfull * MT + i) * kWave + lane] = acc[i];
+  }
+  __syncthreads();
+  // Ordered fold: one thread per (m-tile, lane) of the MFMA result layout.
+  for (int idx = threadIdx.x; idx < MT * kWave; idx += kWave * W) {
+    const int i = idx / kWave, l = idx % kWave;
+    f32x4 total = {0.f, 0.f, 0.f, 0.f};
+    for (int gg = 0; gg < G; ++gg) total = total + part[(gg * MT + i) * kWave + l];
+    const int col = n_base + l % 16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = m_base + 16 * i + 4 * (l / 16) + e;
+      if (m < M && col < N) out[(int64_t)m * N + col] = to_store<T>(total[e]);
+    }
+  }
+}
+
 // Left fold of the group partials, exactly the fused kernels' fold:
 // total = 0; total = total + part[g] for g = 0 .. G-1; out = T(total).
 // Loads are issued eight groups at a time; the adds stay in group order.
@@ -334,6 +423,9 @@ static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b)
 // Launch-shape policy (kernels/matmul.py:279-314): M <= 32 with more than one
 // group -> split partials + fold; otherwise fused. Bits never depend on it.
 static inline bool use_split(int64_t M, int G) { return M <= kSplitMMax && G > 1; }
+// The in-workgroup fold keeps every group partial in LDS (1 KB per group and
+// 16-row tile); up to 64 KB of it. Larger K takes the split + fold launch.
+static inline bool use_wg(int64_t M, int G) { return M <= kSplitMMax && G * (M <= 16 ? 1 : 2) <= 64; }
 
 template <typename T, class BSrc, int BM, int BN>
 static void launch_lds(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K,
@@ -349,6 +441,14 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
                     float* ws, hipStream_t st, const char* what) {
   const int G = ceil_div(K, kGroupK);
   constexpr int WAVES = 4;
+  if (M <= kSplitMMax && use_wg(M, G)) {
+    constexpr int W = 4;
+    dim3 grid(ceil_div(N, 16), 1, 1);
+    const size_t lds = (size_t)G * (M <= 16 ? 1 : 2) * kWave * sizeof(f32x4);
+    if (M <= 16) gemv_wg<T, BSrc, 1, W><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+    else gemv_wg<T, BSrc, 2, W><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+    return bi_host::launch_status(what);
+  }
   if (M <= kSplitMMax) {
     const bool split = use_split(M, G);
     dim3 grid(ceil_div(N, 16 * WAVES), 1, split ? G : 1);
@@ -387,7 +487,7 @@ namespace {
 
 size_t split_ws_bytes(int64_t M, int64_t N, int64_t K) {
   const int64_t G = (K + bi::kGroupK - 1) / bi::kGroupK;
-  if (M <= 0 || N <= 0 || K <= 0 || !bi::use_split(M, (int)G)) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || !bi::use_split(M, (int)G) || bi::use_wg(M, (int)G)) return 0;
   return (size_t)(G * M * N) * sizeof(float);
 }
 

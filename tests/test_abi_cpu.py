@@ -30,11 +30,14 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_sizes():
     lib = _lib.load()
-    assert lib.bi_matmul_workspace_bytes(1, 14336, 4096) == 16 * 1 * 14336 * 4
-    assert lib.bi_matmul_workspace_bytes(32, 100, 896) == 4 * 32 * 100 * 4
-    assert lib.bi_matmul_workspace_bytes(33, 100, 896) == 0          # fused
+    # M <= 32 folds its group partials in LDS up to 64 groups (32 for M > 16)
+    assert lib.bi_matmul_workspace_bytes(1, 14336, 4096) == 0
+    assert lib.bi_matmul_workspace_bytes(32, 100, 896) == 0
+    assert lib.bi_matmul_workspace_bytes(1, 100, 65 * 256) == 65 * 1 * 100 * 4   # split + fold
+    assert lib.bi_matmul_workspace_bytes(20, 100, 33 * 256) == 33 * 20 * 100 * 4
+    assert lib.bi_matmul_workspace_bytes(33, 100, 896) == 0          # fused (LDS tiles)
     assert lib.bi_matmul_workspace_bytes(8, 100, 256) == 0           # one group
-    assert lib.bi_quantized_matmul_workspace_bytes(4, 14336, 4096) == 16 * 4 * 14336 * 4
+    assert lib.bi_quantized_matmul_workspace_bytes(4, 14336, 4096) == 0
     ns = (8192 + 255) // 256
     bh = 256 * 32 * ns
     assert lib.bi_attn_decode_workspace_bytes(256, 32, 8192, 128) == (2 * ((bh + 3) // 4 * 4) + bh * 128) * 4
@@ -51,7 +54,7 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.bi_matmul(p, 12, p, 12, p, 2, 4, 12, 2, None, 0, None) == -1
     assert "multiples of 8" in _err(lib)
     # missing workspace for a split launch
-    assert lib.bi_matmul(p, 512, p, 512, p, 2, 4, 512, 2, None, 0, None) == -3
+    assert lib.bi_matmul(p, 65 * 256, p, 65 * 256, p, 2, 4, 65 * 256, 2, None, 0, None) == -3
     # unsupported quantization
     assert lib.bi_quantized_matmul(p, 64, p, p, p, p, 2, 4, 64, 3, 64, 2, None, 0, None) == -2
     assert lib.bi_quantized_matmul(p, 96, p, p, p, p, 2, 4, 96, 4, 64, 2, None, 0, None) == -1

@@ -98,16 +98,18 @@ def test_matmul_row_position_independence():
     assert not fails, fails
 
 
-def test_matmul_split_equals_fused():
+@pytest.mark.parametrize("K", [4096, 65 * 256 + 128])
+def test_matmul_launch_shapes_agree(K):
+    """M = 1, 16 (workgroup fold, or split partials + fold kernel when K has
+    more than 64 groups), 17..32 (two m-tiles) and 33 (LDS tiles, register
+    fold) give the same bits for the same rows."""
     g = gen(6)
-    K, N = 4096, 512
+    N = 160
     W = randn((N, K), torch.bfloat16, g, scale=0.02)
     x = randn((33, K), torch.bfloat16, g)
-    fused = _mm(x, W.t())                    # M = 33: in-register fold
-    split = _mm(x[:32], W.t())               # M = 32: partials + fold kernel
-    one = _mm(x[:1], W.t())
-    assert bits(fused[:32]) == bits(split)
-    assert bits(fused[:1]) == bits(one)
+    fused = _mm(x, W.t())
+    for M in (1, 16, 20, 32):
+        assert bits(_mm(x[:M], W.t())) == bits(fused[:M]), M
 
 
 def test_matmul_layouts_and_leading_dims():

@@ -2,7 +2,7 @@
 partials (the analogue of the reference's hardware-layout known-answer test,
 tests/test_batch_invariance.py:135-149).
 
-For M <= 32 and more than one K group, bi_matmul writes every group partial
+For M <= 32 and more than 64 K groups, bi_matmul writes every group partial
 acc_g (fp32, before the fold) to the caller's workspace. Reading it back shows
 the MFMA chain's own rounding at fp32 precision, which the bf16 outputs hide.
 The test checks the partials against the oracle's model (each 32-wide step
@@ -46,7 +46,7 @@ def _split_partials(a, bt):
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_split_partials_follow_the_mfma_model(dt):
-    M, N, K = 16, 512, 2048
+    M, N, K = 16, 64, 65 * 256           # > 64 groups: the split launch
     g = gen(21)
     a = randn((M, K), torch.bfloat16 if dt == "bf16" else torch.float16, g)
     bt = randn((N, K), a.dtype, g)
