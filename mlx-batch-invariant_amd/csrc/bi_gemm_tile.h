@@ -90,8 +90,8 @@ struct QuantB {
   static constexpr int kGroupsPerK = kGroupK / GS;         // scales per 256-k group
   struct Raw {
     uint32_t w[kSteps][kWordsPerStep];
-    float scale[kGroupsPerK];
-    float bias[kGroupsPerK];
+    T scale[kGroupsPerK];  // kept in storage type: converted where used, so
+    T bias[kGroupsPerK];   // issuing the loads never waits for them
   };
   const uint32_t* w;
   const T* scales;
@@ -122,16 +122,16 @@ struct QuantB {
 #pragma unroll
     for (int i = 0; i < kGroupsPerK; ++i) {
       const bool ok = FULL || kg + i * GS < K;
-      raw.scale[i] = to_f32(scales[ok ? s0 + i : 0]);
-      raw.bias[i] = to_f32(biases[ok ? s0 + i : 0]);
+      raw.scale[i] = scales[ok ? s0 + i : 0];
+      raw.bias[i] = biases[ok ? s0 + i : 0];
     }
   }
 
   template <bool FULL>
   __device__ __forceinline__ F frag(const Raw& raw, int s, int kg) const {
     const int gi = (32 * s) / GS;
-    const float sc = raw.scale[gi];
-    const float bs = raw.bias[gi];
+    const float sc = to_f32(raw.scale[gi]);
+    const float bs = to_f32(raw.bias[gi]);
     float d[8];
     if constexpr (BITS == 4) {
       // Split the word's nibbles into two registers of four bytes each; the

@@ -149,20 +149,37 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int
   for (int i = 0; i < MT; ++i) rows[i] = min(m_base + 16 * i + r, M - 1);
 
   const int gfull = K / kGroupK;                 // groups lying entirely inside K
-  // Full groups, software-pipelined two deep.
-  int g = wave;
-  if (g < gfull) {
-    GroupLoads<T, BSrc, MT> cur;
-    cur.load(a, lda, bsrc, n, rows, K, g, q);
-    for (; g < gfull; g += W) {
-      GroupLoads<T, BSrc, MT> nxt;
-      const bool more = g + W < gfull;
-      if (more) nxt.load(a, lda, bsrc, n, rows, K, g + W, q);
-      f32x4 acc[MT];
-      cur.compute(bsrc, g, acc);
+  // Full groups, software-pipelined two deep with two fixed buffers: the
+  // loads of a wave's next group are issued before its current group is
+  // computed, and no register copy ties the two together.
+  GroupLoads<T, BSrc, MT> ping, pong;
+  // The prefetch is unconditional (past the wave's last group it re-reads that
+  // group, an L2 hit), so the compiler's wait counters know exactly which
+  // loads are outstanding and never wait for the prefetch before computing.
+  const int last = gfull > wave ? wave + (gfull - 1 - wave) / W * W : -1;
+  if (last >= 0) {
+    int g = wave;
+    ping.load(a, lda, bsrc, n, rows, K, g, q);
+    while (true) {
+      const int g1 = g + W;
+      pong.load(a, lda, bsrc, n, rows, K, min(g1, last), q);
+      {
+        f32x4 acc[MT];
+        ping.compute(bsrc, g, acc);
 #pragma unroll
-      for (int i = 0; i < MT; ++i) part[(g * MT + i) * kWave + lane] = acc[i];
-      if (more) cur = nxt;
+        for (int i = 0; i < MT; ++i) part[(g * MT + i) * kWave + lane] = acc[i];
+      }
+      if (g1 > last) break;
+      const int g2 = g1 + W;
+      ping.load(a, lda, bsrc, n, rows, K, min(g2, last), q);
+      {
+        f32x4 acc[MT];
+        pong.compute(bsrc, g1, acc);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) part[(g1 * MT + i) * kWave + lane] = acc[i];
+      }
+      if (g2 > last) break;
+      g = g2;
     }
   }
   // A last group cut short by K (zero-padded past K).
