@@ -13,9 +13,10 @@
 //       total = total + acc                    # plain fp32 add
 //   out[m, n] = round_to_T(total)
 //
-// with the k-slot map  k(g, s, q, e) = 256 g + 32 s + 8 q + e,  where q in
-// [0,4) is the lane quarter and e in [0,8) the element of the lane's 8-wide
-// fragment: step s of group g covers k in [256 g + 32 s, 256 g + 32 s + 32).
+// with a k-slot map k(g, s, q, e) fixed per op, where q in [0,4) is the lane
+// quarter and e in [0,8) the element of the lane's 8-wide fragment:
+//   dense matmul      k = 256 g + 32 s + 8 q + e   (step s covers 32 consecutive k)
+//   quantized matmul  k = 256 g + 64 q + 8 s + e   (quarter q owns 64 consecutive k)
 // k >= K contributes exact zeros on both operands, and every group always
 // runs all 8 steps. The MFMA instruction (v_mfma_f32_16x16x32_bf16 or _f16; a
 // chain of eight v_mfma_f32_16x16x4_f32 for fp32) is the same for every tile
@@ -70,7 +71,14 @@ struct DenseB {
     }
   }
   template <bool FULL>
-  __device__ __forceinline__ F frag(const Raw& raw, int s, int /*kg*/) const { return raw.f[s]; }
+  __device__ __forceinline__ F frag(const Raw& raw, int s, int /*kq*/) const { return raw.f[s]; }
+
+  // Dense op k-slot map: k(g, s, q, e) = 256 g + 32 s + 8 q + e.
+  static __device__ __forceinline__ int kbase(int g, int q) { return g * kGroupK + 8 * q; }
+  static __device__ __forceinline__ int a_k(int g, int q, int s) { return g * kGroupK + 32 * s + 8 * q; }
+  // LDS staging of steps {2p, 2p+1}: LDS chunk kc (columns 8 kc .. 8 kc + 7,
+  // read by quarter kc % 4 in step 2p + kc / 4) holds these 8 consecutive k.
+  static __device__ __forceinline__ int stage_k(int g, int p, int kc) { return g * kGroupK + 64 * p + 8 * kc; }
 };
 
 // ---------------------------------------------------------------------------
@@ -78,20 +86,28 @@ struct DenseB {
 // codes packed low-to-high in uint32 (32/BITS per word), one scale and bias
 // per GS consecutive k of a row. Dequantised value fed to the MFMA:
 //     T( fmaf(float(code), float(scale), float(bias)) )      (one RNE rounding)
-// and exact zero for k >= K. Step s of a lane needs the 8 codes of k in
-// [256 g + 32 s + 8 q, +8): one word (4-bit) or two (8-bit). The 256/GS
-// scales and biases of the group are the same for all four quarters and are
-// fetched as one small vector per lane.
+// and exact zero for k >= K.
+//
+// The quantized op uses its own k-slot map, the "blocked" map
+//     k(g, s, q, e) = 256 g + 64 q + 8 s + e,
+// so lane quarter q owns the 64 consecutive codes [256 g + 64 q, +64) of its
+// row: two (4-bit) or four (8-bit) 16-byte loads of consecutive words, and for
+// group size 64 exactly one scale and bias. (Weight rows are then read as long
+// contiguous runs per lane; the dense op's map would read them 16 bytes per
+// four lanes, which measured 2.6x slower on the loads alone.) Every launch
+// shape of the quantized op uses this map, so the op is consistent with itself
+// across batch sizes, as the reference requires of each op
+// (kernels/matmul.py:11-12).
 // ---------------------------------------------------------------------------
 template <typename T, int BITS, int GS>
 struct QuantB {
   typedef typename Frag<T>::type F;
-  static constexpr int kWordsPerStep = BITS / 4;          // 1 (4-bit) or 2 (8-bit)
-  static constexpr int kGroupsPerK = kGroupK / GS;         // scales per 256-k group
+  static constexpr int kWords = 64 * BITS / 32;            // words per lane per group: 8 or 16
+  static constexpr int kScales = GS >= 64 ? 1 : 64 / GS;   // scales per lane per group
   struct Raw {
-    uint32_t w[kSteps][kWordsPerStep];
-    T scale[kGroupsPerK];  // kept in storage type: converted where used, so
-    T bias[kGroupsPerK];   // issuing the loads never waits for them
+    u32x4 w[kWords / 4];
+    T scale[kScales];  // kept in storage type: converted where used, so
+    T bias[kScales];   // issuing the loads never waits for them
   };
   const uint32_t* w;
   const T* scales;
@@ -99,46 +115,41 @@ struct QuantB {
   int N, K;
   int64_t words_per_row, groups_per_row;
 
-  // n must already be clamped into [0, N). FULL: the whole group lies inside K
-  // (then its kGroupsPerK scales are contiguous and, with K % 256 == 0, aligned).
+  static __device__ __forceinline__ int kbase(int g, int q) { return g * kGroupK + 64 * q; }
+
+  // n must already be clamped into [0, N). FULL: the whole group lies inside K.
   template <bool FULL>
   __device__ __forceinline__ void load(Raw& raw, int n, int g, int q) const {
-    const int kg = g * kGroupK;
-    const uint32_t* wp = w + (int64_t)n * words_per_row + (int64_t)(kg + 8 * q) * BITS / 32;
+    const int kq = kbase(g, q);
+    const uint32_t* wp = w + (int64_t)n * words_per_row + (int64_t)kq * BITS / 32;
+    constexpr int kPerPiece = 4 * 32 / BITS;                 // codes per 16-byte piece
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      // word offset of step s: 32 s codes further along the row
-      const bool ok = FULL || kg + 32 * s < K;             // K % 32 == 0: whole step in or out
-      const uint32_t* p = ok ? wp + s * (32 * BITS / 32) : w;
-      if constexpr (BITS == 4) {
-        raw.w[s][0] = *p;
-      } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        raw.w[s][0] = v.x;
-        raw.w[s][1] = v.y;
-      }
+    for (int p = 0; p < kWords / 4; ++p) {
+      const bool ok = FULL || kq + p * kPerPiece < K;        // K % 32 == 0: whole piece in or out
+      raw.w[p] = *reinterpret_cast<const u32x4*>(ok ? wp + 4 * p : w);
     }
-    const int64_t s0 = (int64_t)n * groups_per_row + kg / GS;
+    const int64_t s0 = (int64_t)n * groups_per_row + kq / GS;
 #pragma unroll
-    for (int i = 0; i < kGroupsPerK; ++i) {
-      const bool ok = FULL || kg + i * GS < K;
+    for (int i = 0; i < kScales; ++i) {
+      const bool ok = FULL || kq + i * GS < K;
       raw.scale[i] = scales[ok ? s0 + i : 0];
       raw.bias[i] = biases[ok ? s0 + i : 0];
     }
   }
 
   template <bool FULL>
-  __device__ __forceinline__ F frag(const Raw& raw, int s, int kg) const {
-    const int gi = (32 * s) / GS;
-    const float sc = to_f32(raw.scale[gi]);
-    const float bs = to_f32(raw.bias[gi]);
+  __device__ __forceinline__ F frag(const Raw& raw, int s, int kq) const {
+    const int si = (GS >= 64) ? 0 : (8 * s) / GS;
+    const float sc = to_f32(raw.scale[si]);
+    const float bs = to_f32(raw.bias[si]);
     float d[8];
     if constexpr (BITS == 4) {
       // Split the word's nibbles into two registers of four bytes each; the
       // empty asm hides the masks from the optimizer so each code converts
       // with one v_cvt_f32_ubyteN.
-      uint32_t lo = raw.w[s][0] & 0x0F0F0F0Fu;
-      uint32_t hi = (raw.w[s][0] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t word = raw.w[s / 4][s % 4];
+      uint32_t lo = word & 0x0F0F0F0Fu;
+      uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
       asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -146,7 +157,7 @@ struct QuantB {
         d[2 * j + 1] = __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), sc, bs);
       }
     } else {
-      const uint32_t w0 = raw.w[s][0], w1 = raw.w[s][1];
+      const uint32_t w0 = raw.w[s / 2][2 * (s % 2)], w1 = raw.w[s / 2][2 * (s % 2) + 1];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         d[e] = __builtin_fmaf((float)((w0 >> (8 * e)) & 0xFFu), sc, bs);
@@ -170,18 +181,26 @@ struct QuantB {
     if constexpr (FULL) {
       return f;
     } else {
-      return kg + 32 * s < K ? f : frag_zero<F>();
+      return kq + 8 * s < K ? f : frag_zero<F>();
     }
+  }
+
+  // The A operand must follow the same map: element k of lane quarter q, step s.
+  static __device__ __forceinline__ int a_k(int g, int q, int s) { return g * kGroupK + 64 * q + 8 * s; }
+  // LDS staging of steps {2p, 2p+1}: LDS chunk kc (read by quarter kc % 4 in
+  // step 2p + kc / 4) holds these 8 consecutive k.
+  static __device__ __forceinline__ int stage_k(int g, int p, int kc) {
+    return g * kGroupK + 64 * (kc % 4) + 16 * p + 8 * (kc / 4);
   }
 };
 
 // A fragment straight from global memory: row m (already clamped into
-// [0, M)), group g, quarter q, step s. FULL: the group lies inside K.
+// [0, M)), first k of the fragment k0 (from the op's k-slot map). FULL: the
+// group lies inside K.
 template <typename T, bool FULL>
 __device__ __forceinline__ typename Frag<T>::type load_a_frag(const T* a, int64_t lda, int m,
-                                                             int K, int g, int q, int s) {
+                                                             int K, int k0) {
   typedef typename Frag<T>::type F;
-  const int k0 = g * kGroupK + 32 * s + 8 * q;
   if constexpr (FULL) {
     return frag_load(a + (int64_t)m * lda + k0);
   } else {

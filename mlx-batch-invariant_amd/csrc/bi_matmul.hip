@@ -36,13 +36,13 @@ __device__ __forceinline__ void direct_group(const T* a, int64_t lda, const BSrc
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s) af[i][s] = load_a_frag<T, FULL>(a, lda, rows[i], K, g, q, s);
+    for (int s = 0; s < kSteps; ++s) af[i][s] = load_a_frag<T, FULL>(a, lda, rows[i], K, BSrc::a_k(g, q, s));
   // Compute phase.
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const F bf = bsrc.template frag<FULL>(braw, s, g * kGroupK);
+    const F bf = bsrc.template frag<FULL>(braw, s, BSrc::kbase(g, q));
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
   }
@@ -119,14 +119,14 @@ struct GroupLoads {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int s = 0; s < kSteps; ++s) a[i][s] = load_a_frag<T, true>(a_, lda, rows[i], K, g, q, s);
+      for (int s = 0; s < kSteps; ++s) a[i][s] = load_a_frag<T, true>(a_, lda, rows[i], K, BSrc::a_k(g, q, s));
   }
-  __device__ __forceinline__ void compute(const BSrc& bsrc, int g, f32x4 (&acc)[MT]) const {
+  __device__ __forceinline__ void compute(const BSrc& bsrc, int g, int q, f32x4 (&acc)[MT]) const {
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) {
-      const F bf = bsrc.template frag<true>(b, s, g * kGroupK);
+      const F bf = bsrc.template frag<true>(b, s, BSrc::kbase(g, q));
 #pragma unroll
       for (int i = 0; i < MT; ++i) acc[i] = mfma_step(a[i][s], bf, acc[i]);
     }
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int
       pong.load(a, lda, bsrc, n, rows, K, min(g1, last), q);
       {
         f32x4 acc[MT];
-        ping.compute(bsrc, g, acc);
+        ping.compute(bsrc, g, q, acc);
 #pragma unroll
         for (int i = 0; i < MT; ++i) part[(g * MT + i) * kWave + lane] = acc[i];
       }
@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int
       ping.load(a, lda, bsrc, n, rows, K, min(g2, last), q);
       {
         f32x4 acc[MT];
-        pong.compute(bsrc, g1, acc);
+        pong.compute(bsrc, g1, q, acc);
 #pragma unroll
         for (int i = 0; i < MT; ++i) part[(g1 * MT + i) * kWave + lane] = acc[i];
       }
@@ -227,24 +227,26 @@ __global__ __launch_bounds__(256) void fold_groups(const float* __restrict__ par
 
 // ---------------------------------------------------------------------------
 // gemm_lds: BM x BN tile, 4 waves in 2 x 2, each wave (BM/2) x (BN/2).
-// K stage = 64 (two MFMA steps); group g = stages 4g .. 4g+3.
+// K stage = two MFMA steps {2p, 2p+1} of group g (64 k, which k is the op's
+// k-slot map); group g = stages 4g .. 4g+3.
 // ---------------------------------------------------------------------------
 constexpr int kStageK = 64;
 constexpr int kLdsPad = 8;                      // elements; rows 16 B apart in banks
 constexpr int kLdsRow = kStageK + kLdsPad;      // LDS row length (elements)
 
-// Stages one BM x 64 slab of A (rows m0 .., k0 ..) into LDS, 8-element chunks.
-template <typename T, int ROWS>
+// Stages the two MFMA steps {2p, 2p+1} of group g for ROWS rows into LDS as
+// 8-element chunks; MAP (the B source type) says which k each LDS chunk holds.
+template <typename T, int ROWS, class MAP>
 struct StageA {
   static constexpr int kChunks = ROWS * (kStageK / 8) / 256;  // per thread
   typedef typename Frag<T>::type F;
   F v[kChunks];
-  __device__ __forceinline__ void load(const T* a, int64_t lda, int M, int K, int m0, int k0) {
+  __device__ __forceinline__ void load(const T* a, int64_t lda, int M, int K, int m0, int g, int p) {
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int c = threadIdx.x + 256 * i;
       const int row = c / 8, kc = c % 8;
-      const int m = m0 + row, k = k0 + 8 * kc;
+      const int m = m0 + row, k = MAP::stage_k(g, p, kc);
       const bool ok = m < M && k < K;
       const F x = frag_load(a + (ok ? (int64_t)m * lda + k : 0));
       v[i] = ok ? x : frag_zero<F>();
@@ -263,9 +265,9 @@ struct StageA {
 // B stage for dense operands: same chunking as A over bt rows (columns n).
 template <typename T, int ROWS>
 struct StageDenseB {
-  StageA<T, ROWS> s;
-  __device__ __forceinline__ void load(const DenseB<T>& b, int n0, int k0) {
-    s.load(b.bt, b.ldb, b.N, b.K, n0, k0);
+  StageA<T, ROWS, DenseB<T>> s;
+  __device__ __forceinline__ void load(const DenseB<T>& b, int n0, int g, int p) {
+    s.load(b.bt, b.ldb, b.N, b.K, n0, g, p);
   }
   __device__ __forceinline__ void store(T* lds) const { s.store(lds); }
 };
@@ -277,15 +279,16 @@ struct StageQuantB {
   static constexpr int kChunks = ROWS * (kStageK / 8) / 256;
   static constexpr int kWords = BITS / 4;
   typedef typename Frag<T>::type F;
+  typedef QuantB<T, BITS, GS> Src;
   uint32_t w[kChunks][kWords];
-  float sc[kChunks], bs[kChunks];
+  T sc[kChunks], bs[kChunks];
   bool ok[kChunks];
-  __device__ __forceinline__ void load(const QuantB<T, BITS, GS>& b, int n0, int k0) {
+  __device__ __forceinline__ void load(const Src& b, int n0, int g, int p) {
 #pragma unroll
     for (int i = 0; i < kChunks; ++i) {
       const int c = threadIdx.x + 256 * i;
       const int row = c / 8, kc = c % 8;
-      const int n = n0 + row, k = k0 + 8 * kc;
+      const int n = n0 + row, k = Src::stage_k(g, p, kc);
       const bool good = n < b.N && k < b.K;
       const int64_t nn = good ? n : 0;
       const int kk = good ? k : 0;
@@ -298,8 +301,8 @@ struct StageQuantB {
         w[i][1] = x.y;
       }
       const int64_t si = nn * b.groups_per_row + kk / GS;
-      sc[i] = to_f32(b.scales[si]);
-      bs[i] = to_f32(b.biases[si]);
+      sc[i] = b.scales[si];
+      bs[i] = b.biases[si];
       ok[i] = good;
     }
   }
@@ -308,15 +311,16 @@ struct StageQuantB {
     for (int i = 0; i < kChunks; ++i) {
       const int c = threadIdx.x + 256 * i;
       const int row = c / 8, kc = c % 8;
+      const float s = to_f32(sc[i]), bb = to_f32(bs[i]);
       float d[8];
       if constexpr (BITS == 4) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d[e] = __builtin_fmaf((float)((w[i][0] >> (4 * e)) & 0xFu), sc[i], bs[i]);
+        for (int e = 0; e < 8; ++e) d[e] = __builtin_fmaf((float)((w[i][0] >> (4 * e)) & 0xFu), s, bb);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          d[e] = __builtin_fmaf((float)((w[i][0] >> (8 * e)) & 0xFFu), sc[i], bs[i]);
-          d[4 + e] = __builtin_fmaf((float)((w[i][1] >> (8 * e)) & 0xFFu), sc[i], bs[i]);
+          d[e] = __builtin_fmaf((float)((w[i][0] >> (8 * e)) & 0xFFu), s, bb);
+          d[4 + e] = __builtin_fmaf((float)((w[i][1] >> (8 * e)) & 0xFFu), s, bb);
         }
       }
       F f;
@@ -377,11 +381,11 @@ __global__ __launch_bounds__(256) void gemm_lds(const T* __restrict__ a, int64_t
       acc[i][j] = total[i][j];
     }
 
-  StageA<T, BM> sa;
+  StageA<T, BM, BSrc> sa;
   typename StageFor<BSrc, T, BN>::type sb;
   const int nstages = 4 * G;
-  sa.load(a, lda, M, K, m0, 0);
-  sb.load(bsrc, n0, 0);
+  sa.load(a, lda, M, K, m0, 0, 0);
+  sb.load(bsrc, n0, 0, 0);
   sa.store(As[0]);
   sb.store(Bs[0]);
   __syncthreads();
@@ -389,8 +393,8 @@ __global__ __launch_bounds__(256) void gemm_lds(const T* __restrict__ a, int64_t
   for (int st = 0; st < nstages; ++st) {
     const int buf = st & 1;
     if (st + 1 < nstages) {
-      sa.load(a, lda, M, K, m0, (st + 1) * kStageK);
-      sb.load(bsrc, n0, (st + 1) * kStageK);
+      sa.load(a, lda, M, K, m0, (st + 1) >> 2, (st + 1) & 3);
+      sb.load(bsrc, n0, (st + 1) >> 2, (st + 1) & 3);
     }
     const T* Ab = As[buf] + (wm * TM * 16 + r) * kLdsRow + 8 * q;
     const T* Bb = Bs[buf] + (wn * TN * 16 + r) * kLdsRow + 8 * q;

@@ -168,15 +168,20 @@ def dequantize(w_u32, scales, biases, group_size: int, bits: int, dtype: str) ->
 # Matmul — reference kernels/matmul.py:1-38, :81-190 (fixed 256 K groups, MMA
 # steps from a zero accumulator, group partials folded left to right with
 # plain fp32 adds, :174-176 and the combine :226-234).
-# gfx950 k-slot map: group g, step s, lane quarter q, element e ->
-#   k = 256 g + 32 s + 8 q + e   (step s covers k in [256 g + 32 s, +32)).
+# gfx950 k-slot maps (group g, step s, lane quarter q, element e -> k), one per op:
+#   "natural" (dense matmul):     k = 256 g + 32 s + 8 q + e
+#   "blocked" (quantized matmul): k = 256 g + 64 q + 8 s + e
 # ---------------------------------------------------------------------------
 
-def step_indices(g: int, s: int) -> np.ndarray:
-    return np.array([GROUP_K * g + 32 * s + 8 * q + e for q in range(4) for e in range(8)])
+def step_indices(g: int, s: int, kmap: str = "natural") -> np.ndarray:
+    if kmap == "natural":
+        return np.array([GROUP_K * g + 32 * s + 8 * q + e for q in range(4) for e in range(8)])
+    if kmap == "blocked":
+        return np.array([GROUP_K * g + 64 * q + 8 * s + e for q in range(4) for e in range(8)])
+    raise ValueError(kmap)
 
 
-def group_partials(a, bt, dtype: str) -> np.ndarray:
+def group_partials(a, bt, dtype: str, kmap: str = "natural") -> np.ndarray:
     """acc_g[M, N] for every K group (fp32), the values the split launch writes."""
     a = np.asarray(a, np.float32)
     bt = np.asarray(bt, np.float32)
@@ -191,7 +196,7 @@ def group_partials(a, bt, dtype: str) -> np.ndarray:
     for g in range(G):
         acc = np.zeros((M, N), np.float32)
         for s in range(STEPS):
-            idx = step_indices(g, s)
+            idx = step_indices(g, s, kmap)
             if dtype == "f32":
                 for e in range(8):
                     sub = idx[e::8]
@@ -202,12 +207,13 @@ def group_partials(a, bt, dtype: str) -> np.ndarray:
     return out
 
 
-def matmul(a, bt, dtype: str) -> np.ndarray:
+def matmul(a, bt, dtype: str, kmap: str = "natural") -> np.ndarray:
     """out[M, N] = a[M, K] @ bt[N, K].T in the kernels' order.
 
     16-bit types: one MFMA step adds the exact sum of its 32 products to the
     accumulator with one fp32 rounding. fp32: the step is a chain of four-
-    product MFMAs (k = 256 g + 32 s + 8 q + e for q = 0..3, one e at a time).
+    product MFMAs (the four quarters' k for one e at a time). ``kmap`` is the
+    op's k-slot map: "natural" for the dense op, "blocked" for the quantized.
     """
     a = np.asarray(a, np.float32)
     bt = np.asarray(bt, np.float32)
@@ -223,7 +229,7 @@ def matmul(a, bt, dtype: str) -> np.ndarray:
     for g in range(G):
         acc = np.zeros((M, N), np.float32)
         for s in range(STEPS):
-            idx = step_indices(g, s)
+            idx = step_indices(g, s, kmap)
             if dtype == "f32":
                 for e in range(8):
                     sub = idx[e::8]

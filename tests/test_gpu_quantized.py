@@ -51,7 +51,7 @@ def test_quantized_matches_oracle(bits_, gs, dt, M):
     got = to_np(_bi().batch_invariant_quantized_matmul(x, wq.cuda(), s.cuda(), b.cuda(),
                                                        group_size=gs, bits=bits_))
     W = ora.dequantize(wq.view(torch.int32).numpy().view(np.uint32), to_np(s), to_np(b), gs, bits_, dt)
-    want = ora.matmul(to_np(x), W, dt)
+    want = ora.matmul(to_np(x), W, dt, kmap="blocked")
     atol = ora.matmul_error_bound(to_np(x), W)
     assert ora.max_ulp_excess(got, want, dt, atol=atol) <= 1.0, ora.isclose_report(got, want)
 
@@ -65,25 +65,24 @@ def test_quantized_partial_last_group(bits_, gs, K, M):
     x = randn((M, K), torch.bfloat16, gen(K))
     got = to_np(_bi().batch_invariant_quantized_matmul(x, wq.cuda(), s.cuda(), b.cuda(), group_size=gs, bits=bits_))
     W = ora.dequantize(wq.view(torch.int32).numpy().view(np.uint32), to_np(s), to_np(b), gs, bits_, "bf16")
-    want = ora.matmul(to_np(x), W, "bf16")
+    want = ora.matmul(to_np(x), W, "bf16", kmap="blocked")
     assert ora.max_ulp_excess(got, want, "bf16", atol=ora.matmul_error_bound(to_np(x), W)) <= 1.0
     one = _bi().batch_invariant_quantized_matmul(x[:1], wq.cuda(), s.cuda(), b.cuda(), group_size=gs, bits=bits_)
     assert bits(one) == bits(torch.tensor(got[:1]).to(torch.bfloat16).cuda())
 
 
-@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128)])
-def test_quantized_equals_dense_on_dequantized_weight(bits_, gs):
-    """Same tile body: the quantized kernel and the dense kernel on the
-    dequantized bf16 weight give identical bits."""
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
+def test_quantized_launch_shapes_agree(bits_, gs):
+    """M = 1 and 16 (one m-tile, workgroup fold), 20 and 32 (two m-tiles), 33
+    and 100 (LDS tiles, register fold) give the same bits for the same rows."""
     N, K = 512, 2048
     wq, s, b = _qweights(N, K, bits_, gs, "bf16", seed=9)
-    W = torch.tensor(ora.dequantize(wq.view(torch.int32).numpy().view(np.uint32), to_np(s), to_np(b),
-                                    gs, bits_, "bf16")).to(torch.bfloat16).cuda()
-    for M in (1, 7, 32, 33, 100):
-        x = randn((M, K), torch.bfloat16, gen(M))
-        q = _bi().batch_invariant_quantized_matmul(x, wq.cuda(), s.cuda(), b.cuda(), group_size=gs, bits=bits_)
-        d = _bi().batch_invariant_matmul(x, W.t())
-        assert bits(q) == bits(d), M
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    x = randn((100, K), torch.bfloat16, gen(3))
+    full = _bi().batch_invariant_quantized_matmul(x, wq, s, b, group_size=gs, bits=bits_)
+    for M in (1, 16, 20, 32, 33):
+        got = _bi().batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=gs, bits=bits_)
+        assert bits(got) == bits(full[:M]), M
 
 
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])

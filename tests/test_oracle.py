@@ -122,10 +122,22 @@ def test_matmul_integer_known_answer(M, N, K):
     assert np.array_equal(ora.matmul(a, b, "f32"), (a.astype(np.int64) @ b.T.astype(np.int64)).astype(np.float32))
 
 
-def test_matmul_k_slot_map_covers_each_k_once():
+@pytest.mark.parametrize("kmap", ["natural", "blocked"])
+def test_matmul_k_slot_map_covers_each_k_once(kmap):
     for g in range(3):
-        ks = np.concatenate([ora.step_indices(g, s) for s in range(ora.STEPS)])
+        ks = np.concatenate([ora.step_indices(g, s, kmap) for s in range(ora.STEPS)])
         assert sorted(ks.tolist()) == list(range(256 * g, 256 * g + 256))
+    # the maps differ: natural steps are 32 consecutive k, blocked steps are 4 runs of 8
+    assert ora.step_indices(0, 0, "natural").tolist() == list(range(32))
+    assert ora.step_indices(0, 1, "blocked").tolist()[:9] == [8, 9, 10, 11, 12, 13, 14, 15, 72]
+
+
+def test_matmul_integer_known_answer_blocked_map():
+    rng = np.random.default_rng(12)
+    a = rng.integers(-3, 4, size=(4, 640)).astype(np.float32)
+    b = rng.integers(-3, 4, size=(6, 640)).astype(np.float32)
+    want = (a.astype(np.int64) @ b.T.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(ora.matmul(a, b, "f32", kmap="blocked"), want)
 
 
 def test_matmul_identity_and_transpose():
