@@ -144,17 +144,39 @@ struct QuantB {
     const float bs = to_f32(raw.bias[si]);
     float d[8];
     if constexpr (BITS == 4) {
-      // Split the word's nibbles into two registers of four bytes each; the
-      // empty asm hides the masks from the optimizer so each code converts
-      // with one v_cvt_f32_ubyteN.
+      // Split the word's nibbles into two registers of four bytes each (even
+      // codes, odd codes). A byte holding a code c <= 15 read as an FP8 E4M3
+      // value is exactly c * u with u a power of two (2^-9 for the OCP
+      // encoding: denormal for c < 8, exponent field 1 for c >= 8), so one
+      // v_cvt_pk_f32_fp8 converts two codes and
+      //     fmaf(c * u, scale / u, bias) == fmaf(c, scale, bias)
+      // bit for bit (both scalings are exact; the product is the same real
+      // number). A scale so large that scale / u would overflow takes the
+      // integer conversion instead.
       const uint32_t word = raw.w[s / 4][s % 4];
-      uint32_t lo = word & 0x0F0F0F0Fu;
-      uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
-      asm volatile("" : "+v"(lo), "+v"(hi));
+      const uint32_t lo = word & 0x0F0F0F0Fu;
+      const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
+      if (__builtin_expect(fabsf(sc) < 0x1p100f, 1)) {
+        const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1u, false)[0];
+        const float sc_u = sc / unit;
+        const auto c02 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
+        const auto c46 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+        const auto c13 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
+        const auto c57 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+        d[0] = __builtin_fmaf(c02[0], sc_u, bs);
+        d[1] = __builtin_fmaf(c13[0], sc_u, bs);
+        d[2] = __builtin_fmaf(c02[1], sc_u, bs);
+        d[3] = __builtin_fmaf(c13[1], sc_u, bs);
+        d[4] = __builtin_fmaf(c46[0], sc_u, bs);
+        d[5] = __builtin_fmaf(c57[0], sc_u, bs);
+        d[6] = __builtin_fmaf(c46[1], sc_u, bs);
+        d[7] = __builtin_fmaf(c57[1], sc_u, bs);
+      } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        d[2 * j] = __builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), sc, bs);
-        d[2 * j + 1] = __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), sc, bs);
+        for (int j = 0; j < 4; ++j) {
+          d[2 * j] = __builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), sc, bs);
+          d[2 * j + 1] = __builtin_fmaf((float)((hi >> (8 * j)) & 0xFFu), sc, bs);
+        }
       }
     } else {
       const uint32_t w0 = raw.w[s / 2][2 * (s % 2)], w1 = raw.w[s / 2][2 * (s % 2) + 1];

@@ -99,45 +99,26 @@ __global__ __launch_bounds__(kWave* WAVES) void gemm_direct(const T* __restrict_
 }
 
 // ---------------------------------------------------------------------------
-// gemv_wg: M <= 32, the decode-shaped launch. One workgroup per 16 columns
-// covers every K group: wave w computes groups w, w + W, w + 2W, ... (the
-// loads of its next group are in flight while it computes the current one)
+// gemv_wg: M <= 32, the decode-shaped launch. One workgroup of W waves per 16
+// columns covers every K group: wave w computes groups w, w + W, w + 2W, ...,
 // and writes each raw fp32 group partial to LDS; after a barrier the
 // workgroup folds the partials in group order, ((0 + p0) + p1) + ..., exactly
-// the fold of the other launches. Concurrent waves of a workgroup read
-// neighbouring 256-k stretches of the same 16 weight rows.
-// Dynamic LDS: G * MT * 64 f32x4 (1 KB per group and m-tile).
+// the fold of the other launches. A wave issues the B-operand loads of up to
+// NB of its groups before computing any of them (all unconditional, so the
+// wait counters only ever wait for the group being computed). With ALDS the
+// M rows of A are staged once per workgroup into LDS (while the first weight
+// loads are in flight) and A fragments are read from there.
+// Dynamic LDS: G * MT * 64 f32x4 partials, then (ALDS) M rows of K + 8 elements.
 // ---------------------------------------------------------------------------
-template <typename T, class BSrc, int MT>
-struct GroupLoads {
-  typedef typename Frag<T>::type F;
-  typename BSrc::Raw b;
-  F a[MT][kSteps];
-  __device__ __forceinline__ void load(const T* a_, int64_t lda, const BSrc& bsrc, int n,
-                                       const int (&rows)[MT], int K, int g, int q) {
-    bsrc.template load<true>(b, n, g, q);
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) a[i][s] = load_a_frag<T, true>(a_, lda, rows[i], K, BSrc::a_k(g, q, s));
-  }
-  __device__ __forceinline__ void compute(const BSrc& bsrc, int g, int q, f32x4 (&acc)[MT]) const {
-#pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const F bf = bsrc.template frag<true>(b, s, BSrc::kbase(g, q));
-#pragma unroll
-      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(a[i][s], bf, acc[i]);
-    }
-  }
-};
-
-template <typename T, class BSrc, int MT, int W>
+template <typename T, class BSrc, int MT, int W, int NB, bool ALDS>
 __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int64_t lda,
                                                     BSrc bsrc, T* __restrict__ out, int M, int N,
                                                     int K, int G) {
-  extern __shared__ __attribute__((aligned(16))) f32x4 part[];  // [G][MT][64]
+  typedef typename Frag<T>::type F;
+  extern __shared__ __attribute__((aligned(16))) f32x4 smem[];
+  f32x4* part = smem;                                        // [G][MT][64]
+  T* As = reinterpret_cast<T*>(smem + (size_t)G * MT * kWave);  // [M][K + 8]
+  const int lds_row = K + 8;
   const int lane = threadIdx.x % kWave;
   const int wave = threadIdx.x / kWave;
   const int r = lane % 16, q = lane / 16;
@@ -149,40 +130,63 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int
   for (int i = 0; i < MT; ++i) rows[i] = min(m_base + 16 * i + r, M - 1);
 
   const int gfull = K / kGroupK;                 // groups lying entirely inside K
-  // Full groups, software-pipelined two deep with two fixed buffers: the
-  // loads of a wave's next group are issued before its current group is
-  // computed, and no register copy ties the two together.
-  GroupLoads<T, BSrc, MT> ping, pong;
-  // The prefetch is unconditional (past the wave's last group it re-reads that
-  // group, an L2 hit), so the compiler's wait counters know exactly which
-  // loads are outstanding and never wait for the prefetch before computing.
-  const int last = gfull > wave ? wave + (gfull - 1 - wave) / W * W : -1;
-  if (last >= 0) {
-    int g = wave;
-    ping.load(a, lda, bsrc, n, rows, K, g, q);
-    while (true) {
-      const int g1 = g + W;
-      pong.load(a, lda, bsrc, n, rows, K, min(g1, last), q);
-      {
+  const int nw = gfull > wave ? (gfull - 1 - wave) / W + 1 : 0;   // this wave's full groups
+  const int last = wave + (nw - 1) * W;
+
+  auto compute = [&](const typename BSrc::Raw& braw, int g, f32x4 (&acc)[MT]) {
+    F af[MT][kSteps];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const int k0 = BSrc::a_k(g, q, s);
+        if constexpr (ALDS)
+          af[i][s] = *reinterpret_cast<const F*>(As + (size_t)(rows[i] - m_base) * lds_row + k0);
+        else
+          af[i][s] = load_a_frag<T, true>(a, lda, rows[i], K, k0);
+      }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const F bf = bsrc.template frag<true>(braw, s, BSrc::kbase(g, q));
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
+    }
+  };
+
+  typename BSrc::Raw braw[NB];
+  // First chunk of weight loads, then (ALDS) stage A while they are in flight.
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+    if (nw > 0) bsrc.template load<true>(braw[j], n, min(wave + j * W, last), q);
+  if constexpr (ALDS) {
+    const int mrows = min(M - m_base, 16 * MT);
+    const int chunks = mrows * (K / 8);
+    for (int c = threadIdx.x; c < chunks; c += kWave * W) {
+      const int rr = c / (K / 8), kc = c % (K / 8);
+      *reinterpret_cast<F*>(As + (size_t)rr * lds_row + 8 * kc) =
+          frag_load(a + (int64_t)(m_base + rr) * lda + 8 * kc);
+    }
+    __syncthreads();
+  }
+  for (int c0 = 0; c0 < nw; c0 += NB) {
+    if (c0 > 0) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) bsrc.template load<true>(braw[j], n, min(wave + (c0 + j) * W, last), q);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (c0 + j < nw) {
+        const int g = wave + (c0 + j) * W;
         f32x4 acc[MT];
-        ping.compute(bsrc, g, q, acc);
+        compute(braw[j], g, acc);
 #pragma unroll
         for (int i = 0; i < MT; ++i) part[(g * MT + i) * kWave + lane] = acc[i];
       }
-      if (g1 > last) break;
-      const int g2 = g1 + W;
-      ping.load(a, lda, bsrc, n, rows, K, min(g2, last), q);
-      {
-        f32x4 acc[MT];
-        pong.compute(bsrc, g1, q, acc);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) part[(g1 * MT + i) * kWave + lane] = acc[i];
-      }
-      if (g2 > last) break;
-      g = g2;
     }
   }
-  // A last group cut short by K (zero-padded past K).
+  // A last group cut short by K (zero-padded past K), A from global memory.
   if (gfull < G && wave == gfull % W) {
     f32x4 acc[MT];
     direct_group<T, BSrc, MT, false>(a, lda, bsrc, n, rows, K, gfull, q, acc);
@@ -463,11 +467,19 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   const int G = ceil_div(K, kGroupK);
   constexpr int WAVES = 4;
   if (M <= kSplitMMax && use_wg(M, G)) {
-    constexpr int W = 4;
+    constexpr int W = 8;
     dim3 grid(ceil_div(N, 16), 1, 1);
-    const size_t lds = (size_t)G * (M <= 16 ? 1 : 2) * kWave * sizeof(f32x4);
-    if (M <= 16) gemv_wg<T, BSrc, 1, W><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
-    else gemv_wg<T, BSrc, 2, W><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+    const int mt = M <= 16 ? 1 : 2;
+    const size_t part_bytes = (size_t)G * mt * kWave * sizeof(f32x4);
+    const size_t a_bytes = (size_t)M * (K + 8) * sizeof(T);
+    const bool alds = (K % kGroupK == 0) && a_bytes <= 32768 && part_bytes + a_bytes <= 65536;
+    const size_t lds = part_bytes + (alds ? a_bytes : 0);
+    if (M <= 16) {
+      if (alds) gemv_wg<T, BSrc, 1, W, 4, true><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+      else gemv_wg<T, BSrc, 1, W, 2, false><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+    } else {
+      gemv_wg<T, BSrc, 2, W, 2, false><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+    }
     return bi_host::launch_status(what);
   }
   if (M <= kSplitMMax) {
