@@ -70,8 +70,9 @@ struct DenseB {
       }
     }
   }
-  template <bool FULL>
+  template <bool FULL, bool FAST>
   __device__ __forceinline__ F frag(const Raw& raw, int s, int /*kq*/) const { return raw.f[s]; }
+  __device__ __forceinline__ bool huge_scale(const Raw&) const { return false; }
 
   // Dense op k-slot map: k(g, s, q, e) = 256 g + 32 s + 8 q + e.
   static __device__ __forceinline__ int kbase(int g, int q) { return g * kGroupK + 8 * q; }
@@ -137,7 +138,22 @@ struct QuantB {
     }
   }
 
-  template <bool FULL>
+  // A scale this large would overflow scale * 512 in the fp8 conversion path;
+  // such a group takes the integer conversion (chosen wave-uniformly).
+  __device__ __forceinline__ bool huge_scale(const Raw& raw) const {
+    bool big = false;
+#pragma unroll
+    for (int i = 0; i < kScales; ++i) big |= !(fabsf(to_f32(raw.scale[i])) < 0x1p100f);
+    return big;
+  }
+
+  // FAST (4-bit only): A byte holding a code c <= 15 read as an OCP FP8 E4M3
+  // value is exactly c * 2^-9 (denormal for c < 8, exponent field 1 for
+  // c >= 8), so one v_cvt_pk_f32_fp8 converts two codes and
+  //     fmaf(c * 2^-9, scale * 2^9, bias) == fmaf(c, scale, bias)
+  // bit for bit: both scalings are exact and the product is the same real
+  // number. Otherwise each code converts with one v_cvt_f32_ubyteN.
+  template <bool FULL, bool FAST>
   __device__ __forceinline__ F frag(const Raw& raw, int s, int kq) const {
     const int si = (GS >= 64) ? 0 : (8 * s) / GS;
     const float sc = to_f32(raw.scale[si]);
@@ -145,20 +161,12 @@ struct QuantB {
     float d[8];
     if constexpr (BITS == 4) {
       // Split the word's nibbles into two registers of four bytes each (even
-      // codes, odd codes). A byte holding a code c <= 15 read as an FP8 E4M3
-      // value is exactly c * u with u a power of two (2^-9 for the OCP
-      // encoding: denormal for c < 8, exponent field 1 for c >= 8), so one
-      // v_cvt_pk_f32_fp8 converts two codes and
-      //     fmaf(c * u, scale / u, bias) == fmaf(c, scale, bias)
-      // bit for bit (both scalings are exact; the product is the same real
-      // number). A scale so large that scale / u would overflow takes the
-      // integer conversion instead.
+      // codes, odd codes).
       const uint32_t word = raw.w[s / 4][s % 4];
-      const uint32_t lo = word & 0x0F0F0F0Fu;
-      const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
-      if (__builtin_expect(fabsf(sc) < 0x1p100f, 1)) {
-        const float unit = __builtin_amdgcn_cvt_pk_f32_fp8(1u, false)[0];
-        const float sc_u = sc / unit;
+      uint32_t lo = word & 0x0F0F0F0Fu;
+      uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;
+      if constexpr (FAST) {
+        const float sc_u = sc * 512.0f;
         const auto c02 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false);
         const auto c46 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
         const auto c13 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false);
@@ -172,6 +180,8 @@ struct QuantB {
         d[6] = __builtin_fmaf(c46[1], sc_u, bs);
         d[7] = __builtin_fmaf(c57[1], sc_u, bs);
       } else {
+        // the empty asm hides the masks so each code is one v_cvt_f32_ubyteN
+        asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           d[2 * j] = __builtin_fmaf((float)((lo >> (8 * j)) & 0xFFu), sc, bs);

@@ -24,6 +24,33 @@ constexpr int kSplitMMax = 32;
 // gemm_direct: MT m-tiles x 1 n-tile per wave, WAVES waves per workgroup
 // along n. SPLIT: one group per workgroup (blockIdx.z), raw partial out.
 // ---------------------------------------------------------------------------
+// The eight MFMA steps of one group from acc = 0, B fragments dequantized (or
+// taken) on the fly. The fast/slow B conversion is chosen once per group for
+// the whole wave, so the step loop has no divergent branch.
+template <typename T, class BSrc, int MT, bool FULL>
+__device__ __forceinline__ void mma_group(const BSrc& bsrc, const typename BSrc::Raw& braw,
+                                          const typename Frag<T>::type (&af)[MT][kSteps], int g,
+                                          int q, f32x4 (&acc)[MT]) {
+  typedef typename Frag<T>::type F;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (!__any(bsrc.huge_scale(braw))) {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const F bf = bsrc.template frag<FULL, true>(braw, s, BSrc::kbase(g, q));
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const F bf = bsrc.template frag<FULL, false>(braw, s, BSrc::kbase(g, q));
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
+    }
+  }
+}
+
 template <typename T, class BSrc, int MT, bool FULL>
 __device__ __forceinline__ void direct_group(const T* a, int64_t lda, const BSrc& bsrc, int n,
                                              const int (&rows)[MT], int K, int g, int q,
@@ -38,14 +65,7 @@ __device__ __forceinline__ void direct_group(const T* a, int64_t lda, const BSrc
 #pragma unroll
     for (int s = 0; s < kSteps; ++s) af[i][s] = load_a_frag<T, FULL>(a, lda, rows[i], K, BSrc::a_k(g, q, s));
   // Compute phase.
-#pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < kSteps; ++s) {
-    const F bf = bsrc.template frag<FULL>(braw, s, BSrc::kbase(g, q));
-#pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
-  }
+  mma_group<T, BSrc, MT, FULL>(bsrc, braw, af, g, q, acc);
 }
 
 template <typename T, class BSrc, int MT, int WAVES, bool SPLIT>
@@ -145,14 +165,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int
         else
           af[i][s] = load_a_frag<T, true>(a, lda, rows[i], K, k0);
       }
-#pragma unroll
-    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const F bf = bsrc.template frag<true>(braw, s, BSrc::kbase(g, q));
-#pragma unroll
-      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
-    }
+    mma_group<T, BSrc, MT, true>(bsrc, braw, af, g, q, acc);
   };
 
   typename BSrc::Raw braw[NB];
