@@ -169,19 +169,32 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int
   };
 
   typename BSrc::Raw braw[NB];
-  // First chunk of weight loads, then (ALDS) stage A while they are in flight.
-#pragma unroll
-  for (int j = 0; j < NB; ++j)
-    if (nw > 0) bsrc.template load<true>(braw[j], n, min(wave + j * W, last), q);
+  const int lastc = nw > 0 ? last : 0;                 // clamp target (any valid group)
   if constexpr (ALDS) {
+    // A first (the LDS write below must only wait for these loads), then the
+    // first NB groups of weights, then the LDS write and the barrier.
     const int mrows = min(M - m_base, 16 * MT);
-    const int chunks = mrows * (K / 8);
-    for (int c = threadIdx.x; c < chunks; c += kWave * W) {
-      const int rr = c / (K / 8), kc = c % (K / 8);
-      *reinterpret_cast<F*>(As + (size_t)rr * lds_row + 8 * kc) =
-          frag_load(a + (int64_t)(m_base + rr) * lda + 8 * kc);
+    const int kch = K / 8;
+    constexpr int kMaxA = 4;                             // A chunks per thread (checked on the host)
+    F av[kMaxA];
+#pragma unroll
+    for (int j = 0; j < kMaxA; ++j) {
+      const int c = threadIdx.x + j * kWave * W;
+      const int cc = c < mrows * kch ? c : 0;
+      av[j] = frag_load(a + (int64_t)(m_base + cc / kch) * lda + 8 * (cc % kch));
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) bsrc.template load<true>(braw[j], n, min(wave + j * W, lastc), q);
+#pragma unroll
+    for (int j = 0; j < kMaxA; ++j) {
+      const int c = threadIdx.x + j * kWave * W;
+      if (c < mrows * kch)
+        *reinterpret_cast<F*>(As + (size_t)(c / kch) * lds_row + 8 * (c % kch)) = av[j];
     }
     __syncthreads();
+  } else {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) bsrc.template load<true>(braw[j], n, min(wave + j * W, lastc), q);
   }
   for (int c0 = 0; c0 < nw; c0 += NB) {
     if (c0 > 0) {
@@ -485,11 +498,19 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
     const int mt = M <= 16 ? 1 : 2;
     const size_t part_bytes = (size_t)G * mt * kWave * sizeof(f32x4);
     const size_t a_bytes = (size_t)M * (K + 8) * sizeof(T);
-    const bool alds = (K % kGroupK == 0) && a_bytes <= 32768 && part_bytes + a_bytes <= 65536;
+    // A in LDS: at most 4 16-byte chunks per thread (M * K <= 4 * 8 * 512).
+    const bool alds = (K % kGroupK == 0) && (int64_t)M * K <= 4 * 8 * kWave * W &&
+                      part_bytes + a_bytes <= 65536;
     const size_t lds = part_bytes + (alds ? a_bytes : 0);
+    const int per_wave = ceil_div(K / kGroupK, W);       // full groups per wave
     if (M <= 16) {
-      if (alds) gemv_wg<T, BSrc, 1, W, 4, true><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
-      else gemv_wg<T, BSrc, 1, W, 2, false><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+      if (alds) {
+        if (per_wave <= 1) gemv_wg<T, BSrc, 1, W, 1, true><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+        else if (per_wave <= 2) gemv_wg<T, BSrc, 1, W, 2, true><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+        else gemv_wg<T, BSrc, 1, W, 4, true><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+      } else {
+        gemv_wg<T, BSrc, 1, W, 2, false><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
+      }
     } else {
       gemv_wg<T, BSrc, 2, W, 2, false><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
     }
