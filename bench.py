@@ -9,7 +9,7 @@ of distinct copies so every step streams them from HBM (the 256 MB Infinity
 Cache would otherwise hold them). Time is measured with HIP events on the
 stream the kernels run on.
 
-    python bench.py [--steps K] [--warmup W] [--op qmm4|qmm8|linear|rmsnorm|decode|prefill|gemm|all]
+    python bench.py [--steps K] [--warmup W] [--op qmm4|qmm8|linear|rmsnorm|decode|prefill|gemm|llama|all]
 
 Prints one JSON line per op (the default op only, unless --op is given).
 `value` is the achieved fraction of the op's roofline in percent (HBM 8 TB/s,
@@ -153,7 +153,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
                    "M": 1, "M_sweep": list(Ms), "weights_rotated_MB": round(ncopy * per / 2**20)},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
-                     "algorithmic_bytes": by1, "kernel": "bi_quantized_matmul (gemm_direct split + fold_groups)"},
+                     "algorithmic_bytes": by1, "kernel": "gemv_wg (bi_quantized_matmul, M <= 32: one launch)"},
         "per_m": table,
         "bitwise_invariant_M1_vs_all": inv,
         "stock_gpu": {"dequant_plus_matmul_us": round(stock_deq * 1e6, 2),
@@ -279,12 +279,84 @@ def bench_gemm(args):
     return {"metric": METRIC, "op": "bf16 GEMM (large M)", "per_m": res}
 
 
+def _llama_generate(model, prompt, steps):
+    """Prefill + `steps` greedy decode steps; returns (prefill s, decode s,
+    bytes of row 0's logits at every step)."""
+    import torch
+    B, T = prompt.shape
+    cache = model.new_cache(B, T + steps)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    _sync()
+    ev[0].record()
+    logits = model(prompt, cache, 0)
+    ev[1].record()
+    rows = [logits[0:1].clone()]
+    tok = logits.argmax(-1, keepdim=True)
+    for s in range(steps):
+        logits = model(tok, cache, T + s)
+        rows.append(logits[0:1].clone())
+        tok = logits.argmax(-1, keepdim=True)
+    ev[2].record()
+    _sync()
+    out = _bits(torch.cat(rows))
+    del cache
+    return ev[0].elapsed_time(ev[1]) * 1e-3, ev[1].elapsed_time(ev[2]) * 1e-3, out
+
+
+def bench_llama(args):
+    """random-init Llama-3-8B-shape decoder (32 layers),
+    prefill of 512 random tokens then 128 greedy decode steps at batch 1, 4,
+    16, 64; 4-bit g64 linears and bf16 linears. Row 0 holds the same prompt at
+    every batch size; its logits at all 129 steps must be bitwise identical.
+    Tokens/s under the mode next to the stock (non-invariant) torch path."""
+    import torch
+    import mlx_batch_invariant_amd as bi
+    from mlx_batch_invariant_amd.llama import LlamaConfig, LlamaShaped
+    T, steps, batches = args.llama_prompt, args.llama_steps, (1, 4, 16, 64)
+    res = {}
+    for bits in (4, None):
+        tag = f"q{bits}g64" if bits else "bf16"
+        cfg = LlamaConfig(layers=args.llama_layers, bits=bits)
+        model = LlamaShaped(cfg, device="cuda", dtype=torch.bfloat16, seed=0)
+        g = torch.Generator().manual_seed(0)
+        row0 = torch.randint(0, cfg.vocab, (1, T), generator=g)
+        per_b, ref = {}, {}
+        for B in batches:
+            fill = torch.randint(0, cfg.vocab, (B - 1, T), generator=torch.Generator().manual_seed(B))
+            prompt = torch.cat([row0, fill]).cuda()
+            entry = {}
+            for label, on in (("invariant", True), ("stock", False)):
+                bi.reset_stats()
+                with bi.set_batch_invariant_mode(enabled=on, strict=on):
+                    _llama_generate(model, prompt[:, :16], 2)          # warm-up
+                    tp, td, lg = _llama_generate(model, prompt, steps)
+                ref.setdefault(label, lg)
+                entry[label] = {"prefill_tok_s": round(B * T / tp, 1), "decode_tok_s": round(B * steps / td, 1),
+                                "prefill_s": round(tp, 3), "decode_s": round(td, 3),
+                                "row0_logits_equal_B1": lg == ref[label]}
+                if on:
+                    entry[label]["fallbacks"] = sum(bi.stats()["fallbacks"].values())
+                print(f"# llama {tag} B={B} {label}: {entry[label]}", file=sys.stderr, flush=True)
+            per_b[B] = entry
+        res[tag] = {"per_b": per_b,
+                    "bitwise_invariant_all_b": all(e["invariant"]["row0_logits_equal_B1"] for e in per_b.values())}
+        del model
+        torch.cuda.empty_cache()
+    return {"metric": METRIC, "op": "Llama-3-8B-shape forward (config 5)",
+            "config": {"workload": f"{args.llama_layers}-layer Llama-3-8B-shape decoder, prefill {T} tokens + "
+                                   f"{steps} greedy decode steps, batch 1/4/16/64", "dtype": "bf16 activations"},
+            "models": res}
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--op", default="qmm4", choices=["qmm4", "qmm8", "linear", "rmsnorm", "decode", "prefill", "gemm", "all"])
+    p.add_argument("--op", default="qmm4", choices=["qmm4", "qmm8", "linear", "rmsnorm", "decode", "prefill", "gemm", "llama", "all"])
+    p.add_argument("--llama-layers", type=int, default=32)
+    p.add_argument("--llama-prompt", type=int, default=512)
+    p.add_argument("--llama-steps", type=int, default=128)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     a = p.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -309,6 +381,8 @@ def main(argv=None) -> int:
             r = bench_decode(a)
         elif op == "prefill":
             r = bench_prefill(a)
+        elif op == "llama":
+            r = bench_llama(a)
         else:
             r = bench_gemm(a)
         r.setdefault("n_gpus", 1)

@@ -23,6 +23,8 @@ from collections import Counter
 
 import torch
 import torch.nn.functional as F
+from torch.nn.attention.bias import CausalBias as _CausalBias
+from torch.nn.attention.bias import CausalVariant as _CausalVariant
 
 from . import _lib
 from .kernels import (
@@ -166,32 +168,60 @@ def rms_norm(input, normalized_shape, weight=None, eps=None):
     return _orig_rms_norm(input, normalized_shape, weight, eps)
 
 
+def _causal_variant(attn_mask, is_causal, Tq, L):
+    """(supported, variant) for the mask arguments: variant None, "upper_left"
+    (torch's ``is_causal`` / ``causal_upper_left``) or "lower_right"
+    (``causal_lower_right``, MLX's ``mask="causal"``)."""
+    if isinstance(attn_mask, _CausalBias):
+        if is_causal or (attn_mask.seq_len_q, attn_mask.seq_len_kv) != (Tq, L):
+            return False, None
+        if attn_mask.variant == _CausalVariant.LOWER_RIGHT:
+            return True, "lower_right"
+        return True, "upper_left"
+    if attn_mask is not None:
+        return False, None
+    return True, ("upper_left" if is_causal else None)
+
+
 def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.0,
                                  is_causal=False, scale=None, enable_gqa=False, **kwargs):
-    """``F.scaled_dot_product_attention``. ``is_causal`` follows torch's
-    top-left alignment; for T_q <= L that equals the kernel's bottom-right
-    causal mask on the first T_q keys, so that is what is run."""
+    """``F.scaled_dot_product_attention``. The kernel's causal mask is
+    bottom-right aligned (query t of T_q sees ``L - T_q + t + 1`` keys): that is
+    what ``attn_mask=causal_lower_right(T_q, L)`` asks for (chunked prefill
+    over a KV cache). ``is_causal`` / ``causal_upper_left`` follow torch's
+    top-left alignment; for T_q <= L that equals the bottom-right mask on the
+    first T_q keys, so that is what is run."""
     q, k, v = query, key, value
-    ok = (attn_mask is None and dropout_p == 0.0 and not kwargs
-          and isinstance(q, torch.Tensor) and q.ndim == 4 and k.ndim == 4
+    shapes = (isinstance(q, torch.Tensor) and isinstance(k, torch.Tensor)
+              and q.ndim == 4 and k.ndim == 4)
+    mask_ok, variant = (_causal_variant(attn_mask, is_causal, q.shape[2], k.shape[2]) if shapes
+                        else (False, None))
+    ok = (shapes and mask_ok and dropout_p == 0.0 and not kwargs
           and (q.shape[1] == k.shape[1] or enable_gqa)
-          and not (is_causal and q.shape[2] > k.shape[2]))
+          and not (variant is not None and q.shape[2] > k.shape[2]))
     if ok:
-        if is_causal and q.shape[2] < k.shape[2]:
+        if variant == "upper_left" and q.shape[2] < k.shape[2]:
             k = k[:, :, : q.shape[2]]
             v = v[:, :, : q.shape[2]]
-        mask = "causal" if is_causal else None
+        mask = None if variant is None else "causal"
         if _attn.supports(q, k, v, mask):
             handled["sdpa_decode" if q.shape[2] == 1 else "sdpa_prefill"] += 1
             sc = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
             return batch_invariant_attention(q, k, v, scale=sc, mask=mask)
-    if isinstance(attn_mask, torch.Tensor):
+    if isinstance(attn_mask, torch.Tensor) and not (mask_ok and isinstance(attn_mask, _CausalBias)):
         reason = "array-mask"
     elif ok and not _on_gpu(q, k, v):
         reason = "non-gpu-tensor"
     else:
         reason = "sinks-or-shape"
     _fallback("sdpa", reason)
+    if isinstance(attn_mask, _CausalBias):
+        # CausalBias dispatches through __torch_function__ only when it sees
+        # torch's own F.scaled_dot_product_attention, which is patched here:
+        # hand the stock op the equivalent boolean mask instead.
+        Tq, L = attn_mask.seq_len_q, attn_mask.seq_len_kv
+        diag = L - Tq if attn_mask.variant == _CausalVariant.LOWER_RIGHT else 0
+        attn_mask = torch.ones((Tq, L), dtype=torch.bool, device=query.device).tril(diag)
     extra = {"enable_gqa": enable_gqa} if enable_gqa else {}
     return _orig_sdpa(query, key, value, attn_mask=attn_mask, dropout_p=dropout_p,
                       is_causal=is_causal, scale=scale, **extra, **kwargs)

@@ -60,3 +60,23 @@ def test_strict_mode_raises_on_array_mask():
     with bi.set_batch_invariant_mode(strict=True):
         with pytest.raises(RuntimeError):
             F.scaled_dot_product_attention(q, q, q, attn_mask=m)
+
+
+def test_causal_lower_right_is_the_kernel_causal_mask():
+    """``attn_mask=causal_lower_right(T_q, L)`` (chunked prefill over a cache)
+    runs the kernel's bottom-right causal mask; ``is_causal`` with T_q < L is
+    top-left, i.e. the kernel on the first T_q keys."""
+    bi = _bi()
+    from torch.nn.attention.bias import causal_lower_right
+    q = randn((2, 8, 5, 128), torch.bfloat16, gen(5))
+    kv = randn((2, 2, 300, 128), torch.bfloat16, gen(6))
+    bi.reset_stats()
+    with bi.set_batch_invariant_mode(strict=True):
+        lr = F.scaled_dot_product_attention(q, kv, kv, attn_mask=causal_lower_right(5, 300), enable_gqa=True)
+        ul = F.scaled_dot_product_attention(q, kv, kv, is_causal=True, enable_gqa=True)
+    assert bi.stats()["handled"] == {"sdpa_prefill": 2}
+    assert bits(lr) == bits(bi.batch_invariant_attention(q, kv, kv, mask="causal"))
+    assert bits(ul) == bits(bi.batch_invariant_attention(q, kv[:, :, :5], kv[:, :, :5], mask="causal"))
+    stock = F.scaled_dot_product_attention(q.float(), kv.float(), kv.float(),
+                                           attn_mask=causal_lower_right(5, 300), enable_gqa=True)
+    assert torch.allclose(lr.float(), stock, atol=2e-2, rtol=2e-2)

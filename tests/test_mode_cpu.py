@@ -155,3 +155,27 @@ def test_split_size_is_a_contract_constant():
     q = torch.randn(1, 2, 1, 64)
     with pytest.raises(ValueError, match="contract constant"):
         bi.batch_invariant_decode_attention(q, q, q, scale=1.0, split_size=128)
+
+
+def test_causal_bias_masks_are_not_array_masks():
+    """torch's CausalBias (causal_lower_right / causal_upper_left) maps to the
+    kernel's causal mask; on CPU tensors it falls back as non-gpu-tensor and
+    the stock result is returned unchanged."""
+    from torch.nn.attention.bias import causal_lower_right, causal_upper_left
+    torch.manual_seed(1)
+    q = torch.randn((1, 2, 3, 32))
+    kv = torch.randn((1, 2, 7, 32))
+    lr, ul = causal_lower_right(3, 7), causal_upper_left(3, 7)
+    ref_lr = F.scaled_dot_product_attention(q, kv, kv, attn_mask=lr)
+    ref_ul = F.scaled_dot_product_attention(q, kv, kv, attn_mask=ul)
+    bi.reset_stats()
+    with bi.set_batch_invariant_mode():
+        assert torch.equal(F.scaled_dot_product_attention(q, kv, kv, attn_mask=lr), ref_lr)
+        assert torch.equal(F.scaled_dot_product_attention(q, kv, kv, attn_mask=ul), ref_ul)
+        F.scaled_dot_product_attention(q, kv, kv, attn_mask=torch.ones((3, 7), dtype=torch.bool))
+    assert bi.stats()["fallbacks"] == {"sdpa:non-gpu-tensor": 2, "sdpa:array-mask": 1}
+    assert ops._causal_variant(lr, False, 3, 7) == (True, "lower_right")
+    assert ops._causal_variant(ul, False, 3, 7) == (True, "upper_left")
+    assert ops._causal_variant(None, True, 3, 7) == (True, "upper_left")
+    assert ops._causal_variant(lr, True, 3, 7) == (False, None)
+    assert ops._causal_variant(causal_lower_right(3, 6), False, 3, 7) == (False, None)
