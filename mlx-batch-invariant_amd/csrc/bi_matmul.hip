@@ -7,13 +7,19 @@
 //                more than one K group it runs one workgroup per (column
 //                tile, group) and writes the raw fp32 group partial.
 //   fold_groups  out = T(((0 + part[0]) + part[1]) + ...), the split fold.
-//   gemm_lds     M > 32. A BM x BN tile per 256-thread workgroup, K staged
-//                64 at a time through double-buffered LDS (quantized B is
-//                dequantized while it is staged), all groups folded in
+//   gemm_big     dense 2-byte types, K % 256 == 0, enough 256 x 128 tiles to
+//                fill the chip: operands copied straight into LDS in MFMA
+//                fragment order, three stages in flight (bi_gemm_big.h).
+//   gemm_lds     other M > 32. A BM x BN tile per 256-thread workgroup, K
+//                staged 64 at a time through double-buffered LDS (quantized B
+//                is dequantized while it is staged), all groups folded in
 //                registers.
 // Reference launchers: kernels/matmul.py:279-314 (launch_tiled: split for
 // M <= SPLIT_M_MAX and more than one group, fused otherwise), the combine
 // kernel kernels/matmul.py:226-234, and kernels/quantized.py:106-125.
+#include <type_traits>
+
+#include "bi_gemm_big.h"
 #include "bi_gemm_tile.h"
 
 namespace bi {
@@ -534,6 +540,15 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   }
   // M > 32: LDS-tiled; the largest tile that still gives the chip >= 256 tiles.
   auto tiles = [&](int bm, int bn) { return (int64_t)ceil_div(M, bm) * ceil_div(N, bn); };
+  if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
+    if (K % kGroupK == 0 && tiles(kBigBM, kBigBN) >= 256) {
+      const int tn = ceil_div(N, kBigBN);
+      const int total = (int)tiles(kBigBM, kBigBN);
+      const int grid = ((total + 7) / 8) * 8;
+      gemm_big<T><<<grid, 256, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K, tn, total);
+      return bi_host::launch_status(what);
+    }
+  }
   if constexpr (sizeof(T) == 4) {
     if (tiles(64, 128) >= 256) launch_lds<T, BSrc, 64, 128>(a, lda, bsrc, out, M, N, K, G, st);
     else launch_lds<T, BSrc, 64, 64>(a, lda, bsrc, out, M, N, K, G, st);

@@ -112,6 +112,25 @@ def test_matmul_launch_shapes_agree(K):
         assert bits(_mm(x[:M], W.t())) == bits(fused[:M]), M
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("K", [512, 4096])
+def test_matmul_large_tiles_agree(dt, K):
+    """Large M x N (the 256 x 128 direct-to-LDS tile; partial last tiles in
+    both m and n) gives the decode launches' bits for the same rows, and
+    matches the oracle on a sample of rows."""
+    g = gen(9)
+    M, N = 2100, 4136                      # 9 x 33 tiles of 256 x 128
+    W = randn((N, K), DT[dt], g, scale=0.02)
+    x = randn((M, K), DT[dt], g)
+    big = _mm(x, W.t())
+    for lo, hi in ((0, 1), (255, 256), (256, 272), (2099, 2100), (1000, 1032)):
+        assert bits(_mm(x[lo:hi], W.t())) == bits(big[lo:hi]), (lo, hi)
+    rows = [0, 1, 255, 256, 1337, 2048, 2099]
+    want = ora.matmul(to_np(x[rows]), to_np(W), dt)
+    atol = ora.matmul_error_bound(to_np(x[rows]), to_np(W))
+    assert ora.max_ulp_excess(to_np(big[rows]), want, dt, atol=atol) <= 1
+
+
 def test_matmul_layouts_and_leading_dims():
     g = gen(7)
     a = randn((2, 3, 200), torch.bfloat16, g)
