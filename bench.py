@@ -117,7 +117,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
         return lambda i: bi.batch_invariant_quantized_matmul(xs[:M], *copies[i], group_size=gs, bits=bits)
 
     table = {}
-    for M in Ms:
+    for M in (() if args.headline_only else Ms):
         t = statistics.median(_time_calls(call(M), args.steps, args.warmup, ncopy))
         by = qmm_bytes(M, N, K, bits, gs)
         table[M] = {"us": round(t * 1e6, 3), "GBps": round(by / t / 1e9, 1),
@@ -127,16 +127,21 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     t0 = time.perf_counter()
     durs = _time_calls(call(1), args.steps, args.warmup, ncopy, replays=1)
     wall = time.perf_counter() - t0
-    eager = statistics.median(_time_calls(call(1), args.steps, args.warmup, ncopy, graph=False))
-    # bitwise invariance in the same run: row 0 at M = 1 vs inside M = 64
-    inv = all(_bits(call(1)(0)[0]) == _bits(call(M)(0)[0]) for M in Ms)
-    # stock, non-invariant baselines: dequantize + hipBLASLt, and bf16 GEMV on the
-    # pre-dequantized weight
-    Wd = bi.dequantize(copies[0][0], copies[0][1], copies[0][2], gs, bits, dtype=torch.bfloat16)
-    stock_deq = statistics.median(_time_calls(
-        lambda i: torch.matmul(xs[:1], bi.dequantize(*copies[i], gs, bits, dtype=torch.bfloat16).t()), 5, 2, ncopy,
-        graph=False))
-    stock_bf16 = statistics.median(_time_calls(lambda i: torch.matmul(xs[:1], Wd.t()), args.steps, args.warmup, 1))
+    if args.headline_only:
+        eager = stock_deq = stock_bf16 = None
+        inv = None
+    else:
+        eager = statistics.median(_time_calls(call(1), args.steps, args.warmup, ncopy, graph=False))
+        # bitwise invariance in the same run: row 0 at M = 1 vs inside M = 64
+        inv = all(_bits(call(1)(0)[0]) == _bits(call(M)(0)[0]) for M in Ms)
+        # stock, non-invariant baselines: dequantize + hipBLASLt, and bf16 GEMV on
+        # the pre-dequantized weight
+        Wd = bi.dequantize(copies[0][0], copies[0][1], copies[0][2], gs, bits, dtype=torch.bfloat16)
+        stock_deq = statistics.median(_time_calls(
+            lambda i: torch.matmul(xs[:1], bi.dequantize(*copies[i], gs, bits, dtype=torch.bfloat16).t()), 5, 2,
+            ncopy, graph=False))
+        stock_bf16 = statistics.median(_time_calls(lambda i: torch.matmul(xs[:1], Wd.t()), args.steps,
+                                                   args.warmup, 1))
     t_med = statistics.median(durs)
     by1 = qmm_bytes(1, N, K, bits, gs)
     achieved = by1 / t_med
@@ -146,7 +151,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
         "value": round(100 * achieved / PEAK_HBM, 2),
         "unit": "% of HBM roofline (4-bit g64 qmatmul, M=1)" if bits == 4 else f"% of HBM roofline ({bits}-bit g{gs} qmatmul, M=1)",
         "ms_per_step": round(sum(durs) / len(durs) * 1e3, 5),
-        "eager_us_per_call": round(eager * 1e6, 2),
+        "eager_us_per_call": None if eager is None else round(eager * 1e6, 2),
         "wall_s_timed": round(wall, 4),
         "dtype": "bf16",
         "config": {"workload": f"qmatmul {bits}-bit g{gs} affine, x[M,4096] @ W[14336,4096]^T, Llama-3-8B MLP shape",
@@ -156,8 +161,8 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
                      "algorithmic_bytes": by1, "kernel": "gemv_wg (bi_quantized_matmul, M <= 32: one launch)"},
         "per_m": table,
         "bitwise_invariant_M1_vs_all": inv,
-        "stock_gpu": {"dequant_plus_matmul_us": round(stock_deq * 1e6, 2),
-                      "bf16_hipblaslt_gemv_us": round(stock_bf16 * 1e6, 2),
+        "stock_gpu": {"dequant_plus_matmul_us": None if stock_deq is None else round(stock_deq * 1e6, 2),
+                      "bf16_hipblaslt_gemv_us": None if stock_bf16 is None else round(stock_bf16 * 1e6, 2),
                       "note": "non-invariant torch paths, reported only"},
         "cpu_baseline": cpu,
     }
@@ -358,6 +363,8 @@ def main(argv=None) -> int:
     p.add_argument("--llama-prompt", type=int, default=512)
     p.add_argument("--llama-steps", type=int, default=128)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--headline-only", action="store_true",
+                   help="qmm: time only the M=1 headline (no M sweep, eager or stock legs); for profiling")
     a = p.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every kernel here is single-GPU and no multi-GPU "

@@ -70,6 +70,19 @@ struct DenseB {
       }
     }
   }
+  // Per-lane pointer for whole-group loads (row n clamped, quarter q): the
+  // group offset is then one wave-uniform add.
+  struct Lane {
+    const T* b;
+  };
+  __device__ __forceinline__ Lane lane(int n, int q) const { return Lane{bt + (int64_t)n * ldb + 8 * q}; }
+  __device__ __forceinline__ void load_full(Raw& raw, const Lane& l, int g) const {
+    const T* p = l.b + g * kGroupK;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) raw.f[s] = frag_load(p + 32 * s);
+  }
+  // Dense operands carry no per-group metadata.
+  static constexpr bool kMeta = false;
   template <bool FULL, bool FAST>
   __device__ __forceinline__ F frag(const Raw& raw, int s, int /*kq*/) const { return raw.f[s]; }
   __device__ __forceinline__ bool huge_scale(const Raw&) const { return false; }
@@ -135,6 +148,56 @@ struct QuantB {
       const bool ok = FULL || kq + i * GS < K;
       raw.scale[i] = scales[ok ? s0 + i : 0];
       raw.bias[i] = biases[ok ? s0 + i : 0];
+    }
+  }
+
+  // Per-lane pointers for whole-group loads (row n clamped, quarter q): the
+  // group offset is then one wave-uniform add.
+  struct Lane {
+    const uint32_t* w;
+    const T* s;
+    const T* b;
+  };
+  __device__ __forceinline__ Lane lane(int n, int q) const {
+    const int64_t s0 = (int64_t)n * groups_per_row + (64 * q) / GS;
+    return Lane{w + (int64_t)n * words_per_row + 64 * q * BITS / 32, scales + s0, biases + s0};
+  }
+  __device__ __forceinline__ void load_codes(Raw& raw, const Lane& l, int g) const {
+    const uint32_t* wp = l.w + g * (kGroupK * BITS / 32);
+#pragma unroll
+    for (int p = 0; p < kWords / 4; ++p) raw.w[p] = *reinterpret_cast<const u32x4*>(wp + 4 * p);
+  }
+  __device__ __forceinline__ void load_full(Raw& raw, const Lane& l, int g) const {
+    load_codes(raw, l, g);
+    const int so = g * (kGroupK / GS);
+#pragma unroll
+    for (int i = 0; i < kScales; ++i) {
+      raw.scale[i] = l.s[so + i];
+      raw.bias[i] = l.b[so + i];
+    }
+  }
+  // Per-group metadata (scales, biases) can be staged in LDS for a 16-row
+  // tile: scales of rows n0 .. n0 + 15 are the contiguous block
+  // scales[n0 * gpr, (n0 + 16) * gpr), likewise biases. LDS layout:
+  // [16][gpr] scales, then [16][gpr] biases.
+  static constexpr bool kMeta = true;
+  // Element i (of the 32 * gpr staged) lives at this global address; indices
+  // past the arrays' end read element 0 (those rows are never used).
+  __device__ __forceinline__ const T* meta_src(int n0, int64_t i) const {
+    const int64_t gpr = groups_per_row, half = 16 * gpr;
+    const bool second = i >= half;
+    const int64_t e = (int64_t)n0 * gpr + (second ? i - half : i);
+    const T* base = second ? biases : scales;
+    return e + 8 <= (int64_t)N * gpr ? base + e : base;
+  }
+  // Scale and bias of group g for lane quarter q of tile row rt from LDS.
+  __device__ __forceinline__ void meta_from_lds(Raw& raw, const T* ms, int rt, int g, int q) const {
+    const int gpr = (int)groups_per_row;
+    const int so = rt * gpr + (g * kGroupK + 64 * q) / GS;
+#pragma unroll
+    for (int i = 0; i < kScales; ++i) {
+      raw.scale[i] = ms[so + i];
+      raw.bias[i] = ms[16 * gpr + so + i];
     }
   }
 

@@ -1,565 +1,6 @@
-// bi_matmul.hip — batch-invariant dense and affine-quantized matmul for gfx950.
-//
-// Kernels (all run the arithmetic of bi_gemm_tile.h):
-//   gemm_direct  M <= 32. Each wave owns 16 columns x MT 16-row tiles; its A
-//                and B fragments go straight from global memory into
-//                registers (quantized B is dequantized in registers). With
-//                more than one K group it runs one workgroup per (column
-//                tile, group) and writes the raw fp32 group partial.
-//   fold_groups  out = T(((0 + part[0]) + part[1]) + ...), the split fold.
-//   gemm_big     dense 2-byte types, K % 256 == 0, enough 256 x 128 tiles to
-//                fill the chip: 8 waves, operands copied straight into
-//                swizzled LDS rows, three stages in flight (bi_gemm_big.h).
-//   gemm_lds     other M > 32. A BM x BN tile per 256-thread workgroup, K
-//                staged 64 at a time through double-buffered LDS (quantized B
-//                is dequantized while it is staged), all groups folded in
-//                registers.
-// Reference launchers: kernels/matmul.py:279-314 (launch_tiled: split for
-// M <= SPLIT_M_MAX and more than one group, fused otherwise), the combine
-// kernel kernels/matmul.py:226-234, and kernels/quantized.py:106-125.
-#include <type_traits>
-
-#include "bi_gemm_big.h"
-#include "bi_gemm_tile.h"
-
-namespace bi {
-
-constexpr int kSplitMMax = 32;
-
-// ---------------------------------------------------------------------------
-// gemm_direct: MT m-tiles x 1 n-tile per wave, WAVES waves per workgroup
-// along n. SPLIT: one group per workgroup (blockIdx.z), raw partial out.
-// ---------------------------------------------------------------------------
-// The eight MFMA steps of one group from acc = 0, B fragments dequantized (or
-// taken) on the fly. The fast/slow B conversion is chosen once per group for
-// the whole wave, so the step loop has no divergent branch.
-template <typename T, class BSrc, int MT, bool FULL>
-__device__ __forceinline__ void mma_group(const BSrc& bsrc, const typename BSrc::Raw& braw,
-                                          const typename Frag<T>::type (&af)[MT][kSteps], int g,
-                                          int q, f32x4 (&acc)[MT]) {
-  typedef typename Frag<T>::type F;
-#pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (!__any(bsrc.huge_scale(braw))) {
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const F bf = bsrc.template frag<FULL, true>(braw, s, BSrc::kbase(g, q));
-#pragma unroll
-      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      const F bf = bsrc.template frag<FULL, false>(braw, s, BSrc::kbase(g, q));
-#pragma unroll
-      for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[i][s], bf, acc[i]);
-    }
-  }
-}
-
-template <typename T, class BSrc, int MT, bool FULL>
-__device__ __forceinline__ void direct_group(const T* a, int64_t lda, const BSrc& bsrc, int n,
-                                             const int (&rows)[MT], int K, int g, int q,
-                                             f32x4 (&acc)[MT]) {
-  typedef typename Frag<T>::type F;
-  // Load phase: every fragment of the group is requested before any is used.
-  typename BSrc::Raw braw;
-  bsrc.template load<FULL>(braw, n, g, q);
-  F af[MT][kSteps];
-#pragma unroll
-  for (int i = 0; i < MT; ++i)
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) af[i][s] = load_a_frag<T, FULL>(a, lda, rows[i], K, BSrc::a_k(g, q, s));
-  // Compute phase.
-  mma_group<T, BSrc, MT, FULL>(bsrc, braw, af, g, q, acc);
-}
-
-template <typename T, class BSrc, int MT, int WAVES, bool SPLIT>
-__global__ __launch_bounds__(kWave* WAVES) void gemm_direct(const T* __restrict__ a, int64_t lda,
-                                                            BSrc bsrc, T* __restrict__ out,
-                                                            float* __restrict__ part, int M,
-                                                            int N, int K, int G) {
-  const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
-  const int r = lane % 16, q = lane / 16;
-  const int n_base = (blockIdx.x * WAVES + wave) * 16;
-  const int m_base = blockIdx.y * 16 * MT;
-  if (n_base >= N) return;  // wave-uniform; the kernel has no block barrier
-  const int n = min(n_base + r, N - 1);          // clamped: padding columns are not stored
-  int rows[MT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i) rows[i] = min(m_base + 16 * i + r, M - 1);
-  const int g0 = SPLIT ? (int)blockIdx.z : 0;
-  const int g1 = SPLIT ? g0 + 1 : G;
-
-  f32x4 total[MT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i) total[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (int g = g0; g < g1; ++g) {
-    f32x4 acc[MT];
-    if ((g + 1) * kGroupK <= K) direct_group<T, BSrc, MT, true>(a, lda, bsrc, n, rows, K, g, q, acc);
-    else direct_group<T, BSrc, MT, false>(a, lda, bsrc, n, rows, K, g, q, acc);
-    if constexpr (SPLIT) {
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = m_base + 16 * i + 4 * q + e;
-          if (m < M && n_base + r < N) part[((int64_t)g * M + m) * N + n] = acc[i][e];
-        }
-    } else {
-#pragma unroll
-      for (int i = 0; i < MT; ++i) total[i] = total[i] + acc[i];
-    }
-  }
-  if constexpr (!SPLIT) {
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m_base + 16 * i + 4 * q + e;
-        if (m < M && n_base + r < N) out[(int64_t)m * N + n] = to_store<T>(total[i][e]);
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// gemv_wg: M <= 32, the decode-shaped launch. One workgroup of W waves per 16
-// columns covers every K group: wave w computes groups w, w + W, w + 2W, ...,
-// and writes each raw fp32 group partial to LDS; after a barrier the
-// workgroup folds the partials in group order, ((0 + p0) + p1) + ..., exactly
-// the fold of the other launches. A wave issues the B-operand loads of up to
-// NB of its groups before computing any of them (all unconditional, so the
-// wait counters only ever wait for the group being computed). With ALDS the
-// M rows of A are staged once per workgroup into LDS (while the first weight
-// loads are in flight) and A fragments are read from there.
-// Dynamic LDS: G * MT * 64 f32x4 partials, then (ALDS) M rows of K + 8 elements.
-// ---------------------------------------------------------------------------
-template <typename T, class BSrc, int MT, int W, int NB, bool ALDS>
-__global__ __launch_bounds__(kWave* W) void gemv_wg(const T* __restrict__ a, int64_t lda,
-                                                    BSrc bsrc, T* __restrict__ out, int M, int N,
-                                                    int K, int G) {
-  typedef typename Frag<T>::type F;
-  extern __shared__ __attribute__((aligned(16))) f32x4 smem[];
-  f32x4* part = smem;                                        // [G][MT][64]
-  T* As = reinterpret_cast<T*>(smem + (size_t)G * MT * kWave);  // [M][K + 8]
-  const int lds_row = K + 8;
-  const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
-  const int r = lane % 16, q = lane / 16;
-  const int n_base = blockIdx.x * 16;
-  const int m_base = blockIdx.y * 16 * MT;
-  const int n = min(n_base + r, N - 1);          // clamped: padding columns are not stored
-  int rows[MT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i) rows[i] = min(m_base + 16 * i + r, M - 1);
-
-  const int gfull = K / kGroupK;                 // groups lying entirely inside K
-  const int nw = gfull > wave ? (gfull - 1 - wave) / W + 1 : 0;   // this wave's full groups
-  const int last = wave + (nw - 1) * W;
-
-  auto compute = [&](const typename BSrc::Raw& braw, int g, f32x4 (&acc)[MT]) {
-    F af[MT][kSteps];
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        const int k0 = BSrc::a_k(g, q, s);
-        if constexpr (ALDS)
-          af[i][s] = *reinterpret_cast<const F*>(As + (size_t)(rows[i] - m_base) * lds_row + k0);
-        else
-          af[i][s] = load_a_frag<T, true>(a, lda, rows[i], K, k0);
-      }
-    mma_group<T, BSrc, MT, true>(bsrc, braw, af, g, q, acc);
-  };
-
-  typename BSrc::Raw braw[NB];
-  const int lastc = nw > 0 ? last : 0;                 // clamp target (any valid group)
-  if constexpr (ALDS) {
-    // A first (the LDS write below must only wait for these loads), then the
-    // first NB groups of weights, then the LDS write and the barrier.
-    const int mrows = min(M - m_base, 16 * MT);
-    const int kch = K / 8;
-    constexpr int kMaxA = 4;                             // A chunks per thread (checked on the host)
-    F av[kMaxA];
-#pragma unroll
-    for (int j = 0; j < kMaxA; ++j) {
-      const int c = threadIdx.x + j * kWave * W;
-      const int cc = c < mrows * kch ? c : 0;
-      av[j] = frag_load(a + (int64_t)(m_base + cc / kch) * lda + 8 * (cc % kch));
-    }
-#pragma unroll
-    for (int j = 0; j < NB; ++j) bsrc.template load<true>(braw[j], n, min(wave + j * W, lastc), q);
-#pragma unroll
-    for (int j = 0; j < kMaxA; ++j) {
-      const int c = threadIdx.x + j * kWave * W;
-      if (c < mrows * kch)
-        *reinterpret_cast<F*>(As + (size_t)(c / kch) * lds_row + 8 * (c % kch)) = av[j];
-    }
-    __syncthreads();
-  } else {
-#pragma unroll
-    for (int j = 0; j < NB; ++j) bsrc.template load<true>(braw[j], n, min(wave + j * W, lastc), q);
-  }
-  for (int c0 = 0; c0 < nw; c0 += NB) {
-    if (c0 > 0) {
-#pragma unroll
-      for (int j = 0; j < NB; ++j) bsrc.template load<true>(braw[j], n, min(wave + (c0 + j) * W, last), q);
-    }
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      if (c0 + j < nw) {
-        const int g = wave + (c0 + j) * W;
-        f32x4 acc[MT];
-        compute(braw[j], g, acc);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) part[(g * MT + i) * kWave + lane] = acc[i];
-      }
-    }
-  }
-  // A last group cut short by K (zero-padded past K), A from global memory.
-  if (gfull < G && wave == gfull % W) {
-    f32x4 acc[MT];
-    direct_group<T, BSrc, MT, false>(a, lda, bsrc, n, rows, K, gfull, q, acc);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) part[(gfull * MT + i) * kWave + lane] = acc[i];
-  }
-  __syncthreads();
-  // Ordered fold: one thread per (m-tile, lane) of the MFMA result layout.
-  for (int idx = threadIdx.x; idx < MT * kWave; idx += kWave * W) {
-    const int i = idx / kWave, l = idx % kWave;
-    f32x4 total = {0.f, 0.f, 0.f, 0.f};
-    for (int gg = 0; gg < G; ++gg) total = total + part[(gg * MT + i) * kWave + l];
-    const int col = n_base + l % 16;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = m_base + 16 * i + 4 * (l / 16) + e;
-      if (m < M && col < N) out[(int64_t)m * N + col] = to_store<T>(total[e]);
-    }
-  }
-}
-
-// Left fold of the group partials, exactly the fused kernels' fold:
-// total = 0; total = total + part[g] for g = 0 .. G-1; out = T(total).
-// Loads are issued eight groups at a time; the adds stay in group order.
-template <typename T>
-__global__ __launch_bounds__(256) void fold_groups(const float* __restrict__ part,
-                                                   T* __restrict__ out, int64_t MN, int G) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= MN) return;
-  float total = 0.0f;
-  int g = 0;
-  for (; g + 8 <= G; g += 8) {
-    float v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = part[(int64_t)(g + j) * MN + idx];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) total = total + v[j];
-  }
-  for (; g < G; ++g) total = total + part[(int64_t)g * MN + idx];
-  out[idx] = to_store<T>(total);
-}
-
-// ---------------------------------------------------------------------------
-// gemm_lds: BM x BN tile, 4 waves in 2 x 2, each wave (BM/2) x (BN/2).
-// K stage = two MFMA steps {2p, 2p+1} of group g (64 k, which k is the op's
-// k-slot map); group g = stages 4g .. 4g+3.
-// ---------------------------------------------------------------------------
-constexpr int kStageK = 64;
-constexpr int kLdsPad = 8;                      // elements; rows 16 B apart in banks
-constexpr int kLdsRow = kStageK + kLdsPad;      // LDS row length (elements)
-
-// Stages the two MFMA steps {2p, 2p+1} of group g for ROWS rows into LDS as
-// 8-element chunks; MAP (the B source type) says which k each LDS chunk holds.
-template <typename T, int ROWS, class MAP>
-struct StageA {
-  static constexpr int kChunks = ROWS * (kStageK / 8) / 256;  // per thread
-  typedef typename Frag<T>::type F;
-  F v[kChunks];
-  __device__ __forceinline__ void load(const T* a, int64_t lda, int M, int K, int m0, int g, int p) {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int row = c / 8, kc = c % 8;
-      const int m = m0 + row, k = MAP::stage_k(g, p, kc);
-      const bool ok = m < M && k < K;
-      const F x = frag_load(a + (ok ? (int64_t)m * lda + k : 0));
-      v[i] = ok ? x : frag_zero<F>();
-    }
-  }
-  __device__ __forceinline__ void store(T* lds) const {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int row = c / 8, kc = c % 8;
-      *reinterpret_cast<F*>(lds + row * kLdsRow + 8 * kc) = v[i];
-    }
-  }
-};
-
-// B stage for dense operands: same chunking as A over bt rows (columns n).
-template <typename T, int ROWS>
-struct StageDenseB {
-  StageA<T, ROWS, DenseB<T>> s;
-  __device__ __forceinline__ void load(const DenseB<T>& b, int n0, int g, int p) {
-    s.load(b.bt, b.ldb, b.N, b.K, n0, g, p);
-  }
-  __device__ __forceinline__ void store(T* lds) const { s.store(lds); }
-};
-
-// B stage for quantized operands: each chunk is 8 consecutive codes of one
-// row, dequantized with the row's scale/bias for that k and rounded to T.
-template <typename T, int BITS, int GS, int ROWS>
-struct StageQuantB {
-  static constexpr int kChunks = ROWS * (kStageK / 8) / 256;
-  static constexpr int kWords = BITS / 4;
-  typedef typename Frag<T>::type F;
-  typedef QuantB<T, BITS, GS> Src;
-  uint32_t w[kChunks][kWords];
-  T sc[kChunks], bs[kChunks];
-  bool ok[kChunks];
-  __device__ __forceinline__ void load(const Src& b, int n0, int g, int p) {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int row = c / 8, kc = c % 8;
-      const int n = n0 + row, k = Src::stage_k(g, p, kc);
-      const bool good = n < b.N && k < b.K;
-      const int64_t nn = good ? n : 0;
-      const int kk = good ? k : 0;
-      const uint32_t* wp = b.w + nn * b.words_per_row + (int64_t)kk * BITS / 32;
-      if constexpr (BITS == 4) {
-        w[i][0] = wp[0];
-      } else {
-        const uint2 x = *reinterpret_cast<const uint2*>(wp);
-        w[i][0] = x.x;
-        w[i][1] = x.y;
-      }
-      const int64_t si = nn * b.groups_per_row + kk / GS;
-      sc[i] = b.scales[si];
-      bs[i] = b.biases[si];
-      ok[i] = good;
-    }
-  }
-  __device__ __forceinline__ void store(T* lds) const {
-#pragma unroll
-    for (int i = 0; i < kChunks; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      const int row = c / 8, kc = c % 8;
-      const float s = to_f32(sc[i]), bb = to_f32(bs[i]);
-      float d[8];
-      if constexpr (BITS == 4) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d[e] = __builtin_fmaf((float)((w[i][0] >> (4 * e)) & 0xFu), s, bb);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          d[e] = __builtin_fmaf((float)((w[i][0] >> (8 * e)) & 0xFFu), s, bb);
-          d[4 + e] = __builtin_fmaf((float)((w[i][1] >> (8 * e)) & 0xFFu), s, bb);
-        }
-      }
-      F f;
-      if constexpr (sizeof(T) == 2) {
-        typedef T vec8 __attribute__((ext_vector_type(8)));
-        vec8 rr;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) rr[e] = to_store<T>(d[e]);
-        f = __builtin_bit_cast(F, rr);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          f.lo[e] = d[e];
-          f.hi[e] = d[4 + e];
-        }
-      }
-      *reinterpret_cast<F*>(lds + row * kLdsRow + 8 * kc) = ok[i] ? f : frag_zero<F>();
-    }
-  }
-};
-
-template <class BSrc, typename T, int ROWS> struct StageFor;
-template <typename T, int ROWS> struct StageFor<DenseB<T>, T, ROWS> { typedef StageDenseB<T, ROWS> type; };
-template <typename T, int BITS, int GS, int ROWS> struct StageFor<QuantB<T, BITS, GS>, T, ROWS> {
-  typedef StageQuantB<T, BITS, GS, ROWS> type;
-};
-
-template <typename T, class BSrc, int BM, int BN>
-__global__ __launch_bounds__(256) void gemm_lds(const T* __restrict__ a, int64_t lda, BSrc bsrc,
-                                                T* __restrict__ out, int M, int N, int K, int G,
-                                                int tiles_n, int tiles_total) {
-  typedef typename Frag<T>::type F;
-  constexpr int TM = BM / 32, TN = BN / 32;  // 16x16 tiles per wave along m and n
-  __shared__ __attribute__((aligned(16))) T As[2][BM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) T Bs[2][BN * kLdsRow];
-
-  // XCD-aware tile order: consecutive workgroup ids are dealt round-robin to
-  // the 8 XCDs; give each XCD a contiguous run of tiles so neighbouring tiles
-  // share that XCD's L2. Launch order only.
-  const int bid = blockIdx.x;
-  const int per_xcd = (tiles_total + 7) / 8;
-  const int tile = (bid % 8) * per_xcd + bid / 8;
-  if (tile >= tiles_total) return;  // uniform per workgroup, before any barrier
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
-  const int m0 = tm * BM, n0 = tn * BN;
-
-  const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
-  const int wm = wave / 2, wn = wave % 2;
-  const int r = lane % 16, q = lane / 16;
-
-  f32x4 total[TM][TN], acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      total[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      acc[i][j] = total[i][j];
-    }
-
-  StageA<T, BM, BSrc> sa;
-  typename StageFor<BSrc, T, BN>::type sb;
-  const int nstages = 4 * G;
-  sa.load(a, lda, M, K, m0, 0, 0);
-  sb.load(bsrc, n0, 0, 0);
-  sa.store(As[0]);
-  sb.store(Bs[0]);
-  __syncthreads();
-
-  for (int st = 0; st < nstages; ++st) {
-    const int buf = st & 1;
-    if (st + 1 < nstages) {
-      sa.load(a, lda, M, K, m0, (st + 1) >> 2, (st + 1) & 3);
-      sb.load(bsrc, n0, (st + 1) >> 2, (st + 1) & 3);
-    }
-    const T* Ab = As[buf] + (wm * TM * 16 + r) * kLdsRow + 8 * q;
-    const T* Bb = Bs[buf] + (wn * TN * 16 + r) * kLdsRow + 8 * q;
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      F af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const F*>(Ab + 16 * i * kLdsRow + 32 * s2);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const F*>(Bb + 16 * j * kLdsRow + 32 * s2);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma_step(af[i], bf[j], acc[i][j]);
-    }
-    if ((st & 3) == 3) {  // end of a 256-k group: fold and restart from zero
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          total[i][j] = total[i][j] + acc[i][j];
-          acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    if (st + 1 < nstages) {
-      sa.store(As[buf ^ 1]);
-      sb.store(Bs[buf ^ 1]);
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + wn * TN * 16 + 16 * j + r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + wm * TM * 16 + 16 * i + 4 * q + e;
-        if (m < M && n < N) out[(int64_t)m * N + n] = to_store<T>(total[i][j][e]);
-      }
-    }
-}
-
-static inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
-
-// Launch-shape policy (kernels/matmul.py:279-314): M <= 32 with more than one
-// group -> split partials + fold; otherwise fused. Bits never depend on it.
-static inline bool use_split(int64_t M, int G) { return M <= kSplitMMax && G > 1; }
-// The in-workgroup fold keeps every group partial in LDS (1 KB per group and
-// 16-row tile); up to 64 KB of it. Larger K takes the split + fold launch.
-static inline bool use_wg(int64_t M, int G) { return M <= kSplitMMax && G * (M <= 16 ? 1 : 2) <= 64; }
-
-template <typename T, class BSrc, int BM, int BN>
-static void launch_lds(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K,
-                       int G, hipStream_t st) {
-  const int tn = ceil_div(N, BN), tmm = ceil_div(M, BM);
-  const int total = tn * tmm;
-  const int grid = ((total + 7) / 8) * 8;
-  gemm_lds<T, BSrc, BM, BN><<<grid, 256, 0, st>>>(a, lda, bsrc, out, M, N, K, G, tn, total);
-}
-
-template <typename T, class BSrc>
-static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K,
-                    float* ws, hipStream_t st, const char* what) {
-  const int G = ceil_div(K, kGroupK);
-  constexpr int WAVES = 4;
-  if (M <= kSplitMMax && use_wg(M, G)) {
-    constexpr int W = 8;
-    dim3 grid(ceil_div(N, 16), 1, 1);
-    const int mt = M <= 16 ? 1 : 2;
-    const size_t part_bytes = (size_t)G * mt * kWave * sizeof(f32x4);
-    const size_t a_bytes = (size_t)M * (K + 8) * sizeof(T);
-    // A in LDS: at most 4 16-byte chunks per thread (M * K <= 4 * 8 * 512).
-    const bool alds = (K % kGroupK == 0) && (int64_t)M * K <= 4 * 8 * kWave * W &&
-                      part_bytes + a_bytes <= 65536;
-    const size_t lds = part_bytes + (alds ? a_bytes : 0);
-    const int per_wave = ceil_div(K / kGroupK, W);       // full groups per wave
-    if (M <= 16) {
-      if (alds) {
-        if (per_wave <= 1) gemv_wg<T, BSrc, 1, W, 1, true><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
-        else if (per_wave <= 2) gemv_wg<T, BSrc, 1, W, 2, true><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
-        else gemv_wg<T, BSrc, 1, W, 4, true><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
-      } else {
-        gemv_wg<T, BSrc, 1, W, 2, false><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
-      }
-    } else {
-      gemv_wg<T, BSrc, 2, W, 2, false><<<grid, kWave * W, lds, st>>>(a, lda, bsrc, out, M, N, K, G);
-    }
-    return bi_host::launch_status(what);
-  }
-  if (M <= kSplitMMax) {
-    const bool split = use_split(M, G);
-    dim3 grid(ceil_div(N, 16 * WAVES), 1, split ? G : 1);
-    if (M <= 16) {
-      if (split) gemm_direct<T, BSrc, 1, WAVES, true><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G);
-      else gemm_direct<T, BSrc, 1, WAVES, false><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G);
-    } else {
-      if (split) gemm_direct<T, BSrc, 2, WAVES, true><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G);
-      else gemm_direct<T, BSrc, 2, WAVES, false><<<grid, kWave * WAVES, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G);
-    }
-    int rc = bi_host::launch_status(what);
-    if (rc || !split) return rc;
-    const int64_t MN = (int64_t)M * N;
-    fold_groups<T><<<(unsigned)((MN + 255) / 256), 256, 0, st>>>(ws, out, MN, G);
-    return bi_host::launch_status(what);
-  }
-  // M > 32: LDS-tiled; the largest tile that still gives the chip >= 256 tiles.
-  auto tiles = [&](int bm, int bn) { return (int64_t)ceil_div(M, bm) * ceil_div(N, bn); };
-  if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
-    if (K % kGroupK == 0 && tiles(kBigBM, kBigBN) >= 256) {
-      const int tmm = ceil_div(M, kBigBM), tn = ceil_div(N, kBigBN);
-      const int grid = ((tmm * tn + 7) / 8) * 8;
-      gemm_big<T><<<grid, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K, tmm, tn);
-      return bi_host::launch_status(what);
-    }
-  }
-  if constexpr (sizeof(T) == 4) {
-    if (tiles(64, 128) >= 256) launch_lds<T, BSrc, 64, 128>(a, lda, bsrc, out, M, N, K, G, st);
-    else launch_lds<T, BSrc, 64, 64>(a, lda, bsrc, out, M, N, K, G, st);
-  } else {
-    if (tiles(128, 128) >= 256) launch_lds<T, BSrc, 128, 128>(a, lda, bsrc, out, M, N, K, G, st);
-    else if (tiles(64, 128) >= 256) launch_lds<T, BSrc, 64, 128>(a, lda, bsrc, out, M, N, K, G, st);
-    else launch_lds<T, BSrc, 64, 64>(a, lda, bsrc, out, M, N, K, G, st);
-  }
-  return bi_host::launch_status(what);
-}
-
-}  // namespace bi
+// bi_matmul.hip — C ABI of the batch-invariant dense and affine-quantized
+// matmul for gfx950 (kernels and launch policy: bi_matmul_impl.h).
+#include "bi_matmul_impl.h"
 
 // ---------------------------------------------------------------------------
 // C ABI
@@ -638,36 +79,6 @@ extern "C" int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb
   }
 }
 
-namespace {
-
-template <typename T, int BITS, int GS>
-int run_quant(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
-              const void* biases, void* out, int M, int N, int K, void* ws, hipStream_t st) {
-  bi::QuantB<T, BITS, GS> b;
-  b.w = w;
-  b.scales = static_cast<const T*>(scales);
-  b.biases = static_cast<const T*>(biases);
-  b.N = N;
-  b.K = K;
-  b.words_per_row = (int64_t)K * BITS / 32;
-  b.groups_per_row = K / GS;
-  return bi::run_gemm(static_cast<const T*>(x), ldx, b, static_cast<T*>(out), M, N, K,
-                      static_cast<float*>(ws), st, "bi_quantized_matmul");
-}
-
-template <typename T>
-int dispatch_quant(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w,
-                   const void* scales, const void* biases, void* out, int M, int N, int K,
-                   void* ws, hipStream_t st) {
-#define BI_Q(B, G)                                                                       \
-  if (bits == B && gs == G)                                                              \
-    return run_quant<T, B, G>(x, ldx, w, scales, biases, out, M, N, K, ws, st);
-  BI_Q(4, 32) BI_Q(4, 64) BI_Q(4, 128) BI_Q(8, 32) BI_Q(8, 64) BI_Q(8, 128)
-#undef BI_Q
-  return bi_host::fail(BI_E_UNSUPPORTED, "bi_quantized_matmul: bits=%d group_size=%d", bits, gs);
-}
-
-}  // namespace
 
 extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w,
                                    const void* scales, const void* biases, void* out, int64_t M,
@@ -692,11 +103,11 @@ extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w
   const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
   switch (dtype) {
     case BI_BF16:
-      return dispatch_quant<bi::bf16>(bits, group_size, x, ldx, w, scales, biases, out, Mi, Ni, Ki, ws, st);
+      return bi::qmm_bf16(bits, group_size, x, ldx, w, scales, biases, out, Mi, Ni, Ki, ws, st);
     case BI_F16:
-      return dispatch_quant<bi::f16>(bits, group_size, x, ldx, w, scales, biases, out, Mi, Ni, Ki, ws, st);
+      return bi::qmm_f16(bits, group_size, x, ldx, w, scales, biases, out, Mi, Ni, Ki, ws, st);
     case BI_F32:
-      return dispatch_quant<float>(bits, group_size, x, ldx, w, scales, biases, out, Mi, Ni, Ki, ws, st);
+      return bi::qmm_f32(bits, group_size, x, ldx, w, scales, biases, out, Mi, Ni, Ki, ws, st);
     default: return fail(BI_E_UNSUPPORTED, "bi_quantized_matmul: unknown dtype %d", dtype);
   }
 }
