@@ -33,6 +33,12 @@ for p in (ROOT, ROOT / "mlx-batch-invariant_amd"):
     sys.path.insert(0, str(p))
 
 PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
+# HBM traffic of the headline kernel per launch, from two rocprofv3 counter
+# passes (FETCH_SIZE, WRITE_SIZE, KiB per dispatch) scaled by the same counters
+# on a 256 MiB device copy (bench.py --op copycal): read x 2.000, write x 1.000.
+# Source: profiles/qmatmul4_g64_llama_mlp_m1.txt. Re-measure after changing
+# the kernel.
+MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 21614, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
 PEAK_BF16 = 2.5e15         # FLOP/s, dense bf16 MFMA
 METRIC = "% of HBM/MFMA roofline per op at batch 1–256, with bitwise batch invariance"
 ROTATE_BYTES = 512 << 20
@@ -146,6 +152,10 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     by1 = qmm_bytes(1, N, K, bits, gs)
     achieved = by1 / t_med
     cpu = None if args.no_cpu else cpu_baseline_qmm(bits, gs)
+    traffic = None
+    if bits == 4 and gs == 64:
+        mt = MEASURED_TRAFFIC_QMM4_M1
+        traffic = int(1024 * (mt["fetch_kib"] * mt["fetch_scale"] + mt["write_kib"] * mt["write_scale"]))
     return {
         "metric": METRIC,
         "value": round(100 * achieved / PEAK_HBM, 2),
@@ -157,7 +167,9 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
         "config": {"workload": f"qmatmul {bits}-bit g{gs} affine, x[M,4096] @ W[14336,4096]^T, Llama-3-8B MLP shape",
                    "M": 1, "M_sweep": list(Ms), "weights_rotated_MB": round(ncopy * per / 2**20)},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
+                     "traffic_source": None if traffic is None else
+                     "rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch x copy-kernel scale (bytes per launch)",
                      "algorithmic_bytes": by1, "kernel": "gemv_wg (bi_quantized_matmul, M <= 32: one launch)"},
         "per_m": table,
         "bitwise_invariant_M1_vs_all": inv,
@@ -353,12 +365,26 @@ def bench_llama(args):
             "models": res}
 
 
+def bench_copycal(args):
+    """Calibration for the HBM traffic counters: a plain device copy of a
+    known size (256 MiB read, 256 MiB written per launch). rocprofv3's
+    FETCH_SIZE / WRITE_SIZE for this kernel against 262144 KiB give the
+    counter scale applied to the other kernels' readings."""
+    import torch
+    n = 256 << 20
+    src = [torch.ones(n // 4, dtype=torch.float32, device="cuda") for _ in range(2)]
+    dst = torch.empty_like(src[0])
+    t = statistics.median(_time_calls(lambda i: dst.copy_(src[i]), max(3, args.steps // 4), 2, 2, graph=False))
+    return {"metric": METRIC, "op": "copy calibration (256 MiB)", "bytes_read": n, "bytes_written": n,
+            "us": round(t * 1e6, 2), "GBps": round(2 * n / t / 1e9, 1)}
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--op", default="qmm4", choices=["qmm4", "qmm8", "linear", "rmsnorm", "decode", "prefill", "gemm", "llama", "all"])
+    p.add_argument("--op", default="qmm4", choices=["qmm4", "qmm8", "linear", "rmsnorm", "decode", "prefill", "gemm", "llama", "copycal", "all"])
     p.add_argument("--llama-layers", type=int, default=32)
     p.add_argument("--llama-prompt", type=int, default=512)
     p.add_argument("--llama-steps", type=int, default=128)
@@ -390,6 +416,8 @@ def main(argv=None) -> int:
             r = bench_prefill(a)
         elif op == "llama":
             r = bench_llama(a)
+        elif op == "copycal":
+            r = bench_copycal(a)
         else:
             r = bench_gemm(a)
         r.setdefault("n_gpus", 1)
