@@ -113,6 +113,138 @@ __global__ __launch_bounds__(kWave) void attn_decode_kernel(DecodeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// attn_decode_wg: the bandwidth-shaped decode launch, one 256-thread workgroup
+// per (sequence, kv head, head chunk of GU, split), GU * D a multiple of 256.
+// Every wave first requests all of its memory at once: the K rows of its 64
+// keys (straight into registers, 16-byte loads, rows past the sequence end
+// clamped to its last key) and a quarter of the split's V rows, which the
+// load unit copies straight into LDS (global_load_lds_dwordx4, [key][D]).
+// Scores (wave w: keys 64 w .. 64 w + 63, GU query heads as MFMA rows) and the
+// per-key weights (one head per wave) run while V lands; the l / acc chains
+// then read V from LDS (thread = (head, DL dims)). Same per-split arithmetic
+// as attn_decode_kernel, same partial layout, same combine.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int GU>
+__global__ __launch_bounds__(256) void attn_decode_wg(DecodeArgs a) {
+  typedef typename Frag<T>::type F;
+  constexpr int kThreads = 256;
+  static_assert((GU * D) % kThreads == 0, "attn_decode_wg: GU * D must be a multiple of 256");
+  constexpr int DL = GU * D / kThreads;        // dims per thread in the l / acc phase
+  constexpr int LPR = D / DL;                  // threads per head row
+  constexpr int CE = 16 / (int)sizeof(T);      // elements per 16-byte chunk
+  constexpr int CPR = D / CE;                  // chunks per V row
+  constexpr int KPI = kWave / CPR;             // V rows per copy instruction
+  constexpr int CPW = kSplit / KPI / 4;        // copy instructions per wave
+  constexpr int KT = kSplit / 4 / 16;          // score tiles per wave
+  static_assert(KPI >= 1 && (kSplit / KPI) % 4 == 0, "attn_decode_wg: V copy tiling");
+  __shared__ __attribute__((aligned(1024))) T Vs[kSplit * D];
+  __shared__ __attribute__((aligned(16))) float S[GU][kSplit];
+  __shared__ __attribute__((aligned(16))) float2 PC[GU][kSplit];
+  __shared__ float mfin[GU];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int split = blockIdx.x;
+  const int hk = blockIdx.y / a.nchunk;
+  const int chunk = blockIdx.y % a.nchunk;
+  const int b = blockIdx.z;
+  // A length outside [0, L] is clamped, so no key past the cache is ever read.
+  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
+  const int j0 = split * kSplit;
+  if (j0 >= len) return;  // uniform per workgroup, before any barrier
+  const int n_act = min(kSplit, len - j0);
+  const int G = a.Hq / a.Hkv;
+  const int h0 = hk * G + chunk * GU;
+
+  const T* qb = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb;
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh +
+                (int64_t)j0 * a.k_sl;
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh +
+                (int64_t)j0 * a.v_sl;
+  const int r = lane % 16, q = lane / 16;
+
+  // Memory requests, in this order: q, this wave's K rows, this wave's V copies.
+  F qf[D / 32];
+  load_q_frags<T, D>(qf, qb + (int64_t)(h0 + (r < GU ? r : 0)) * a.q_sh, r < GU, lane);
+  F kf[KT][D / 32];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const int key = min(64 * wave + 16 * t + r, n_act - 1);
+    const T* kr = kb + (int64_t)key * a.k_sl + 8 * q;
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) kf[t][st] = frag_load(kr + 32 * st);
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int ci = wave * CPW + c;                         // copy instruction of the split
+    const int key = min(ci * KPI + lane / CPR, n_act - 1);
+    copy_to_lds16(vb + (int64_t)key * a.v_sl + CE * (lane % CPR), Vs + ci * KPI * D);
+  }
+
+  // Scores of this wave's 64 keys (rows: the GU heads).
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) acc = mfma_step(qf[st], kf[t][st], acc);
+    const int key = 64 * wave + 16 * t + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * q + i;
+      if (row < GU) S[row][key] = key < n_act ? acc[i] * a.scale : -INFINITY;
+    }
+  }
+  stage_barrier<CPW>();  // scores visible; this wave's V copies may still be in flight
+  // Per-key weights, one head per wave.
+  for (int h = wave; h < GU; h += 4) {
+    const float mf = split_weights(S[h], PC[h], n_act, lane);
+    if (lane == 0) mfin[h] = mf;
+  }
+  // V landed (this wave's copies: vmcnt; everyone's: the barrier).
+  stage_barrier<0>();
+
+  // l / acc chains over the split's keys, V from LDS.
+  const int row = tid / LPR;
+  const int dim0 = (tid % LPR) * DL;
+  float l = 0.0f, acc[DL];
+#pragma unroll
+  for (int d = 0; d < DL; ++d) acc[d] = 0.0f;
+  const float2* pcr = PC[row];
+  const T* vs = Vs + dim0;
+  int j = 0;
+  for (; j + 8 <= n_act; j += 8) {
+    float v[8][DL];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) load_dims<T, DL>(vs + (j + u) * D, v[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float2 pc = pcr[j + u];
+      l = __builtin_fmaf(l, pc.y, pc.x);
+#pragma unroll
+      for (int d = 0; d < DL; ++d) acc[d] = __builtin_fmaf(acc[d], pc.y, pc.x * v[u][d]);
+    }
+  }
+  for (; j < n_act; ++j) {
+    float v[DL];
+    load_dims<T, DL>(vs + j * D, v);
+    const float2 pc = pcr[j];
+    l = __builtin_fmaf(l, pc.y, pc.x);
+#pragma unroll
+    for (int d = 0; d < DL; ++d) acc[d] = __builtin_fmaf(acc[d], pc.y, pc.x * v[d]);
+  }
+
+  const int64_t po = ((int64_t)b * a.Hq + h0 + row) * a.nsplit + split;
+#pragma unroll
+  for (int d = 0; d < DL; ++d) a.pacc[po * D + dim0 + d] = acc[d];
+  if (tid % LPR == 0) {
+    a.pm[po] = mfin[row];
+    a.pl[po] = l;
+  }
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeArgs a) {
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -253,11 +385,19 @@ static int decode_gu(int G) {
 template <typename T, int D>
 static int launch_decode(DecodeArgs& a, hipStream_t st) {
   dim3 grid(a.nsplit, a.Hkv * a.nchunk, a.B);
-  switch (a.GU) {
-    case 8: attn_decode_kernel<T, D, 8><<<grid, kWave, 0, st>>>(a); break;
-    case 4: attn_decode_kernel<T, D, 4><<<grid, kWave, 0, st>>>(a); break;
-    case 2: attn_decode_kernel<T, D, 2><<<grid, kWave, 0, st>>>(a); break;
-    default: attn_decode_kernel<T, D, 1><<<grid, kWave, 0, st>>>(a); break;
+  if (a.GU * D >= 256) {
+    switch (a.GU) {
+      case 8: attn_decode_wg<T, D, 8><<<grid, 256, 0, st>>>(a); break;
+      case 4: attn_decode_wg<T, D, 4><<<grid, 256, 0, st>>>(a); break;
+      default:
+        if constexpr (D == 128) attn_decode_wg<T, D, 2><<<grid, 256, 0, st>>>(a);
+        break;
+    }
+  } else {
+    switch (a.GU) {
+      case 2: attn_decode_kernel<T, D, 2><<<grid, kWave, 0, st>>>(a); break;
+      default: attn_decode_kernel<T, D, 1><<<grid, kWave, 0, st>>>(a); break;
+    }
   }
   int rc = bi_host::launch_status("bi_attn_decode");
   if (rc) return rc;

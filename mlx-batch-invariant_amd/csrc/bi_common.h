@@ -121,6 +121,34 @@ __device__ __forceinline__ float wave_sum_butterfly(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// Direct global -> LDS copies (global_load_lds_dwordx4) and the barrier that
+// waits for them.
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+
+// One 16-byte-per-lane copy global -> LDS; lane l lands at lds_block + 16 l.
+__device__ __forceinline__ void copy_to_lds16(const void* src, void* lds_block) {
+  __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)lds_block, 16, 0, 0);
+}
+
+// Stage barrier: wait until at most N vector-memory operations of this wave
+// are outstanding (vmcnt counts global_load_lds copies until their data is in
+// LDS; they complete in issue order) and all of its LDS reads have returned,
+// then s_barrier. Unlike __syncthreads() this does not drain the copies of
+// later stages that are still in flight. The empty asm statements keep the
+// compiler from moving memory accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("" ::: "memory");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace bi
 
 // ---------------------------------------------------------------------------
