@@ -19,6 +19,8 @@
 //           scores each for all 16 rows, each wave derives the weights of 4
 //           rows and then runs their l/acc chains (lane = (row, D/16 dims)),
 //           merging into registers.
+#include <type_traits>
+
 #include "bi_attn_common.h"
 
 namespace bi {
@@ -328,20 +330,29 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillArgs a) {
   for (int sp = 0; sp < nsplit; ++sp) {
     const int j0 = sp * kSplit;
     const int span = min(kSplit, maxkeys - j0);  // keys any row of the tile needs
-    // Phase 1: wave w scores keys [64 w, 64 w + 64) of the split for all 16 rows.
+    // Phase 1: wave w scores keys [64 w, 64 w + 64) of the split for all 16
+    // rows. All of the wave's K loads are issued before the first MFMA
+    // (unconditional: rows past the tile's last needed key are clamped to it).
+    {
+      const int r = lane % 16, q = lane / 16;
+      const T* ks = kb + (int64_t)j0 * a.k_sl;
+      F kf[4][D / 32];
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      const int key0 = 64 * wave + 16 * cc;
-      const int key = key0 + lane % 16;
-      const int row0 = 4 * (lane / 16);
-      if (key0 >= span) {
+      for (int cc = 0; cc < 4; ++cc) {
+        const int key = min(64 * wave + 16 * cc + r, span - 1);
+        const T* kr = ks + (int64_t)key * a.k_sl + 8 * q;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S[row0 + i][key] = -INFINITY;
-        continue;
+        for (int st = 0; st < D / 32; ++st) kf[cc][st] = frag_load(kr + 32 * st);
       }
-      const f32x4 acc = score_tile<T, D>(qf, kb + (int64_t)j0 * a.k_sl, a.k_sl, key0, span - key0, lane);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) S[row0 + i][key] = key < span ? acc[i] * a.scale : -INFINITY;
+      for (int cc = 0; cc < 4; ++cc) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < D / 32; ++st) acc = mfma_step(qf[st], kf[cc][st], acc);
+        const int key = 64 * wave + 16 * cc + r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) S[4 * q + i][key] = key < span ? acc[i] * a.scale : -INFINITY;
+      }
     }
     __syncthreads();
     // Phase 2: wave w derives the weights of rows 4w .. 4w+3.

@@ -59,12 +59,14 @@ __device__ __forceinline__ void load_q_frags(typename Frag<T>::type* qf, const T
 }
 
 // ---- per-key softmax weights of one split, one row, one wave ----------------
-// S_row: 256 scores in LDS; keys at or beyond n_act (>= 1) are ignored. Writes
-// PC_row[j] = (p_j, corr_j) for every key and returns m at the last active key.
-// Lane l owns keys 4l .. 4l+3.
-__device__ __forceinline__ float split_weights(const float* S_row, float2* PC_row, int n_act,
-                                               int lane) {
-  const f32x4 s = reinterpret_cast<const f32x4*>(S_row)[lane];
+// s: this lane's 4 scores (keys 4l .. 4l+3 of the split); keys at or beyond
+// n_act (>= 1) are ignored by the caller. Returns p_j and corr_j of the
+// lane's keys and, in m_last, m at the last active key.
+struct SplitWeights {
+  f32x4 p, corr;
+  float m_last;
+};
+__device__ __forceinline__ SplitWeights split_weights_core(f32x4 s, int n_act, int lane) {
   float loc = fmaxf(fmaxf(fmaxf(s[0], s[1]), s[2]), s[3]);
   float incl = loc;
 #pragma unroll
@@ -74,28 +76,41 @@ __device__ __forceinline__ float split_weights(const float* S_row, float2* PC_ro
   }
   float prev = __shfl_up(incl, 1, kWave);
   if (lane == 0) prev = -INFINITY;
+  SplitWeights w;
   float mk[4];
-  f32x4 out01, out23;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const float m_new = fmaxf(prev, s[k]);
-    const float corr = expf(prev - m_new);
-    const float p = expf(s[k] - m_new);
+    w.corr[k] = expf(prev - m_new);
+    w.p[k] = expf(s[k] - m_new);
     mk[k] = m_new;
     prev = m_new;
-    if (k < 2) {
-      out01[2 * k] = p;
-      out01[2 * k + 1] = corr;
-    } else {
-      out23[2 * (k - 2)] = p;
-      out23[2 * (k - 2) + 1] = corr;
-    }
   }
-  reinterpret_cast<f32x4*>(PC_row)[2 * lane] = out01;
-  reinterpret_cast<f32x4*>(PC_row)[2 * lane + 1] = out23;
   const int last = n_act - 1;
   const float mine = mk[last & 3];
-  return __shfl(mine, last >> 2, kWave);
+  w.m_last = __shfl(mine, last >> 2, kWave);
+  return w;
+}
+
+// S_row: 256 scores in LDS. Writes PC_row[j] = (p_j, corr_j) for every key
+// and returns m at the last active key. Lane l owns keys 4l .. 4l+3.
+__device__ __forceinline__ float split_weights(const float* S_row, float2* PC_row, int n_act,
+                                               int lane) {
+  const SplitWeights w = split_weights_core(reinterpret_cast<const f32x4*>(S_row)[lane], n_act, lane);
+  const f32x4 out01 = {w.p[0], w.corr[0], w.p[1], w.corr[1]};
+  const f32x4 out23 = {w.p[2], w.corr[2], w.p[3], w.corr[3]};
+  reinterpret_cast<f32x4*>(PC_row)[2 * lane] = out01;
+  reinterpret_cast<f32x4*>(PC_row)[2 * lane + 1] = out23;
+  return w.m_last;
+}
+
+// Same weights, p written over the scores in SP_row and corr into C_row.
+__device__ __forceinline__ float split_weights_inplace(float* SP_row, float* C_row, int n_act,
+                                                       int lane) {
+  const SplitWeights w = split_weights_core(reinterpret_cast<const f32x4*>(SP_row)[lane], n_act, lane);
+  reinterpret_cast<f32x4*>(SP_row)[lane] = w.p;
+  reinterpret_cast<f32x4*>(C_row)[lane] = w.corr;
+  return w.m_last;
 }
 
 // ---- per-key accumulation over one split, one (row, DL dims) per lane -------
