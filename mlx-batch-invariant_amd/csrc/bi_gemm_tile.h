@@ -116,6 +116,7 @@ struct DenseB {
 template <typename T, int BITS, int GS>
 struct QuantB {
   typedef typename Frag<T>::type F;
+  static constexpr int kBits = BITS, kGS = GS;
   static constexpr int kWords = 64 * BITS / 32;            // words per lane per group: 8 or 16
   static constexpr int kScales = GS >= 64 ? 1 : 64 / GS;   // scales per lane per group
   struct Raw {

@@ -1,0 +1,145 @@
+// bi_gemv_stream.h — the decode GEMV for an affine-quantized B with no
+// workgroup-wide staging barrier before compute.
+//
+// Same arithmetic as every other quantized launch (bi_gemm_tile.h, blocked
+// k-slot map; each group's raw fp32 partial, then the ordered fold).
+//
+// One workgroup of W waves per 16 output columns; wave w owns the NB
+// consecutive groups [w NB, w NB + NB). Each wave requests, in this order:
+//   * its slice of A (MR rows x NB * 256 k, 16-byte loads),
+//   * its slice of the scales and biases (16 rows x NB * 256 / GS each;
+//     consecutive groups make every row's slice contiguous),
+//   * the codes of its NB groups (two 16-byte loads per group and lane for
+//     4-bit),
+// then writes A and the scales/biases into a wave-private LDS region (DS
+// operations of one wave complete in order, so no barrier is needed to read
+// them back) and computes its groups as their codes arrive. Issuing the code
+// loads only after A and the metadata have landed measured slower (the
+// weight stream starts later). The only barrier is the one before the fold.
+// A workgroup-wide staging barrier made every wave wait for the slowest of
+// its workgroup's metadata loads, which arrive among the whole weight stream;
+// here a wave waits only for its own.
+//
+// LDS (dynamic): G * 64 f32x4 partials, then per wave: A [MR][NB * 256],
+// scales [16][SPR], biases [16][SPR] (SPR = NB * 256 / GS).
+#pragma once
+
+#include "bi_gemm_tile.h"
+
+namespace bi {
+
+template <typename T, int BITS, int GS, int W, int NB, int MR>
+struct GemvStreamCfg {
+  static constexpr int kCE = 16 / (int)sizeof(T);            // elements per 16-byte load
+  static constexpr int kSPR = NB * kGroupK / GS;              // scales per row per wave
+  static constexpr int kAElems = MR * NB * kGroupK;           // A elements per wave
+  static constexpr int kALoads = kAElems / kCE / kWave;       // A loads per lane
+  static constexpr int kMChunks = 2 * 16 * kSPR / kCE;        // meta chunks per wave
+  static constexpr int kMLoads = (kMChunks + kWave - 1) / kWave;
+  static constexpr int kWaveElems = kAElems + 2 * 16 * kSPR;  // LDS elements per wave
+  static_assert(kAElems % (kCE * kWave) == 0, "A slice must be whole 16-byte loads per lane");
+  static_assert(kSPR % kCE == 0, "scale rows must be whole 16-byte chunks");
+  static size_t lds_bytes(int G) {
+    return (size_t)G * kWave * sizeof(f32x4) + (size_t)W * kWaveElems * sizeof(T);
+  }
+};
+
+template <typename T, int BITS, int GS, int W, int NB, int MR>
+__global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
+                                                        QuantB<T, BITS, GS> bsrc,
+                                                        T* __restrict__ out, int M, int N, int K,
+                                                        int G) {
+  typedef GemvStreamCfg<T, BITS, GS, W, NB, MR> C;
+  typedef QuantB<T, BITS, GS> QB;
+  typedef typename Frag<T>::type F;
+  extern __shared__ __attribute__((aligned(16))) f32x4 smem[];
+  f32x4* part = smem;                                               // [G][64]
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  T* As = reinterpret_cast<T*>(smem + (size_t)G * kWave) + (size_t)wave * C::kWaveElems;
+  T* Ms = As + C::kAElems;                                          // [2][16][SPR]
+  const int r = lane % 16, q = lane / 16;
+  const int n_base = blockIdx.x * 16;
+  const int n = min(n_base + r, N - 1);          // clamped: padding columns are not stored
+  const int g0 = wave * NB;                      // G == W * NB (checked on the host)
+
+  // 1. A slice: row ar, elements [g0 * 256 + ac, +kCE) of the wave's slice.
+  F av[C::kALoads];
+#pragma unroll
+  for (int i = 0; i < C::kALoads; ++i) {
+    const int c = lane + kWave * i;
+    const int ar = c / (NB * kGroupK / C::kCE), ac = (c % (NB * kGroupK / C::kCE)) * C::kCE;
+    av[i] = frag_load(a + (int64_t)min(ar, M - 1) * lda + g0 * kGroupK + ac);
+  }
+  // 2. Scales then biases of rows n_base .. n_base + 15 for the wave's groups.
+  F mv[C::kMLoads];
+  const int gpr = (int)bsrc.groups_per_row;
+#pragma unroll
+  for (int i = 0; i < C::kMLoads; ++i) {
+    const int c0 = lane + kWave * i;
+    const int c = c0 < C::kMChunks ? c0 : 0;
+    const int kind = c / (16 * C::kSPR / C::kCE);
+    const int within = c % (16 * C::kSPR / C::kCE);
+    const int row = within / (C::kSPR / C::kCE), col = (within % (C::kSPR / C::kCE)) * C::kCE;
+    const T* base = kind ? bsrc.biases : bsrc.scales;
+    mv[i] = frag_load(base + (int64_t)min(n_base + row, N - 1) * gpr + g0 * (kGroupK / GS) + col);
+  }
+  // 3. Codes of the wave's groups, after everything above in issue order.
+  asm volatile("" ::: "memory");
+  typename QB::Raw braw[NB];
+  const typename QB::Lane bl = bsrc.lane(n, q);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) bsrc.load_codes(braw[j], bl, g0 + j);
+  // Wave-private LDS: written and read back by this wave only.
+#pragma unroll
+  for (int i = 0; i < C::kALoads; ++i) *reinterpret_cast<F*>(As + (lane + kWave * i) * C::kCE) = av[i];
+#pragma unroll
+  for (int i = 0; i < C::kMLoads; ++i) {
+    const int c = lane + kWave * i;
+    if (c < C::kMChunks) *reinterpret_cast<F*>(Ms + c * C::kCE) = mv[i];
+  }
+  asm volatile("" ::: "memory");
+
+  const int rt = n - n_base;                      // this lane's row of the tile (clamped)
+  const int arow = min(r, MR - 1);                // A rows past MR alias a loaded row (never stored)
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int g = g0 + j;
+#pragma unroll
+    for (int i = 0; i < QB::kScales; ++i) {
+      const int v = j * (kGroupK / GS) + (64 * q) / GS + i;
+      braw[j].scale[i] = Ms[rt * C::kSPR + v];
+      braw[j].bias[i] = Ms[16 * C::kSPR + rt * C::kSPR + v];
+    }
+    F af[1][kSteps];
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s)
+      af[0][s] = *reinterpret_cast<const F*>(As + arow * (NB * kGroupK) + j * kGroupK + 64 * q + 8 * s);
+    f32x4 acc[1];
+    mma_group<T, QB, 1, true>(bsrc, braw[j], af, g, q, acc);
+    part[g * kWave + lane] = acc[0];
+  }
+  __syncthreads();
+  // Ordered fold: one thread per output element (lane l, register e of the
+  // MFMA result layout), eight LDS loads in flight, adds in group order.
+  const float* partf = reinterpret_cast<const float*>(part);
+  for (int idx = threadIdx.x; idx < kWave * 4; idx += kWave * W) {
+    const int e = idx / kWave, l = idx % kWave;
+    const float* pp = partf + l * 4 + e;
+    float total = 0.f;
+    int gg = 0;
+    for (; gg + 8 <= G; gg += 8) {
+      float v[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) v[jj] = pp[(gg + jj) * kWave * 4];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) total = total + v[jj];
+    }
+    for (; gg < G; ++gg) total = total + pp[gg * kWave * 4];
+    const int col = n_base + l % 16;
+    const int m = 4 * (l / 16) + e;
+    if (m < M && col < N) out[(int64_t)m * N + col] = to_store<T>(total);
+  }
+}
+
+}  // namespace bi

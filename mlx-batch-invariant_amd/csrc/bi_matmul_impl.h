@@ -25,6 +25,7 @@
 #include <type_traits>
 
 #include "bi_gemm_big.h"
+#include "bi_gemv_stream.h"
 #include "bi_gemm_tile.h"
 
 namespace bi {
@@ -596,9 +597,48 @@ static void launch_wg_alds(const T* a, int64_t lda, const BSrc& bsrc, T* out, in
   else launch_wg1<T, BSrc, W, 4, true, META, AC>(a, lda, bsrc, out, M, N, K, G, lds, st);
 }
 
+// The barrier-free decode GEMV for a quantized B (bi_gemv_stream.h): 4 waves
+// of G / 4 consecutive groups (G in {4, 8, 16}), M <= 4. Returns false when
+// the shape does not qualify.
+template <typename T, int BITS, int GS, int NB, int MR>
+static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
+                           int K, int G, hipStream_t st) {
+  constexpr int kCE = 16 / (int)sizeof(T);
+  if constexpr ((NB * kGroupK / GS) % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0) {
+    return false;
+  } else {
+    typedef GemvStreamCfg<T, BITS, GS, 4, NB, MR> C;
+    gemv_stream<T, BITS, GS, 4, NB, MR><<<dim3(ceil_div(N, 16)), kWave * 4, C::lds_bytes(G), st>>>(
+        a, lda, b, out, M, N, K, G);
+    return true;
+  }
+}
+
+template <typename T, int BITS, int GS, int NB>
+static bool launch_stream_nb(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
+                             int K, int G, hipStream_t st) {
+  if (M == 1) return launch_stream1<T, BITS, GS, NB, 1>(a, lda, b, out, M, N, K, G, st);
+  return launch_stream1<T, BITS, GS, NB, 4>(a, lda, b, out, M, N, K, G, st);
+}
+
+template <typename T, int BITS, int GS>
+static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N, int K,
+                          int G, hipStream_t st) {
+  if (M > 4 || K % kGroupK || (G != 4 && G != 8 && G != 16)) return false;
+  if (b.groups_per_row % (16 / (int)sizeof(T)) || !bi_host::aligned16(b.scales) || !bi_host::aligned16(b.biases) ||
+      lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a))
+    return false;
+  if (G == 16) return launch_stream_nb<T, BITS, GS, 4>(a, lda, b, out, M, N, K, G, st);
+  if (G == 8) return launch_stream_nb<T, BITS, GS, 2>(a, lda, b, out, M, N, K, G, st);
+  return launch_stream_nb<T, BITS, GS, 1>(a, lda, b, out, M, N, K, G, st);
+}
+
 template <typename T, class BSrc, int W>
 static void launch_wg(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K, int G,
                       hipStream_t st) {
+  if constexpr (BSrc::kMeta) {
+    if (W == 4 && launch_stream<T, BSrc::kBits, BSrc::kGS>(a, lda, bsrc, out, M, N, K, G, st)) return;
+  }
   dim3 grid(ceil_div(N, 16), 1, 1);
   const int mt = M <= 16 ? 1 : 2;
   const size_t part_bytes = (size_t)G * mt * kWave * sizeof(f32x4);
