@@ -38,7 +38,7 @@ PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 # on a 256 MiB device copy (bench.py --op copycal): read x 2.000, write x 1.000.
 # Source: profiles/qmatmul4_g64_llama_mlp_m1.txt. Re-measure after changing
 # the kernel.
-MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 16250, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
+MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 16210, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
 PEAK_BF16 = 2.5e15         # FLOP/s, dense bf16 MFMA
 METRIC = "% of HBM/MFMA roofline per op at batch 1–256, with bitwise batch invariance"
 ROTATE_BYTES = 512 << 20
@@ -170,7 +170,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
                      "traffic_source": None if traffic is None else
                      "rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch x copy-kernel scale (bytes per launch)",
-                     "algorithmic_bytes": by1, "kernel": "gemv_stream (bi_quantized_matmul, M <= 4: one launch)"},
+                     "algorithmic_bytes": by1, "kernel": "gemv_stream<bf16,4,64,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)"},
         "per_m": table,
         "bitwise_invariant_M1_vs_all": inv,
         "stock_gpu": {"dequant_plus_matmul_us": None if stock_deq is None else round(stock_deq * 1e6, 2),

@@ -13,9 +13,13 @@
 //     4-bit),
 // then writes A and the scales/biases into a wave-private LDS region (DS
 // operations of one wave complete in order, so no barrier is needed to read
-// them back) and computes its groups as their codes arrive. Issuing the code
-// loads only after A and the metadata have landed measured slower (the
-// weight stream starts later). The only barrier is the one before the fold.
+// them back) and computes its groups as their codes arrive. Code loads run at
+// most PD groups ahead of compute: with every group requested up front, a
+// wave's loads arrive scattered over the whole weight stream and its compute
+// only starts near the end; a bounded depth keeps each wave's requests close
+// together in the memory queues. Issuing the code loads only after A and the
+// metadata have landed measured slower (the weight stream starts later). The
+// only barrier is the one before the fold.
 // A workgroup-wide staging barrier made every wave wait for the slowest of
 // its workgroup's metadata loads, which arrive among the whole weight stream;
 // here a wave waits only for its own.
@@ -44,7 +48,7 @@ struct GemvStreamCfg {
   }
 };
 
-template <typename T, int BITS, int GS, int W, int NB, int MR>
+template <typename T, int BITS, int GS, int W, int NB, int MR, int PD>
 __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
                                                         QuantB<T, BITS, GS> bsrc,
                                                         T* __restrict__ out, int M, int N, int K,
@@ -84,12 +88,13 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     const T* base = kind ? bsrc.biases : bsrc.scales;
     mv[i] = frag_load(base + (int64_t)min(n_base + row, N - 1) * gpr + g0 * (kGroupK / GS) + col);
   }
-  // 3. Codes of the wave's groups, after everything above in issue order.
+  // 3. Codes of the wave's first PD groups, after everything above in issue
+  // order; group j + PD is requested when group j starts.
   asm volatile("" ::: "memory");
   typename QB::Raw braw[NB];
   const typename QB::Lane bl = bsrc.lane(n, q);
 #pragma unroll
-  for (int j = 0; j < NB; ++j) bsrc.load_codes(braw[j], bl, g0 + j);
+  for (int j = 0; j < PD && j < NB; ++j) bsrc.load_codes(braw[j], bl, g0 + j);
   // Wave-private LDS: written and read back by this wave only.
 #pragma unroll
   for (int i = 0; i < C::kALoads; ++i) *reinterpret_cast<F*>(As + (lane + kWave * i) * C::kCE) = av[i];
@@ -105,6 +110,11 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int g = g0 + j;
+    if (j + PD < NB) {
+      asm volatile("" ::: "memory");
+      bsrc.load_codes(braw[j + PD], bl, g0 + j + PD);
+      asm volatile("" ::: "memory");
+    }
 #pragma unroll
     for (int i = 0; i < QB::kScales; ++i) {
       const int v = j * (kGroupK / GS) + (64 * q) / GS + i;

@@ -597,30 +597,35 @@ static void launch_wg_alds(const T* a, int64_t lda, const BSrc& bsrc, T* out, in
   else launch_wg1<T, BSrc, W, 4, true, META, AC>(a, lda, bsrc, out, M, N, K, G, lds, st);
 }
 
-// The barrier-free decode GEMV for a quantized B (bi_gemv_stream.h): 4 waves
-// of G / 4 consecutive groups (G in {4, 8, 16}), M <= 4. Returns false when
-// the shape does not qualify.
-template <typename T, int BITS, int GS, int NB, int MR>
+// The barrier-free decode GEMV for a quantized B (bi_gemv_stream.h): W waves
+// of NB = G / W consecutive groups (G in {4, 8, 16}), M <= 4, code loads PD
+// groups ahead. Returns false when the shape does not qualify.
+template <typename T, int BITS, int GS, int W, int NB, int MR, int PD>
 static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
                            int K, int G, hipStream_t st) {
   constexpr int kCE = 16 / (int)sizeof(T);
   if constexpr ((NB * kGroupK / GS) % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0) {
     return false;
   } else {
-    typedef GemvStreamCfg<T, BITS, GS, 4, NB, MR> C;
-    gemv_stream<T, BITS, GS, 4, NB, MR><<<dim3(ceil_div(N, 16)), kWave * 4, C::lds_bytes(G), st>>>(
+    if (G != W * NB) return false;
+    typedef GemvStreamCfg<T, BITS, GS, W, NB, MR> C;
+    gemv_stream<T, BITS, GS, W, NB, MR, PD><<<dim3(ceil_div(N, 16)), kWave * W, C::lds_bytes(G), st>>>(
         a, lda, b, out, M, N, K, G);
     return true;
   }
 }
 
-template <typename T, int BITS, int GS, int NB>
-static bool launch_stream_nb(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
-                             int K, int G, hipStream_t st) {
-  if (M == 1) return launch_stream1<T, BITS, GS, NB, 1>(a, lda, b, out, M, N, K, G, st);
-  return launch_stream1<T, BITS, GS, NB, 4>(a, lda, b, out, M, N, K, G, st);
+template <typename T, int BITS, int GS, int W, int NB, int PD>
+static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
+                            int K, int G, hipStream_t st) {
+  if (M == 1) return launch_stream1<T, BITS, GS, W, NB, 1, PD>(a, lda, b, out, M, N, K, G, st);
+  return launch_stream1<T, BITS, GS, W, NB, 4, PD>(a, lda, b, out, M, N, K, G, st);
 }
 
+// Launch shapes in order of preference (measured, Llama MLP shape, M = 1):
+// two groups per wave with one group of codes in flight beyond the one being
+// computed, else four groups per wave two ahead. A shape whose scale slice or
+// A slice is not whole 16-byte loads is skipped.
 template <typename T, int BITS, int GS>
 static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N, int K,
                           int G, hipStream_t st) {
@@ -628,9 +633,18 @@ static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b,
   if (b.groups_per_row % (16 / (int)sizeof(T)) || !bi_host::aligned16(b.scales) || !bi_host::aligned16(b.biases) ||
       lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a))
     return false;
-  if (G == 16) return launch_stream_nb<T, BITS, GS, 4>(a, lda, b, out, M, N, K, G, st);
-  if (G == 8) return launch_stream_nb<T, BITS, GS, 2>(a, lda, b, out, M, N, K, G, st);
-  return launch_stream_nb<T, BITS, GS, 1>(a, lda, b, out, M, N, K, G, st);
+  switch (G) {
+    case 16:
+      return launch_stream_m<T, BITS, GS, 8, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_m<T, BITS, GS, 4, 4, 2>(a, lda, b, out, M, N, K, G, st);
+    case 8:
+      return launch_stream_m<T, BITS, GS, 4, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_m<T, BITS, GS, 2, 4, 2>(a, lda, b, out, M, N, K, G, st);
+    default:
+      return launch_stream_m<T, BITS, GS, 4, 1, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_m<T, BITS, GS, 2, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_m<T, BITS, GS, 1, 4, 2>(a, lda, b, out, M, N, K, G, st);
+  }
 }
 
 template <typename T, class BSrc, int W>
