@@ -1,0 +1,434 @@
+// bi_attn_mfma.h — the split-KV attention kernels (decode, prefill) with every
+// product on the matrix cores. The per-split arithmetic (bi_attn_common.h) is
+// one text shared by both kernels, so a row gets the same bits from either.
+//
+// Layouts (v_mfma_f32_16x16x32_{bf16,f16}; fp32 runs eight 16x16x4 steps per
+// 32-wide step with the same element order):
+//   scores  S^T = MFMA(A = K rows, B = Q^T): A lane (key r, quarter qq) holds
+//           K[key r][32 st + 8 qq + e], B lane (row n, qq) holds
+//           Q[row n][32 st + 8 qq + e]; the result lane (n, qq) holds the
+//           scores of row n with keys 16 t + 4 qq + i (i = 0..3) of tile t.
+//   P.V     acc = MFMA(A = P, B = V^T) per 32-key step ks: A lane (row r, qq)
+//           holds P of keys 32 ks + {4 qq + i, 16 + 4 qq + i} — exactly what
+//           the score layout leaves in that lane for tiles 2 ks, 2 ks + 1 —
+//           and B lane (dim n, qq) holds V of the same keys for dim n; the
+//           result lane (n, qq) holds rows 4 qq + i of dim n.
+//   V^T     V rows sit in LDS as loaded ([key][D], 16-byte chunk c of row r in
+//           slot c ^ (r & 7)); ds_read_b64_tr_b16 returns, in each 16-lane
+//           group, element (t % 4) of the 8 bytes read by lane 4 j + t / 4 as
+//           slot j of lane t, so lane 4 j + c reading V[key j][4 c .. 4 c + 3]
+//           hands every lane 4 keys of one dim. fp32 V is read one element
+//           per lane (ds_read_b32).
+#pragma once
+
+#include "bi_attn_common.h"
+
+namespace bi {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// LDS tile of K or V rows: row r, 16-byte chunk c at byte offset off(r, c).
+template <typename T, int D>
+struct KVTile {
+  static constexpr int kRowBytes = D * (int)sizeof(T);
+  static constexpr int kCPR = kRowBytes / 16;          // chunks per row (>= 8)
+  static constexpr int kRowsPerCopy = kWave / kCPR;    // rows per 1 KB copy instruction
+  static_assert(kCPR >= 8 && kWave % kCPR == 0, "KVTile: D * sizeof(T) must be 128..1024 bytes");
+  static __device__ __forceinline__ int off(int r, int c) { return r * kRowBytes + ((c ^ (r & 7)) << 4); }
+  // Copy instruction ci of a tile: rows ci * kRowsPerCopy .. + kRowsPerCopy - 1
+  // (global row index clamped by the caller). Lane l fetches the chunk that
+  // belongs in slot l % kCPR of its row, landing at tile + 1024 ci + 16 l.
+  static __device__ __forceinline__ void copy(char* tile, int ci, const T* rows, int64_t stride,
+                                              int nrows_valid, int lane) {
+    const int r = ci * kRowsPerCopy + lane / kCPR;
+    const int c = (lane % kCPR) ^ (r & 7);
+    const T* src = rows + (int64_t)min(r, nrows_valid - 1) * stride + c * (16 / (int)sizeof(T));
+    copy_to_lds16(src, tile + 1024 * ci);
+  }
+  // A-operand fragment of the score MFMA: row r, dims 32 st + 8 qq .. + 7.
+  static __device__ __forceinline__ typename Frag<T>::type kfrag(const char* tile, int r, int st, int qq) {
+    typedef typename Frag<T>::type F;
+    if constexpr (sizeof(T) == 2) {
+      return __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(tile + off(r, 4 * st + qq)));
+    } else {
+      F f;
+      f.lo = *reinterpret_cast<const f32x4*>(tile + off(r, 8 * st + 2 * qq));
+      f.hi = *reinterpret_cast<const f32x4*>(tile + off(r, 8 * st + 2 * qq + 1));
+      return f;
+    }
+  }
+  // B-operand fragment of the P.V MFMA for the 32 keys key0 .. key0 + 31 of
+  // the tile and dims 16 dt .. 16 dt + 15: slot e of lane (n, qq) holds
+  // V[key0 + (e < 4 ? 4 qq + e : 16 + 4 qq + e - 4)][16 dt + n].
+  static __device__ __forceinline__ typename Frag<T>::type vfrag(const char* tile, int key0, int dt, int lane) {
+    typedef typename Frag<T>::type F;
+    const int qq = lane / 16, u = lane % 16;
+    if constexpr (sizeof(T) == 2) {
+      const int j = u / 4, c = u % 4;
+      const int chunk = 2 * dt + (c >> 1);
+      const int r0 = key0 + 4 * qq + j, r1 = r0 + 16;
+      const s16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)(tile + off(r0, chunk) + ((c & 1) << 3)));
+      const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)(tile + off(r1, chunk) + ((c & 1) << 3)));
+      const s16x8 v = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+      return __builtin_bit_cast(F, v);
+    } else {
+      const int dim = 16 * dt + u;
+      const int chunk = dim >> 2, within = (dim & 3) << 2;
+      F f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f.lo[e] = *reinterpret_cast<const float*>(tile + off(key0 + 4 * qq + e, chunk) + within);
+        f.hi[e] = *reinterpret_cast<const float*>(tile + off(key0 + 16 + 4 * qq + e, chunk) + within);
+      }
+      return f;
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Decode: one 256-thread workgroup per (sequence, kv head, head chunk of GU,
+// split). GU query heads are the 16 columns of the score tile (GU <= 16).
+// Every wave first requests all of its memory: Q^T, the K rows of its 64 keys
+// (registers, 16-byte loads, rows past the sequence end clamped to its last
+// key) and a quarter of the split's V rows, which the load unit copies
+// straight into LDS. Wave w scores keys 64 w .. 64 w + 63; the split maximum
+// is exchanged through LDS; each wave writes its keys' weights to LDS; then
+// wave w computes the P.V tiles of dims 16 dt, dt = w, w + 4, ..., and wave 0
+// also the weight sum. Writes (m, l, acc) of its split.
+// ---------------------------------------------------------------------------
+template <typename T, int D, int GU>
+__global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
+  typedef typename Frag<T>::type F;
+  typedef KVTile<T, D> KV;
+  constexpr int KT = 4;                                 // score tiles per wave
+  constexpr int NDT = D / 16;                           // P.V dim tiles
+  constexpr int NCOPY = kSplit / KV::kRowsPerCopy;      // copy instructions per split
+  constexpr int CPW = NCOPY / 4;                        // ... per wave
+  static_assert(GU >= 1 && GU <= 16, "attn_decode_mfma: 1..16 heads per workgroup");
+  __shared__ __attribute__((aligned(1024))) char Vs[kSplit * KV::kRowBytes];
+  __shared__ __attribute__((aligned(16))) float Ps[GU][kSplit];
+  __shared__ float mxs[4][16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int split = blockIdx.x;
+  const int hk = blockIdx.y / a.nchunk;
+  const int chunk = blockIdx.y % a.nchunk;
+  const int b = blockIdx.z;
+  // A length outside [0, L] is clamped, so no key past the cache is ever read.
+  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
+  const int j0 = split * kSplit;
+  if (j0 >= len) return;  // uniform per workgroup, before any barrier
+  const int n_act = min(kSplit, len - j0);
+  const int G = a.Hq / a.Hkv;
+  const int h0 = hk * G + chunk * GU;
+  const int r = lane % 16, qq = lane / 16;
+
+  const T* qb = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb;
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh +
+                (int64_t)j0 * a.k_sl;
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh +
+                (int64_t)j0 * a.v_sl;
+
+  // Memory requests, in this order: Q^T, this wave's K rows, its V copies.
+  F qf[D / 32];
+  {
+    const T* qrow = qb + (int64_t)(h0 + (r < GU ? r : 0)) * a.q_sh;
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) qf[st] = r < GU ? frag_load(qrow + 32 * st + 8 * qq) : frag_zero<F>();
+  }
+  F kf[KT][D / 32];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    const T* kr = kb + (int64_t)min(64 * wave + 16 * t + r, n_act - 1) * a.k_sl + 8 * qq;
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) kf[t][st] = frag_load(kr + 32 * st);
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) KV::copy(Vs, wave * CPW + c, vb, a.v_sl, n_act, lane);
+
+  // Scores of this wave's 64 keys; lane (r, qq) holds row r, keys 64 w + 16 t + 4 qq + i.
+  float s[KT][4];
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) acc = mfma_step(kf[t][st], qf[st], acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = 64 * wave + 16 * t + 4 * qq + i;
+      s[t][i] = key < n_act ? acc[i] * a.scale_log2 : -INFINITY;
+      mloc = fmaxf(mloc, s[t][i]);
+    }
+  }
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 16, kWave));
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+  if (qq == 0) mxs[wave][r] = mloc;
+  stage_barrier<CPW>();  // the wave maxima visible; V copies may still be in flight
+  const float m = fmaxf(fmaxf(mxs[0][r], mxs[1][r]), fmaxf(mxs[2][r], mxs[3][r]));
+  if (r < GU) {
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const int key0 = 64 * wave + 16 * t + 4 * qq;
+      f32x4 p;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = split_weight(s[t][i], m, key0 + i < n_act);
+      *reinterpret_cast<f32x4*>(&Ps[r][key0]) = p;
+    }
+  }
+  const int64_t pbase = ((int64_t)b * a.Hq + h0) * a.nsplit + split;
+  if (wave == 0 && qq == 0 && r < GU) a.pm[pbase + (int64_t)r * a.nsplit] = m;
+  stage_barrier<0>();  // V landed (own copies: vmcnt; everyone's: the barrier); weights visible
+
+  // P.V over the split's 8 key steps, this wave's dim tiles; wave 0: weight sum.
+  f32x4 acc[(NDT + 3) / 4];
+  f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < (NDT + 3) / 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+  for (int ks = 0; ks < kSplit / 32; ++ks) {
+    float p8[8];
+    if (r < GU) {
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(&Ps[r][32 * ks + 4 * qq]);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(&Ps[r][32 * ks + 16 + 4 * qq]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        p8[e] = x0[e];
+        p8[4 + e] = x1[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) p8[e] = 0.f;
+    }
+    const PFrag<T> pf = make_pfrag<T>(p8);
+#pragma unroll
+    for (int j = 0; j < (NDT + 3) / 4; ++j) {
+      const int dt = wave + 4 * j;
+      if (dt < NDT) acc[j] = pv_step<T>(pf, KV::vfrag(Vs, 32 * ks, dt, lane), acc[j]);
+    }
+    if (wave == 0) lsum = pv_step<T>(pf, ones_frag<T>(), lsum);
+  }
+
+#pragma unroll
+  for (int j = 0; j < (NDT + 3) / 4; ++j) {
+    const int dt = wave + 4 * j;
+    if (dt >= NDT) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * qq + i;
+      if (row < GU) a.pacc[(pbase + (int64_t)row * a.nsplit) * D + 16 * dt + r] = acc[j][i];
+    }
+  }
+  if (wave == 0 && r == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 4 * qq + i;
+      if (row < GU) a.pl[pbase + (int64_t)row * a.nsplit] = lsum[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill: one 256-thread workgroup per (sequence, kv head, 64 (token, head)
+// rows, token-major); wave w owns the 16 rows 16 w .. 16 w + 15 of them (the
+// columns of its score tiles). K and V stream through a ring of three LDS
+// buffers of 64 keys, shared by the four waves: per split, the K chunks (each
+// wave scores its rows against the chunk's 64 keys, scores kept in
+// registers), the split maximum and weights (in registers), then the V
+// chunks (P.V and the weight sum), then the in-register merge. Chunk c + 2 is
+// requested right after the barrier that opens chunk c. Only the chunks the
+// workgroup's rows need are loaded (the last split may be short); rows past
+// a row's causal or kv_lens limit are masked.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
+  typedef typename Frag<T>::type F;
+  typedef KVTile<T, D> KV;
+  constexpr int CH = 64;                                // keys per chunk
+  constexpr int NBUF = 3;
+  constexpr int CHB = CH * KV::kRowBytes;               // bytes per chunk
+  constexpr int CPW = CH / KV::kRowsPerCopy / 4;        // copy instructions per wave per chunk
+  constexpr int NDT = D / 16;
+  static_assert(CPW >= 1, "attn_prefill_mfma: chunk copy tiling");
+  __shared__ __attribute__((aligned(1024))) char ring[NBUF * CHB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int r = lane % 16, qq = lane / 16;
+  const int wg = gridDim.x - 1 - blockIdx.x;            // heaviest (latest tokens) first
+  const int hk = blockIdx.y;
+  const int b = blockIdx.z;
+  const int G = a.Hq / a.Hkv;
+  const int npairs = a.Tq * G;
+  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
+  auto nkeys_of = [&](int pair) -> int {
+    if (pair >= npairs) return 0;
+    return a.causal ? len - a.Tq + pair / G + 1 : len;
+  };
+  const int last_pair = min(64 * wg + 63, npairs - 1);
+  const int maxkeys = nkeys_of(last_pair);              // keys the workgroup needs (nkeys grows with the token)
+  const int my_pair = 64 * wg + 16 * wave + r;          // score-layout row of this lane
+  const int my_nkeys = nkeys_of(my_pair);
+  int acc_nkeys[4];                                     // accumulator-layout rows 4 qq + i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc_nkeys[i] = nkeys_of(64 * wg + 16 * wave + 4 * qq + i);
+
+  const T* qb = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb;
+  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+
+  F qf[D / 32];
+  {
+    const bool ok = my_pair < npairs;
+    const T* qrow = qb + (ok ? (int64_t)(hk * G + my_pair % G) * a.q_sh + (int64_t)(my_pair / G) * a.q_st : 0);
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) qf[st] = ok ? frag_load(qrow + 32 * st + 8 * qq) : frag_zero<F>();
+  }
+
+  // Chunk schedule: split sp has nkc(sp) = 4 chunks of 64 keys (the last
+  // split: enough for maxkeys), K chunks then V chunks.
+  const int nsplit = maxkeys > 0 ? (maxkeys + kSplit - 1) / kSplit : 0;
+  const int last_keys = nsplit > 0 ? maxkeys - (nsplit - 1) * kSplit : 0;
+  const int nkc_last = (last_keys + CH - 1) / CH;
+  const int nchunks = nsplit > 0 ? 8 * (nsplit - 1) + 2 * nkc_last : 0;
+  auto issue = [&](int c) {
+    if (c >= nchunks) return;
+    int sp, kind, kc;
+    if (c < 8 * (nsplit - 1)) {
+      sp = c / 8; kind = (c % 8) / 4; kc = c % 4;
+    } else {
+      const int cl = c - 8 * (nsplit - 1);
+      sp = nsplit - 1; kind = cl / nkc_last; kc = cl % nkc_last;
+    }
+    const int key0 = sp * kSplit + kc * CH;
+    const T* rows = (kind ? vb : kb) + (int64_t)key0 * (kind ? a.v_sl : a.k_sl);
+    char* buf = ring + (c % NBUF) * CHB;
+#pragma unroll
+    for (int i = 0; i < CPW; ++i)
+      KV::copy(buf, wave * CPW + i, rows, kind ? a.v_sl : a.k_sl, len - key0, lane);
+  };
+  auto open_chunk = [&](int c) {
+    if (c + 1 < nchunks) stage_barrier<CPW>();  // chunk c landed; c + 1 may be in flight
+    else stage_barrier<0>();
+    issue(c + 2);                               // every wave is past chunk c - 1: its buffer is free
+  };
+
+  float M[4], Lsum[4];
+  f32x4 A[NDT];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    M[i] = -INFINITY;
+    Lsum[i] = 0.0f;
+  }
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) A[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  issue(0);
+  issue(1);
+  int ci = 0;
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const int j0 = sp * kSplit;
+    const int nkc = sp + 1 < nsplit ? 4 : nkc_last;
+    // Scores of the wave's 16 rows against the split's keys (tile t: keys j0 + 16 t + ...).
+    float s[16][4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      if (kc < nkc) {
+        open_chunk(ci);
+        const char* buf = ring + (ci % NBUF) * CHB;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int st = 0; st < D / 32; ++st) acc = mfma_step(KV::kfrag(buf, 16 * t + r, st, qq), qf[st], acc);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = j0 + 64 * kc + 16 * t + 4 * qq + i;
+            s[4 * kc + t][i] = key < my_nkeys ? acc[i] * a.scale_log2 : -INFINITY;
+          }
+        }
+        ++ci;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s[4 * kc + t][i] = -INFINITY;
+      }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = fmaxf(m, s[t][i]);
+    m = fmaxf(m, __shfl_xor(m, 16, kWave));
+    m = fmaxf(m, __shfl_xor(m, 32, kWave));
+#pragma unroll
+    for (int t = 0; t < 16; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[t][i] = split_weight(s[t][i], m, j0 + 16 * t + 4 * qq + i < my_nkeys);
+
+    // P.V and the weight sum over the split's V chunks.
+    f32x4 acc[NDT];
+    f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      if (kc < nkc) {
+        open_chunk(ci);
+        const char* buf = ring + (ci % NBUF) * CHB;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int t0 = 4 * kc + 2 * h;
+          float p8[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            p8[e] = s[t0][e];
+            p8[4 + e] = s[t0 + 1][e];
+          }
+          const PFrag<T> pf = make_pfrag<T>(p8);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) acc[dt] = pv_step<T>(pf, KV::vfrag(buf, 32 * h, dt, lane), acc[dt]);
+          lsum = pv_step<T>(pf, ones_frag<T>(), lsum);
+        }
+        ++ci;
+      }
+    }
+    // Merge into the running state (accumulator layout: rows 4 qq + i).
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float mi = __shfl(m, 4 * qq + i, kWave);
+      if (acc_nkeys[i] > j0) {
+        float ai[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) ai[dt] = A[dt][i];
+        float acci[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acci[dt] = acc[dt][i];
+        merge_split<NDT>(M[i], Lsum[i], ai, mi, lsum[i], acci);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) A[dt][i] = ai[dt];
+      }
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pair = 64 * wg + 16 * wave + 4 * qq + i;
+    if (pair >= npairs) continue;
+    T* o = static_cast<T*>(a.out) +
+           ((((int64_t)b * a.Hq + hk * G + pair % G) * a.Tq) + pair / G) * D + r;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[16 * dt] = to_store<T>(A[dt][i] / Lsum[i]);
+  }
+}
+
+}  // namespace bi
