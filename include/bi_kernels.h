@@ -120,7 +120,7 @@ int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* k
  * keys [0, len_b - Tq + t + 1) (bottom-right aligned, so a later chunk of a
  * prompt run against the whole cache is a valid prefill); otherwise all len_b.
  * len_b = kv_lens[b] (device int32[B], may be NULL = L), Tq <= len_b <= L when
- * causal. Same split order and per-key update as bi_attn_decode, so a token's
+ * causal. Same split order and per-split arithmetic as bi_attn_decode, so a token's
  * output equals a later decode step's and chunked equals one-shot prefill.
  * Replaces: kernels/attention.py:368-390 (batch_invariant_prefill_attention),
  * kernels :173-254. */

@@ -1,6 +1,6 @@
 // bi_attn_common.h — the per-split arithmetic of batch-invariant attention,
 // shared verbatim by the decode kernel, the decode combine kernel and the
-// prefill kernel (the reference keeps its per-key update and split merge as
+// prefill kernel (the reference keeps its in-split update and split merge as
 // one source text used by both of its kernels for the same reason:
 // kernels/attention.py:44-85, `_KEY_UPDATE` and `_MERGE`).
 //

@@ -6,8 +6,10 @@
 // -ffp-contract=off and no fast-math flag):
 //   * every fused multiply-add is written as an explicit __builtin_fmaf;
 //   * fp32 division and sqrtf are IEEE correctly rounded (hipcc's default
-//     -fhip-fp32-correctly-rounded-divide-sqrt), expf is the device library's
-//     full-precision expf, never __expf;
+//     -fhip-fp32-correctly-rounded-divide-sqrt); exp is the device library's
+//     full-precision expf, or, for the attention weights and split merge, the
+//     hardware exp2 (v_exp_f32) on log2-scaled scores — one fixed choice per
+//     quantity, shared by every kernel that computes it;
 //   * fp32 -> bf16 / fp16 conversion rounds to nearest even;
 //   * denormals are kept (no flush-to-zero).
 // This is the HIP counterpart of the reference's `metal::precise::` policy

@@ -7,12 +7,14 @@ the floating-point reduction order of an output element never depends on how man
 * matmul / quantized matmul: fixed 256-wide K groups, one MFMA instruction and one
   k-slot map for every tile shape, group partials folded left to right in fp32;
 * rmsnorm: one workgroup per row, fixed-stride partials, fixed-shape wave/LDS tree;
-* attention: fixed 256-key splits folded in index order, one shared per-key update.
+* attention: fixed 256-key splits folded in index order, one shared per-split
+  sequence (split maximum, exp2 weights, MFMA P.V) for decode and prefill.
 
 Only the launch shape adapts to the batch. Division and sqrt are correctly
-rounded, expf is the full-precision device expf, every fma is explicit and the
-build forbids fp contraction and fast math, so compiler choices cannot make two
-kernels disagree.
+rounded, exp is either the full-precision device expf or the hardware exp2
+(attention), always the same one for a given quantity, every fma is explicit and
+the build forbids fp contraction and fast math, so compiler choices cannot make
+two kernels disagree.
 """
 
 from .matmul import batch_invariant_matmul

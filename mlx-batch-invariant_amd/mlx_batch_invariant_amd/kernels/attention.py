@@ -5,18 +5,24 @@ mlx_batch_invariant/kernels/attention.py:1-32):
 
 * keys are processed in fixed splits of ``SPLIT_SIZE`` = 256 in index order;
   key ``j`` always lands in split ``j // 256`` at the same position;
-* the score is ``fp32(dot(q, k_j) * scale)`` with the dot taken by a fixed
-  chain of ``v_mfma_f32_16x16x32`` steps over the head dimension;
-* inside a split the online softmax runs key by key:
-  ``m' = max(m, s); corr = exp(m - m'); p = exp(s - m'); l = fma(l, corr, p);
-  acc = fma(acc, corr, p * v)`` from exact zeros;
-* splits are merged left to right with ``c_old = exp(M - M'); c_new = exp(m - M');
+* the score is ``fp32(dot(k_j, q) * scale * log2(e))`` with the dot taken by a
+  fixed chain of ``v_mfma_f32_16x16x32`` steps over the head dimension;
+* inside a split: the maximum ``m`` of the active scores, the weights
+  ``p = exp2(s - m)`` (exactly 0 for masked keys), and ``acc = P.V``,
+  ``l = P.1`` as fixed MFMA chains over the split's 32-key steps (for 16-bit
+  types ``P`` enters as a high and a low part, 16 / 22 significant bits);
+* splits are merged left to right with ``c_old = exp2(M - M'); c_new = exp2(m - M');
   L = fma(L, c_old, l * c_new); A = fma(A, c_old, acc * c_new)``, and the
   output is ``T(A / L)``.
 
+The reference runs the softmax key by key inside a split; this is the same
+quantity in an order whose products all run on the matrix cores (the
+reference's own matrix-unit variant, kernels/attention_mma.py, also
+reorders). Values agree with the reference order to fp32 rounding.
+
 Decode (T_q == 1) writes per-split partials and folds them in a combine
-kernel; prefill folds in registers. Both kernels include the same per-key
-update and merge source, so a token's output from prefill equals the output
+kernel; prefill folds in registers. Both kernels run the same per-split
+sequence and merge source, so a token's output from prefill equals the output
 of a later decode step for that position, and chunked prefill equals one-shot
 prefill. Causal masking is bottom-right aligned (query t of a T_q-token chunk
 sees ``len - T_q + t + 1`` keys), as in MLX.

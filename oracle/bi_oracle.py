@@ -27,10 +27,13 @@ Pinning (how each function is checked, tests/test_oracle.py):
 
 Parity of the hardware MFMA's internal summation is modelled, not pinned:
 ``matmul`` and the attention scores assume each 32-wide MFMA step adds the
-exact sum of its products to the accumulator with one fp32 rounding. The GPU
-tests therefore compare matmul/attention at a stated tolerance (1 ulp of the
-output type plus an fp32 accumulation bound), and bit-exactly only where the
-arithmetic is exactly specified (RMSNorm, dequantization, integer KATs).
+exact sum of its products to the accumulator with one fp32 rounding. ``attention``
+follows the reference's key-by-key softmax recurrence; the gfx950 kernels take
+the split maximum first and run P.V on the matrix cores (the same quantity in
+another order). The GPU tests therefore compare matmul/attention at a stated
+tolerance (1 ulp of the output type plus an fp32 accumulation bound), and
+bit-exactly only where the arithmetic is exactly specified (RMSNorm,
+dequantization, integer KATs).
 """
 
 from __future__ import annotations
