@@ -26,6 +26,7 @@
 
 #include "bi_gemm_big.h"
 #include "bi_gemv_stream.h"
+#include "bi_gemm_mid.h"
 #include "bi_gemm_tile.h"
 
 namespace bi {
@@ -685,11 +686,40 @@ static void launch_wg(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, 
   else gemv_wg<T, BSrc, 2, W, 2, false><<<grid, kWave * W, part_bytes, st>>>(a, lda, bsrc, out, M, N, K, G);
 }
 
+// Mid-M launch (bi_gemm_mid.h): quantized B with 4 < M <= 64, 2-byte T,
+// whole groups, and enough 64-column blocks to fill the chip.
+template <typename T, class BSrc>
+static bool use_mid(int M, int N, int K, int64_t lda, const T* a) {
+  if constexpr (sizeof(T) != 2 || !BSrc::kMeta) {
+    return false;
+  } else {
+    return M > 4 && M <= 64 && K % kGroupK == 0 && lda % 8 == 0 && bi_host::aligned16(a) &&
+           ceil_div(N, 64) >= 128;
+  }
+}
+
+template <typename T, class BSrc>
+static void launch_mid(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K, int G,
+                       hipStream_t st) {
+  if constexpr (sizeof(T) == 2 && BSrc::kMeta) {
+    constexpr int PD = 8;
+    const int mt = ceil_div(M, 16);
+    dim3 grid(ceil_div(N, 64), 1, 1);
+    if (mt <= 1) gemm_mid<T, BSrc, 1, PD><<<grid, 256, 0, st>>>(a, lda, bsrc, out, M, N, K, G);
+    else if (mt <= 2) gemm_mid<T, BSrc, 2, PD><<<grid, 256, 0, st>>>(a, lda, bsrc, out, M, N, K, G);
+    else gemm_mid<T, BSrc, 4, PD><<<grid, 256, 0, st>>>(a, lda, bsrc, out, M, N, K, G);
+  }
+}
+
 template <typename T, class BSrc>
 static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K,
                     float* ws, hipStream_t st, const char* what) {
   const int G = ceil_div(K, kGroupK);
   constexpr int WAVES = 4;
+  if (use_mid<T, BSrc>(M, N, K, lda, a)) {
+    launch_mid<T, BSrc>(a, lda, bsrc, out, M, N, K, G, st);
+    return bi_host::launch_status(what);
+  }
   if (M <= kSplitMMax && use_wg(M, G)) {
     // 4 waves per workgroup when there are enough column tiles for every
     // workgroup to be resident at once (4 per CU at <= 128 VGPRs), so the whole

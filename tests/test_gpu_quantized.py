@@ -85,6 +85,32 @@ def test_quantized_launch_shapes_agree(bits_, gs):
         assert bits(got) == bits(full[:M]), M
 
 
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (4, 128), (8, 32)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_quantized_mid_m_launch_matches_oracle(bits_, gs, dt):
+    """4 < M <= 128 with >= 128 blocks of 64 columns takes the mid-M launch
+    (A staged per 256-k group in LDS, B straight to registers): rows of every
+    M-tile count equal the oracle within the stated bound and equal the same
+    rows computed alone (M = 1, the GEMV launch), bit for bit."""
+    N, K = 8200, 768          # 129 column blocks, the last one partial
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 7 + gs)
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    x = randn((128, K), DT[dt], gen(11))
+    run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+    W = ora.dequantize(wq.cpu().view(torch.int32).numpy().view(np.uint32), to_np(s.cpu()), to_np(b.cpu()),
+                       gs, bits_, dt)
+    cols = np.r_[0:40, N - 40:N]
+    for M in (5, 17, 33, 64, 100, 128):
+        got = run(x[:M])
+        rows = sorted({0, M // 2, M - 1})
+        want = ora.matmul(to_np(x[rows]), W[cols], dt, kmap="blocked")
+        g = to_np(got)[rows][:, cols]
+        atol = ora.matmul_error_bound(to_np(x[rows]), W[cols])
+        assert ora.max_ulp_excess(g, want, dt, atol=atol) <= 1.0, (M, ora.isclose_report(g, want))
+        for rr in rows:
+            assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
+
+
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
 def test_quantized_batch_invariant_llama_mlp(bits_, gs):
     """W [14336, 4096], x [M, 4096], M in 1..64 (and beyond)."""
