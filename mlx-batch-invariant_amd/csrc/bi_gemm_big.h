@@ -42,6 +42,10 @@ constexpr int kBigStage = kBigRows * 64;                       // elements (48 K
 constexpr int kBigBufs = 3;
 constexpr int kBigCopiesPerWave = kBigRows / 8 / kBigWaves;    // 6
 constexpr int kBigGroupM = 4;
+// The large tile is taken from M = 256 with at least this many tiles (fewer
+// tiles than CUs still beat the smaller LDS tiles at these shapes).
+constexpr int kBigMinM = 256;
+constexpr int kBigMinTiles = 96;
 
 template <typename T>
 __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__ a, int64_t lda,

@@ -39,8 +39,18 @@ extern "C" size_t bi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return split_ws_bytes(M, N, K);
 }
 
-extern "C" size_t bi_quantized_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+// Quantized: the small-M split partials, or for large M (2-byte types) the
+// dequantized weight and the reordered activations of the large-tile launch.
+// The query has no dtype: it reports the larger need, which an fp32 call may
+// also pass.
+static size_t quant_ws_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (bi::qmm_use_big(M, N, K, 2)) return bi::qmm_big_ws_bytes(M, N, K);
   return split_ws_bytes(M, N, K);
+}
+
+extern "C" size_t bi_quantized_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return quant_ws_bytes(M, N, K);
 }
 
 extern "C" int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out,
@@ -99,6 +109,12 @@ extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w
   if (ldx % 8 || ldx < K || !aligned16(x) || !aligned16(w))
     return fail(BI_E_INVALID_ARG,
                 "bi_quantized_matmul: needs ldx %% 8 == 0, ldx >= K, 16-byte aligned x and w");
+  if (dtype != BI_F32 && bi::qmm_use_big(M, N, K, 2)) {
+    const size_t need = bi::qmm_big_ws_bytes(M, N, K);
+    if (!ws || ws_bytes < need || !aligned16(ws))
+      return fail(BI_E_WORKSPACE, "bi_quantized_matmul: 16-byte aligned workspace of %zu bytes required, got %zu",
+                  need, ws ? ws_bytes : (size_t)0);
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
   switch (dtype) {

@@ -27,6 +27,7 @@
 #include "bi_gemm_big.h"
 #include "bi_gemv_stream.h"
 #include "bi_gemm_mid.h"
+#include "bi_qmm_big.h"
 #include "bi_gemm_tile.h"
 
 namespace bi {
@@ -747,7 +748,7 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   // M > 32: LDS-tiled; the largest tile that still gives the chip >= 256 tiles.
   auto tiles = [&](int bm, int bn) { return (int64_t)ceil_div(M, bm) * ceil_div(N, bn); };
   if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
-    if (K % kGroupK == 0 && tiles(kBigBM, kBigBN) >= 256) {
+    if (K % kGroupK == 0 && M >= kBigMinM && tiles(kBigBM, kBigBN) >= kBigMinTiles) {
       const int tmm = ceil_div(M, kBigBM), tn = ceil_div(N, kBigBN);
       const int grid = ((tmm * tn + 7) / 8) * 8;
       gemm_big<T><<<grid, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K, tmm, tn);
@@ -768,6 +769,22 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
 template <typename T, int BITS, int GS>
 int run_quant(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
               const void* biases, void* out, int M, int N, int K, void* ws, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    if (bi::qmm_use_big(M, N, K, 2)) {
+      // Large M (bi_qmm_big.h): B dequantized and A copied, both in the dense
+      // tile's k order, into the caller's workspace; then the dense tile.
+      T* bq = static_cast<T*>(ws);
+      T* ap = bq + (size_t)N * K;
+      const int64_t nb = (int64_t)N * (K / 8), na = (int64_t)M * (K / 8);
+      bi::qmm_dequant_rows<T, BITS, GS><<<(unsigned)((nb + 255) / 256), 256, 0, st>>>(
+          w, static_cast<const T*>(scales), static_cast<const T*>(biases), bq, N, K);
+      bi::qmm_permute_a<T><<<(unsigned)((na + 255) / 256), 256, 0, st>>>(static_cast<const T*>(x), ldx, ap, M, K);
+      const int tmm = ceil_div(M, bi::kBigBM), tn = ceil_div(N, bi::kBigBN);
+      const int grid = ((tmm * tn + 7) / 8) * 8;
+      bi::gemm_big<T><<<grid, 64 * bi::kBigWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), M, N, K, tmm, tn);
+      return bi_host::launch_status("bi_quantized_matmul");
+    }
+  }
   bi::QuantB<T, BITS, GS> b;
   b.w = w;
   b.scales = static_cast<const T*>(scales);

@@ -38,6 +38,14 @@ def test_workspace_sizes():
     assert lib.bi_matmul_workspace_bytes(33, 100, 896) == 0          # fused (LDS tiles)
     assert lib.bi_matmul_workspace_bytes(8, 100, 256) == 0           # one group
     assert lib.bi_quantized_matmul_workspace_bytes(4, 14336, 4096) == 0
+    # large M: dequantized weight + reordered activations, 2 bytes each
+    assert lib.bi_quantized_matmul_workspace_bytes(800, 14336, 1024) == (14336 + 800) * 1024 * 2
+    assert lib.bi_quantized_matmul_workspace_bytes(2048, 4096, 4096) == (4096 + 2048) * 4096 * 2
+    assert lib.bi_quantized_matmul_workspace_bytes(300, 14336, 4096) == (14336 + 300) * 4096 * 2
+    # below the large-tile threshold (M < 256, or < 96 tiles of 256 x 128) or K not whole groups: none
+    assert lib.bi_quantized_matmul_workspace_bytes(200, 14336, 4096) == 0
+    assert lib.bi_quantized_matmul_workspace_bytes(300, 4096, 4096) == 0
+    assert lib.bi_quantized_matmul_workspace_bytes(2048, 4096, 4000) == 0
     ns = (8192 + 255) // 256
     bh = 256 * 32 * ns
     assert lib.bi_attn_decode_workspace_bytes(256, 32, 8192, 128) == (2 * ((bh + 3) // 4 * 4) + bh * 128) * 4

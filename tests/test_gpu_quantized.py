@@ -111,6 +111,33 @@ def test_quantized_mid_m_launch_matches_oracle(bits_, gs, dt):
             assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
 
 
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_quantized_large_m_launch_agrees(bits_, gs, dt):
+    """Large M takes the dequantize-once launch (weights dequantized into the
+    workspace in the dense tile's k order, then the large dense tile): its rows
+    equal the same rows computed alone (M = 1, the GEMV launch) bit for bit,
+    and the oracle within the stated bound."""
+    N, K, M = 14336, 1024, 800             # 4 x 112 tiles of 256 x 128
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ + gs + 5)
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    from mlx_batch_invariant_amd import _lib
+    assert _lib.load().bi_quantized_matmul_workspace_bytes(M, N, K) == (N + M) * K * 2
+    x = randn((M, K), DT[dt], gen(21))
+    run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+    full = run(x)
+    rows = [0, 257, M - 1]
+    for rr in rows:
+        assert bits(full[rr:rr + 1]) == bits(run(x[rr:rr + 1])), rr
+    W = ora.dequantize(wq.cpu().view(torch.int32).numpy().view(np.uint32), to_np(s.cpu()), to_np(b.cpu()),
+                       gs, bits_, dt)
+    cols = np.r_[0:32, 7000:7032, N - 32:N]
+    want = ora.matmul(to_np(x[rows]), W[cols], dt, kmap="blocked")
+    got = to_np(full)[rows][:, cols]
+    atol = ora.matmul_error_bound(to_np(x[rows]), W[cols])
+    assert ora.max_ulp_excess(got, want, dt, atol=atol) <= 1.0, ora.isclose_report(got, want)
+
+
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
 def test_quantized_batch_invariant_llama_mlp(bits_, gs):
     """W [14336, 4096], x [M, 4096], M in 1..64 (and beyond)."""
