@@ -104,6 +104,15 @@ def qmm_bytes(M, N, K, bits, gs):
     return N * K * bits // 8 + 2 * 2 * N * (K // gs) + 2 * M * K + 2 * M * N
 
 
+# The kernel the M = 1 call launches (bi_quantized_matmul's policy for K = 4096,
+# bf16 x, N / 16 >= 512): the barrier-free stream GEMV, in the instance the
+# group count and scale-slice alignment select.
+HEADLINE_KERNEL = {
+    (4, 64): "gemv_stream<bf16,4,64,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)",
+    (8, 128): "gemv_stream<bf16,8,128,W=4,NB=4,MR=1,PD=2> (bi_quantized_matmul, M <= 4: one launch)",
+}
+
+
 def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     import torch
     import mlx_batch_invariant_amd as bi
@@ -170,7 +179,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
                      "traffic_source": None if traffic is None else
                      "rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch x copy-kernel scale (bytes per launch)",
-                     "algorithmic_bytes": by1, "kernel": "gemv_stream<bf16,4,64,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)"},
+                     "algorithmic_bytes": by1, "kernel": HEADLINE_KERNEL[(bits, gs)]},
         "per_m": table,
         "bitwise_invariant_M1_vs_all": inv,
         "stock_gpu": {"dequant_plus_matmul_us": None if stock_deq is None else round(stock_deq * 1e6, 2),
@@ -233,6 +242,32 @@ def bench_linear(args):
     return {"metric": METRIC, "op": "rmsnorm+linear (config 1)", "per_m": out}
 
 
+def bench_rmsnorm(args):
+    """RMSNorm alone: the config-1 rows (D = 896, M = 1..256, launch-bound) and
+    two HBM-bound shapes (D = 4096, 16384 / 65536 rows; inputs 128 / 512 MiB,
+    so the 256 MB Infinity Cache cannot hold input and output)."""
+    import torch
+    import mlx_batch_invariant_amd as bi
+    g = torch.Generator().manual_seed(0)
+    shapes = [] if args.headline_only else [(M, 896) for M in (1, 4, 16, 64, 256)]
+    shapes += [(16384, 4096), (65536, 4096)]
+    res = {}
+    for R, D in shapes:
+        x = torch.randn((R, D), generator=g).to(torch.bfloat16).cuda()
+        gam = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+        t = statistics.median(_time_calls(lambda i: bi.batch_invariant_rms_norm(x, gam, 1e-6), args.steps, args.warmup, 1))
+        by = 4 * R * D + 2 * D
+        e = {"us": round(t * 1e6, 2), "GBps": round(by / t / 1e9, 1), "frac_hbm": round(by / t / PEAK_HBM, 4)}
+        if not args.headline_only:
+            ts = statistics.median(_time_calls(lambda i: torch.nn.functional.rms_norm(x, (D,), gam, 1e-6),
+                                               args.steps, args.warmup, 1))
+            e["stock_us"] = round(ts * 1e6, 2)
+        res[f"{R}x{D}"] = e
+        del x
+    return {"metric": METRIC, "op": "rms_norm (bf16, eps 1e-6)", "kernel": "rms_norm_kernel",
+            "algorithmic_bytes": "4*R*D + 2*D (read x, write out, read gamma)", "per_shape": res}
+
+
 def bench_decode(args):
     """split-KV decode, GQA 32/8, D 128, ragged lengths."""
     import numpy as np
@@ -240,7 +275,7 @@ def bench_decode(args):
     import mlx_batch_invariant_amd as bi
     g = torch.Generator().manual_seed(0)
     res = {}
-    for B in (1, 16, 64, 256):
+    for B in ((256,) if args.headline_only else (1, 16, 64, 256)):
         rng = np.random.default_rng(B)
         lens = rng.integers(1, 8193, size=B)
         L = 8192
@@ -264,17 +299,18 @@ def bench_prefill(args):
     g = torch.Generator().manual_seed(0)
     res = {}
     T = 2048
-    for B in (1, 4, 16):
+    for B in ((16,) if args.headline_only else (1, 4, 16)):
         q = torch.randn((B, 32, T, 128), generator=g).to(torch.bfloat16).cuda()
         k = torch.randn((B, 8, T, 128), generator=g).to(torch.bfloat16).cuda()
         v = torch.randn((B, 8, T, 128), generator=g).to(torch.bfloat16).cuda()
         t = statistics.median(_time_calls(lambda i: bi.batch_invariant_prefill_attention(
             q, k, v, scale=128 ** -0.5, causal=True), max(3, args.steps // 4), 2, 1))
-        ts = statistics.median(_time_calls(lambda i: torch.nn.functional.scaled_dot_product_attention(
-            q, k, v, is_causal=True, enable_gqa=True), max(3, args.steps // 4), 2, 1))
+        ts = None if args.headline_only else statistics.median(_time_calls(
+            lambda i: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True),
+            max(3, args.steps // 4), 2, 1))
         fl = 4 * B * 32 * 128 * T * (T + 1) / 2
         res[B] = {"ms": round(t * 1e3, 3), "TFLOPs": round(fl / t / 1e12, 1), "frac_mfma": round(fl / t / PEAK_BF16, 4),
-                  "stock_sdpa_ms": round(ts * 1e3, 3)}
+                  "stock_sdpa_ms": None if ts is None else round(ts * 1e3, 3)}
     return {"metric": METRIC, "op": "prefill attention (config 4)", "per_b": res}
 
 
@@ -286,13 +322,15 @@ def bench_gemm(args):
     N, K = 14336, 4096
     W = (0.02 * torch.randn((N, K), generator=g)).to(torch.bfloat16).cuda()
     res = {}
-    for M in (256, 4096):
+    for M in ((4096,) if args.headline_only else (256, 4096)):
         x = torch.randn((M, K), generator=g).to(torch.bfloat16).cuda()
         t = statistics.median(_time_calls(lambda i: bi.batch_invariant_matmul(x, W.t()), max(3, args.steps // 2), 2, 1))
-        ts = statistics.median(_time_calls(lambda i: torch.matmul(x, W.t()), max(3, args.steps // 2), 2, 1))
+        ts = None if args.headline_only else statistics.median(
+            _time_calls(lambda i: torch.matmul(x, W.t()), max(3, args.steps // 2), 2, 1))
         fl = 2 * M * N * K
         res[M] = {"ms": round(t * 1e3, 3), "TFLOPs": round(fl / t / 1e12, 1), "frac_mfma": round(fl / t / PEAK_BF16, 4),
-                  "stock_ms": round(ts * 1e3, 3), "stock_TFLOPs": round(fl / ts / 1e12, 1)}
+                  "stock_ms": None if ts is None else round(ts * 1e3, 3),
+                  "stock_TFLOPs": None if ts is None else round(fl / ts / 1e12, 1)}
     return {"metric": METRIC, "op": "bf16 GEMM (large M)", "per_m": res}
 
 
@@ -390,7 +428,8 @@ def main(argv=None) -> int:
     p.add_argument("--llama-steps", type=int, default=128)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--headline-only", action="store_true",
-                   help="qmm: time only the M=1 headline (no M sweep, eager or stock legs); for profiling")
+                   help="time only each op's headline shape (qmm M=1, rmsnorm D=4096, decode B=256, "
+                        "prefill B=16, gemm M=4096) without sweeps or stock legs; for profiling")
     a = p.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every kernel here is single-GPU and no multi-GPU "
@@ -402,14 +441,16 @@ def main(argv=None) -> int:
         return 2
     import mlx_batch_invariant_amd as bi
     bi._lib.load()
-    ops = ["qmm4", "qmm8", "linear", "decode", "prefill", "gemm"] if a.op == "all" else [a.op]
+    ops = ["qmm4", "qmm8", "linear", "rmsnorm", "decode", "prefill", "gemm"] if a.op == "all" else [a.op]
     for op in ops:
         if op == "qmm4":
             r = bench_qmm(a, 4, 64)
         elif op == "qmm8":
             r = bench_qmm(a, 8, 128)
-        elif op in ("linear", "rmsnorm"):
+        elif op == "linear":
             r = bench_linear(a)
+        elif op == "rmsnorm":
+            r = bench_rmsnorm(a)
         elif op == "decode":
             r = bench_decode(a)
         elif op == "prefill":
