@@ -1,34 +1,51 @@
 // bi_gemm_big.h — the large-M dense tile: 256 x 128 outputs per workgroup of
-// 8 waves, operands copied global -> LDS by the load unit
-// (global_load_lds_dwordx4, no VGPR staging), three stage buffers.
+// 8 waves (4 x 2, 64 x 64 outputs each, two waves per SIMD), operands copied
+// global -> LDS by the load unit (buffer_load ... lds, no VGPR staging).
 //
 // Same arithmetic as every other matmul launch (bi_gemm_tile.h, dense k-slot
 // map k = 256 g + 32 s + 8 q + e): per 256-k group eight MFMA steps from zero,
-// then total = total + acc. Only the staging differs.
+// then total = total + acc. Only the staging and the instruction order differ.
 //
-// Stage = 64 k of 256 A rows and 128 B rows (48 KB). In LDS each of the 384
-// rows is 128 bytes (8 chunks of 8 elements) with chunk c of row r stored in
-// slot c ^ (r & 7). One copy instruction moves 8 whole rows: lane l fetches
-// row 8b + l/8, chunk (l % 8) ^ (l / 8), and lands at 16 l, which is exactly
-// that chunk's swizzled slot. Each row is thus read as one full 128-byte line
-// (16 rows x 64 bytes per instruction measured half the L2 throughput), and
-// the MFMA fragment reads (lane 16 q + r: row r, chunk 4 s + q) hit 8
-// distinct slots in every 8-lane group: no LDS bank conflicts.
+// Stage = 64 k (two MFMA steps) of 256 A rows and 128 B rows. Each row is 128
+// bytes in LDS (8 chunks of 8 elements) with chunk c of row r stored in slot
+// c ^ (r & 7). One copy instruction moves 8 whole rows: lane l fetches row
+// l / 8, chunk (l % 8) ^ (l / 8), and lands at 16 l, which is exactly that
+// chunk's swizzled slot. Rows are read as whole 128-byte lines, and the MFMA
+// fragment reads (lane 16 q + r: row r, chunk 4 s + q) hit 8 distinct slots
+// in every 8-lane group: no LDS bank conflicts.
 //
-// Wave roles: 8 waves in 4 x 2, each 64 x 64 outputs (4 x 4 MFMA tiles; fp32
-// acc + total = 128 registers, so two waves share a SIMD). Wave w copies rows
-// 48 w .. 48 w + 47 of each stage (6 instructions). Stage st + 2 is requested
-// right after the barrier that opens stage st, so copies have two stages of
-// MFMA work to land.
+// Copies go through buffer resources whose range ends at the last valid row
+// of the tile: rows past M (N) read as zero without touching memory, so no
+// address is clamped. Past the last stage the copies use an empty resource
+// (no memory traffic), which keeps the stage loop free of branches.
+//
+// Rings: A in 3 stage buffers (3 x 32 KB), B in 4 (4 x 16 KB) = 160 KB. Each
+// stage has one mid-stage barrier, between its two MFMA steps:
+//   step (st, 0): MFMAs on fragments already in registers; the fragment
+//                 reads of step (st, 1); the B copies of stage st + 3 (B buffer
+//                 (st + 3) % 4 was last read before the previous barrier);
+//   barrier:      this wave's copies of stage st + 1 have landed and its reads
+//                 of stage st are done, then every wave's;
+//   step (st, 1): MFMAs; the reads of step (st + 1, 0); the A copies of stage
+//                 st + 3 (A buffer st % 3, free since the barrier).
+// Copies and fragment reads are spread one per MFMA pair with hard scheduling
+// fences, so the load unit, the LDS and the matrix core work side by side
+// instead of in bursts. An A fragment is re-read for the next step right
+// after its last MFMA of the current step (single-buffered); B fragments are
+// double-buffered.
+//
+// The group fold (total += acc, one VALU add per accumulator) is spread over
+// the last step of a group (tiles already final) and the first step of the
+// next (each tile just before its first MFMA overwrites acc).
 //
 // Tile order: workgroup ids are dealt round-robin to the 8 XCDs; each XCD
 // takes a contiguous run of tile indices, and the run walks groups of 4 tile
-// rows column by column, so the ~32 tiles an XCD runs at once share 4 rows of
-// A and 8 columns of B in its L2.
+// rows column by column, so the tiles an XCD runs at once share 4 rows of A
+// and 8 columns of B in its L2.
 //
 // Requirements (checked by the host policy): 2-byte T, K % 256 == 0, rows of
-// A and B 16-byte aligned (lda, ldb % 8 == 0). Rows past M / columns past N
-// are clamped to the last valid one (never stored).
+// A and B 16-byte aligned (lda, ldb % 8 == 0), lda, ldb < 2^22 (a tile's
+// rows are addressed with 32-bit byte offsets).
 #pragma once
 
 #include "bi_gemm_tile.h"
@@ -36,16 +53,29 @@
 namespace bi {
 
 constexpr int kBigBM = 256, kBigBN = 128;
-constexpr int kBigWaves = 8;
-constexpr int kBigRows = kBigBM + kBigBN;                      // 384 rows per stage
-constexpr int kBigStage = kBigRows * 64;                       // elements (48 KB)
-constexpr int kBigBufs = 3;
-constexpr int kBigCopiesPerWave = kBigRows / 8 / kBigWaves;    // 6
+constexpr int kBigWavesM = 4, kBigWavesN = 2, kBigWaves = kBigWavesM * kBigWavesN;
+constexpr int kBigTI = kBigBM / 16 / kBigWavesM;            // 4 row blocks of 16 per wave
+constexpr int kBigTJ = kBigBN / 16 / kBigWavesN;            // 4 column blocks of 16 per wave
+constexpr int kBigACopies = kBigBM / 8 / kBigWaves;         // 4 copy instructions per wave per stage
+constexpr int kBigBCopies = kBigBN / 8 / kBigWaves;         // 2
+constexpr int kBigAStage = kBigBM * 64, kBigBStage = kBigBN * 64;  // elements per stage buffer
+constexpr int kBigABufs = 3, kBigBBufs = 4;
 constexpr int kBigGroupM = 4;
+constexpr int64_t kBigMaxLd = (int64_t)1 << 22;
 // The large tile is taken from M = 256 with at least this many tiles (fewer
 // tiles than CUs still beat the smaller LDS tiles at these shapes).
 constexpr int kBigMinM = 256;
 constexpr int kBigMinTiles = 96;
+
+// s_waitcnt vmcnt(N) lgkmcnt(0); the empty asm statements keep the compiler
+// from moving memory accesses across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+  asm volatile("" ::: "memory");
+}
 
 template <typename T>
 __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__ a, int64_t lda,
@@ -54,7 +84,8 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
                                                            int tiles_m, int tiles_n) {
   static_assert(sizeof(T) == 2, "gemm_big: 2-byte element types only");
   typedef typename Frag<T>::type F;
-  __shared__ __attribute__((aligned(1024))) T lds[kBigBufs * kBigStage];
+  constexpr int TI = kBigTI, TJ = kBigTJ, NT = TI * TJ, NCH = NT / 2;
+  __shared__ __attribute__((aligned(1024))) T lds[kBigABufs * kBigAStage + kBigBBufs * kBigBStage];
 
   const int tiles_total = tiles_m * tiles_n;
   const int bid = blockIdx.x;
@@ -70,77 +101,124 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int r = lane % 16, q = lane / 16;
-  const int wm = wave / 2, wn = wave % 2;
+  const int wm = wave / kBigWavesN, wn = wave % kBigWavesN;
 
-  // Copy sources: instruction c of this wave moves stage rows 8 b .. 8 b + 7,
-  // b = 6 wave + c (rows 0..255 are A, 256..383 are B).
-  const T* src[kBigCopiesPerWave];
-  {
-    const int rr = lane / 8, ch = (lane % 8) ^ rr;
-#pragma unroll
-    for (int c = 0; c < kBigCopiesPerWave; ++c) {
-      const int row = 8 * (wave * kBigCopiesPerWave + c) + rr;
-      src[c] = row < kBigBM ? a + (int64_t)min(m0 + row, M - 1) * lda + 8 * ch
-                            : bt + (int64_t)min(n0 + row - kBigBM, N - 1) * ldb + 8 * ch;
-    }
-  }
-  auto issue = [&](int st) {
-    T* buf = lds + (st % kBigBufs) * kBigStage + wave * kBigCopiesPerWave * 512;
-#pragma unroll
-    for (int c = 0; c < kBigCopiesPerWave; ++c) copy_to_lds16(src[c] + 64 * st, buf + c * 512);
+  // LDS element offset of row `row` of stage st (A rows 0..255, B rows 0..127).
+  auto a_row = [&](int st, int row) { return (st % kBigABufs) * kBigAStage + row * 64; };
+  auto b_row = [&](int st, int row) { return kBigABufs * kBigAStage + (st % kBigBBufs) * kBigBStage + row * 64; };
+
+  // Copy c of this wave moves the 8-row block c * 8 + wave of A (or of B):
+  // lane l takes row l / 8 of the block, chunk (l % 8) ^ (l / 8).
+  const int rr = lane / 8, ch = (lane % 8) ^ rr;
+  const int rows_a = min(M - m0, kBigBM), rows_b = min(N - n0, kBigBN);
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a + (int64_t)m0 * lda), (short)0, (int)(rows_a * lda * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(bt + (int64_t)n0 * ldb), (short)0, (int)(rows_b * ldb * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t r_none = __builtin_amdgcn_make_buffer_rsrc((void*)a, (short)0, 0, 0x00020000);
+  const unsigned voa = (unsigned)(((8 * wave + rr) * lda + 8 * ch) * 2);
+  const unsigned vob = (unsigned)(((8 * wave + rr) * ldb + 8 * ch) * 2);
+  auto copy_a = [&](int st, bool real, int c) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(real ? ra : r_none, (lds_void_t*)(lds + a_row(st, 8 * (c * kBigWaves + wave))),
+                                             16, voa + (unsigned)(c * 8 * kBigWaves * lda * 2), st * 128, 0, 0);
+  };
+  auto copy_b = [&](int st, bool real, int c) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(real ? rb : r_none, (lds_void_t*)(lds + b_row(st, 8 * (c * kBigWaves + wave))),
+                                             16, vob + (unsigned)(c * 8 * kBigWaves * ldb * 2), st * 128, 0, 0);
   };
 
-  // Fragment read offsets (elements): row r of a 16-row block, chunk 4 s + q.
+  // Fragment reads: row r of a 16-row block, chunk 4 s + q of step s.
   const int frag_off[2] = {r * 64 + ((q ^ (r & 7)) << 3), r * 64 + (((4 + q) ^ (r & 7)) << 3)};
+  auto read_a = [&](F& f, int st, int s, int i) {
+    f = *reinterpret_cast<const F*>(lds + a_row(st, 16 * TI * wm + 16 * i) + frag_off[s]);
+  };
+  auto read_b = [&](F& f, int st, int s, int j) {
+    f = *reinterpret_cast<const F*>(lds + b_row(st, 16 * TJ * wn + 16 * j) + frag_off[s]);
+  };
 
-  f32x4 total[4][4], acc[4][4];
+  f32x4 total[TI][TJ], acc[TI][TJ];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) total[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TJ; ++j) {
+      total[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};  // the first group's "previous" partial
+    }
+  auto fold = [&](int tt) { total[tt / TJ][tt % TJ] = total[tt / TJ][tt % TJ] + acc[tt / TJ][tt % TJ]; };
+  constexpr int kFoldLast = NCH - 1;  // tiles 0 .. kFoldLast-1 fold during a group's last step
 
   const int nst = K / 64;  // K % 256 == 0: 4 stages per group
-  issue(0);
-  if (nst > 1) issue(1);
+#pragma unroll
+  for (int st = 0; st < 3; ++st) {
+#pragma unroll
+    for (int c = 0; c < kBigACopies; ++c) copy_a(st, true, c);
+#pragma unroll
+    for (int c = 0; c < kBigBCopies; ++c) copy_b(st, true, c);
+  }
+  wait_vm_lgkm0<2 * (kBigACopies + kBigBCopies)>();
+  __builtin_amdgcn_s_barrier();
+  F fa[TI], fb0[TJ], fb1[TJ];
+#pragma unroll
+  for (int i = 0; i < TI; ++i) read_a(fa[i], 0, 0, i);
+#pragma unroll
+  for (int j = 0; j < TJ; ++j) read_b(fb0[j], 0, 0, j);
+
+  // One MFMA step: NCH chunks of two MFMAs (tiles 2x, 2x + 1; tile tt is A
+  // block tt / TJ, B block tt % TJ), each chunk fenced.
+  //   bc / bn: this step's B fragments / the next step's (read here);
+  //   (rst, rs): the stage and step the reads are for;
+  //   copies: 0 none, 1 the B rows of stage cst, 2 the A rows of stage cst;
+  //   fold_mode: 0 none, 1 a group's last step, 2 a group's first step.
+  auto step = [&](F (&bc)[TJ], F (&bn)[TJ], int rst, int rs, int copies, int cst, bool real, bool first,
+                  int fold_mode) {
+    int f = fold_mode == 1 ? 0 : kFoldLast;
+#pragma unroll
+    for (int x = 0; x < NCH; ++x) {
+      if (copies == 1 && x < kBigBCopies) copy_b(cst, real, x);
+      if (copies == 2 && x < kBigACopies) copy_a(cst, real, x);
+      if (x < TJ) read_b(bn[x], rst, rs, x);
+      if (fold_mode == 1) {
+        if (x >= 1 && f < 2 * x && f < kFoldLast) fold(f++);  // tiles final in earlier chunks
+      } else if (fold_mode == 2) {
+        if (f < NT) fold(f++);
+        while (f < 2 * x + 2) fold(f++);                       // before their first MFMA
+      }
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        const int tt = 2 * x + y, i = tt / TJ, j = tt % TJ;
+        acc[i][j] = mfma_step(fa[i], bc[j], first ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
+        if (j == TJ - 1) read_a(fa[i], rst, rs, i);  // last use this step: read the next step's
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
   for (int g = 0; g < nst / 4; ++g) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int st = 4 * g + p;
-      // stage st visible to all waves; stage st - 1 no longer read by any wave
-      if (st + 1 < nst) stage_barrier<kBigCopiesPerWave>();
-      else stage_barrier<0>();
-      if (st + 2 < nst) issue(st + 2);
-      const T* buf = lds + (st % kBigBufs) * kBigStage;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        F af[4], bf[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          af[i] = *reinterpret_cast<const F*>(buf + (64 * wm + 16 * i) * 64 + frag_off[s]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          bf[j] = *reinterpret_cast<const F*>(buf + (kBigBM + 64 * wn + 16 * j) * 64 + frag_off[s]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            acc[i][j] = mfma_step(af[i], bf[j], (p == 0 && s == 0) ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j]);
-      }
+      step(fb0, fb1, st, 1, 1, st + 3, st + 3 < nst, p == 0, p == 0 ? 2 : 0);
+      // stage st + 1 landed (younger: stage st + 2 and the B rows of st + 3);
+      // this wave's reads of stage st are done; then every wave's are.
+      wait_vm_lgkm0<kBigACopies + 2 * kBigBCopies>();
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      step(fb1, fb0, st + 1, 0, 2, st + 3, st + 3 < nst, false, p == 3 ? 1 : 0);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) total[i][j] = total[i][j] + acc[i][j];
   }
+  wait_vm_lgkm0<0>();  // no copy may still be writing this workgroup's LDS when it exits
+#pragma unroll
+  for (int tt = kFoldLast; tt < NT; ++tt) fold(tt);
 
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + 64 * wn + 16 * j + r;
+    for (int j = 0; j < TJ; ++j) {
+      const int n = n0 + 16 * TJ * wn + 16 * j + r;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int m = m0 + 64 * wm + 16 * i + 4 * q + e;
+        const int m = m0 + 16 * TI * wm + 16 * i + 4 * q + e;
         if (m < M && n < N) out[(int64_t)m * N + n] = to_store<T>(total[i][j][e]);
       }
     }

@@ -12,7 +12,8 @@
 //   fold_groups  out = T(((0 + part[0]) + part[1]) + ...), the split fold.
 //   gemm_big     dense 2-byte types, K % 256 == 0, enough 256 x 128 tiles to
 //                fill the chip: 8 waves, operands copied straight into
-//                swizzled LDS rows, three stages in flight (bi_gemm_big.h).
+//                swizzled LDS rows through buffer resources, copies and
+//                fragment reads interleaved with the MFMAs (bi_gemm_big.h).
 //   gemm_lds     other M > 32. A BM x BN tile per 256-thread workgroup, K
 //                staged 64 at a time through double-buffered LDS (quantized B
 //                is dequantized while it is staged), all groups folded in
@@ -748,7 +749,8 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   // M > 32: LDS-tiled; the largest tile that still gives the chip >= 256 tiles.
   auto tiles = [&](int bm, int bn) { return (int64_t)ceil_div(M, bm) * ceil_div(N, bn); };
   if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
-    if (K % kGroupK == 0 && M >= kBigMinM && tiles(kBigBM, kBigBN) >= kBigMinTiles) {
+    if (K % kGroupK == 0 && M >= kBigMinM && tiles(kBigBM, kBigBN) >= kBigMinTiles && lda < kBigMaxLd &&
+        bsrc.ldb < kBigMaxLd) {
       const int tmm = ceil_div(M, kBigBM), tn = ceil_div(N, kBigBN);
       const int grid = ((tmm * tn + 7) / 8) * 8;
       gemm_big<T><<<grid, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K, tmm, tn);
