@@ -8,13 +8,15 @@
 // kernels: bi_attn_mfma.h.
 //
 // gfx950 launches:
-//   decode  one 256-thread workgroup per (sequence, kv head, head chunk of GU
-//           <= 16 heads, split); writes (m, l, acc) of its split.
+//   decode  a resident grid of 256-thread workgroups walking the active items
+//           (sequence, split, kv head, head chunk of GU <= 16 heads); each
+//           item writes (m, l, acc) of its split.
 //   combine one thread per (sequence, head, d); merges the sequence's own
 //           ceil(len/256) splits left to right and divides.
 //   prefill one 256-thread workgroup per (sequence, kv head, 64 (token, head)
 //           rows, token-major), K/V streamed through LDS in 64-key chunks,
 //           splits merged in registers.
+#include <algorithm>
 #include <type_traits>
 
 #include "bi_attn_mfma.h"
@@ -49,16 +51,48 @@ static int decode_gu(int G) {
   return 1;
 }
 
+// Workgroups of `kern` (256 threads) that the current device holds at once:
+// compute units x resident workgroups per unit, queried once per device and
+// kept in the caller's per-kernel cache.
+constexpr int kMaxDev = 64;
+template <typename K>
+static int resident_grid(K kern, int (&cache)[kMaxDev]) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  if (cache[dev] > 0) return cache[dev];  // benign race: every writer stores the same value
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || cus <= 0 ||
+      per_cu <= 0)
+    return 0;
+  cache[dev] = cus * per_cu;
+  return cache[dev];
+}
+
+template <typename T, int D, int GU>
+static int launch_decode_gu(DecodeArgs& a, hipStream_t st) {
+  // Enough resident workgroups to fill the chip, never more than the number
+  // of possible items (every sequence at full length).
+  const int64_t most = (int64_t)a.B * a.nsplit * a.Hkv * a.nchunk;
+  static int cache[kMaxDev] = {};
+  int grid = resident_grid(attn_decode_mfma<T, D, GU>, cache);
+  if (grid <= 0) return bi_host::fail(BI_E_UNSUPPORTED, "bi_attn_decode: device occupancy query failed");
+  grid = (int)std::min<int64_t>(grid, most);
+  attn_decode_mfma<T, D, GU><<<grid, 256, 0, st>>>(a);
+  return 0;
+}
+
 template <typename T, int D>
 static int launch_decode(DecodeArgs& a, hipStream_t st) {
-  dim3 grid(a.nsplit, a.Hkv * a.nchunk, a.B);
+  int rc0 = 0;
   switch (a.GU) {
-    case 16: attn_decode_mfma<T, D, 16><<<grid, 256, 0, st>>>(a); break;
-    case 8: attn_decode_mfma<T, D, 8><<<grid, 256, 0, st>>>(a); break;
-    case 4: attn_decode_mfma<T, D, 4><<<grid, 256, 0, st>>>(a); break;
-    case 2: attn_decode_mfma<T, D, 2><<<grid, 256, 0, st>>>(a); break;
-    default: attn_decode_mfma<T, D, 1><<<grid, 256, 0, st>>>(a); break;
+    case 16: rc0 = launch_decode_gu<T, D, 16>(a, st); break;
+    case 8: rc0 = launch_decode_gu<T, D, 8>(a, st); break;
+    case 4: rc0 = launch_decode_gu<T, D, 4>(a, st); break;
+    case 2: rc0 = launch_decode_gu<T, D, 2>(a, st); break;
+    default: rc0 = launch_decode_gu<T, D, 1>(a, st); break;
   }
+  if (rc0) return rc0;
   int rc = bi_host::launch_status("bi_attn_decode");
   if (rc) return rc;
   const int64_t n = (int64_t)a.B * a.Hq * D;

@@ -90,15 +90,22 @@ struct KVTile {
 };
 
 // ---------------------------------------------------------------------------
-// Decode: one 256-thread workgroup per (sequence, kv head, head chunk of GU,
-// split). GU query heads are the 16 columns of the score tile (GU <= 16).
+// Decode: a resident grid of 256-thread workgroups walks the active work items
+// (sequence b, split, kv head, head chunk of GU) in that nesting order; only
+// splits below a sequence's own length are items, so a ragged batch launches
+// no workgroup that has nothing to do (with a grid over every possible split,
+// the empty workgroups of short sequences cost as much dispatch time as the
+// real work). Workgroup w takes items w, w + P, w + 2P, ... (P = grid size)
+// and finds each item's sequence by walking the lengths forward.
+// Per item: GU query heads are the 16 columns of the score tile (GU <= 16).
 // Every wave first requests all of its memory: Q^T, the K rows of its 64 keys
 // (registers, 16-byte loads, rows past the sequence end clamped to its last
 // key) and a quarter of the split's V rows, which the load unit copies
 // straight into LDS. Wave w scores keys 64 w .. 64 w + 63; the split maximum
 // is exchanged through LDS; each wave writes its keys' weights to LDS; then
 // wave w computes the P.V tiles of dims 16 dt, dt = w, w + 4, ..., and wave 0
-// also the weight sum. Writes (m, l, acc) of its split.
+// also the weight sum. Writes (m, l, acc) of its split. The arithmetic of an
+// item does not depend on which workgroup runs it.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int GU>
 __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
@@ -116,14 +123,25 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int split = blockIdx.x;
-  const int hk = blockIdx.y / a.nchunk;
-  const int chunk = blockIdx.y % a.nchunk;
-  const int b = blockIdx.z;
-  // A length outside [0, L] is clamped, so no key past the cache is ever read.
-  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
+  const int per_split = a.Hkv * a.nchunk;  // items per (sequence, split)
+  int b = 0;
+  int64_t base = 0;                         // items of sequences before b
+  int len = 0;
+  for (int64_t item = blockIdx.x;; item += gridDim.x) {
+  // Advance to the sequence holding `item` (uniform per workgroup). A length
+  // outside [0, L] is clamped, so no key past the cache is ever read.
+  for (; b < a.B; ++b) {
+    len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
+    const int64_t nb = (int64_t)((len + kSplit - 1) / kSplit) * per_split;
+    if (item < base + nb) break;
+    base += nb;
+  }
+  if (b >= a.B) break;
+  const int64_t local = item - base;
+  const int split = (int)(local / per_split);
+  const int hk = (int)(local % per_split) / a.nchunk;
+  const int chunk = (int)(local % per_split) % a.nchunk;
   const int j0 = split * kSplit;
-  if (j0 >= len) return;  // uniform per workgroup, before any barrier
   const int n_act = min(kSplit, len - j0);
   const int G = a.Hq / a.Hkv;
   const int h0 = hk * G + chunk * GU;
@@ -232,6 +250,8 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
       const int row = 4 * qq + i;
       if (row < GU) a.pl[pbase + (int64_t)row * a.nsplit] = lsum[i];
     }
+  }
+  __syncthreads();  // every wave is done with Vs, Ps and mxs before the next item's copies
   }
 }
 
