@@ -105,7 +105,8 @@ int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w, const voi
  * be NULL = all L) gives each sequence's own key count, 1 <= len <= L; a
  * sequence's output depends only on its own first len keys. Hq % Hkv == 0,
  * D in {64, 128}. Keys go in fixed splits of BI_SPLIT_KEYS; the workspace
- * holds per-split (m, l, acc) partials (bi_attn_decode_workspace_bytes).
+ * holds per-split (m, l, acc) partials and a work-item counter
+ * (bi_attn_decode_workspace_bytes); calls that overlap must not share it.
  * Replaces: kernels/attention.py:326-365 (batch_invariant_decode_attention),
  * kernels :47-171; kv_lens is an extension the reference lacks. */
 size_t bi_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t L, int64_t D);

@@ -69,16 +69,29 @@ static int resident_grid(K kern, int (&cache)[kMaxDev]) {
   return cache[dev];
 }
 
+__global__ void zero_counter_kernel(unsigned* c) { *c = 0u; }
+
+// With more possible items than DYN_MIN_ROUNDS rounds of the resident grid,
+// items are handed out dynamically (one more tiny launch zeroes the counter:
+// a fill kernel, not a memset, so the call can be captured into a graph);
+// with fewer, the static order costs nothing extra.
+constexpr int kDynMinRounds = 4;
+
 template <typename T, int D, int GU>
 static int launch_decode_gu(DecodeArgs& a, hipStream_t st) {
   // Enough resident workgroups to fill the chip, never more than the number
   // of possible items (every sequence at full length).
   const int64_t most = (int64_t)a.B * a.nsplit * a.Hkv * a.nchunk;
   static int cache[kMaxDev] = {};
-  int grid = resident_grid(attn_decode_mfma<T, D, GU>, cache);
+  int grid = resident_grid(attn_decode_mfma<T, D, GU, true>, cache);
   if (grid <= 0) return bi_host::fail(BI_E_UNSUPPORTED, "bi_attn_decode: device occupancy query failed");
-  grid = (int)std::min<int64_t>(grid, most);
-  attn_decode_mfma<T, D, GU><<<grid, 256, 0, st>>>(a);
+  if (most > (int64_t)kDynMinRounds * grid) {
+    zero_counter_kernel<<<1, 1, 0, st>>>(a.ctr);
+    attn_decode_mfma<T, D, GU, true><<<grid, 256, 0, st>>>(a);
+  } else {
+    grid = (int)std::min<int64_t>(grid, most);
+    attn_decode_mfma<T, D, GU, false><<<grid, 256, 0, st>>>(a);
+  }
   return 0;
 }
 
@@ -133,9 +146,9 @@ extern "C" size_t bi_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t 
   if (B <= 0 || Hq <= 0 || L <= 0 || D <= 0) return 0;
   const int64_t ns = (L + bi::kSplit - 1) / bi::kSplit;
   const int64_t bh = B * Hq * ns;
-  // pm | pl | pacc, each 16-byte aligned
+  // pm | pl | pacc | item counter (16 bytes), each 16-byte aligned
   auto up = [](int64_t x) { return (x + 3) / 4 * 4; };
-  return (size_t)(up(bh) * 2 + bh * D) * sizeof(float);
+  return (size_t)(up(bh) * 2 + bh * D + 4) * sizeof(float);
 }
 
 extern "C" int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* kv_lens,
@@ -175,6 +188,7 @@ extern "C" int bi_attn_decode(const void* q, const void* k, const void* v, const
   a.pm = static_cast<float*>(ws);
   a.pl = a.pm + up;
   a.pacc = a.pl + up;
+  a.ctr = reinterpret_cast<unsigned*>(a.pacc + bh * D);
   if ((int64_t)a.Hkv * a.nchunk > 65535 || a.nsplit > 0x7fffffff)
     return fail(BI_E_UNSUPPORTED, "bi_attn_decode: grid too large");
   hipStream_t st = static_cast<hipStream_t>(stream);

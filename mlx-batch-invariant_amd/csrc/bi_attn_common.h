@@ -50,6 +50,7 @@ struct DecodeArgs {
   float* pm;
   float* pl;
   float* pacc;
+  unsigned* ctr;  // decode item counter (dynamic item order only), zero at launch
   void* out;
   int B, Hq, Hkv, L, nsplit, nchunk, GU;
   int64_t q_sb, q_sh, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;

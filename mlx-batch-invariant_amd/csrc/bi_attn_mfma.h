@@ -95,8 +95,11 @@ struct KVTile {
 // splits below a sequence's own length are items, so a ragged batch launches
 // no workgroup that has nothing to do (with a grid over every possible split,
 // the empty workgroups of short sequences cost as much dispatch time as the
-// real work). Workgroup w takes items w, w + P, w + 2P, ... (P = grid size)
-// and finds each item's sequence by walking the lengths forward.
+// real work). DYN = false: workgroup w takes items w, w + P, w + 2P, ...
+// (P = grid size). DYN = true: each workgroup takes the next item from a
+// counter (a.ctr, zero at launch), so workgroups that finish early take more
+// items. Either way items come in increasing order per workgroup, which finds
+// each item's sequence by walking the lengths forward.
 // Per item: GU query heads are the 16 columns of the score tile (GU <= 16).
 // Every wave first requests all of its memory: Q^T, the K rows of its 64 keys
 // (registers, 16-byte loads, rows past the sequence end clamped to its last
@@ -107,7 +110,7 @@ struct KVTile {
 // also the weight sum. Writes (m, l, acc) of its split. The arithmetic of an
 // item does not depend on which workgroup runs it.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int GU>
+template <typename T, int D, int GU, bool DYN>
 __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   typedef typename Frag<T>::type F;
   typedef KVTile<T, D> KV;
@@ -119,6 +122,7 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   __shared__ __attribute__((aligned(1024))) char Vs[kSplit * KV::kRowBytes];
   __shared__ __attribute__((aligned(16))) float Ps[GU][kSplit];
   __shared__ float mxs[4][16];
+  __shared__ unsigned item_s;
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -127,7 +131,15 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   int b = 0;
   int64_t base = 0;                         // items of sequences before b
   int len = 0;
-  for (int64_t item = blockIdx.x;; item += gridDim.x) {
+  for (int64_t next = blockIdx.x;; next += gridDim.x) {
+  int64_t item = next;
+  if constexpr (DYN) {
+    // The end-of-item barrier below keeps thread 0 from overwriting item_s
+    // before every thread has read it.
+    if (tid == 0) item_s = atomicAdd(a.ctr, 1u);
+    __syncthreads();
+    item = item_s;
+  }
   // Advance to the sequence holding `item` (uniform per workgroup). A length
   // outside [0, L] is clamped, so no key past the cache is ever read.
   for (; b < a.B; ++b) {

@@ -48,7 +48,8 @@ def test_workspace_sizes():
     assert lib.bi_quantized_matmul_workspace_bytes(2048, 4096, 4000) == 0
     ns = (8192 + 255) // 256
     bh = 256 * 32 * ns
-    assert lib.bi_attn_decode_workspace_bytes(256, 32, 8192, 128) == (2 * ((bh + 3) // 4 * 4) + bh * 128) * 4
+    # pm | pl | pacc | 16-byte item counter
+    assert lib.bi_attn_decode_workspace_bytes(256, 32, 8192, 128) == (2 * ((bh + 3) // 4 * 4) + bh * 128 + 4) * 4
 
 
 def _err(lib):

@@ -112,6 +112,42 @@ def test_decode_ragged_kv_lens_equal_alone():
         assert bits(out[b:b + 1]) == bits(alone), (b, n)
 
 
+def test_decode_dynamic_items_equal_alone_and_replay():
+    """A ragged batch with many more split items than the resident grid takes
+    the dynamic item order (a counter in the workspace, zeroed by a fill
+    kernel per call). Each sequence must equal running it alone (the static
+    order), on repeated calls and on replays of a captured graph."""
+    Hq, Hkv, D, L = 32, 8, 128, 4096
+    rng = np.random.default_rng(3)
+    B = 48
+    lens = rng.integers(1, L + 1, size=B)
+    lens[0], lens[1], lens[2], lens[-1] = 1, 256, 257, L
+    q, k, v = _qkv(B, Hq, Hkv, 1, L, D, "bf16", seed=9)
+    kl = torch.tensor(lens, dtype=torch.int32).cuda()
+    run = lambda: _bi().batch_invariant_decode_attention(q, k, v, scale=D ** -0.5, kv_lens=kl)
+    out = run()
+    for b in range(B):
+        n = int(lens[b])
+        alone = _bi().batch_invariant_decode_attention(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n],
+                                                       scale=D ** -0.5)
+        assert bits(out[b:b + 1]) == bits(alone), (b, n)
+    assert bits(run()) == bits(out)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        gout = run()
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert bits(gout) == bits(out)
+        assert bits(run()) == bits(out)   # eager work between replays
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 def test_chunked_prefill_and_decode_equivalence(dt):
     """Reference attention_structure_checks (harness/sweep.py:188-207): T=600,
