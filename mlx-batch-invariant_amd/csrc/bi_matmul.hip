@@ -7,14 +7,20 @@
 // ---------------------------------------------------------------------------
 namespace {
 
-size_t split_ws_bytes(int64_t M, int64_t N, int64_t K) {
+// Group partials [G, M, N] fp32 of the small-M split launch; for a dense B
+// also of the mid-M launch when it splits K (2-byte types; the query has no
+// dtype and reports the need of either).
+size_t split_ws_bytes(int64_t M, int64_t N, int64_t K, bool dense) {
   const int64_t G = (K + bi::kGroupK - 1) / bi::kGroupK;
-  if (M <= 0 || N <= 0 || K <= 0 || !bi::use_split(M, (int)G) || bi::use_wg(M, (int)G)) return 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  const bool small_split = bi::use_split(M, (int)G) && !bi::use_wg(M, (int)G);
+  const bool tall_split = dense && bi::tall_plan(M, N, K).chunks > 1;
+  if (!small_split && !tall_split) return 0;
   return (size_t)(G * M * N) * sizeof(float);
 }
 
 int check_common(const char* what, int64_t M, int64_t N, int64_t K, void* out, void* ws,
-                 size_t ws_bytes) {
+                 size_t ws_bytes, bool dense) {
   using namespace bi_host;
   if (M < 0 || N <= 0 || K <= 0)
     return fail(BI_E_INVALID_ARG, "%s: bad shape M=%lld N=%lld K=%lld", what, (long long)M,
@@ -23,7 +29,7 @@ int check_common(const char* what, int64_t M, int64_t N, int64_t K, void* out, v
       ((M + 63) / 64) * ((N + 63) / 64) > 0x7fffffffLL - 8)
     return fail(BI_E_UNSUPPORTED, "%s: shape too large", what);
   if (M > 0 && !out) return fail(BI_E_INVALID_ARG, "%s: null out", what);
-  const size_t need = split_ws_bytes(M, N, K);
+  const size_t need = split_ws_bytes(M, N, K, dense);
   if (need && (!ws || ws_bytes < need))
     return fail(BI_E_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", what, need,
                 ws ? ws_bytes : (size_t)0);
@@ -36,7 +42,7 @@ int check_common(const char* what, int64_t M, int64_t N, int64_t K, void* out, v
 extern "C" int bi_split_m_max(void) { return bi::kSplitMMax; }
 
 extern "C" size_t bi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  return split_ws_bytes(M, N, K);
+  return split_ws_bytes(M, N, K, true);
 }
 
 // Quantized: the small-M split partials, or for large M (2-byte types) the
@@ -46,7 +52,7 @@ extern "C" size_t bi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 static size_t quant_ws_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   if (bi::qmm_use_big(M, N, K, 2)) return bi::qmm_big_ws_bytes(M, N, K);
-  return split_ws_bytes(M, N, K);
+  return split_ws_bytes(M, N, K, false);
 }
 
 extern "C" size_t bi_quantized_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
@@ -57,7 +63,7 @@ extern "C" int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb
                          int64_t M, int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes,
                          void* stream) {
   using namespace bi_host;
-  int rc = check_common("bi_matmul", M, N, K, out, ws, ws_bytes);
+  int rc = check_common("bi_matmul", M, N, K, out, ws, ws_bytes, true);
   if (rc) return rc;
   if (M == 0) return BI_OK;
   if (!a || !bt) return fail(BI_E_INVALID_ARG, "bi_matmul: null operand");
@@ -98,7 +104,7 @@ extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w
   if ((bits != 4 && bits != 8) || (group_size != 32 && group_size != 64 && group_size != 128))
     return fail(BI_E_UNSUPPORTED, "bi_quantized_matmul: bits=%d group_size=%d not in {4,8}x{32,64,128}",
                 bits, group_size);
-  int rc = check_common("bi_quantized_matmul", M, N, K, out, ws, ws_bytes);
+  int rc = check_common("bi_quantized_matmul", M, N, K, out, ws, ws_bytes, false);
   if (rc) return rc;
   if (K % group_size)
     return fail(BI_E_INVALID_ARG, "bi_quantized_matmul: K=%lld not a multiple of group_size=%d",

@@ -25,9 +25,12 @@
 
 #include <type_traits>
 
+#include <algorithm>
+
 #include "bi_gemm_big.h"
 #include "bi_gemv_stream.h"
 #include "bi_gemm_mid.h"
+#include "bi_gemm_tall.h"
 #include "bi_qmm_big.h"
 #include "bi_gemm_tile.h"
 
@@ -574,6 +577,75 @@ static inline bool use_split(int64_t M, int G) { return M <= kSplitMMax && G > 1
 // 16-row tile); up to 64 KB of it. Larger K takes the split + fold launch.
 static inline bool use_wg(int64_t M, int G) { return M <= kSplitMMax && G * (M <= 16 ? 1 : 2) <= 64; }
 
+// Dense mid-M launch (bi_gemm_tall.h) for 2-byte types: 16 < M <= 128,
+// K % 64 == 0. The widest column tile that still gives kTallMinTiles
+// workgroups; with too few even at the narrowest, K is split into chunks of
+// groups whose raw partials fold_groups folds. A function of the shape only,
+// so the workspace query and the launch agree.
+constexpr int kTallMinTiles = 200;
+struct TallPlan {
+  bool use = false;
+  int bm = 0, bn = 0, chunks = 1, cg = 0;
+};
+static inline TallPlan tall_plan(int64_t M, int64_t N, int64_t K) {
+  TallPlan p;
+  if (M <= 16 || M > 128 || K <= 0 || K % 64) return p;
+  const int G = ceil_div(K, kGroupK);
+  p.bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+  const int narrowest = p.bm == 32 ? 32 : 16;
+  for (int bn : {64, 32, 16}) {
+    if (bn < narrowest) break;
+    p.bn = bn;
+    if (ceil_div(N, bn) >= kTallMinTiles) break;
+  }
+  const int64_t t = ceil_div(N, p.bn);
+  p.cg = G;
+  if (t < kTallMinTiles && G > 1) {
+    const int want = std::min<int64_t>(G, ceil_div(kTallMinTiles, t));
+    p.cg = ceil_div(G, want);
+    p.chunks = ceil_div(G, p.cg);
+  }
+  p.use = true;
+  return p;
+}
+
+template <typename T, int TI, int WM, int WN, int SK>
+static void launch_tall2(const T* a, int64_t lda, const DenseB<T>& b, T* out, float* ws, int M, int N, int K,
+                         int G, const TallPlan& p, hipStream_t st) {
+  dim3 grid(ceil_div(N, 16 * WN), ceil_div(M, 16 * TI * WM), p.chunks);
+  if (p.chunks > 1) {
+    gemm_tall<T, TI, WM, WN, SK, true><<<grid, 256, 0, st>>>(a, lda, b.bt, b.ldb, out, ws, M, N, K, G, p.cg);
+    const int64_t MN = (int64_t)M * N;
+    fold_groups<T><<<(unsigned)((MN + 255) / 256), 256, 0, st>>>(ws, out, MN, G);
+  } else {
+    gemm_tall<T, TI, WM, WN, SK, false><<<grid, 256, 0, st>>>(a, lda, b.bt, b.ldb, out, ws, M, N, K, G, G);
+  }
+}
+
+// 128-k stages (256-byte row pieces) when K allows, else 64-k.
+template <typename T, int TI, int WM, int WN>
+static void launch_tall1(const T* a, int64_t lda, const DenseB<T>& b, T* out, float* ws, int M, int N, int K,
+                         int G, const TallPlan& p, hipStream_t st) {
+  if (K % 128 == 0) launch_tall2<T, TI, WM, WN, 128>(a, lda, b, out, ws, M, N, K, G, p, st);
+  else launch_tall2<T, TI, WM, WN, 64>(a, lda, b, out, ws, M, N, K, G, p, st);
+}
+
+template <typename T>
+static void launch_tall(const T* a, int64_t lda, const DenseB<T>& b, T* out, float* ws, int M, int N, int K,
+                        int G, const TallPlan& p, hipStream_t st) {
+  const int key = p.bm * 1000 + p.bn;
+  switch (key) {
+    case 32064: launch_tall1<T, 2, 1, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case 32032: launch_tall1<T, 1, 2, 2>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case 64064: launch_tall1<T, 4, 1, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case 64032: launch_tall1<T, 2, 2, 2>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case 64016: launch_tall1<T, 1, 4, 1>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case 128064: launch_tall1<T, 8, 1, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case 128032: launch_tall1<T, 4, 2, 2>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    default: launch_tall1<T, 2, 4, 1>(a, lda, b, out, ws, M, N, K, G, p, st); break;  // 128 x 16
+  }
+}
+
 template <typename T, class BSrc, int BM, int BN>
 static void launch_lds(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K,
                        int G, hipStream_t st) {
@@ -721,6 +793,13 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   if (use_mid<T, BSrc>(M, N, K, lda, a)) {
     launch_mid<T, BSrc>(a, lda, bsrc, out, M, N, K, G, st);
     return bi_host::launch_status(what);
+  }
+  if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
+    const TallPlan tp = tall_plan(M, N, K);
+    if (tp.use && lda < kBigMaxLd && bsrc.ldb < kBigMaxLd) {
+      launch_tall<T>(a, lda, bsrc, out, ws, M, N, K, G, tp, st);
+      return bi_host::launch_status(what);
+    }
   }
   if (M <= kSplitMMax && use_wg(M, G)) {
     // 4 waves per workgroup when there are enough column tiles for every

@@ -76,7 +76,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
         for f in futs:
             f.result()
     tmp = OUT.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)], verbose)
+    # -z defs: a kernel whose host stub was not emitted fails here, not at dlopen
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, OUT)
     return OUT
 

@@ -32,10 +32,16 @@ def test_workspace_sizes():
     lib = _lib.load()
     # M <= 32 folds its group partials in LDS up to 64 groups (32 for M > 16)
     assert lib.bi_matmul_workspace_bytes(1, 14336, 4096) == 0
-    assert lib.bi_matmul_workspace_bytes(32, 100, 896) == 0
+    # dense 16 < M <= 128 with too few column tiles: the mid-M launch splits K
+    assert lib.bi_matmul_workspace_bytes(32, 100, 896) == 4 * 32 * 100 * 4
     assert lib.bi_matmul_workspace_bytes(1, 100, 65 * 256) == 65 * 1 * 100 * 4   # split + fold
     assert lib.bi_matmul_workspace_bytes(20, 100, 33 * 256) == 33 * 20 * 100 * 4
-    assert lib.bi_matmul_workspace_bytes(33, 100, 896) == 0          # fused (LDS tiles)
+    assert lib.bi_matmul_workspace_bytes(33, 100, 896) == 4 * 33 * 100 * 4
+    assert lib.bi_matmul_workspace_bytes(64, 14336, 4096) == 0       # mid-M, enough column tiles
+    assert lib.bi_matmul_workspace_bytes(64, 4096, 14336) == 0       # 16-column tiles fill the chip
+    assert lib.bi_matmul_workspace_bytes(64, 1024, 4096) == 16 * 64 * 1024 * 4   # 4 chunks of 4 groups
+    assert lib.bi_matmul_workspace_bytes(129, 100, 896) == 0         # fused (LDS tiles)
+    assert lib.bi_quantized_matmul_workspace_bytes(32, 100, 896) == 0   # no mid-M split for quantized B
     assert lib.bi_matmul_workspace_bytes(8, 100, 256) == 0           # one group
     assert lib.bi_quantized_matmul_workspace_bytes(4, 14336, 4096) == 0
     # large M: dequantized weight + reordered activations, 2 bytes each
