@@ -1,0 +1,162 @@
+"""Bit hashes of the invariant kernels' outputs (and a model's logits), so two
+software stacks or two machines can be compared.
+
+    python -m mlx_batch_invariant_amd.dump_bits --out bits_<tag>.json [--model llama[:LAYERS]]
+    python -m mlx_batch_invariant_amd.dump_bits --compare bits_a.json bits_b.json
+
+Counterpart of mlx-batch-invariant's harness/dump_bits.py:32-78. Determinism
+is promised per (kernel library build, GPU, ROCm); this measures how far it
+carries. Hashes (blake2b, 8 bytes, of the output's raw bytes) cover each op of
+the reference's sweep (harness/sweep.py:65-179: matmul, addmm, 4-bit and
+8-bit quantized matmul, RMSNorm, decode and causal prefill attention) on a
+fixed probe input at batch 1, in fp16, bf16 and fp32, under the stock torch
+path and under the batch-invariant mode; and, with --model, the row-0 logits
+of a random-init Llama-shaped decoder in prefill and decode under both modes.
+--compare prints, per section and mode, how many hashes agree and exits 1 if
+an invariant-mode hash differs.
+"""
+
+from __future__ import annotations
+
+import argparse
+import hashlib
+import json
+import platform
+import sys
+from pathlib import Path
+
+import torch
+
+DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+
+
+def _h(t: torch.Tensor) -> str:
+    return hashlib.blake2b(t.detach().contiguous().view(torch.uint8).cpu().numpy().tobytes(),
+                           digest_size=8).hexdigest()
+
+
+def _ops(dt: torch.dtype, dev: str):
+    """(name, fn) pairs; every input is drawn from a fixed CPU generator."""
+    import mlx_batch_invariant_amd as bi
+    from mlx_batch_invariant_amd import nn as bnn
+    F = torch.nn.functional
+    g = torch.Generator().manual_seed(0)
+    rn = lambda *s: torch.randn(s, generator=g).to(dt).to(dev)
+    K = N = 4096
+    W = rn(N, K)
+    x = rn(1, K)
+    lin_b = rn(N)
+    out = [("matmul", lambda: torch.matmul(x, W.t())),
+           ("addmm", lambda: F.linear(x, W, lin_b))]
+    for name, bits, gs in (("qmatmul_4b", 4, 64), ("qmatmul_8b", 8, 32)):
+        wq, s, b = bi.quantize(W.float().cpu(), group_size=gs, bits=bits, dtype=dt)
+        wq, s, b = wq.view(torch.int32).to(dev), s.to(dev), b.to(dev)
+        out.append((name, lambda wq=wq, s=s, b=b, bits=bits, gs=gs: bnn.quantized_matmul(
+            x, wq, s, b, transpose=True, group_size=gs, bits=bits)))
+    D = 4096
+    w_n, x_n = rn(D), rn(1, D)
+    out.append(("rms_norm", lambda: F.rms_norm(x_n, (D,), w_n, 1e-5)))
+    Hq, Hkv, Dh = 8, 2, 128
+    q, k, v = rn(1, Hq, 1, Dh), rn(1, Hkv, 1000, Dh), rn(1, Hkv, 1000, Dh)
+    out.append(("sdpa_decode", lambda: F.scaled_dot_product_attention(q, k, v, scale=Dh ** -0.5, enable_gqa=True)))
+    Tq, L = 48, 300
+    qp, kp, vp = rn(1, Hq, Tq, Dh), rn(1, Hkv, L, Dh), rn(1, Hkv, L, Dh)
+    from torch.nn.attention.bias import causal_lower_right
+    out.append(("sdpa_prefill", lambda: F.scaled_dot_product_attention(
+        qp, kp, vp, attn_mask=causal_lower_right(Tq, L), scale=Dh ** -0.5, enable_gqa=True)))
+    return out
+
+
+def _library_hash() -> str | None:
+    from mlx_batch_invariant_amd import _lib
+    p = Path(_lib.__file__).with_name("libbi_kernels.so")
+    return hashlib.blake2b(p.read_bytes(), digest_size=8).hexdigest() if p.exists() else None
+
+
+def dump(model: str | None = None, dev: str = "cuda") -> dict:
+    import mlx_batch_invariant_amd as bi
+    props = torch.cuda.get_device_properties(0)
+    out = {"torch": torch.__version__, "hip": getattr(torch.version, "hip", None),
+           "device": props.name, "arch": getattr(props, "gcnArchName", None), "library": _library_hash(),
+           "os": platform.platform(), "ops": {}, "model": {}}
+    for dt_name, dt in DTYPES.items():
+        for op_name, fn in _ops(dt, dev):
+            for inv in (False, True):
+                with bi.set_batch_invariant_mode(enabled=inv, strict=inv):
+                    y = fn()
+                torch.cuda.synchronize()
+                out["ops"][f"{op_name}/{dt_name}/{'inv' if inv else 'stock'}"] = _h(y)
+    if model:
+        name, _, layers = model.partition(":")
+        if name != "llama":
+            raise ValueError(f"unknown model {name!r} (supported: llama[:LAYERS])")
+        from mlx_batch_invariant_amd.llama import LlamaConfig, LlamaShaped
+        for bits in (4, None):
+            cfg = LlamaConfig(layers=int(layers or 2), bits=bits)
+            m = LlamaShaped(cfg, device=dev, dtype=torch.bfloat16, seed=0)
+            prompt = torch.randint(0, cfg.vocab, (1, 16), generator=torch.Generator().manual_seed(0)).to(dev)
+            tag = f"llama{cfg.layers}-{'q4g64' if bits else 'bf16'}"
+            for inv in (False, True):
+                with bi.set_batch_invariant_mode(enabled=inv, strict=inv):
+                    cache = m.new_cache(1, 17)
+                    pre = m(prompt, cache, 0)
+                    nxt = pre.argmax(-1, keepdim=True)
+                    dec = m(nxt, cache, 16)
+                torch.cuda.synchronize()
+                mode = "inv" if inv else "stock"
+                out["model"][f"{tag}/prefill/{mode}"] = _h(pre[0:1])
+                out["model"][f"{tag}/decode/{mode}"] = _h(dec[0:1])
+            del m
+    return out
+
+
+def compare(a: dict, b: dict, file=sys.stdout) -> int:
+    """Print agreement per section and mode; 1 if an invariant hash differs."""
+    for tag, d in (("A", a), ("B", b)):
+        print(f"{tag}: torch {d.get('torch')} hip {d.get('hip')} on {d.get('device')} ({d.get('arch')}), "
+              f"library {d.get('library')}", file=file)
+    print(file=file)
+    rc = 0
+    for section in ("ops", "model"):
+        keys = sorted(set(a.get(section, {})) & set(b.get(section, {})))
+        if not keys:
+            continue
+        same = {"stock": [0, 0], "inv": [0, 0]}
+        diff = []
+        for k in keys:
+            mode = "inv" if k.endswith("/inv") else "stock"
+            same[mode][1] += 1
+            if a[section][k] == b[section][k]:
+                same[mode][0] += 1
+            else:
+                diff.append(k)
+                if mode == "inv":
+                    rc = 1
+        for mode, (n, tot) in same.items():
+            print(f"{section:<6} {mode:<6} identical: {n}/{tot}", file=file)
+        if diff:
+            print("  differing: " + ", ".join(diff), file=file)
+    return rc
+
+
+def main(argv=None) -> int:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--out")
+    p.add_argument("--model", help="llama[:LAYERS] — a random-init Llama-3-8B-shape decoder (default 2 layers)")
+    p.add_argument("--compare", nargs=2)
+    a = p.parse_args(argv)
+    if a.compare:
+        return compare(json.loads(Path(a.compare[0]).read_text()), json.loads(Path(a.compare[1]).read_text()))
+    if not a.out:
+        p.error("--out or --compare is required")
+    if not torch.cuda.is_available():
+        print("dump_bits needs a GPU", file=sys.stderr)
+        return 2
+    d = dump(a.model)
+    Path(a.out).write_text(json.dumps(d, indent=1))
+    print(f"wrote {a.out}: {len(d['ops'])} op hashes, {len(d['model'])} model hashes")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,49 @@
+"""Bit-hash dump / compare tool (mlx_batch_invariant_amd.dump_bits): the
+compare report on hand-made dumps (CPU), and a real dump on the GPU, which
+must reproduce itself within one process and cover every op, dtype and mode."""
+
+import io
+import json
+
+import pytest
+
+from mlx_batch_invariant_amd import dump_bits as db
+
+
+def _d(ops, model=None, **meta):
+    return {"torch": "t", "hip": "h", "device": "d", "arch": "gfx950", "library": "x", **meta,
+            "ops": ops, "model": model or {}}
+
+
+def test_compare_counts_and_exit_code():
+    a = _d({"matmul/bf16/inv": "1", "matmul/bf16/stock": "2", "rms_norm/fp32/inv": "3"})
+    b = _d({"matmul/bf16/inv": "1", "matmul/bf16/stock": "9", "rms_norm/fp32/inv": "3"})
+    buf = io.StringIO()
+    assert db.compare(a, b, file=buf) == 0        # only a stock hash differs
+    text = buf.getvalue()
+    assert "ops    inv    identical: 2/2" in text and "ops    stock  identical: 0/1" in text
+    assert "differing: matmul/bf16/stock" in text
+    c = _d({"matmul/bf16/inv": "7", "matmul/bf16/stock": "2", "rms_norm/fp32/inv": "3"})
+    assert db.compare(a, c, file=io.StringIO()) == 1   # an invariant hash differs
+
+
+def test_compare_cli(tmp_path):
+    a, b = tmp_path / "a.json", tmp_path / "b.json"
+    a.write_text(json.dumps(_d({"matmul/bf16/inv": "1"}, {"llama2-bf16/decode/inv": "5"})))
+    b.write_text(json.dumps(_d({"matmul/bf16/inv": "1"}, {"llama2-bf16/decode/inv": "6"})))
+    assert db.main(["--compare", str(a), str(b)]) == 1
+    with pytest.raises(SystemExit):
+        db.main([])
+
+
+@pytest.mark.gpu
+def test_dump_reproduces_itself(tmp_path):
+    out = tmp_path / "bits.json"
+    assert db.main(["--out", str(out), "--model", "llama:1"]) == 0
+    d1 = json.loads(out.read_text())
+    d2 = db.dump("llama:1")
+    names = {"matmul", "addmm", "qmatmul_4b", "qmatmul_8b", "rms_norm", "sdpa_decode", "sdpa_prefill"}
+    assert {k.split("/")[0] for k in d1["ops"]} == names
+    assert len(d1["ops"]) == len(names) * 3 * 2 and len(d1["model"]) == 2 * 2 * 2
+    assert d1["ops"] == d2["ops"] and d1["model"] == d2["model"]
+    assert db.compare(d1, d2, file=io.StringIO()) == 0
