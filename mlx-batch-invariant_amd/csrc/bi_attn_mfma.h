@@ -21,6 +21,8 @@
 //           per lane (ds_read_b32).
 #pragma once
 
+#include <type_traits>
+
 #include "bi_attn_common.h"
 
 namespace bi {
@@ -366,7 +368,13 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   issue(0);
   issue(1);
   int ci = 0;
-  for (int sp = 0; sp < nsplit; ++sp) {
+  // A split entirely below every valid row's key limit needs no per-key mask
+  // (the wave's first row has the smallest limit; padding rows past npairs
+  // are never stored and MFMA rows do not interact): the same arithmetic on
+  // every active key, without the compares and selects.
+  const int wave_min_nkeys = __builtin_amdgcn_readfirstlane(nkeys_of(64 * wg + 16 * wave));
+  auto split_body = [&](const int sp, auto masked) {
+    constexpr bool MASKED = decltype(masked)::value;
     const int j0 = sp * kSplit;
     const int nkc = sp + 1 < nsplit ? 4 : nkc_last;
     // Scores of the wave's 16 rows against the split's keys (tile t: keys j0 + 16 t + ...).
@@ -384,7 +392,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = j0 + 64 * kc + 16 * t + 4 * qq + i;
-            s[4 * kc + t][i] = key < my_nkeys ? acc[i] * a.scale_log2 : -INFINITY;
+            s[4 * kc + t][i] = (!MASKED || key < my_nkeys) ? acc[i] * a.scale_log2 : -INFINITY;
           }
         }
         ++ci;
@@ -405,7 +413,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
 #pragma unroll
     for (int t = 0; t < 16; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[t][i] = split_weight(s[t][i], m, j0 + 16 * t + 4 * qq + i < my_nkeys);
+      for (int i = 0; i < 4; ++i) s[t][i] = split_weight(s[t][i], m, !MASKED || j0 + 16 * t + 4 * qq + i < my_nkeys);
 
     // P.V and the weight sum over the split's V chunks.
     f32x4 acc[NDT];
@@ -450,6 +458,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
         for (int dt = 0; dt < NDT; ++dt) A[dt][i] = ai[dt];
       }
     }
+  };
+  for (int sp = 0; sp < nsplit; ++sp) {
+    if (sp * kSplit + kSplit <= wave_min_nkeys) split_body(sp, std::false_type());
+    else split_body(sp, std::true_type());
   }
 
 #pragma unroll
