@@ -135,6 +135,16 @@ __device__ __forceinline__ void copy_to_lds16(const void* src, void* lds_block) 
   __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)lds_block, 16, 0, 0);
 }
 
+// s_waitcnt vmcnt(N) lgkmcnt(0); the empty asm statements keep the compiler
+// from moving memory accesses across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
+  asm volatile("" ::: "memory");
+}
+
 // Stage barrier: wait until at most N vector-memory operations of this wave
 // are outstanding (vmcnt counts global_load_lds copies until their data is in
 // LDS; they complete in issue order) and all of its LDS reads have returned,

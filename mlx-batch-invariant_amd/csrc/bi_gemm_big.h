@@ -67,16 +67,6 @@ constexpr int64_t kBigMaxLd = (int64_t)1 << 22;
 constexpr int kBigMinM = 256;
 constexpr int kBigMinTiles = 96;
 
-// s_waitcnt vmcnt(N) lgkmcnt(0); the empty asm statements keep the compiler
-// from moving memory accesses across it.
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0x0 << 8) | ((N >> 4) << 14));
-  asm volatile("" ::: "memory");
-}
-
 template <typename T>
 __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__ a, int64_t lda,
                                                            const T* __restrict__ bt, int64_t ldb,

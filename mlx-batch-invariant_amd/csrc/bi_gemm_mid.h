@@ -1,23 +1,27 @@
-// bi_gemm_mid.h — the mid-M launch (4 < M <= 64): every weight element is
-// read from HBM once and (for a quantized B) dequantized once, then used for
-// all M rows.
+// bi_gemm_mid.h — the mid-M launch (4 < M < 256, quantized B): every weight
+// element of a workgroup's column block and K chunk is read from HBM once and
+// dequantized once, then used for all of the block's rows.
 //
 // Same arithmetic as every other launch (bi_gemm_tile.h: the B source's k-slot
 // map, eight MFMA steps per 256-k group from zero, total = total + acc in group
 // order).
 //
-// One 256-thread workgroup per 64 output columns and up to 16 MT rows; wave w
-// owns columns 16 w .. 16 w + 15 of the block for the whole of K, so the group
-// fold stays in registers. Per group g:
+// One 256-thread workgroup per 64 output columns, 16 MT rows and a chunk of CG
+// consecutive 256-k groups; wave w owns columns 16 w .. 16 w + 15 of the block.
+// Per group g of the chunk:
 //   * A rows [m0, m0 + 16 MT) x k [256 g, 256 g + 256) sit in a ring of NA LDS
-//     buffers (8 groups for MT <= 2, 4 for MT = 4), copied by the
-//     load unit (global_load_lds_dwordx4, two 512-byte rows per instruction;
-//     16-byte chunk c of row r in slot c ^ (r & 15), so the 16 rows of a
-//     fragment read hit 16 distinct slots). Group g + NA - 1 is requested
-//     right after the barrier that opens group g.
+//     buffers, copied by the load unit (global_load_lds_dwordx4, two 512-byte
+//     rows per instruction; 16-byte chunk c of row r in slot c ^ (r & 15), so
+//     the 16 rows of a fragment read hit 16 distinct slots). Group g + NA - 1
+//     is requested right after the barrier that opens group g.
 //   * each wave's B operand (codes + scale/bias for a quantized B, the bf16/
 //     fp16 rows for a dense one) goes global -> registers PD groups ahead and
 //     is converted once per step, then multiplied with the MT A fragments.
+// With one chunk (CG = G) the group fold stays in registers and the kernel
+// writes the output; with several (SPLIT) every group's raw fp32 partial goes
+// to part[g][M][N] and fold_groups adds them in group order afterwards, so the
+// bits are the same either way. Splitting K only adds workgroups: it is the
+// launch's answer to too few column blocks (N <= 4096) to fill the chip.
 // Requirements (host policy): 2-byte T, K % 256 == 0, lda % 8 == 0, a 16-byte
 // aligned. Rows past M are clamped to row M - 1 (never stored); columns past N
 // to column N - 1 (never stored).
@@ -27,7 +31,7 @@
 
 namespace bi {
 
-template <typename T, int MT>
+template <typename T, int MT, int NA>
 struct MidCfg {
   static constexpr int kRows = 16 * MT;
   static constexpr int kRowBytes = kGroupK * (int)sizeof(T);      // 512
@@ -35,10 +39,10 @@ struct MidCfg {
   static constexpr int kCopies = kRows / kRowsPerCopy;             // per group
   static constexpr int kCopiesPerWave = kCopies / 4;
   static constexpr int kBufBytes = kRows * kRowBytes;
-  static constexpr int kRing = (128 * 1024 / kBufBytes) < 8 ? (128 * 1024 / kBufBytes) : 8;  // A groups in LDS
+  static constexpr int kRing = NA;                                 // A groups in LDS
   static_assert(sizeof(T) == 2, "gemm_mid: 2-byte element types only");
   static_assert(kCopies % 4 == 0, "gemm_mid: copies must split over 4 waves");
-  static_assert(kRing >= 2, "gemm_mid: at least two A buffers");
+  static_assert(kRing >= 2 && kRing * kBufBytes <= 160 * 1024, "gemm_mid: 2 or more A buffers within LDS");
   static __device__ __forceinline__ int off(int r, int c) { return r * kRowBytes + ((c ^ (r & 15)) << 4); }
 };
 
@@ -51,12 +55,11 @@ template <typename T, int BITS, int GS> struct MidLoads<QuantB<T, BITS, GS>> {
   static constexpr int kMin = QuantB<T, BITS, GS>::kWords / 4 + 2;
 };
 
-template <typename T, class BSrc, int MT, int PD>
+template <typename T, class BSrc, int MT, int PD, int NA, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bsrc, T* __restrict__ out,
-                                                int M, int N, int K, int G) {
-  typedef MidCfg<T, MT> C;
+                                                float* __restrict__ part, int M, int N, int K, int G, int CG) {
+  typedef MidCfg<T, MT, NA> C;
   typedef typename Frag<T>::type F;
-  constexpr int NA = C::kRing;
   // Outstanding vector-memory instructions that are certainly issued after
   // the copies of group g when its barrier is reached (copies of NA - 2 later
   // groups and at least min(PD, NA - 1) groups of B loads): waiting down to
@@ -75,10 +78,12 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
   const int n_out = blockIdx.x * 64 + 16 * wave + r;
   const int n = min(n_out, N - 1);
   const typename BSrc::Lane bl = bsrc.lane(n, q);
+  const int gb = blockIdx.z * CG;             // the chunk's first group
+  const int gn = min(CG, G - gb);             // and its group count (>= 1)
 
-  auto copy_a = [&](int g) {  // group min(g, G - 1) into buffer g % NA
-    char* buf = As[g % NA];
-    const int gg = min(g, G - 1);
+  auto copy_a = [&](int j) {  // chunk group min(j, gn - 1) into buffer j % NA
+    char* buf = As[j % NA];
+    const int gg = gb + min(j, gn - 1);
 #pragma unroll
     for (int i = 0; i < C::kCopiesPerWave; ++i) {
       const int ci = wave * C::kCopiesPerWave + i;
@@ -102,23 +107,24 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
 #pragma unroll
   for (int j = 0; j < PD; ++j) {
     asm volatile("" ::: "memory");
-    bsrc.load_full(raw[j], bl, min(j, G - 1));
+    bsrc.load_full(raw[j], bl, gb + min(j, gn - 1));
   }
   asm volatile("" ::: "memory");
 
-  // One group: wait for its A, request A of group g + NA - 1, compute, fold,
-  // request B of group g + PD into the registers it released.
-  auto group = [&](int g, int j) {
-    // Group g's A landed for every wave; every wave is past group g - 1,
-    // whose buffer now takes group g + NA - 1.
+  // One chunk group l: wait for its A, request A of group l + NA - 1,
+  // compute, fold (or store the partial), request B of group l + PD into the
+  // registers it released.
+  auto group = [&](int l, int j) {
+    // Group l's A landed for every wave; every wave is past group l - 1,
+    // whose buffer now takes group l + NA - 1.
     stage_barrier<kWaitA>();
-    copy_a(g + NA - 1);
+    copy_a(l + NA - 1);
     asm volatile("" ::: "memory");
-    const char* buf = As[g % NA];
+    const char* buf = As[l % NA];
     f32x4 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const int gc = min(g, G - 1);
+    const int gc = gb + min(l, gn - 1);
     const int kq = BSrc::kbase(gc, q);
     auto steps = [&](auto fast) {
 #pragma unroll
@@ -134,29 +140,44 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
     };
     if (!__any(bsrc.huge_scale(raw[j]))) steps(std::true_type());
     else steps(std::false_type());
-    const bool live = g < G;
+    const bool live = l < gn;
+    if constexpr (SPLIT) {
+      if (live && n_out < N) {
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const f32x4 t = total[i] + acc[i];
-      total[i] = live ? t : total[i];
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int m = m0 + 16 * i + 4 * q + e;
+            if (m < M) part[((int64_t)gc * M + m) * N + n_out] = acc[i][e];
+          }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const f32x4 t = total[i] + acc[i];
+        total[i] = live ? t : total[i];
+      }
     }
     asm volatile("" ::: "memory");
-    bsrc.load_full(raw[j], bl, min(g + PD, G - 1));
+    bsrc.load_full(raw[j], bl, gb + min(l + PD, gn - 1));
     asm volatile("" ::: "memory");
   };
   // A whole number of PD-group rounds (padding groups recompute the last group
   // and are not folded), the first one peeled: the loop body then has no
   // branch around memory instructions and the loop is entered from a state
   // shaped like its own back edge, so the compiler's wait counts stay exact.
-  const int Gp = (G + PD - 1) / PD * PD;
+  const int Gp = (gn + PD - 1) / PD * PD;
 #pragma unroll
   for (int j = 0; j < PD; ++j) group(j, j);
-  for (int g0 = PD; g0 < Gp; g0 += PD) {
+  for (int l0 = PD; l0 < Gp; l0 += PD) {
 #pragma unroll
-    for (int j = 0; j < PD; ++j) group(g0 + j, j);
+    for (int j = 0; j < PD; ++j) group(l0 + j, j);
   }
+  // The ring's last requests (past the chunk they repeat its last group) are
+  // still in flight: drain them before the workgroup's LDS can be reused.
+  wait_vm_lgkm0<0>();
 
-  if (n_out < N) {
+  if (!SPLIT && n_out < N) {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll

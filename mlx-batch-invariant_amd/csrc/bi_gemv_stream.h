@@ -25,7 +25,10 @@
 // here a wave waits only for its own.
 //
 // LDS (dynamic): G * 64 f32x4 partials, then per wave: A [MR][NB * 256],
-// scales [16][SPR], biases [16][SPR] (SPR = NB * 256 / GS).
+// scales [16][SPR], biases [16][SPR] (SPR = NB * 256 / GS). A's 8-element
+// chunk c of row r sits in slot c ^ (r & 15) of its row, so the 16 rows of a
+// fragment read (same chunk, row stride a multiple of 256 bytes) hit 16
+// distinct bank groups instead of one.
 #pragma once
 
 #include "bi_gemm_tile.h"
@@ -41,6 +44,12 @@ struct GemvStreamCfg {
   static constexpr int kMChunks = 2 * 16 * kSPR / kCE;        // meta chunks per wave
   static constexpr int kMLoads = (kMChunks + kWave - 1) / kWave;
   static constexpr int kWaveElems = kAElems + 2 * 16 * kSPR;  // LDS elements per wave
+  static constexpr int kRowElems = NB * kGroupK;               // A row of the wave's slice
+  // LDS element offset of A element k (0 <= k < kRowElems) of slice row ar.
+  static __device__ __forceinline__ int a_off(int ar, int k) {
+    return ar * kRowElems + ((((k >> 3) ^ (ar & 15))) << 3) + (k & 7);
+  }
+  static_assert(sizeof(T) == 2, "gemv_stream: 2-byte element types only (16-byte pieces = one fragment)");
   static_assert(kAElems % (kCE * kWave) == 0, "A slice must be whole 16-byte loads per lane");
   static_assert(kSPR % kCE == 0, "scale rows must be whole 16-byte chunks");
   static size_t lds_bytes(int G) {
@@ -97,7 +106,11 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   for (int j = 0; j < PD && j < NB; ++j) bsrc.load_codes(braw[j], bl, g0 + j);
   // Wave-private LDS: written and read back by this wave only.
 #pragma unroll
-  for (int i = 0; i < C::kALoads; ++i) *reinterpret_cast<F*>(As + (lane + kWave * i) * C::kCE) = av[i];
+  for (int i = 0; i < C::kALoads; ++i) {
+    const int c = lane + kWave * i;
+    const int ar = c / (NB * kGroupK / C::kCE), ac = (c % (NB * kGroupK / C::kCE)) * C::kCE;
+    *reinterpret_cast<F*>(As + C::a_off(ar, ac)) = av[i];
+  }
 #pragma unroll
   for (int i = 0; i < C::kMLoads; ++i) {
     const int c = lane + kWave * i;
@@ -124,7 +137,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     F af[1][kSteps];
 #pragma unroll
     for (int s = 0; s < kSteps; ++s)
-      af[0][s] = *reinterpret_cast<const F*>(As + arow * (NB * kGroupK) + j * kGroupK + 64 * q + 8 * s);
+      af[0][s] = *reinterpret_cast<const F*>(As + C::a_off(arow, j * kGroupK + 64 * q + 8 * s));
     f32x4 acc[1];
     mma_group<T, QB, 1, true>(bsrc, braw[j], af, g, q, acc);
     part[g * kWave + lane] = acc[0];

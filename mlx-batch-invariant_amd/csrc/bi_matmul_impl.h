@@ -37,6 +37,7 @@
 namespace bi {
 
 constexpr int kSplitMMax = 32;
+constexpr int kStreamMMax = 16;   // rows the streaming GEMV's one 16-row MFMA tile covers
 // gemv_wg with A staged in LDS: at most kGemvAChunks / W 16-byte chunks of A
 // per thread (M * K <= kGemvAChunks * 64 * 8).
 constexpr int kGemvAChunks = 32;
@@ -679,7 +680,9 @@ template <typename T, int BITS, int GS, int W, int NB, int MR, int PD>
 static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
                            int K, int G, hipStream_t st) {
   constexpr int kCE = 16 / (int)sizeof(T);
-  if constexpr ((NB * kGroupK / GS) % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0) {
+  // 2-byte T only: the kernel's 16-byte staging pieces are whole 8-element
+  // fragments only there.
+  if constexpr (sizeof(T) != 2 || (NB * kGroupK / GS) % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0) {
     return false;
   } else {
     if (G != W * NB) return false;
@@ -694,7 +697,9 @@ template <typename T, int BITS, int GS, int W, int NB, int PD>
 static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
                             int K, int G, hipStream_t st) {
   if (M == 1) return launch_stream1<T, BITS, GS, W, NB, 1, PD>(a, lda, b, out, M, N, K, G, st);
-  return launch_stream1<T, BITS, GS, W, NB, 4, PD>(a, lda, b, out, M, N, K, G, st);
+  if (M <= 4) return launch_stream1<T, BITS, GS, W, NB, 4, PD>(a, lda, b, out, M, N, K, G, st);
+  if (M <= 8) return launch_stream1<T, BITS, GS, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
+  return launch_stream1<T, BITS, GS, W, NB, 16, PD>(a, lda, b, out, M, N, K, G, st);
 }
 
 // Launch shapes in order of preference (measured, Llama MLP shape, M = 1):
@@ -704,7 +709,7 @@ static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& 
 template <typename T, int BITS, int GS>
 static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N, int K,
                           int G, hipStream_t st) {
-  if (M > 4 || K % kGroupK || (G != 4 && G != 8 && G != 16)) return false;
+  if (M > kStreamMMax || K % kGroupK || (G != 4 && G != 8 && G != 16)) return false;
   if (b.groups_per_row % (16 / (int)sizeof(T)) || !bi_host::aligned16(b.scales) || !bi_host::aligned16(b.biases) ||
       lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a))
     return false;
@@ -760,28 +765,72 @@ static void launch_wg(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, 
   else gemv_wg<T, BSrc, 2, W, 2, false><<<grid, kWave * W, part_bytes, st>>>(a, lda, bsrc, out, M, N, K, G);
 }
 
-// Mid-M launch (bi_gemm_mid.h): quantized B with 4 < M <= 64, 2-byte T,
-// whole groups, and enough 64-column blocks to fill the chip.
+// Mid-M launch (bi_gemm_mid.h) for a quantized B, 2-byte T, K % 256 == 0:
+// 16 < M < kBigMinM at any N, and 4 < M <= 16 with >= 128 blocks of 64
+// columns. Row blocks of 16 MT rows (MT = 1, 2, 4; M > 64 takes several);
+// when the (column block, row block) tiles are fewer than kMidMinTiles, K is
+// split into chunks of cg groups (per-group fp32 partials in the workspace,
+// then fold_groups) so that about kMidTargetWG workgroups run.
+constexpr int kMidMinTiles = 160;
+constexpr int kMidTargetWG = 512;
+struct MidPlan {
+  bool use = false;
+  int mt = 1, mtiles = 1, chunks = 1, cg = 0;
+};
+static inline MidPlan mid_plan(int64_t M, int64_t N, int64_t K) {
+  MidPlan p;
+  if (M <= 4 || M >= kBigMinM || N <= 0 || K <= 0 || K % kGroupK) return p;
+  if (M <= 16 && ceil_div(N, 64) < 128) return p;
+  const int G = (int)(K / kGroupK);
+  p.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  p.mtiles = (int)ceil_div(M, 16 * p.mt);
+  const int64_t t = ceil_div(N, 64) * p.mtiles;
+  p.cg = G;
+  if (t < kMidMinTiles && G > 1) {
+    const int want = (int)std::min<int64_t>(G, ceil_div(kMidTargetWG, t));
+    p.cg = ceil_div(G, want);
+    p.chunks = ceil_div(G, p.cg);
+  }
+  p.use = true;
+  return p;
+}
+
 template <typename T, class BSrc>
-static bool use_mid(int M, int N, int K, int64_t lda, const T* a) {
+static bool use_mid(const MidPlan& p, int64_t lda, const T* a) {
   if constexpr (sizeof(T) != 2 || !BSrc::kMeta) {
     return false;
   } else {
-    return M > 4 && M <= 64 && K % kGroupK == 0 && lda % 8 == 0 && bi_host::aligned16(a) &&
-           ceil_div(N, 64) >= 128;
+    return p.use && lda % 8 == 0 && bi_host::aligned16(a);
+  }
+}
+
+// Unsplit (at most about one workgroup per CU): the deepest A ring that fits
+// and B loads 8 groups ahead. Split K: short chunks and several workgroups
+// per CU, so a shallow ring and B loads kMidSplitPD groups ahead (a chunk runs
+// in whole rounds of that many groups; the padding groups are not folded).
+constexpr int kMidSplitPD = 2;
+template <typename T, class BSrc, int MT, int NA_ONE, int NA_SPLIT>
+static void launch_mid2(const T* a, int64_t lda, const BSrc& bsrc, T* out, float* ws, int M, int N, int K,
+                        int G, const MidPlan& p, hipStream_t st) {
+  constexpr int PD = 8;
+  const dim3 grid(ceil_div(N, 64), p.mtiles, p.chunks);
+  if (p.chunks > 1) {
+    gemm_mid<T, BSrc, MT, kMidSplitPD, NA_SPLIT, true><<<grid, 256, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G,
+                                                                             p.cg);
+    const int64_t MN = (int64_t)M * N;
+    fold_groups<T><<<(unsigned)((MN + 255) / 256), 256, 0, st>>>(ws, out, MN, G);
+  } else {
+    gemm_mid<T, BSrc, MT, PD, NA_ONE, false><<<grid, 256, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G, G);
   }
 }
 
 template <typename T, class BSrc>
-static void launch_mid(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K, int G,
-                       hipStream_t st) {
+static void launch_mid(const T* a, int64_t lda, const BSrc& bsrc, T* out, float* ws, int M, int N, int K,
+                       int G, const MidPlan& p, hipStream_t st) {
   if constexpr (sizeof(T) == 2 && BSrc::kMeta) {
-    constexpr int PD = 8;
-    const int mt = ceil_div(M, 16);
-    dim3 grid(ceil_div(N, 64), 1, 1);
-    if (mt <= 1) gemm_mid<T, BSrc, 1, PD><<<grid, 256, 0, st>>>(a, lda, bsrc, out, M, N, K, G);
-    else if (mt <= 2) gemm_mid<T, BSrc, 2, PD><<<grid, 256, 0, st>>>(a, lda, bsrc, out, M, N, K, G);
-    else gemm_mid<T, BSrc, 4, PD><<<grid, 256, 0, st>>>(a, lda, bsrc, out, M, N, K, G);
+    if (p.mt == 1) launch_mid2<T, BSrc, 1, 8, 4>(a, lda, bsrc, out, ws, M, N, K, G, p, st);
+    else if (p.mt == 2) launch_mid2<T, BSrc, 2, 8, 4>(a, lda, bsrc, out, ws, M, N, K, G, p, st);
+    else launch_mid2<T, BSrc, 4, 4, 2>(a, lda, bsrc, out, ws, M, N, K, G, p, st);
   }
 }
 
@@ -790,9 +839,17 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
                     float* ws, hipStream_t st, const char* what) {
   const int G = ceil_div(K, kGroupK);
   constexpr int WAVES = 4;
-  if (use_mid<T, BSrc>(M, N, K, lda, a)) {
-    launch_mid<T, BSrc>(a, lda, bsrc, out, M, N, K, G, st);
-    return bi_host::launch_status(what);
+  if constexpr (BSrc::kMeta) {
+    if (M > 4 && ceil_div(N, 16) >= 512 && G >= 8 &&
+        launch_stream<T, BSrc::kBits, BSrc::kGS>(a, lda, bsrc, out, M, N, K, G, st))
+      return bi_host::launch_status(what);
+  }
+  if constexpr (BSrc::kMeta) {
+    const MidPlan mp = mid_plan(M, N, K);
+    if (use_mid<T, BSrc>(mp, lda, a)) {
+      launch_mid<T, BSrc>(a, lda, bsrc, out, ws, M, N, K, G, mp, st);
+      return bi_host::launch_status(what);
+    }
   }
   if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
     const TallPlan tp = tall_plan(M, N, K);

@@ -41,7 +41,12 @@ def test_workspace_sizes():
     assert lib.bi_matmul_workspace_bytes(64, 4096, 14336) == 0       # 16-column tiles fill the chip
     assert lib.bi_matmul_workspace_bytes(64, 1024, 4096) == 16 * 64 * 1024 * 4   # 4 chunks of 4 groups
     assert lib.bi_matmul_workspace_bytes(129, 100, 896) == 0         # fused (LDS tiles)
-    assert lib.bi_quantized_matmul_workspace_bytes(32, 100, 896) == 0   # no mid-M split for quantized B
+    assert lib.bi_quantized_matmul_workspace_bytes(32, 100, 896) == 0   # quantized mid-M needs whole groups
+    # quantized mid-M with too few (64-column, row block) tiles splits K: ~512 workgroups
+    assert lib.bi_quantized_matmul_workspace_bytes(64, 4096, 14336) == 56 * 64 * 4096 * 4   # 8 chunks of 7
+    assert lib.bi_quantized_matmul_workspace_bytes(17, 1024, 4096) == 16 * 17 * 1024 * 4    # 16 chunks of 1
+    assert lib.bi_quantized_matmul_workspace_bytes(64, 14336, 4096) == 0    # 224 column blocks: no split
+    assert lib.bi_quantized_matmul_workspace_bytes(8, 1024, 4096) == 0      # GEMV launch, LDS fold
     assert lib.bi_matmul_workspace_bytes(8, 100, 256) == 0           # one group
     assert lib.bi_quantized_matmul_workspace_bytes(4, 14336, 4096) == 0
     # large M: dequantized weight + reordered activations, 2 bytes each

@@ -112,6 +112,62 @@ def test_quantized_mid_m_launch_matches_oracle(bits_, gs, dt):
 
 
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_quantized_stream_launch_up_to_16_rows(bits_, gs, dt):
+    """M <= 16 with >= 512 tiles of 16 columns and 8 or 16 groups takes the
+    streaming GEMV for 2-byte types (one 16-row MFMA tile, A rows past M
+    clamped; fp32 takes the workgroup-fold GEMV): rows equal the oracle within
+    the stated bound and the same rows computed alone, bit for bit."""
+    N, K = 8192 + 40, 4096     # 515 column tiles, the last one partial; G = 16
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 3 + gs)
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    x = randn((16, K), DT[dt], gen(13))
+    run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+    W = ora.dequantize(wq.cpu().view(torch.int32).numpy().view(np.uint32), to_np(s.cpu()), to_np(b.cpu()),
+                       gs, bits_, dt)
+    cols = np.r_[0:24, 4100:4124, N - 24:N]
+    for M in (1, 4, 5, 8, 9, 16):
+        got = run(x[:M])
+        rows = sorted({0, M // 2, M - 1})
+        want = ora.matmul(to_np(x[rows]), W[cols], dt, kmap="blocked")
+        g = to_np(got)[rows][:, cols]
+        atol = ora.matmul_error_bound(to_np(x[rows]), W[cols])
+        assert ora.max_ulp_excess(g, want, dt, atol=atol) <= 1.0, (M, ora.isclose_report(g, want))
+        for rr in rows:
+            assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
+
+
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_quantized_mid_m_split_k_matches_oracle(bits_, gs, dt):
+    """Few column blocks (N = 4136: 65 blocks of 64) make the mid-M launch split
+    K into chunks (15 groups: 8 chunks of 2, the last of 1) with per-group
+    partials folded afterwards; M = 200 (four 64-row blocks, 260 tiles) runs
+    unsplit. Rows equal the oracle within the stated bound and the same rows
+    computed alone, bit for bit."""
+    N, K = 4096 + 40, 15 * 256
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 5 + gs + 1)
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    from mlx_batch_invariant_amd import _lib
+    assert _lib.load().bi_quantized_matmul_workspace_bytes(64, N, K) == 15 * 64 * N * 4
+    assert _lib.load().bi_quantized_matmul_workspace_bytes(200, N, K) == 0
+    x = randn((200, K), DT[dt], gen(17))
+    run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+    W = ora.dequantize(wq.cpu().view(torch.int32).numpy().view(np.uint32), to_np(s.cpu()), to_np(b.cpu()),
+                       gs, bits_, dt)
+    cols = np.r_[0:24, 2050:2074, N - 24:N]
+    for M in (17, 33, 64, 200):
+        got = run(x[:M])
+        rows = sorted({0, M // 2, M - 1})
+        want = ora.matmul(to_np(x[rows]), W[cols], dt, kmap="blocked")
+        g = to_np(got)[rows][:, cols]
+        atol = ora.matmul_error_bound(to_np(x[rows]), W[cols])
+        assert ora.max_ulp_excess(g, want, dt, atol=atol) <= 1.0, (M, ora.isclose_report(g, want))
+        for rr in rows:
+            assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
+
+
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_quantized_large_m_launch_agrees(bits_, gs, dt):
     """Large M takes the dequantize-once launch (weights dequantized into the
