@@ -85,9 +85,12 @@ int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out
  * w is contiguous uint32 [N, K*bits/32]; scales, biases contiguous
  * [N, K/group_size]. bits in {4, 8}, group_size in {32, 64, 128},
  * K % group_size == 0. x rows are ldx elements apart (ldx % 8 == 0).
- * Workspace (bi_quantized_matmul_workspace_bytes): fp32 group partials for
- * small M; for large M with K % 256 == 0 (bf16/fp16) the dequantized weight
- * and a reordered copy of x, (N + M) * K elements of 2 bytes.
+ * Workspace (bi_quantized_matmul_workspace_bytes): fp32 group partials
+ * [K/256, M, N] for small M and for mid M (M < 256, K % 256 == 0) when there
+ * are too few 64-column blocks to fill the GPU; for large M with
+ * K % 256 == 0 (bf16/fp16) the dequantized weight and a reordered copy of x,
+ * (N + M) * K elements of 2 bytes. The query has no dtype: it reports the
+ * need of the 2-byte launches, which an fp32 call also accepts.
  * Replaces: kernels/quantized.py:106-125 (batch_invariant_quantized_matmul),
  * kernels :33-67 (dequant-on-stage). */
 size_t bi_quantized_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K);
