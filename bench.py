@@ -268,6 +268,31 @@ def bench_rmsnorm(args):
             "algorithmic_bytes": "4*R*D + 2*D (read x, write out, read gamma)", "per_shape": res}
 
 
+def bench_layernorm(args):
+    """LayerNorm (no kernel in the reference; its roadmap item) at the RMSNorm
+    bench's HBM-bound shapes, weight and bias given, against F.layer_norm."""
+    import torch
+    import mlx_batch_invariant_amd as bi
+    g = torch.Generator().manual_seed(0)
+    res = {}
+    for R, D in ((16384, 4096), (65536, 4096)):
+        x = torch.randn((R, D), generator=g).to(torch.bfloat16).cuda()
+        gam = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+        bet = (0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+        t = statistics.median(_time_calls(lambda i: bi.batch_invariant_layer_norm(x, gam, bet, 1e-5),
+                                          args.steps, args.warmup, 1))
+        by = 4 * R * D + 4 * D
+        e = {"us": round(t * 1e6, 2), "GBps": round(by / t / 1e9, 1), "frac_hbm": round(by / t / PEAK_HBM, 4)}
+        if not args.headline_only:
+            ts = statistics.median(_time_calls(lambda i: torch.nn.functional.layer_norm(x, (D,), gam, bet, 1e-5),
+                                               args.steps, args.warmup, 1))
+            e["stock_us"] = round(ts * 1e6, 2)
+        res[f"{R}x{D}"] = e
+        del x
+    return {"metric": METRIC, "op": "layer_norm (bf16, eps 1e-5, weight and bias)", "kernel": "layer_norm_kernel",
+            "algorithmic_bytes": "4*R*D + 4*D (read x, write out, read gamma and beta)", "per_shape": res}
+
+
 def bench_decode(args):
     """split-KV decode, GQA 32/8, D 128, ragged lengths."""
     import numpy as np
@@ -422,7 +447,8 @@ def main(argv=None) -> int:
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--op", default="qmm4", choices=["qmm4", "qmm8", "linear", "rmsnorm", "decode", "prefill", "gemm", "llama", "copycal", "all"])
+    p.add_argument("--op", default="qmm4", choices=["qmm4", "qmm8", "linear", "rmsnorm", "layernorm", "decode", "prefill", "gemm", "llama",
+                                                     "copycal", "all"])
     p.add_argument("--llama-layers", type=int, default=32)
     p.add_argument("--llama-prompt", type=int, default=512)
     p.add_argument("--llama-steps", type=int, default=128)
@@ -441,7 +467,7 @@ def main(argv=None) -> int:
         return 2
     import mlx_batch_invariant_amd as bi
     bi._lib.load()
-    ops = ["qmm4", "qmm8", "linear", "rmsnorm", "decode", "prefill", "gemm"] if a.op == "all" else [a.op]
+    ops = ["qmm4", "qmm8", "linear", "rmsnorm", "layernorm", "decode", "prefill", "gemm"] if a.op == "all" else [a.op]
     for op in ops:
         if op == "qmm4":
             r = bench_qmm(a, 4, 64)
@@ -451,6 +477,8 @@ def main(argv=None) -> int:
             r = bench_linear(a)
         elif op == "rmsnorm":
             r = bench_rmsnorm(a)
+        elif op == "layernorm":
+            r = bench_layernorm(a)
         elif op == "decode":
             r = bench_decode(a)
         elif op == "prefill":

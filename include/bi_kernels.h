@@ -63,6 +63,17 @@ int bi_split_m_max(void);
 int bi_rms_norm(const void* x, int64_t x_row_stride, const void* w, void* out,
                 int64_t rows, int64_t D, float eps, int dtype, void* stream);
 
+/* ---- LayerNorm over the last dimension -------------------------------------
+ * out = T(((x - mean) * inv) * w + b) per row, mean and the biased variance
+ * in a fixed two-pass order that depends on D only; w and b may be NULL (the
+ * multiply / add is then skipped). x rows are x_row_stride elements apart; out
+ * is contiguous [rows, D].
+ * Replaces: nothing in the reference's kernels (it falls back to the stock
+ * mx.fast.layer_norm, README.md:250-251); its roadmap item "a batch-invariant
+ * mx.fast.layer_norm" (README.md:257-260). */
+int bi_layer_norm(const void* x, int64_t x_row_stride, const void* w, const void* b, void* out,
+                  int64_t rows, int64_t D, float eps, int dtype, void* stream);
+
 /* ---- Dense matmul ---------------------------------------------------------
  * out[M, N] = a[M, K] @ b[K, N], with b given transposed: element b[k, n] is at
  * bt[n * ldb + k] (the k-contiguous nn.Linear weight layout). a rows are lda
@@ -77,6 +88,19 @@ size_t bi_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out,
               int64_t M, int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes,
               void* stream);
+
+/* Strided batch of dense matmuls (a [batch][M, K], bt [batch][N, K],
+ * out [batch][M, N]; batch strides in elements, 0 broadcasts a or bt): slice i
+ * is exactly bi_matmul on the slice's pointers, so its bits equal a 2-D call
+ * and do not depend on batch. Same requirements and workspace as bi_matmul
+ * (shared by the slices, which run in order on the stream).
+ * Replaces: the reference's fallback for a non-2-D right-hand side
+ * (ops.py:46-51, "matmul:non-2d-rhs-or-non-float"); its roadmap's batched
+ * matmul (README.md:257-268). */
+int bi_matmul_batched(const void* a, int64_t a_batch_stride, int64_t lda, const void* bt,
+                      int64_t b_batch_stride, int64_t ldb, void* out, int64_t out_batch_stride,
+                      int64_t batch, int64_t M, int64_t N, int64_t K, int dtype, void* ws,
+                      size_t ws_bytes, void* stream);
 
 /* ---- Affine quantized matmul (MLX packed format) ---------------------------
  * out[M, N] = x[M, K] @ W^T with W[n, k] = T(fmaf(code(n,k), scale, bias)),

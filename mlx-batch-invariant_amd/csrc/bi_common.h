@@ -123,6 +123,42 @@ __device__ __forceinline__ float wave_sum_butterfly(float v) {
   return v;
 }
 
+// Eight consecutive elements of a row as fp32 (one 16-byte load for 2-byte
+// types, two for fp32), and back with round-to-nearest-even stores.
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float* out) {
+  if constexpr (sizeof(T) == 2) {
+    u32x4 raw = *reinterpret_cast<const u32x4*>(p);
+    const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = (float)e[i];
+  } else {
+    f32x4 a = *reinterpret_cast<const f32x4*>(p);
+    f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[i] = a[i];
+      out[4 + i] = b[i];
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float* in) {
+  if constexpr (sizeof(T) == 2) {
+    u32x4 raw;
+    T* e = reinterpret_cast<T*>(&raw);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = to_store<T>(in[i]);
+    *reinterpret_cast<u32x4*>(p) = raw;
+  } else {
+    f32x4 a = {in[0], in[1], in[2], in[3]};
+    f32x4 b = {in[4], in[5], in[6], in[7]};
+    *reinterpret_cast<f32x4*>(p) = a;
+    *reinterpret_cast<f32x4*>(p + 4) = b;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Direct global -> LDS copies (global_load_lds_dwordx4) and the barrier that
 // waits for them.

@@ -96,6 +96,30 @@ extern "C" int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb
   }
 }
 
+// Strided batch of independent matmuls: slice i is exactly bi_matmul on
+// a + i * a_batch_stride, bt + i * b_batch_stride, out + i * out_batch_stride
+// (element strides; 0 broadcasts an operand). The slices run one after the
+// other on the stream and share the workspace.
+extern "C" int bi_matmul_batched(const void* a, int64_t a_batch_stride, int64_t lda, const void* bt,
+                                 int64_t b_batch_stride, int64_t ldb, void* out, int64_t out_batch_stride,
+                                 int64_t batch, int64_t M, int64_t N, int64_t K, int dtype, void* ws,
+                                 size_t ws_bytes, void* stream) {
+  using namespace bi_host;
+  if (batch < 0) return fail(BI_E_INVALID_ARG, "bi_matmul_batched: batch=%lld", (long long)batch);
+  if (a_batch_stride < 0 || b_batch_stride < 0 || out_batch_stride < M * N)
+    return fail(BI_E_INVALID_ARG, "bi_matmul_batched: negative batch stride or out_batch_stride < M*N");
+  if (dtype != BI_BF16 && dtype != BI_F16 && dtype != BI_F32)
+    return fail(BI_E_UNSUPPORTED, "bi_matmul_batched: unknown dtype %d", dtype);
+  const size_t es = dtype == BI_F32 ? 4 : 2;
+  for (int64_t i = 0; i < batch; ++i) {
+    const char* ai = static_cast<const char*>(a) + (size_t)(i * a_batch_stride) * es;
+    const char* bi_ = static_cast<const char*>(bt) + (size_t)(i * b_batch_stride) * es;
+    char* oi = static_cast<char*>(out) + (size_t)(i * out_batch_stride) * es;
+    const int rc = bi_matmul(ai, lda, bi_, ldb, oi, M, N, K, dtype, ws, ws_bytes, stream);
+    if (rc) return rc;
+  }
+  return BI_OK;
+}
 
 extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w,
                                    const void* scales, const void* biases, void* out, int64_t M,

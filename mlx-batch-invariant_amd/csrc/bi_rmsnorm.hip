@@ -23,45 +23,6 @@ namespace bi {
 constexpr int kNormThreads = 256;
 constexpr int kNormVec = 8;
 
-template <typename T>
-struct Vec8 {
-  float v[8];
-};
-
-template <typename T>
-__device__ __forceinline__ void load8(const T* p, float* out) {
-  if constexpr (sizeof(T) == 2) {
-    u32x4 raw = *reinterpret_cast<const u32x4*>(p);
-    const T* e = reinterpret_cast<const T*>(&raw);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = (float)e[i];
-  } else {
-    f32x4 a = *reinterpret_cast<const f32x4*>(p);
-    f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      out[i] = a[i];
-      out[4 + i] = b[i];
-    }
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void store8(T* p, const float* in) {
-  if constexpr (sizeof(T) == 2) {
-    u32x4 raw;
-    T* e = reinterpret_cast<T*>(&raw);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = to_store<T>(in[i]);
-    *reinterpret_cast<u32x4*>(p) = raw;
-  } else {
-    f32x4 a = {in[0], in[1], in[2], in[3]};
-    f32x4 b = {in[4], in[5], in[6], in[7]};
-    *reinterpret_cast<f32x4*>(p) = a;
-    *reinterpret_cast<f32x4*>(p + 4) = b;
-  }
-}
-
 // NC = chunks each thread keeps in registers (D <= NC * 2048); VECTOR selects
 // 16-byte loads (needs D % 8 == 0 and 16-byte aligned rows). The scalar path
 // walks exactly the same elements in the same order.

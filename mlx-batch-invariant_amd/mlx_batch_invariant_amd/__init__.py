@@ -15,6 +15,8 @@ from .kernels import (
     batch_invariant_attention,
     batch_invariant_decode_attention,
     batch_invariant_prefill_attention,
+    batch_invariant_bmm,
+    batch_invariant_layer_norm,
     batch_invariant_matmul,
     batch_invariant_quantized_matmul,
     batch_invariant_rms_norm,
@@ -27,7 +29,9 @@ __all__ = [
     "stats",
     "reset_stats",
     "batch_invariant_matmul",
+    "batch_invariant_bmm",
     "batch_invariant_rms_norm",
+    "batch_invariant_layer_norm",
     "batch_invariant_quantized_matmul",
     "batch_invariant_decode_attention",
     "batch_invariant_prefill_attention",

@@ -36,9 +36,13 @@ _SIGNATURES = {
     "bi_last_error": (ctypes.c_char_p, []),
     "bi_split_m_max": (ctypes.c_int, []),
     "bi_rms_norm": (ctypes.c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, ctypes.c_float, ctypes.c_int, _vp]),
+    "bi_layer_norm": (ctypes.c_int, [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, ctypes.c_float, ctypes.c_int,
+                                     _vp]),
     "bi_matmul_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
     "bi_matmul": (ctypes.c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
                                  _vp, ctypes.c_size_t, _vp]),
+    "bi_matmul_batched": (ctypes.c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64,
+                                         _c_i64, _c_i64, ctypes.c_int, _vp, ctypes.c_size_t, _vp]),
     "bi_quantized_matmul_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
     "bi_quantized_matmul": (ctypes.c_int, [_vp, _c_i64, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64,
                                            ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t, _vp]),

@@ -97,3 +97,61 @@ def batch_invariant_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         b = b.to(out_dtype)
     out = matmul_bt(a2, b.t())
     return out.reshape(*lead, N)
+
+
+def _prep_batched(t: torch.Tensor, K8: int) -> torch.Tensor:
+    """[Bt, R, K] -> rows k-contiguous, 16-byte aligned, padded to K8, with one
+    batch stride (0 kept for a broadcast operand)."""
+    Bt, R, K = t.shape
+    es = t.element_size()
+    ok = (K8 == K and t.stride(2) == 1 and t.stride(1) >= K and (t.stride(1) * es) % 16 == 0
+          and (t.stride(0) * es) % 16 == 0 and t.data_ptr() % 16 == 0)
+    if ok:
+        return t
+    out = torch.zeros((Bt, R, K8), dtype=t.dtype, device=t.device)
+    out[:, :, :K] = t
+    return out
+
+
+def batch_invariant_bmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """``a @ b`` for ``a [..., M, K]`` and ``b [..., K, N]`` with broadcast batch
+    dims (``torch.matmul`` semantics for operands of 2 or more dims).
+
+    Every batch slice is computed exactly as the 2-D ``batch_invariant_matmul``
+    of that slice, so its bits depend neither on M nor on the batch. The
+    reference falls back for a non-2-D right-hand side (ops.py:46-51); its
+    roadmap lists the batched matmul (README.md:257-268).
+    """
+    if a.ndim < 2 or b.ndim < 2:
+        raise ValueError("batch_invariant_bmm: operands need 2 or more dims")
+    M, K = a.shape[-2:]
+    N = b.shape[-1]
+    if K != b.shape[-2]:
+        raise ValueError(f"shape mismatch {tuple(a.shape)} @ {tuple(b.shape)}")
+    out_dtype = torch.result_type(a, b)
+    if out_dtype not in _lib.FLOAT_DTYPES:
+        raise ValueError(f"batch_invariant_bmm: unsupported dtype {out_dtype}")
+    _lib.require_gpu("batch_invariant_bmm", a, b)
+    batch = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    Bt = 1
+    for d in batch:
+        Bt *= d
+    out = torch.empty((*batch, M, N), dtype=out_dtype, device=a.device)
+    if Bt == 0 or M == 0:
+        return out
+    if N == 0 or K == 0:
+        return out.zero_()
+    a3 = a.to(out_dtype).expand(*batch, M, K).reshape(Bt, M, K)
+    bt3 = b.to(out_dtype).expand(*batch, K, N).reshape(Bt, K, N).transpose(1, 2)
+    K8 = (K + 7) // 8 * 8
+    a3 = _prep_batched(a3, K8)
+    bt3 = _prep_batched(bt3, K8)
+    lib = _lib.load()
+    ws_bytes = lib.bi_matmul_workspace_bytes(M, N, K8)
+    ws = _lib.workspace(ws_bytes, a.device)
+    o3 = out.view(Bt, M, N)
+    rc = lib.bi_matmul_batched(a3.data_ptr(), a3.stride(0), a3.stride(1), bt3.data_ptr(), bt3.stride(0),
+                               bt3.stride(1), o3.data_ptr(), M * N, Bt, M, N, K8, _lib.DTYPE_CODE[out_dtype],
+                               _lib.ptr(ws), ws_bytes, _lib.stream_of(a3))
+    _lib.check(rc, "bi_matmul_batched")
+    return out

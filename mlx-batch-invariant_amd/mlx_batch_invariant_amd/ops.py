@@ -14,6 +14,12 @@ fallbacks ``matmul:non-2d-rhs-or-non-float``, ``addmm:non-2d-rhs-or-non-float``,
 ``quantized_matmul:{mode}-{bits}bit-g{gs}-{T|N}``, ``rms_norm:non-float``,
 ``sdpa:array-mask``, ``sdpa:sinks-or-shape``. One reason is new: inputs
 that are not GPU tensors fall back as ``{op}:non-gpu-tensor``.
+
+Beyond the reference's op set: right-hand sides with batch dims (``torch.matmul``
+of 2+-D operands, ``torch.bmm``) run the batched kernel and count as
+``matmul`` (the reference falls back there, ``matmul:non-2d-rhs-or-non-float``;
+a 1-D operand still does); ``F.layer_norm`` over the last dim counts as
+``layer_norm`` (fallbacks ``layer_norm:non-float``, ``layer_norm:non-last-dim``).
 """
 
 from __future__ import annotations
@@ -29,6 +35,8 @@ from torch.nn.attention.bias import CausalVariant as _CausalVariant
 from . import _lib
 from .kernels import (
     batch_invariant_attention,
+    batch_invariant_bmm,
+    batch_invariant_layer_norm,
     batch_invariant_matmul,
     batch_invariant_quantized_matmul,
     batch_invariant_rms_norm,
@@ -39,10 +47,12 @@ from .kernels import quantized as _quant
 # Stock implementations, captured at import so patching never recurses.
 _orig_matmul = torch.matmul
 _orig_mm = torch.mm
+_orig_bmm = torch.bmm
 _orig_addmm = torch.addmm
 _orig_tensor_matmul = torch.Tensor.__matmul__
 _orig_linear = F.linear
 _orig_rms_norm = F.rms_norm
+_orig_layer_norm = F.layer_norm
 _orig_sdpa = F.scaled_dot_product_attention
 
 handled: Counter = Counter()
@@ -64,22 +74,43 @@ def _on_gpu(*ts) -> bool:
     return all(_lib.is_gpu_tensor(t) for t in ts if t is not None)
 
 
-def _mm_reason(a, b) -> str | None:
-    """None if the dense kernel takes (a, b); else the fallback reason."""
-    if not (_is_float(a) and _is_float(b) and b.ndim == 2 and a.ndim >= 1):
+def _mm_reason(a, b, batched_ok: bool = False) -> str | None:
+    """None if the dense kernel takes (a, b); else the fallback reason. With
+    ``batched_ok`` a right-hand side with batch dims is taken too (both
+    operands 2+-D)."""
+    if not (_is_float(a) and _is_float(b)):
+        return "non-2d-rhs-or-non-float"
+    two_d = b.ndim == 2 and a.ndim >= 1
+    batched = batched_ok and b.ndim >= 3 and a.ndim >= 2
+    if not (two_d or batched):
         return "non-2d-rhs-or-non-float"
     if not _on_gpu(a, b) or a.device != b.device:
         return "non-gpu-tensor"
     return None
 
 
+def _matmul_any(a, b):
+    return batch_invariant_matmul(a, b) if b.ndim == 2 else batch_invariant_bmm(a, b)
+
+
 def matmul(a, b, *, out=None):
-    reason = "out-argument" if out is not None else _mm_reason(a, b)
+    reason = "out-argument" if out is not None else _mm_reason(a, b, batched_ok=True)
     if reason is None:
         handled["matmul"] += 1
-        return batch_invariant_matmul(a, b)
+        return _matmul_any(a, b)
     _fallback("matmul", reason)
     return _orig_matmul(a, b) if out is None else _orig_matmul(a, b, out=out)
+
+
+def bmm(a, b, *, out=None):
+    reason = "out-argument" if out is not None else _mm_reason(a, b, batched_ok=True)
+    if reason is None and not (a.ndim == 3 and b.ndim == 3 and a.shape[0] == b.shape[0]):
+        reason = "non-2d-rhs-or-non-float"     # let the stock op raise its own shape error
+    if reason is None:
+        handled["matmul"] += 1
+        return batch_invariant_bmm(a, b)
+    _fallback("matmul", reason)
+    return _orig_bmm(a, b) if out is None else _orig_bmm(a, b, out=out)
 
 
 def mm(a, b, *, out=None):
@@ -92,10 +123,10 @@ def mm(a, b, *, out=None):
 
 
 def tensor_matmul(self, other):
-    reason = _mm_reason(self, other)
+    reason = _mm_reason(self, other, batched_ok=True)
     if reason is None:
         handled["matmul"] += 1
-        return batch_invariant_matmul(self, other)
+        return _matmul_any(self, other)
     _fallback("matmul", reason)
     return _orig_tensor_matmul(self, other)
 
@@ -166,6 +197,30 @@ def rms_norm(input, normalized_shape, weight=None, eps=None):
     else:
         _fallback("rms_norm", "non-float")
     return _orig_rms_norm(input, normalized_shape, weight, eps)
+
+
+def layer_norm(input, normalized_shape, weight=None, bias=None, eps=1e-5):
+    """``F.layer_norm``; the kernel normalises over the last dim, so a
+    multi-dim ``normalized_shape`` is taken by flattening those dims."""
+    if isinstance(normalized_shape, int):
+        normalized_shape = (normalized_shape,)
+    nd = len(normalized_shape)
+    shape_ok = (isinstance(input, torch.Tensor) and nd >= 1
+                and tuple(input.shape[input.ndim - nd:]) == tuple(normalized_shape))
+    if not (_is_float(input) and (weight is None or _is_float(weight)) and (bias is None or _is_float(bias))):
+        _fallback("layer_norm", "non-float")
+    elif not shape_ok:
+        _fallback("layer_norm", "non-last-dim")
+    elif not _on_gpu(input, weight, bias):
+        _fallback("layer_norm", "non-gpu-tensor")
+    else:
+        handled["layer_norm"] += 1
+        D = math.prod(normalized_shape)
+        x2 = input.reshape(*input.shape[:input.ndim - nd], D)
+        w2 = None if weight is None else weight.reshape(D)
+        b2 = None if bias is None else bias.reshape(D)
+        return batch_invariant_layer_norm(x2, w2, b2, eps).reshape(input.shape)
+    return _orig_layer_norm(input, normalized_shape, weight, bias, eps)
 
 
 def _causal_variant(attn_mask, is_causal, Tq, L):

@@ -7,15 +7,17 @@ checker (or the timed CPU baseline). The product path never calls it.
 Each function restates one canonical reduction order of the reference,
 mlx-batch-invariant (files cited per function), in the concrete form the
 gfx950 kernels commit to. All arithmetic is float32 unless stated;
-``fma(a, b, c)`` is emulated as one float64 evaluation rounded once to
-float32, which is exact whenever ``a * b`` fits 53 bits and the sum does not
-straddle a float32 rounding tie (always true for the bf16/fp16 products used
-here; otherwise it can differ from a hardware fma in the last float32 bit).
+``fma(a, b, c)`` is emulated exactly (``fma32``: float64 evaluation, with
+the rare float32-midpoint results re-rounded from the exact rational).
 
 Pinning (how each function is checked, tests/test_oracle.py):
 
 * ``rms_norm``          float64 closed form (tolerance), permutation/scale
                         invariants, bit-exact squares-sum cases.
+* ``layer_norm``        float64 closed form (tolerance), constant rows -> b
+                        exactly, two-value rows (exact mean and variance),
+                        torch's CPU layer_norm (tolerance), a planted
+                        unbiased-variance mistake that the checks catch.
 * ``unpack`` /
   ``dequantize``        hand-packed known-answer words (tests/golden), brute
                         force over all 16/256 codes, closed form with Fraction.
@@ -81,8 +83,34 @@ def round_to(x, dtype: str) -> np.ndarray:
 
 
 def fma32(a, b, c) -> np.ndarray:
-    """fmaf emulated through float64 (see the module docstring for exactness)."""
-    return (np.asarray(a, np.float64) * np.asarray(b, np.float64) + np.asarray(c, np.float64)).astype(np.float32)
+    """fmaf on float32 operands, correctly rounded. a * b of two float32 values
+    is exact in float64; adding c rounds once in float64 and the cast to
+    float32 rounds again. That second rounding differs from a single one only
+    when the float64 result sits exactly on a float32 rounding midpoint; those
+    (rare) elements are re-rounded from the exact rational value."""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    c = np.asarray(c, np.float32)
+    r = a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)
+    f = r.astype(np.float32)
+    f64 = f.astype(np.float64)
+    other = np.where(r >= f64, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf)))
+    tie = np.isfinite(r) & (r != f64) & (2 * r == f64 + other.astype(np.float64))
+    if np.any(tie):
+        from fractions import Fraction
+        a, b, c = np.broadcast_arrays(a, b, c)
+        f = np.array(f, np.float32, copy=True)
+        other = np.broadcast_to(other, f.shape)
+        for idx in zip(*np.nonzero(np.broadcast_to(tie, f.shape))):
+            exact = Fraction(float(a[idx])) * Fraction(float(b[idx])) + Fraction(float(c[idx]))
+            lo, hi = sorted((float(f[idx]), float(other[idx])))
+            dl, dh = exact - Fraction(lo), Fraction(hi) - exact
+            if dl != dh:
+                f[idx] = np.float32(lo if dl < dh else hi)
+            else:   # exact tie: the even significand
+                even = lo if (np.float32(lo).view(np.uint32) & 1) == 0 else hi
+                f[idx] = np.float32(even)
+    return f
 
 
 def ulp(x, dtype: str) -> np.ndarray:
@@ -134,6 +162,70 @@ def rms_norm(x, w, eps: float, dtype: str) -> np.ndarray:
     wv = np.ones(D, np.float32) if w is None else np.asarray(w, np.float32)
     out = ((x * inv[:, None]).astype(np.float32) * wv[None, :]).astype(np.float32)
     return round_to(out, dtype)
+
+
+def _row_sum(v: np.ndarray) -> np.ndarray:
+    """[rows, TG] per-thread partials -> [rows]: butterfly per wave, waves
+    added left to right."""
+    rows = v.shape[0]
+    sums = _butterfly64(v.reshape(rows, TG // 64, 64))
+    total = sums[:, 0]
+    for i in range(1, TG // 64):
+        total = (total + sums[:, i]).astype(np.float32)
+    return total
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm — no kernel in the reference (roadmap item, README.md:257-260;
+# GPT-2 uses the stock op, README.md:250-251). Order committed to by the gfx950
+# kernel (bi_layernorm.hip): the RMSNorm chunk ownership and tree, two passes:
+# s = s + x -> mean = S / D; d = x - mean, ss = fma(d, d, ss) over k < D ->
+# var = SS / D; inv = 1 / sqrt(var + eps); out = T(((d * inv) * w) + b), the
+# multiply / add skipped when w / b is None.
+# ---------------------------------------------------------------------------
+
+def layer_norm(x, w, b, eps: float, dtype: str) -> np.ndarray:
+    """x [rows, D] float32 values representable in ``dtype``; w, b [D] or None."""
+    x = np.asarray(x, np.float32)
+    rows, D = x.shape
+    nchunks = -(-D // VEC)
+    nc = max(1, -(-nchunks // TG))
+    pad = np.zeros((rows, nc * TG * VEC), np.float32)
+    pad[:, :D] = x
+    valid = np.zeros(nc * TG * VEC, bool)
+    valid[:D] = True
+    chunks = pad.reshape(rows, nc, TG, VEC)
+    vmask = valid.reshape(nc, TG, VEC)
+    s = np.zeros((rows, TG), np.float32)
+    for c in range(nc):
+        for e in range(VEC):
+            s = (s + chunks[:, c, :, e]).astype(np.float32)
+    mean = (_row_sum(s) / np.float32(D)).astype(np.float32)
+    ss = np.zeros((rows, TG), np.float32)
+    for c in range(nc):
+        for e in range(VEC):
+            d = np.where(vmask[c, :, e][None, :], (chunks[:, c, :, e] - mean[:, None]).astype(np.float32),
+                         np.float32(0))
+            ss = fma32(d, d, ss)
+    var = (_row_sum(ss) / np.float32(D)).astype(np.float32)
+    inv = (np.float32(1.0) / np.sqrt((var + np.float32(eps)).astype(np.float32))).astype(np.float32)
+    y = ((x - mean[:, None]).astype(np.float32) * inv[:, None]).astype(np.float32)
+    if w is not None:
+        y = (y * np.asarray(w, np.float32)[None, :]).astype(np.float32)
+    if b is not None:
+        y = (y + np.asarray(b, np.float32)[None, :]).astype(np.float32)
+    return round_to(y, dtype)
+
+
+def layer_norm_float64(x, w, b, eps: float) -> np.ndarray:
+    x = np.asarray(x, np.float64)
+    mu = x.mean(-1, keepdims=True)
+    y = (x - mu) / np.sqrt(((x - mu) ** 2).mean(-1, keepdims=True) + eps)
+    if w is not None:
+        y = y * np.asarray(w, np.float64)
+    if b is not None:
+        y = y + np.asarray(b, np.float64)
+    return y
 
 
 # ---------------------------------------------------------------------------

@@ -155,3 +155,56 @@ def test_matmul_errors():
     with pytest.raises(ValueError):
         bi.batch_invariant_matmul(a, torch.zeros((2, 8, 4), dtype=torch.bfloat16, device="cuda"))
     assert bi.batch_invariant_matmul(a[:0], torch.zeros((8, 4), dtype=torch.bfloat16, device="cuda")).shape == (0, 4)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("ashape,bshape,trans", [((3, 40, 256), (3, 256, 100), False),
+                                                 ((2, 1, 17, 96), (5, 96, 33), False),
+                                                 ((4, 33, 128), (4, 70, 128), True),
+                                                 ((40, 512), (3, 512, 64), False)])
+def test_batched_matmul_slices_equal_2d_calls(dt, ashape, bshape, trans):
+    """Every slice of the batched launch is the 2-D kernel on that slice (bits),
+    with broadcast batch dims and a transposed right-hand side (q @ k^T)."""
+    bi = _bi()
+    g = gen(sum(ashape) + sum(bshape))
+    a = randn(ashape, DT[dt], g)
+    b = randn(bshape, DT[dt], g)
+    if trans:
+        b = b.transpose(-1, -2)                   # [..., K, N] view of a k-contiguous [..., N, K]
+    got = bi.batch_invariant_bmm(a, b)
+    batch = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    assert tuple(got.shape) == (*batch, a.shape[-2], b.shape[-1])
+    ae = a.expand(*batch, *a.shape[-2:])
+    be = b.expand(*batch, *b.shape[-2:])
+    for idx in np.ndindex(*batch):
+        assert bits(got[idx]) == bits(bi.batch_invariant_matmul(ae[idx], be[idx])), idx
+    i0 = (0,) * len(batch)
+    want = ora.matmul(to_np(ae[i0]), to_np(be[i0]).T, dt)
+    atol = ora.matmul_error_bound(to_np(ae[i0]), to_np(be[i0]).T)
+    assert ora.max_ulp_excess(to_np(got[i0]), want, dt, atol=atol) <= 1.0
+
+
+def test_batched_matmul_rows_independent_of_m_and_batch():
+    bi = _bi()
+    g = gen(8)
+    a = randn((6, 64, 1024), torch.bfloat16, g)
+    b = randn((6, 1024, 300), torch.bfloat16, g)
+    full = bi.batch_invariant_bmm(a, b)
+    for m in (1, 16, 33):
+        assert bits(bi.batch_invariant_bmm(a[:, :m], b)) == bits(full[:, :m]), m
+    assert bits(bi.batch_invariant_bmm(a[2:3], b[2:3])) == bits(full[2:3])
+
+
+def test_batched_matmul_intercepted_by_mode():
+    bi = _bi()
+    g = gen(9)
+    q = randn((2, 4, 16, 64), torch.bfloat16, g)
+    k = randn((2, 4, 40, 64), torch.bfloat16, g)
+    bi.reset_stats()
+    with bi.set_batch_invariant_mode(strict=True):
+        s1 = torch.matmul(q, k.transpose(-1, -2))
+        s2 = q @ k.transpose(-1, -2)
+        s3 = torch.bmm(q[0], k[0].transpose(-1, -2))
+    assert bi.stats()["handled"] == {"matmul": 3}
+    assert bits(s1) == bits(s2) == bits(bi.batch_invariant_bmm(q, k.transpose(-1, -2)))
+    assert bits(s3) == bits(s1[0])

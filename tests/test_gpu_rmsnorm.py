@@ -32,9 +32,8 @@ def test_rms_norm_weight_none_and_fp32():
     x = randn((5, 4096), torch.float32, g)
     got = _bi().batch_invariant_rms_norm(x, None, 1e-5)
     want = ora.rms_norm(to_np(x), None, 1e-5, "f32")
-    # fp32 squares are not exact in fp32, so the oracle's fma emulation may
-    # differ in the last bit of the sum: allow 2 fp32 ulps.
-    assert ora.max_ulp_excess(to_np(got), want, "f32") <= 2
+    # the oracle's fma is correctly rounded for any fp32 operands: bit-exact
+    np.testing.assert_array_equal(to_np(got), want)
 
 
 def test_rms_norm_strided_rows():

@@ -15,8 +15,8 @@ from mlx_batch_invariant_amd import ops
 
 
 def _symbols():
-    return (torch.matmul, torch.mm, torch.addmm, torch.Tensor.__matmul__, F.linear, F.rms_norm,
-            F.scaled_dot_product_attention, bnn.quantized_matmul)
+    return (torch.matmul, torch.mm, torch.bmm, torch.addmm, torch.Tensor.__matmul__, F.linear, F.rms_norm,
+            F.layer_norm, F.scaled_dot_product_attention, bnn.quantized_matmul)
 
 
 def test_mode_patches_and_restores():
@@ -26,6 +26,7 @@ def test_mode_patches_and_restores():
         assert bi.is_batch_invariant_mode_enabled()
         assert torch.matmul is ops.matmul and F.linear is ops.linear
         assert torch.Tensor.__matmul__ is ops.tensor_matmul
+        assert torch.bmm is ops.bmm and F.layer_norm is ops.layer_norm
         with bi.set_batch_invariant_mode():  # re-entrant
             assert bi.is_batch_invariant_mode_enabled()
         assert bi.is_batch_invariant_mode_enabled()
@@ -84,6 +85,7 @@ def test_fallback_returns_stock_result_and_counts():
     ref_mm = torch.matmul(x, W.T)
     ref_lin = F.linear(x, W, b)
     ref_norm = F.rms_norm(x, (16,), None, 1e-6)
+    ref_bmm = torch.bmm(x[None], W.T[None])
     bi.reset_stats()
     with bi.set_batch_invariant_mode():
         assert torch.equal(x @ W.T, ref_mm)
@@ -91,11 +93,17 @@ def test_fallback_returns_stock_result_and_counts():
         assert torch.equal(F.linear(x, W, b), ref_lin)
         assert torch.equal(F.rms_norm(x, (16,), None, 1e-6), ref_norm)
         torch.matmul(torch.ones(2, 3, dtype=torch.int64), torch.ones(3, 2, dtype=torch.int64))
-        torch.matmul(x, torch.randn(2, 16, 4))      # 3-D rhs
+        torch.matmul(x, torch.randn(2, 16, 4))      # 3-D rhs: the batched kernel's (GPU only)
+        torch.matmul(x, torch.randn(16))            # 1-D rhs: no kernel
+        assert torch.equal(torch.bmm(x[None], W.T[None]), ref_bmm)
+        ref_ln = torch.nn.LayerNorm(16)(x)
+        assert torch.equal(torch.nn.LayerNorm(16)(x), ref_ln)
+        F.layer_norm(x, (3, 16))                    # trailing dims flattened: still the kernel's
     st = bi.stats()
     assert st["handled"] == {}
-    assert st["fallbacks"] == {"matmul:non-gpu-tensor": 2, "addmm:non-gpu-tensor": 1,
-                               "rms_norm:non-gpu-tensor": 1, "matmul:non-2d-rhs-or-non-float": 2}
+    assert st["fallbacks"] == {"matmul:non-gpu-tensor": 4, "addmm:non-gpu-tensor": 1,
+                               "rms_norm:non-gpu-tensor": 1, "matmul:non-2d-rhs-or-non-float": 2,
+                               "layer_norm:non-gpu-tensor": 3}
 
 
 def test_quantized_fallback_key_and_stock_path():

@@ -112,6 +112,99 @@ def test_rms_norm_weight_none_is_ones_and_rows_independent():
     assert np.array_equal(ora.rms_norm(x[4:5], None, 1e-6, "bf16"), a[4:5])
 
 
+# ---- fma32 (the emulation every fp32 fma of the oracle goes through) ----------
+
+def test_fma32_is_correctly_rounded_on_a_double_rounding_case():
+    """(1 + 2^-12)^2 = 1 + 2^-11 + 2^-24 is a float32 midpoint; adding 2^-80
+    (below float64 resolution there) must round up, subtracting it down, and
+    the exact midpoint to the even neighbour. A plain float64 evaluation
+    rounds the first case to the midpoint and then down: wrong."""
+    a = np.array([1 + 2 ** -12], np.float32)
+    up, down, even = np.float32(1 + 2 ** -11 + 2 ** -23), np.float32(1 + 2 ** -11), np.float32(1 + 2 ** -11)
+    assert ora.fma32(a, a, np.array([2 ** -80], np.float32))[0] == up
+    assert ora.fma32(a, a, np.array([-2 ** -80], np.float32))[0] == down
+    assert ora.fma32(a, a, np.array([0.0], np.float32))[0] == even
+    naive = np.float32(np.float64(a[0]) * np.float64(a[0]) + 2.0 ** -80)
+    assert naive != up
+
+
+def test_fma32_matches_exact_rational_rounding():
+    from fractions import Fraction
+    rng = np.random.default_rng(5)
+    a, b = (rng.standard_normal(400).astype(np.float32) for _ in range(2))
+    c = (rng.standard_normal(400) * 10.0 ** rng.integers(-8, 8, 400)).astype(np.float32)
+    got = ora.fma32(a, b, c)
+    for i in range(400):
+        e = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        f = np.float32(float(e))
+        cands = [f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf))]
+        best = min(cands, key=lambda v: (abs(Fraction(float(v)) - e), int(np.float32(v).view(np.uint32) & 1)))
+        assert got[i] == best, i
+
+
+# ---- layer_norm -----------------------------------------------------------------
+
+def _ln_rel(got, ref):
+    return np.max(np.abs(got - ref) / (np.abs(ref) + 1.0))
+
+
+@pytest.mark.parametrize("D", [2, 7, 896, 4096, 9000])
+def test_layer_norm_close_to_float64_closed_form(D):
+    rng = np.random.default_rng(D)
+    x = ora.round_to((3.0 + rng.standard_normal((5, D))).astype(np.float32), "bf16")   # mean far from 0
+    w = ora.round_to((1 + 0.1 * rng.standard_normal(D)).astype(np.float32), "bf16")
+    b = ora.round_to((0.1 * rng.standard_normal(D)).astype(np.float32), "bf16")
+    for eps in (1e-5, 0.5):           # a dropped or misplaced eps fails at eps = 0.5
+        got = ora.layer_norm(x, w, b, eps, "f32")
+        assert _ln_rel(got, ora.layer_norm_float64(x, w, b, eps)) < 2e-5
+        assert _ln_rel(ora.layer_norm(x, None, None, eps, "f32"), ora.layer_norm_float64(x, None, None, eps)) < 2e-5
+
+
+def test_layer_norm_check_catches_unbiased_variance_and_missing_mean():
+    """The closed-form check above discriminates the plausible mistakes: a
+    variance divided by D - 1, or x not centred, is far outside its bound."""
+    rng = np.random.default_rng(11)
+    D = 64
+    x = ora.round_to((3.0 + rng.standard_normal((4, D))).astype(np.float32), "bf16")
+    got = ora.layer_norm(x, None, None, 1e-5, "f32")
+    x64 = x.astype(np.float64)
+    mu = x64.mean(-1, keepdims=True)
+    unbiased = (x64 - mu) / np.sqrt(((x64 - mu) ** 2).sum(-1, keepdims=True) / (D - 1) + 1e-5)
+    uncentred = x64 / np.sqrt(((x64 - mu) ** 2).mean(-1, keepdims=True) + 1e-5)
+    assert _ln_rel(got, unbiased) > 1e-3 and _ln_rel(got, uncentred) > 1e-1
+
+
+def test_layer_norm_constant_row_gives_bias_exactly():
+    D = 300
+    x = np.full((2, D), 1.75, np.float32)
+    b = ora.round_to(np.linspace(-1, 1, D).astype(np.float32), "bf16")
+    w = np.full(D, 3.0, np.float32)
+    assert np.array_equal(ora.layer_norm(x, w, b, 1e-5, "f32"), np.broadcast_to(b, (2, D)))
+    assert np.all(ora.layer_norm(x, None, None, 1e-5, "f32") == 0)
+
+
+def test_layer_norm_two_value_rows_known_answer():
+    """x alternates c + a, c - a (powers of two): the sum, the mean c, the
+    deviations +-a and the variance a^2 are exact, so out = +-a * inv with
+    inv = 1 / sqrt(a^2 + eps), each step correctly rounded."""
+    D, c, a, eps = 1000, 4.0, 0.25, 1e-5
+    x = np.where(np.arange(D) % 2 == 0, c + a, c - a).astype(np.float32)[None, :]
+    inv = np.float32(1) / np.sqrt(np.float32(np.float32(a * a) + np.float32(eps)))
+    want = np.where(np.arange(D) % 2 == 0, np.float32(a) * inv, np.float32(-a) * inv).astype(np.float32)
+    assert np.array_equal(ora.layer_norm(x, None, None, eps, "f32")[0], want)
+
+
+def test_layer_norm_close_to_torch_cpu():
+    import torch
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((6, 1000)).astype(np.float32) * 2 + 1
+    w = (1 + 0.1 * rng.standard_normal(1000)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(1000)).astype(np.float32)
+    ref = torch.nn.functional.layer_norm(torch.from_numpy(x), (1000,), torch.from_numpy(w), torch.from_numpy(b),
+                                         1e-5).numpy()
+    assert ora.max_ulp_excess(ora.layer_norm(x, w, b, 1e-5, "f32"), ref, "f32", atol=1e-6) <= 8
+
+
 # ---- matmul -------------------------------------------------------------------
 
 @pytest.mark.parametrize("M,N,K", [(3, 5, 256), (7, 9, 1000), (1, 33, 8)])
