@@ -22,6 +22,7 @@ from .kernels import (
     batch_invariant_rms_norm,
 )
 from .kernels.quantized import quantize, dequantize, pack, unpack
+from . import library  # registers torch.ops.mlx_bi.*
 
 __all__ = [
     "set_batch_invariant_mode",
