@@ -142,6 +142,24 @@ int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* k
                    const int64_t* strides, float scale, int dtype, void* ws,
                    size_t ws_bytes, void* stream);
 
+/* Paged K/V variant of bi_attn_decode: k_pages / v_pages are pools of pages of
+ * page_size keys (a power of two, 1 .. 2^24); strides[2..4] / [5..7] are the
+ * (page, head, position-in-page) element strides. Key p of sequence b is row
+ * p mod page_size of page block_table[b * table_stride + p / page_size]
+ * (device int32; table_stride >= ceil(L / page_size); every page index a
+ * sequence reaches must be valid). L is the longest sequence the table can
+ * hold (it sizes the workspace, as in bi_attn_decode). Same arithmetic as
+ * bi_attn_decode: the output equals the contiguous call on the same keys, bit
+ * for bit.
+ * Replaces: nothing in the reference (its decode reads one contiguous cache,
+ * kernels/attention.py:87-147); the paged-KV item of its roadmap of adjacent
+ * ops. */
+int bi_attn_decode_paged(const void* q, const void* k_pages, const void* v_pages,
+                         const int32_t* block_table, int64_t table_stride, int64_t page_size,
+                         const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
+                         int64_t L, int64_t D, const int64_t* strides, float scale, int dtype,
+                         void* ws, size_t ws_bytes, void* stream);
+
 /* ---- Prefill attention (any number of query tokens) ------------------------
  * q [B, Hq, Tq, D], k/v [B, Hkv, L, D] through element strides
  *   strides[0..2] = q (batch, head, token)
@@ -159,6 +177,18 @@ int bi_attn_prefill(const void* q, const void* k, const void* v, const int32_t* 
                     void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
                     int64_t D, const int64_t* strides, int causal, float scale, int dtype,
                     void* stream);
+
+/* Paged K/V variant of bi_attn_prefill (page pool, strides[3..5] / [6..8] =
+ * (page, head, position-in-page), block table as in bi_attn_decode_paged): a
+ * prompt chunk run against a paged cache. Bit-identical to bi_attn_prefill on
+ * the same keys.
+ * Replaces: nothing in the reference (kernels/attention.py:173-254 reads a
+ * contiguous cache); the paged-KV prefill item of its roadmap of adjacent ops. */
+int bi_attn_prefill_paged(const void* q, const void* k_pages, const void* v_pages,
+                          const int32_t* block_table, int64_t table_stride, int64_t page_size,
+                          const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
+                          int64_t Tq, int64_t L, int64_t D, const int64_t* strides, int causal,
+                          float scale, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

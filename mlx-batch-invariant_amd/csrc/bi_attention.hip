@@ -77,20 +77,41 @@ __global__ void zero_counter_kernel(unsigned* c) { *c = 0u; }
 // with fewer, the static order costs nothing extra.
 constexpr int kDynMinRounds = 4;
 
+// K/V addressing mode (bi_attn_common.h): contiguous, pages of >= 64 keys, or
+// smaller pages.
+template <class Args>
+static int kv_mode(const Args& a) {
+  return !a.table ? kKvContig : a.page_shift >= 6 ? kKvPaged : kKvRowPaged;
+}
+
+// Paged caches always take the dynamic item order (one instantiation each).
+template <typename T, int D, int GU, int MODE>
+static int launch_decode_paged(DecodeArgs& a, int64_t most, hipStream_t st) {
+  static int cache[kMaxDev] = {};
+  const int grid = resident_grid(attn_decode_mfma<T, D, GU, true, MODE>, cache);
+  if (grid <= 0) return bi_host::fail(BI_E_UNSUPPORTED, "bi_attn_decode: device occupancy query failed");
+  zero_counter_kernel<<<1, 1, 0, st>>>(a.ctr);
+  attn_decode_mfma<T, D, GU, true, MODE><<<(int)std::min<int64_t>(grid, most), 256, 0, st>>>(a);
+  return 0;
+}
+
 template <typename T, int D, int GU>
 static int launch_decode_gu(DecodeArgs& a, hipStream_t st) {
   // Enough resident workgroups to fill the chip, never more than the number
   // of possible items (every sequence at full length).
   const int64_t most = (int64_t)a.B * a.nsplit * a.Hkv * a.nchunk;
+  const int mode = kv_mode(a);
+  if (mode == kKvPaged) return launch_decode_paged<T, D, GU, kKvPaged>(a, most, st);
+  if (mode == kKvRowPaged) return launch_decode_paged<T, D, GU, kKvRowPaged>(a, most, st);
   static int cache[kMaxDev] = {};
-  int grid = resident_grid(attn_decode_mfma<T, D, GU, true>, cache);
+  int grid = resident_grid(attn_decode_mfma<T, D, GU, true, kKvContig>, cache);
   if (grid <= 0) return bi_host::fail(BI_E_UNSUPPORTED, "bi_attn_decode: device occupancy query failed");
   if (most > (int64_t)kDynMinRounds * grid) {
     zero_counter_kernel<<<1, 1, 0, st>>>(a.ctr);
-    attn_decode_mfma<T, D, GU, true><<<grid, 256, 0, st>>>(a);
+    attn_decode_mfma<T, D, GU, true, kKvContig><<<grid, 256, 0, st>>>(a);
   } else {
     grid = (int)std::min<int64_t>(grid, most);
-    attn_decode_mfma<T, D, GU, false><<<grid, 256, 0, st>>>(a);
+    attn_decode_mfma<T, D, GU, false, kKvContig><<<grid, 256, 0, st>>>(a);
   }
   return 0;
 }
@@ -118,7 +139,11 @@ static int launch_prefill(PrefillArgs& a, hipStream_t st) {
   const int G = a.Hq / a.Hkv;
   const int64_t wgs = ((int64_t)a.Tq * G + 63) / 64;
   dim3 grid((unsigned)wgs, a.Hkv, a.B);
-  attn_prefill_mfma<T, D><<<grid, 256, 0, st>>>(a);
+  switch (kv_mode(a)) {
+    case kKvPaged: attn_prefill_mfma<T, D, kKvPaged><<<grid, 256, 0, st>>>(a); break;
+    case kKvRowPaged: attn_prefill_mfma<T, D, kKvRowPaged><<<grid, 256, 0, st>>>(a); break;
+    default: attn_prefill_mfma<T, D, kKvContig><<<grid, 256, 0, st>>>(a); break;
+  }
   return bi_host::launch_status("bi_attn_prefill");
 }
 
@@ -151,29 +176,48 @@ extern "C" size_t bi_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t 
   return (size_t)(up(bh) * 2 + bh * D + 4) * sizeof(float);
 }
 
-extern "C" int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* kv_lens,
-                              void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
-                              const int64_t* strides, float scale, int dtype, void* ws,
-                              size_t ws_bytes, void* stream) {
+namespace {
+
+// Page table of a paged call: power-of-two page size, one row of
+// table_stride >= ceil(L / page_size) page indices per sequence.
+int check_pages(const char* what, const int32_t* table, int64_t table_stride, int64_t page_size, int64_t L,
+                int* shift) {
   using namespace bi_host;
-  int rc = check_attn_shape("bi_attn_decode", B, Hq, Hkv, L, D);
-  if (rc) return rc;
+  if (!table) return fail(BI_E_INVALID_ARG, "%s: null block table", what);
+  if (page_size <= 0 || page_size > ((int64_t)1 << 24) || (page_size & (page_size - 1)))
+    return fail(BI_E_INVALID_ARG, "%s: page size %lld must be a power of two in [1, 2^24]", what,
+                (long long)page_size);
+  if (table_stride < (L + page_size - 1) / page_size)
+    return fail(BI_E_INVALID_ARG, "%s: table stride %lld < ceil(L / page size) = %lld", what,
+                (long long)table_stride, (long long)((L + page_size - 1) / page_size));
+  int sh = 0;
+  while (((int64_t)1 << sh) < page_size) ++sh;
+  *shift = sh;
+  return BI_OK;
+}
+
+int decode_impl(const char* what, const void* q, const void* k, const void* v, const int32_t* kv_lens, void* out,
+                int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D, const int64_t* strides, float scale,
+                int dtype, void* ws, size_t ws_bytes, void* stream, const int32_t* table, int64_t table_stride,
+                int page_shift) {
+  using namespace bi_host;
   if (B == 0) return BI_OK;
   if (!q || !k || !v || !out || !strides)
-    return fail(BI_E_INVALID_ARG, "bi_attn_decode: null pointer argument");
+    return fail(BI_E_INVALID_ARG, "%s: null pointer argument", what);
   const size_t need = bi_attn_decode_workspace_bytes(B, Hq, L, D);
   if (!ws || ws_bytes < need)
-    return fail(BI_E_WORKSPACE, "bi_attn_decode: workspace of %zu bytes required, got %zu", need,
+    return fail(BI_E_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", what, need,
                 ws ? ws_bytes : (size_t)0);
   const size_t es = dtype_size(dtype);
   for (int i = 0; i < 8; ++i)
     if (strides[i] < 0 || ((strides[i] * (int64_t)es) % 16))
-      return fail(BI_E_INVALID_ARG, "bi_attn_decode: stride %d (%lld) must be >= 0 and 16-byte aligned",
-                  i, (long long)strides[i]);
+      return fail(BI_E_INVALID_ARG, "%s: stride %d (%lld) must be >= 0 and 16-byte aligned", what, i,
+                  (long long)strides[i]);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(ws))
-    return fail(BI_E_INVALID_ARG, "bi_attn_decode: q, k, v and workspace must be 16-byte aligned");
+    return fail(BI_E_INVALID_ARG, "%s: q, k, v and workspace must be 16-byte aligned", what);
   bi::DecodeArgs a;
   a.q = q; a.k = k; a.v = v; a.kv_lens = kv_lens; a.out = out;
+  a.table = table; a.table_stride = table_stride; a.page_shift = page_shift;
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.L = (int)L;
   a.nsplit = (int)((L + bi::kSplit - 1) / bi::kSplit);
   const int G = (int)(Hq / Hkv);
@@ -190,7 +234,7 @@ extern "C" int bi_attn_decode(const void* q, const void* k, const void* v, const
   a.pacc = a.pl + up;
   a.ctr = reinterpret_cast<unsigned*>(a.pacc + bh * D);
   if ((int64_t)a.Hkv * a.nchunk > 65535 || a.nsplit > 0x7fffffff)
-    return fail(BI_E_UNSUPPORTED, "bi_attn_decode: grid too large");
+    return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define BI_DEC(TY)                                                         \
   return D == 64 ? bi::launch_decode<TY, 64>(a, st) : bi::launch_decode<TY, 128>(a, st);
@@ -198,37 +242,34 @@ extern "C" int bi_attn_decode(const void* q, const void* k, const void* v, const
     case BI_BF16: BI_DEC(bi::bf16)
     case BI_F16: BI_DEC(bi::f16)
     case BI_F32: BI_DEC(float)
-    default: return fail(BI_E_UNSUPPORTED, "bi_attn_decode: unknown dtype %d", dtype);
+    default: return fail(BI_E_UNSUPPORTED, "%s: unknown dtype %d", what, dtype);
   }
 #undef BI_DEC
 }
 
-extern "C" int bi_attn_prefill(const void* q, const void* k, const void* v, const int32_t* kv_lens,
-                               void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
-                               int64_t D, const int64_t* strides, int causal, float scale, int dtype,
-                               void* stream) {
+int prefill_impl(const char* what, const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                 void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L, int64_t D,
+                 const int64_t* strides, int causal, float scale, int dtype, void* stream, const int32_t* table,
+                 int64_t table_stride, int page_shift) {
   using namespace bi_host;
-  int rc = check_attn_shape("bi_attn_prefill", B, Hq, Hkv, L, D);
-  if (rc) return rc;
-  if (Tq <= 0) return fail(BI_E_INVALID_ARG, "bi_attn_prefill: Tq=%lld", (long long)Tq);
+  if (Tq <= 0) return fail(BI_E_INVALID_ARG, "%s: Tq=%lld", what, (long long)Tq);
   if (causal && Tq > L)
-    return fail(BI_E_INVALID_ARG, "bi_attn_prefill: causal needs Tq (%lld) <= L (%lld)",
-                (long long)Tq, (long long)L);
+    return fail(BI_E_INVALID_ARG, "%s: causal needs Tq (%lld) <= L (%lld)", what, (long long)Tq, (long long)L);
   if (B == 0) return BI_OK;
-  if (!q || !k || !v || !out || !strides)
-    return fail(BI_E_INVALID_ARG, "bi_attn_prefill: null pointer argument");
+  if (!q || !k || !v || !out || !strides) return fail(BI_E_INVALID_ARG, "%s: null pointer argument", what);
   const size_t es = dtype_size(dtype);
   for (int i = 0; i < 9; ++i)
     if (strides[i] < 0 || ((strides[i] * (int64_t)es) % 16))
-      return fail(BI_E_INVALID_ARG, "bi_attn_prefill: stride %d (%lld) must be >= 0 and 16-byte aligned",
-                  i, (long long)strides[i]);
+      return fail(BI_E_INVALID_ARG, "%s: stride %d (%lld) must be >= 0 and 16-byte aligned", what, i,
+                  (long long)strides[i]);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
-    return fail(BI_E_INVALID_ARG, "bi_attn_prefill: q, k, v, out must be 16-byte aligned");
+    return fail(BI_E_INVALID_ARG, "%s: q, k, v, out must be 16-byte aligned", what);
   const int64_t wgs = (Tq * (Hq / Hkv) + 63) / 64;
   if (wgs > 0x7fffffffLL || Tq * (Hq / Hkv) > 0x7fffffffLL - 64)
-    return fail(BI_E_UNSUPPORTED, "bi_attn_prefill: grid too large");
+    return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   bi::PrefillArgs a;
   a.q = q; a.k = k; a.v = v; a.kv_lens = kv_lens; a.out = out;
+  a.table = table; a.table_stride = table_stride; a.page_shift = page_shift;
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.Tq = (int)Tq; a.L = (int)L;
   a.causal = causal ? 1 : 0;
   a.q_sb = strides[0]; a.q_sh = strides[1]; a.q_st = strides[2];
@@ -242,7 +283,57 @@ extern "C" int bi_attn_prefill(const void* q, const void* k, const void* v, cons
     case BI_BF16: BI_PRE(bi::bf16)
     case BI_F16: BI_PRE(bi::f16)
     case BI_F32: BI_PRE(float)
-    default: return fail(BI_E_UNSUPPORTED, "bi_attn_prefill: unknown dtype %d", dtype);
+    default: return fail(BI_E_UNSUPPORTED, "%s: unknown dtype %d", what, dtype);
   }
 #undef BI_PRE
+}
+
+}  // namespace
+
+extern "C" int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                              void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                              const int64_t* strides, float scale, int dtype, void* ws,
+                              size_t ws_bytes, void* stream) {
+  int rc = check_attn_shape("bi_attn_decode", B, Hq, Hkv, L, D);
+  if (rc) return rc;
+  return decode_impl("bi_attn_decode", q, k, v, kv_lens, out, B, Hq, Hkv, L, D, strides, scale, dtype, ws,
+                     ws_bytes, stream, nullptr, 0, 0);
+}
+
+extern "C" int bi_attn_decode_paged(const void* q, const void* k_pages, const void* v_pages,
+                                    const int32_t* block_table, int64_t table_stride, int64_t page_size,
+                                    const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
+                                    int64_t L, int64_t D, const int64_t* strides, float scale, int dtype,
+                                    void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_attn_shape("bi_attn_decode_paged", B, Hq, Hkv, L, D);
+  if (rc) return rc;
+  int shift = 0;
+  if (B > 0 && (rc = check_pages("bi_attn_decode_paged", block_table, table_stride, page_size, L, &shift)))
+    return rc;
+  return decode_impl("bi_attn_decode_paged", q, k_pages, v_pages, kv_lens, out, B, Hq, Hkv, L, D, strides, scale,
+                     dtype, ws, ws_bytes, stream, block_table, table_stride, shift);
+}
+
+extern "C" int bi_attn_prefill(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                               void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
+                               int64_t D, const int64_t* strides, int causal, float scale, int dtype,
+                               void* stream) {
+  int rc = check_attn_shape("bi_attn_prefill", B, Hq, Hkv, L, D);
+  if (rc) return rc;
+  return prefill_impl("bi_attn_prefill", q, k, v, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides, causal, scale,
+                      dtype, stream, nullptr, 0, 0);
+}
+
+extern "C" int bi_attn_prefill_paged(const void* q, const void* k_pages, const void* v_pages,
+                                     const int32_t* block_table, int64_t table_stride, int64_t page_size,
+                                     const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
+                                     int64_t Tq, int64_t L, int64_t D, const int64_t* strides, int causal,
+                                     float scale, int dtype, void* stream) {
+  int rc = check_attn_shape("bi_attn_prefill_paged", B, Hq, Hkv, L, D);
+  if (rc) return rc;
+  int shift = 0;
+  if (B > 0 && (rc = check_pages("bi_attn_prefill_paged", block_table, table_stride, page_size, L, &shift)))
+    return rc;
+  return prefill_impl("bi_attn_prefill_paged", q, k_pages, v_pages, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides,
+                      causal, scale, dtype, stream, block_table, table_stride, shift);
 }

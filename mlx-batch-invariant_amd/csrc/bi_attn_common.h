@@ -55,6 +55,10 @@ struct DecodeArgs {
   int B, Hq, Hkv, L, nsplit, nchunk, GU;
   int64_t q_sb, q_sh, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
   float scale_log2;  // scale * log2(e), rounded once on the host
+  // Paged K/V (null table = contiguous): see kv_row_off.
+  const int32_t* table;
+  int64_t table_stride;
+  int page_shift;
 };
 
 struct PrefillArgs {
@@ -66,7 +70,56 @@ struct PrefillArgs {
   int B, Hq, Hkv, Tq, L, causal;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
   float scale_log2;
+  const int32_t* table;
+  int64_t table_stride;
+  int page_shift;
 };
+
+// Element offset of key `pos` of (sequence b, kv head hk) in a K or V cache
+// with strides (sb, sh, sl). Contiguous (a.table null): b sb + hk sh + pos sl.
+// Paged: the cache is a pool of pages of 2^page_shift keys, sb the page
+// stride; key pos of sequence b lives in page table[b table_stride +
+// (pos >> page_shift)] at row pos mod 2^page_shift. Addressing only: the
+// arithmetic of every split is the same either way.
+template <class Args>
+__device__ __forceinline__ int64_t kv_row_off(const Args& a, int64_t sb, int64_t sh, int64_t sl, int b, int hk,
+                                              int pos) {
+  if (a.table) {
+    const int page = a.table[(int64_t)b * a.table_stride + (pos >> a.page_shift)];
+    return (int64_t)page * sb + (int64_t)hk * sh + (int64_t)(pos & ((1 << a.page_shift) - 1)) * sl;
+  }
+  return (int64_t)b * sb + (int64_t)hk * sh + (int64_t)pos * sl;
+}
+
+// A 32-bit read through the scalar data cache, for a wave-uniform address: it
+// does not queue behind the wave's (or the CU's) vector memory traffic. The
+// wait is inside the statement, so the compiler's own counters stay exact.
+__device__ __forceinline__ int load_uniform_i32(const int32_t* p) {
+  int v;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(v) : "s"(p) : "memory");
+  return v;
+}
+
+// K/V addressing mode of a kernel instantiation: a contiguous cache, a paged
+// one with pages of 64 keys or more, or one with smaller pages.
+enum KvMode { kKvContig = 0, kKvPaged = 1, kKvRowPaged = 2 };
+
+// The K/V rows a kernel reads come in aligned 64-key segments (a decode wave's
+// keys of a split, a prefill chunk). Pointer to the first element of segment
+// key `key0` (a multiple of 64) of (sequence b, kv head hk) for kKvContig and
+// kKvPaged (one wave-uniform table read per segment; a page of 64 keys or
+// more holds the whole segment); rows of the segment are then `sl` elements
+// apart. kKvRowPaged kernels resolve every row through kv_row_off instead.
+template <int MODE, typename T, class Args>
+__device__ __forceinline__ const T* kv_segment(const Args& a, const T* base, int64_t sb, int64_t sh, int64_t sl,
+                                               int b, int hk, int key0) {
+  if constexpr (MODE == kKvContig) {
+    return base + (int64_t)b * sb + (int64_t)hk * sh + (int64_t)key0 * sl;
+  } else {
+    const int page = load_uniform_i32(a.table + (int64_t)b * a.table_stride + (key0 >> a.page_shift));
+    return base + (int64_t)page * sb + (int64_t)hk * sh + (int64_t)(key0 & ((1 << a.page_shift) - 1)) * sl;
+  }
+}
 
 // Weight of one key of a split: exp2(s - m) if active, exactly 0 otherwise.
 __device__ __forceinline__ float split_weight(float s, float m, bool active) {

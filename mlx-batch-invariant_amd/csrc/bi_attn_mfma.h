@@ -42,11 +42,12 @@ struct KVTile {
   // Copy instruction ci of a tile: rows ci * kRowsPerCopy .. + kRowsPerCopy - 1
   // (global row index clamped by the caller). Lane l fetches the chunk that
   // belongs in slot l % kCPR of its row, landing at tile + 1024 ci + 16 l.
-  static __device__ __forceinline__ void copy(char* tile, int ci, const T* rows, int64_t stride,
-                                              int nrows_valid, int lane) {
+  // `row(i)` gives the first element of tile row i (0 <= i < nrows_valid).
+  template <class RowPtr>
+  static __device__ __forceinline__ void copy(char* tile, int ci, RowPtr row, int nrows_valid, int lane) {
     const int r = ci * kRowsPerCopy + lane / kCPR;
     const int c = (lane % kCPR) ^ (r & 7);
-    const T* src = rows + (int64_t)min(r, nrows_valid - 1) * stride + c * (16 / (int)sizeof(T));
+    const T* src = row(min(r, nrows_valid - 1)) + c * (16 / (int)sizeof(T));
     copy_to_lds16(src, tile + 1024 * ci);
   }
   // A-operand fragment of the score MFMA: row r, dims 32 st + 8 qq .. + 7.
@@ -112,8 +113,9 @@ struct KVTile {
 // also the weight sum. Writes (m, l, acc) of its split. The arithmetic of an
 // item does not depend on which workgroup runs it.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int GU, bool DYN>
+template <typename T, int D, int GU, bool DYN, int MODE>
 __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
+  constexpr bool ROWPAGED = MODE == kKvRowPaged;
   typedef typename Frag<T>::type F;
   typedef KVTile<T, D> KV;
   constexpr int KT = 4;                                 // score tiles per wave
@@ -162,10 +164,22 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   const int r = lane % 16, qq = lane / 16;
 
   const T* qb = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb;
-  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh +
-                (int64_t)j0 * a.k_sl;
-  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh +
-                (int64_t)j0 * a.v_sl;
+  const T* kbase = static_cast<const T*>(a.k);
+  const T* vbase = static_cast<const T*>(a.v);
+  // This wave's K rows and V copies are keys 64 w .. 64 w + 63 of the split,
+  // clamped to the last active key: one 64-key segment (the last active one
+  // for a wave past the end).
+  const int seg = __builtin_amdgcn_readfirstlane(min(wave, (n_act - 1) >> 6));
+  const T* kseg = ROWPAGED ? kbase : kv_segment<MODE>(a, kbase, a.k_sb, a.k_sh, a.k_sl, b, hk, j0 + 64 * seg);
+  const T* vseg = ROWPAGED ? vbase : kv_segment<MODE>(a, vbase, a.v_sb, a.v_sh, a.v_sl, b, hk, j0 + 64 * seg);
+  auto krow = [&](int key) {
+    if constexpr (ROWPAGED) return kbase + kv_row_off(a, a.k_sb, a.k_sh, a.k_sl, b, hk, j0 + key);
+    else return kseg + (int64_t)(key - 64 * seg) * a.k_sl;
+  };
+  auto vrow = [&](int key) {
+    if constexpr (ROWPAGED) return vbase + kv_row_off(a, a.v_sb, a.v_sh, a.v_sl, b, hk, j0 + key);
+    else return vseg + (int64_t)(key - 64 * seg) * a.v_sl;
+  };
 
   // Memory requests, in this order: Q^T, this wave's K rows, its V copies.
   F qf[D / 32];
@@ -177,13 +191,13 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   F kf[KT][D / 32];
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
-    const T* kr = kb + (int64_t)min(64 * wave + 16 * t + r, n_act - 1) * a.k_sl + 8 * qq;
+    const T* kr = krow(min(64 * wave + 16 * t + r, n_act - 1)) + 8 * qq;
 #pragma unroll
     for (int st = 0; st < D / 32; ++st) kf[t][st] = frag_load(kr + 32 * st);
   }
   asm volatile("" ::: "memory");
 #pragma unroll
-  for (int c = 0; c < CPW; ++c) KV::copy(Vs, wave * CPW + c, vb, a.v_sl, n_act, lane);
+  for (int c = 0; c < CPW; ++c) KV::copy(Vs, wave * CPW + c, vrow, n_act, lane);
 
   // Scores of this wave's 64 keys; lane (r, qq) holds row r, keys 64 w + 16 t + 4 qq + i.
   float s[KT][4];
@@ -281,8 +295,9 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
 // workgroup's rows need are loaded (the last split may be short); rows past
 // a row's causal or kv_lens limit are masked.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, int MODE>
 __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
+  constexpr bool ROWPAGED = MODE == kKvRowPaged;
   typedef typename Frag<T>::type F;
   typedef KVTile<T, D> KV;
   constexpr int CH = 64;                                // keys per chunk
@@ -316,8 +331,11 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   for (int i = 0; i < 4; ++i) acc_nkeys[i] = nkeys_of(64 * wg + 16 * wave + 4 * qq + i);
 
   const T* qb = static_cast<const T*>(a.q) + (int64_t)b * a.q_sb;
-  const T* kb = static_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
-  const T* vb = static_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+  const T* kbase = static_cast<const T*>(a.k);
+  const T* vbase = static_cast<const T*>(a.v);
+  // Contiguous cache: this (sequence, kv head)'s rows, once per workgroup.
+  const T* kb = kbase + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+  const T* vb = vbase + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
 
   F qf[D / 32];
   {
@@ -343,11 +361,23 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
       sp = nsplit - 1; kind = cl / nkc_last; kc = cl % nkc_last;
     }
     const int key0 = sp * kSplit + kc * CH;
-    const T* rows = (kind ? vb : kb) + (int64_t)key0 * (kind ? a.v_sl : a.k_sl);
+    const int64_t sl = kind ? a.v_sl : a.k_sl;
+    const T* segp = nullptr;                            // chunks are aligned 64-key segments
+    if constexpr (MODE == kKvContig) {
+      segp = (kind ? vb : kb) + (int64_t)key0 * sl;
+    } else if constexpr (MODE == kKvPaged) {
+      segp = kind ? kv_segment<MODE>(a, vbase, a.v_sb, a.v_sh, sl, b, hk, key0)
+                  : kv_segment<MODE>(a, kbase, a.k_sb, a.k_sh, sl, b, hk, key0);
+    }
+    auto row = [&](int i) {
+      if constexpr (ROWPAGED)
+        return kind ? vbase + kv_row_off(a, a.v_sb, a.v_sh, sl, b, hk, key0 + i)
+                    : kbase + kv_row_off(a, a.k_sb, a.k_sh, sl, b, hk, key0 + i);
+      else return segp + (int64_t)i * sl;
+    };
     char* buf = ring + (c % NBUF) * CHB;
 #pragma unroll
-    for (int i = 0; i < CPW; ++i)
-      KV::copy(buf, wave * CPW + i, rows, kind ? a.v_sl : a.k_sl, len - key0, lane);
+    for (int i = 0; i < CPW; ++i) KV::copy(buf, wave * CPW + i, row, len - key0, lane);
   };
   auto open_chunk = [&](int c) {
     if (c + 1 < nchunks) stage_barrier<CPW>();  // chunk c landed; c + 1 may be in flight

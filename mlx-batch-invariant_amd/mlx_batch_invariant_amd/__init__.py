@@ -14,6 +14,7 @@ from .ops import reset_stats, stats
 from .kernels import (
     batch_invariant_attention,
     batch_invariant_decode_attention,
+    batch_invariant_paged_attention,
     batch_invariant_prefill_attention,
     batch_invariant_bmm,
     batch_invariant_layer_norm,
@@ -37,6 +38,7 @@ __all__ = [
     "batch_invariant_decode_attention",
     "batch_invariant_prefill_attention",
     "batch_invariant_attention",
+    "batch_invariant_paged_attention",
     "quantize",
     "dequantize",
     "pack",

@@ -25,6 +25,7 @@ from .quantized import batch_invariant_quantized_matmul
 from .attention import (
     batch_invariant_attention,
     batch_invariant_decode_attention,
+    batch_invariant_paged_attention,
     batch_invariant_prefill_attention,
 )
 
@@ -37,4 +38,5 @@ __all__ = [
     "batch_invariant_decode_attention",
     "batch_invariant_prefill_attention",
     "batch_invariant_attention",
+    "batch_invariant_paged_attention",
 ]

@@ -172,3 +172,66 @@ def batch_invariant_attention(q, k, v, *, scale: float | None = None, mask=None,
         return batch_invariant_decode_attention(q, k, v, scale=scale, kv_lens=kv_lens)
     return batch_invariant_prefill_attention(q, k, v, scale=scale, causal=(mask == "causal"),
                                              kv_lens=kv_lens)
+
+
+def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=None, *, scale: float | None = None,
+                                    mask=None) -> torch.Tensor:
+    """Attention over a paged K/V cache: decode for T_q == 1, prefill otherwise.
+
+    ``k_pages`` / ``v_pages``: ``[num_pages, Hkv, page_size, D]`` (any strides
+    with ``d`` contiguous, e.g. a permuted ``[num_pages, page_size, Hkv, D]``
+    pool); ``block_table``: int32 ``[B, max_pages]``, key ``p`` of sequence ``b``
+    lives at row ``p % page_size`` of page ``block_table[b, p // page_size]``;
+    ``kv_lens``: int32 ``[B]`` (None: every sequence spans the whole table).
+    ``page_size`` must be a power of two. The output is bit for bit the
+    contiguous call on the same keys: paging changes addresses only. The
+    reference reads one contiguous cache (kernels/attention.py:87-254); paged
+    KV is an item of its roadmap of adjacent ops.
+    """
+    if scale is None:
+        scale = 1.0 / math.sqrt(q.shape[-1])
+    if mask is not None and mask != "causal":
+        raise ValueError("batch_invariant_paged_attention: mask must be None or 'causal'")
+    B, Hq, Tq, D = q.shape
+    _, Hkv, page_size, Dk = k_pages.shape
+    if v_pages.shape != k_pages.shape or Dk != D or D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
+        raise ValueError(f"paged attention: unsupported shapes q {tuple(q.shape)} k {tuple(k_pages.shape)} "
+                         f"v {tuple(v_pages.shape)}")
+    if page_size & (page_size - 1):
+        raise ValueError(f"paged attention: page size {page_size} is not a power of two")
+    if block_table.ndim != 2 or block_table.shape[0] != B:
+        raise ValueError(f"paged attention: block table {tuple(block_table.shape)} for batch {B}")
+    dt, k_pages, v_pages = _prep(q, k_pages, v_pages)
+    _lib.require_gpu("batch_invariant_paged_attention", q, k_pages, v_pages, block_table)
+    k_pages, v_pages = _fix(k_pages), _fix(v_pages)
+    table = block_table.to(torch.int32).contiguous()
+    L = table.shape[1] * page_size
+    kl = _lens(kv_lens, B, L, q.device)
+    causal = mask == "causal"
+    if causal and kl is None and Tq > L:
+        raise ValueError(f"causal prefill needs T_q <= L (T_q={Tq}, L={L})")
+    out = torch.empty((B, Hq, Tq, D), dtype=dt, device=q.device)
+    if B == 0 or Tq == 0:
+        return out
+    lib = _lib.load()
+    ks = (k_pages.stride(0), k_pages.stride(1), k_pages.stride(2))
+    vs = (v_pages.stride(0), v_pages.stride(1), v_pages.stride(2))
+    if Tq == 1:
+        q3 = _fix(q[:, :, 0, :])
+        ws_bytes = lib.bi_attn_decode_workspace_bytes(B, Hq, L, D)
+        ws = _lib.workspace(ws_bytes, q.device)
+        strides = (_lib._c_i64 * 8)(q3.stride(0), q3.stride(1), *ks, *vs)
+        rc = lib.bi_attn_decode_paged(q3.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), table.data_ptr(),
+                                      table.stride(0), page_size, _lib.ptr(kl), out.data_ptr(), B, Hq, Hkv, L, D,
+                                      strides, float(scale), _lib.DTYPE_CODE[dt], _lib.ptr(ws), ws_bytes,
+                                      _lib.stream_of(q))
+        _lib.check(rc, "bi_attn_decode_paged")
+        return out
+    q = _fix(q)
+    strides = (_lib._c_i64 * 9)(q.stride(0), q.stride(1), q.stride(2), *ks, *vs)
+    rc = lib.bi_attn_prefill_paged(q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), table.data_ptr(),
+                                   table.stride(0), page_size, _lib.ptr(kl), out.data_ptr(), B, Hq, Hkv, Tq, L, D,
+                                   strides, 1 if causal else 0, float(scale), _lib.DTYPE_CODE[dt],
+                                   _lib.stream_of(q))
+    _lib.check(rc, "bi_attn_prefill_paged")
+    return out

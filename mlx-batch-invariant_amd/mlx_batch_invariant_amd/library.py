@@ -17,7 +17,9 @@ Operators (each the same computation, and bits, as the Python function named):
 * ``quantized_matmul(x, w, scales, biases, group_size, bits)``;
 * ``rms_norm(x, weight, eps)``; ``layer_norm(x, weight, bias, eps)``;
 * ``attention(q, k, v, scale, causal, kv_lens)``: decode for one query token,
-  prefill otherwise (``mask="causal"`` is bottom-right aligned).
+  prefill otherwise (``mask="causal"`` is bottom-right aligned);
+* ``paged_attention(q, k_pages, v_pages, block_table, kv_lens, scale, causal)``:
+  the same over a paged K/V pool (``batch_invariant_paged_attention``).
 
 The ops have no autograd formula (inference kernels, as in the reference).
 """
@@ -86,3 +88,15 @@ def attention(q: Tensor, k: Tensor, v: Tensor, scale: float, causal: bool, kv_le
 @attention.register_fake
 def _attention_fake(q, k, v, scale, causal, kv_lens):
     return q.new_empty((*q.shape[:-1], v.shape[-1]))
+
+
+@torch.library.custom_op(f"{NAMESPACE}::paged_attention", mutates_args=())
+def paged_attention(q: Tensor, k_pages: Tensor, v_pages: Tensor, block_table: Tensor, kv_lens: Optional[Tensor],
+                    scale: float, causal: bool) -> Tensor:
+    return _k.batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens, scale=scale,
+                                              mask="causal" if causal else None)
+
+
+@paged_attention.register_fake
+def _paged_attention_fake(q, k_pages, v_pages, block_table, kv_lens, scale, causal):
+    return q.new_empty((*q.shape[:-1], v_pages.shape[-1]))

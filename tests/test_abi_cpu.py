@@ -75,6 +75,11 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert "multiples of 8" in _err(lib)
     # missing workspace for a split launch
     assert lib.bi_matmul(p, 65 * 256, p, 65 * 256, p, 2, 4, 65 * 256, 2, None, 0, None) == -3
+    # paged attention: the page table is checked before anything runs
+    st = (ctypes.c_int64 * 8)(*([128] * 8))
+    assert lib.bi_attn_decode_paged(p, p, p, p, 4, 3, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20, None) == -1
+    assert lib.bi_attn_decode_paged(p, p, p, None, 4, 4, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20, None) == -1
+    assert lib.bi_attn_decode_paged(p, p, p, p, 2, 4, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20, None) == -1
     # unsupported quantization
     assert lib.bi_quantized_matmul(p, 64, p, p, p, p, 2, 4, 64, 3, 64, 2, None, 0, None) == -2
     assert lib.bi_quantized_matmul(p, 96, p, p, p, p, 2, 4, 96, 4, 64, 2, None, 0, None) == -1

@@ -46,6 +46,15 @@ def test_ops_equal_python_functions():
         bi.batch_invariant_attention(q, k, v, scale=0.125, mask="causal"))
     assert bits(ops.attention(q[:, :, :1], k, v, 0.125, False, None)) == bits(
         bi.batch_invariant_attention(q[:, :, :1], k, v, scale=0.125))
+    # a one-page-per-64-keys pool holding the same keys in order
+    kp = torch.zeros((2, 2, 64, 64), dtype=k.dtype, device=k.device)
+    vp = torch.zeros_like(kp)
+    kp[:, :, :40] = k
+    vp[:, :, :40] = v
+    table = torch.arange(2, dtype=torch.int32, device=k.device).reshape(2, 1)
+    lens = torch.full((2,), 40, dtype=torch.int32, device=k.device)
+    assert bits(ops.paged_attention(q, kp, vp, table, lens, 0.125, True)) == bits(
+        bi.batch_invariant_attention(q, k, v, scale=0.125, mask="causal"))
 
 
 def test_opcheck():

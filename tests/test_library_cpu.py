@@ -7,7 +7,7 @@ from torch._subclasses.fake_tensor import FakeTensorMode
 
 import mlx_batch_invariant_amd  # noqa: F401  (registers the ops)
 
-OPS = ["matmul", "quantized_matmul", "rms_norm", "layer_norm", "attention"]
+OPS = ["matmul", "quantized_matmul", "rms_norm", "layer_norm", "attention", "paged_attention"]
 
 
 def test_ops_are_registered_with_schemas():
@@ -32,6 +32,9 @@ def test_fake_shapes_and_dtypes():
         q = torch.empty(2, 8, 3, 64, dtype=torch.bfloat16)
         kv = torch.empty(2, 2, 40, 64, dtype=torch.bfloat16)
         assert torch.ops.mlx_bi.attention(q, kv, kv, 0.125, True, None).shape == q.shape
+        pool = torch.empty(9, 2, 16, 64, dtype=torch.bfloat16)
+        table = torch.empty(2, 3, dtype=torch.int32)
+        assert torch.ops.mlx_bi.paged_attention(q, pool, pool, table, None, 0.125, True).shape == q.shape
 
 
 def test_cpu_tensors_fail_loudly():
