@@ -31,6 +31,8 @@
 // distinct bank groups instead of one.
 #pragma once
 
+#include <type_traits>
+
 #include "bi_gemm_tile.h"
 
 namespace bi {
@@ -134,13 +136,26 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
       braw[j].scale[i] = Ms[rt * C::kSPR + v];
       braw[j].bias[i] = Ms[16 * C::kSPR + rt * C::kSPR + v];
     }
-    F af[1][kSteps];
+    // A fragments are read from LDS one step ahead of their MFMA (not all
+    // eight up front): 24 fewer live registers, which lets a CU hold every
+    // workgroup of the decode grid at once.
+    auto afrag = [&](int s) {
+      return *reinterpret_cast<const F*>(As + C::a_off(arow, j * kGroupK + 64 * q + 8 * s));
+    };
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    auto steps = [&](auto fast) {
+      F a_cur = afrag(0);
 #pragma unroll
-    for (int s = 0; s < kSteps; ++s)
-      af[0][s] = *reinterpret_cast<const F*>(As + C::a_off(arow, j * kGroupK + 64 * q + 8 * s));
-    f32x4 acc[1];
-    mma_group<T, QB, 1, true>(bsrc, braw[j], af, g, q, acc);
-    part[g * kWave + lane] = acc[0];
+      for (int s = 0; s < kSteps; ++s) {
+        const F a_nxt = afrag(s + 1 < kSteps ? s + 1 : s);
+        const F bf = bsrc.template frag<true, decltype(fast)::value>(braw[j], s, QB::kbase(g, q));
+        acc = mfma_step(a_cur, bf, acc);
+        a_cur = a_nxt;
+      }
+    };
+    if (!__any(bsrc.huge_scale(braw[j]))) steps(std::true_type());
+    else steps(std::false_type());
+    part[g * kWave + lane] = acc;
   }
   __syncthreads();
   // Ordered fold: one thread per output element (lane l, register e of the
