@@ -767,7 +767,8 @@ static void launch_wg(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, 
 
 // Mid-M launch (bi_gemm_mid.h) for a quantized B, 2-byte T, K % 256 == 0:
 // 16 < M < kBigMinM at any N, and 4 < M <= 16 with >= 128 blocks of 64
-// columns. Row blocks of 16 MT rows (MT = 1, 2, 4; M > 64 takes several);
+// columns. Row blocks of 16 MT rows (MT = 1 for M <= 16, 4 for 32 < M <= 64,
+// else 2: M > 64 takes several);
 // when the (column block, row block) tiles are fewer than kMidMinTiles, K is
 // split into chunks of cg groups (per-group fp32 partials in the workspace,
 // then fold_groups) so that about kMidTargetWG workgroups run.
@@ -782,7 +783,9 @@ static inline MidPlan mid_plan(int64_t M, int64_t N, int64_t K) {
   if (M <= 4 || M >= kBigMinM || N <= 0 || K <= 0 || K % kGroupK) return p;
   if (M <= 16 && ceil_div(N, 64) < 128) return p;
   const int G = (int)(K / kGroupK);
-  p.mt = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  // 64-row blocks only for 32 < M <= 64; larger M runs several 32-row blocks
+  // (measured faster: more workgroups per CU, each a shallower register file).
+  p.mt = M <= 16 ? 1 : (M <= 32 || M > 64) ? 2 : 4;
   p.mtiles = (int)ceil_div(M, 16 * p.mt);
   const int64_t t = ceil_div(N, 64) * p.mtiles;
   p.cg = G;
@@ -804,8 +807,8 @@ static bool use_mid(const MidPlan& p, int64_t lda, const T* a) {
   }
 }
 
-// Unsplit (at most about one workgroup per CU): the deepest A ring that fits
-// and B loads 8 groups ahead. Split K: short chunks and several workgroups
+// Unsplit: an 8-group A ring for 16-row blocks, 4 for 32- and 64-row blocks
+// (a deeper ring for 32 rows measured 7% slower), B loads 8 groups ahead. Split K: short chunks and several workgroups
 // per CU, so a shallow ring and B loads kMidSplitPD groups ahead (a chunk runs
 // in whole rounds of that many groups; the padding groups are not folded).
 constexpr int kMidSplitPD = 2;
@@ -829,7 +832,7 @@ static void launch_mid(const T* a, int64_t lda, const BSrc& bsrc, T* out, float*
                        int G, const MidPlan& p, hipStream_t st) {
   if constexpr (sizeof(T) == 2 && BSrc::kMeta) {
     if (p.mt == 1) launch_mid2<T, BSrc, 1, 8, 4>(a, lda, bsrc, out, ws, M, N, K, G, p, st);
-    else if (p.mt == 2) launch_mid2<T, BSrc, 2, 8, 4>(a, lda, bsrc, out, ws, M, N, K, G, p, st);
+    else if (p.mt == 2) launch_mid2<T, BSrc, 2, 4, 4>(a, lda, bsrc, out, ws, M, N, K, G, p, st);
     else launch_mid2<T, BSrc, 4, 4, 2>(a, lda, bsrc, out, ws, M, N, K, G, p, st);
   }
 }
