@@ -188,4 +188,155 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
   }
 }
 
+
+// K-interleaved variant (512 threads): wave w owns columns 16 (w % 4) .. + 15
+// of the block and the chunk's groups of parity w / 4, so two waves share each
+// SIMD and one's dequantisation overlaps the other's MFMAs. Ring stage t holds
+// A of groups 2t and 2t + 1; the odd wave's raw fp32 partial of stage t goes
+// to a double-buffered LDS slot and the even wave folds the stage at the next
+// barrier: total = (total + acc_2t) + acc_2t+1, the same left fold in group
+// order as gemm_mid (SPLIT: every wave stores its own partials).
+template <typename T, class BSrc, int MT, int PD, int NA, bool SPLIT>
+__global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc bsrc, T* __restrict__ out,
+                                                 float* __restrict__ part, int M, int N, int K, int G, int CG) {
+  typedef MidCfg<T, MT, NA> C;  // one group's A buffer; a stage holds two
+  typedef typename Frag<T>::type F;
+  constexpr int kCopiesPerWave = C::kCopies / 4;  // two groups' copies over eight waves
+  // As in gemm_mid: vector-memory instructions certainly issued after a
+  // stage's copies when its barrier is reached (copies of NA - 2 later stages
+  // and at least min(PD, NA - 1) stages of this wave's B loads).
+  constexpr int kAfter = (NA - 2) * kCopiesPerWave + (PD < NA - 1 ? PD : NA - 1) * MidLoads<BSrc>::kMin;
+  constexpr int kWaitA = kAfter < 63 ? kAfter : 63;
+  __shared__ __attribute__((aligned(1024))) char As[NA][2][C::kBufBytes];
+  __shared__ __attribute__((aligned(16))) f32x4 xbuf[2][4][MT][kWave];
+  static_assert(sizeof(As) + sizeof(xbuf) <= 160 * 1024, "gemm_mid2: LDS");
+
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int cw = wave & 3, par = wave >> 2;
+  const int r = lane % 16, q = lane / 16;
+  const int m0 = blockIdx.y * C::kRows;
+  const int n_out = blockIdx.x * 64 + 16 * cw + r;
+  const int n = min(n_out, N - 1);
+  const typename BSrc::Lane bl = bsrc.lane(n, q);
+  const int gb = blockIdx.z * CG;           // the chunk's first group
+  const int gn = min(CG, G - gb);           // its group count (>= 1)
+  const int ns = (gn + 1) / 2;              // stages
+
+  auto copy_stage = [&](int t) {  // groups 2t, 2t + 1 (clamped to the chunk) into As[t % NA]
+#pragma unroll
+    for (int i = 0; i < kCopiesPerWave; ++i) {
+      const int ci = wave * kCopiesPerWave + i;
+      const int h = ci / C::kCopies, cl = ci % C::kCopies;
+      const int gg = gb + min(2 * t + h, gn - 1);
+      const int row = cl * C::kRowsPerCopy + lane / (C::kRowBytes / 16);
+      const int ch = (lane % (C::kRowBytes / 16)) ^ (row & 15);
+      copy_to_lds16(a + (int64_t)min(m0 + row, M - 1) * lda + gg * kGroupK + 8 * ch,
+                    As[t % NA][h] + 1024 * cl);
+    }
+  };
+
+  f32x4 total[MT], held[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) total[i] = held[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  typename BSrc::Raw raw[PD];
+#pragma unroll
+  for (int t = 0; t < NA - 1; ++t) copy_stage(t);
+#pragma unroll
+  for (int j = 0; j < PD; ++j) {
+    asm volatile("" ::: "memory");
+    bsrc.load_full(raw[j], bl, gb + min(2 * j + par, gn - 1));
+  }
+  asm volatile("" ::: "memory");
+
+  // Even waves: fold stage tp (its own partial, kept in `held`, then the odd
+  // wave's from LDS). Runs after a barrier that follows the odd wave's write.
+  auto fold_stage = [&](int tp) {
+    if constexpr (!SPLIT) {
+      if (par == 0 && tp >= 0 && tp < ns) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) total[i] = total[i] + held[i];
+        if (2 * tp + 1 < gn) {
+#pragma unroll
+          for (int i = 0; i < MT; ++i) total[i] = total[i] + xbuf[tp & 1][cw][i][lane];
+        }
+      }
+    }
+  };
+
+  auto stage = [&](int t, int j) {
+    stage_barrier<kWaitA>();
+    fold_stage(t - 1);
+    copy_stage(t + NA - 1);
+    asm volatile("" ::: "memory");
+    const char* buf = As[t % NA][par];
+    f32x4 acc[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int gl = min(2 * t + par, gn - 1);
+    const int gc = gb + gl;
+    const int kq = BSrc::kbase(gc, q);
+    auto steps = [&](auto fast) {
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) {
+        const int ch = (BSrc::a_k(gc, q, s) - gc * kGroupK) / 8;
+        const F bf = bsrc.template frag<true, decltype(fast)::value>(raw[j], s, kq);
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const F af = *reinterpret_cast<const F*>(buf + C::off(16 * i + r, ch));
+          acc[i] = mfma_step(af, bf, acc[i]);
+        }
+      }
+    };
+    if (!__any(bsrc.huge_scale(raw[j]))) steps(std::true_type());
+    else steps(std::false_type());
+    if constexpr (SPLIT) {
+      if (2 * t + par < gn && n_out < N) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int m = m0 + 16 * i + 4 * q + e;
+            if (m < M) part[((int64_t)gc * M + m) * N + n_out] = acc[i][e];
+          }
+      }
+    } else {
+      if (par == 0) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) held[i] = acc[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) xbuf[t & 1][cw][i][lane] = acc[i];
+      }
+    }
+    asm volatile("" ::: "memory");
+    bsrc.load_full(raw[j], bl, gb + min(2 * (t + PD) + par, gn - 1));
+    asm volatile("" ::: "memory");
+  };
+  const int Sp = (ns + PD - 1) / PD * PD;
+#pragma unroll
+  for (int j = 0; j < PD; ++j) stage(j, j);
+  for (int t0 = PD; t0 < Sp; t0 += PD) {
+#pragma unroll
+    for (int j = 0; j < PD; ++j) stage(t0 + j, j);
+  }
+  wait_vm_lgkm0<0>();   // every copy landed and the odd waves' last partials are written
+  __syncthreads();
+  // Stages 0 .. Sp - 2 were folded at the start of the next stage; the last
+  // one here (a padding stage folds nothing: its predecessor ns - 1 < Sp - 1
+  // was folded inside the loop).
+  fold_stage(Sp - 1);
+
+  if (!SPLIT && par == 0 && n_out < N) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 16 * i + 4 * q + e;
+        if (m < M) out[(int64_t)m * N + n_out] = to_store<T>(total[i][e]);
+      }
+  }
+}
+
 }  // namespace bi

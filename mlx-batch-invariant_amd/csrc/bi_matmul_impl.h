@@ -812,11 +812,21 @@ static bool use_mid(const MidPlan& p, int64_t lda, const T* a) {
 // per CU, so a shallow ring and B loads kMidSplitPD groups ahead (a chunk runs
 // in whole rounds of that many groups; the padding groups are not folded).
 constexpr int kMidSplitPD = 2;
+// Unsplit launches of at most this many workgroups (about one per CU) run the
+// K-interleaved eight-wave kernel (two waves per SIMD); larger grids already
+// put several four-wave workgroups on each CU, where it measured slower.
+constexpr int kMidInterleaveMaxTiles = 320;
+constexpr int kMidInterleavePD = 4;
 template <typename T, class BSrc, int MT, int NA_ONE, int NA_SPLIT>
 static void launch_mid2(const T* a, int64_t lda, const BSrc& bsrc, T* out, float* ws, int M, int N, int K,
                         int G, const MidPlan& p, hipStream_t st) {
   constexpr int PD = 8;
   const dim3 grid(ceil_div(N, 64), p.mtiles, p.chunks);
+  if (p.chunks == 1 && G >= 2 && (int64_t)grid.x * grid.y <= kMidInterleaveMaxTiles) {
+    constexpr int NA2 = MT == 4 ? 2 : 4;
+    gemm_mid2<T, BSrc, MT, kMidInterleavePD, NA2, false><<<grid, 512, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G, G);
+    return;
+  }
   if (p.chunks > 1) {
     gemm_mid<T, BSrc, MT, kMidSplitPD, NA_SPLIT, true><<<grid, 256, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G,
                                                                              p.cg);
