@@ -109,7 +109,7 @@ def qmm_bytes(M, N, K, bits, gs):
 # group count and scale-slice alignment select.
 HEADLINE_KERNEL = {
     (4, 64): "gemv_stream<bf16,4,64,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)",
-    (8, 128): "gemv_stream<bf16,8,128,W=4,NB=4,MR=1,PD=2> (bi_quantized_matmul, M <= 4: one launch)",
+    (8, 128): "gemv_stream<bf16,8,128,W=4,NB=4,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)",
 }
 
 

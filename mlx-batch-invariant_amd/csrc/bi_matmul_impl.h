@@ -704,8 +704,9 @@ static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& 
 
 // Launch shapes in order of preference (measured, Llama MLP shape, M = 1):
 // two groups per wave with one group of codes in flight beyond the one being
-// computed, else four groups per wave two ahead. A shape whose scale slice or
-// A slice is not whole 16-byte loads is skipped.
+// computed, else four groups per wave one ahead (8-bit g128, whose two-group
+// scale slice is not a whole 16-byte load: 13.7 us against 14.1 two ahead). A
+// shape whose scale slice or A slice is not whole 16-byte loads is skipped.
 template <typename T, int BITS, int GS>
 static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N, int K,
                           int G, hipStream_t st) {
@@ -716,7 +717,7 @@ static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b,
   switch (G) {
     case 16:
       return launch_stream_m<T, BITS, GS, 8, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
-             launch_stream_m<T, BITS, GS, 4, 4, 2>(a, lda, b, out, M, N, K, G, st);
+             launch_stream_m<T, BITS, GS, 4, 4, 1>(a, lda, b, out, M, N, K, G, st);
     case 8:
       return launch_stream_m<T, BITS, GS, 4, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
              launch_stream_m<T, BITS, GS, 2, 4, 2>(a, lda, b, out, M, N, K, G, st);
