@@ -24,8 +24,10 @@
 // its workgroup's metadata loads, which arrive among the whole weight stream;
 // here a wave waits only for its own.
 //
-// LDS (dynamic): G * 64 f32x4 partials, then per wave: A [MR][NB * 256],
-// scales [16][SPR], biases [16][SPR] (SPR = NB * 256 / GS). A's 8-element
+// LDS (dynamic), per wave: A [MR][NB * 256], scales [16][SPR], biases
+// [16][SPR] (SPR = NB * 256 / GS); once the wave has computed its groups, the
+// same region holds its NB raw fp32 partials (64 lanes x f32x4 each), which
+// the fold reads after the barrier. A's 8-element
 // chunk c of row r sits in slot c ^ (r & 15) of its row, so the 16 rows of a
 // fragment read (same chunk, row stride a multiple of 256 bytes) hit 16
 // distinct bank groups instead of one.
@@ -45,7 +47,10 @@ struct GemvStreamCfg {
   static constexpr int kALoads = kAElems / kCE / kWave;       // A loads per lane
   static constexpr int kMChunks = 2 * 16 * kSPR / kCE;        // meta chunks per wave
   static constexpr int kMLoads = (kMChunks + kWave - 1) / kWave;
-  static constexpr int kWaveElems = kAElems + 2 * 16 * kSPR;  // LDS elements per wave
+  static constexpr int kWaveElems = kAElems + 2 * 16 * kSPR;  // A + metadata elements per wave
+  // Bytes per wave region: A and metadata, or later the NB partials.
+  static constexpr int kWaveBytes = (kWaveElems * (int)sizeof(T) > NB * kWave * 16)
+                                        ? kWaveElems * (int)sizeof(T) : NB * kWave * 16;
   static constexpr int kRowElems = NB * kGroupK;               // A row of the wave's slice
   // LDS element offset of A element k (0 <= k < kRowElems) of slice row ar.
   static __device__ __forceinline__ int a_off(int ar, int k) {
@@ -54,9 +59,7 @@ struct GemvStreamCfg {
   static_assert(sizeof(T) == 2, "gemv_stream: 2-byte element types only (16-byte pieces = one fragment)");
   static_assert(kAElems % (kCE * kWave) == 0, "A slice must be whole 16-byte loads per lane");
   static_assert(kSPR % kCE == 0, "scale rows must be whole 16-byte chunks");
-  static size_t lds_bytes(int G) {
-    return (size_t)G * kWave * sizeof(f32x4) + (size_t)W * kWaveElems * sizeof(T);
-  }
+  static size_t lds_bytes(int /*G*/) { return (size_t)W * kWaveBytes; }
 };
 
 template <typename T, int BITS, int GS, int W, int NB, int MR, int PD>
@@ -68,10 +71,10 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   typedef QuantB<T, BITS, GS> QB;
   typedef typename Frag<T>::type F;
   extern __shared__ __attribute__((aligned(16))) f32x4 smem[];
-  f32x4* part = smem;                                               // [G][64]
+  char* regions = reinterpret_cast<char*>(smem);                   // W x kWaveBytes
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  T* As = reinterpret_cast<T*>(smem + (size_t)G * kWave) + (size_t)wave * C::kWaveElems;
+  T* As = reinterpret_cast<T*>(regions + (size_t)wave * C::kWaveBytes);
   T* Ms = As + C::kAElems;                                          // [2][16][SPR]
   const int r = lane % 16, q = lane / 16;
   const int n_base = blockIdx.x * 16;
@@ -122,6 +125,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
 
   const int rt = n - n_base;                      // this lane's row of the tile (clamped)
   const int arow = min(r, MR - 1);                // A rows past MR alias a loaded row (never stored)
+  f32x4 accs[NB];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int g = g0 + j;
@@ -155,25 +159,34 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     };
     if (!__any(bsrc.huge_scale(braw[j]))) steps(std::true_type());
     else steps(std::false_type());
-    part[g * kWave + lane] = acc;
+    accs[j] = acc;
   }
+  // The wave's A and metadata are dead now (its DS reads complete in order):
+  // its partials take their place.
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+    *reinterpret_cast<f32x4*>(regions + (size_t)wave * C::kWaveBytes + j * kWave * 16 + lane * 16) = accs[j];
   __syncthreads();
   // Ordered fold: one thread per output element (lane l, register e of the
   // MFMA result layout), eight LDS loads in flight, adds in group order.
-  const float* partf = reinterpret_cast<const float*>(part);
+  // Partial of group g: wave g / NB's region, slot g % NB.
+  auto pptr = [&](int g, int l, int e) {
+    return reinterpret_cast<const float*>(regions + (size_t)(g / NB) * C::kWaveBytes + (g % NB) * kWave * 16 +
+                                          l * 16) + e;
+  };
   for (int idx = threadIdx.x; idx < kWave * 4; idx += kWave * W) {
     const int e = idx / kWave, l = idx % kWave;
-    const float* pp = partf + l * 4 + e;
     float total = 0.f;
     int gg = 0;
     for (; gg + 8 <= G; gg += 8) {
       float v[8];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) v[jj] = pp[(gg + jj) * kWave * 4];
+      for (int jj = 0; jj < 8; ++jj) v[jj] = *pptr(gg + jj, l, e);
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) total = total + v[jj];
     }
-    for (; gg < G; ++gg) total = total + pp[gg * kWave * 4];
+    for (; gg < G; ++gg) total = total + *pptr(gg, l, e);
     const int col = n_base + l % 16;
     const int m = 4 * (l / 16) + e;
     if (m < M && col < N) out[(int64_t)m * N + col] = to_store<T>(total);
