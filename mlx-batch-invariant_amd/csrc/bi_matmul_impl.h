@@ -37,7 +37,7 @@
 namespace bi {
 
 constexpr int kSplitMMax = 32;
-constexpr int kStreamMMax = 16;   // rows the streaming GEMV's one 16-row MFMA tile covers
+constexpr int kStreamMMax = 8;    // rows of x the streaming GEMV takes (9..16 measured faster on gemm_mid2)
 // gemv_wg with A staged in LDS: at most kGemvAChunks / W 16-byte chunks of A
 // per thread (M * K <= kGemvAChunks * 64 * 8).
 constexpr int kGemvAChunks = 32;
@@ -698,8 +698,7 @@ static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& 
                             int K, int G, hipStream_t st) {
   if (M == 1) return launch_stream1<T, BITS, GS, W, NB, 1, PD>(a, lda, b, out, M, N, K, G, st);
   if (M <= 4) return launch_stream1<T, BITS, GS, W, NB, 4, PD>(a, lda, b, out, M, N, K, G, st);
-  if (M <= 8) return launch_stream1<T, BITS, GS, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
-  return launch_stream1<T, BITS, GS, W, NB, 16, PD>(a, lda, b, out, M, N, K, G, st);
+  return launch_stream1<T, BITS, GS, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
 }
 
 // Launch shapes in order of preference (measured, Llama MLP shape, M = 1):

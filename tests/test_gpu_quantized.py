@@ -114,10 +114,11 @@ def test_quantized_mid_m_launch_matches_oracle(bits_, gs, dt):
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 def test_quantized_stream_launch_up_to_16_rows(bits_, gs, dt):
-    """M <= 16 with >= 512 tiles of 16 columns and 8 or 16 groups takes the
+    """M <= 8 with >= 512 tiles of 16 columns and 8 or 16 groups takes the
     streaming GEMV for 2-byte types (one 16-row MFMA tile, A rows past M
-    clamped; fp32 takes the workgroup-fold GEMV): rows equal the oracle within
-    the stated bound and the same rows computed alone, bit for bit."""
+    clamped), 9 <= M <= 16 the mid-M launch, fp32 the workgroup-fold GEMV:
+    rows equal the oracle within the stated bound and the same rows computed
+    alone, bit for bit."""
     N, K = 8192 + 40, 4096     # 515 column tiles, the last one partial; G = 16
     wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 3 + gs)
     wq, s, b = wq.cuda(), s.cuda(), b.cuda()
