@@ -459,7 +459,9 @@ def main(argv=None) -> int:
     a = p.parse_args(argv)
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every kernel here is single-GPU and no multi-GPU "
-              "path exists in this build (see DESIGN.md for how it would shard).", file=sys.stderr)
+              "path exists in this build (rows and heads would shard across GPUs without any "
+              "exchange; a K split would all-gather per-group partials and fold them in order).",
+              file=sys.stderr)
         return 2
     import torch
     if not torch.cuda.is_available():
