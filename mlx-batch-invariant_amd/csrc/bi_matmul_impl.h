@@ -584,6 +584,11 @@ static inline bool use_wg(int64_t M, int G) { return M <= kSplitMMax && G * (M <
 // groups whose raw partials fold_groups folds. A function of the shape only,
 // so the workspace query and the launch agree.
 constexpr int kTallMinTiles = 200;
+// With at most 4 groups of K a workgroup's fixed costs and the A tile it
+// re-reads dominate: wider column tiles win (Qwen2-0.5B linear [4864, 896],
+// M = 64: 13.8 -> 9.3 us); with more groups they lose (4096 x 4096, M = 64:
+// 18.4 -> 21.6 us).
+constexpr int kTallMinTilesShortK = 100;
 struct TallPlan {
   bool use = false;
   int bm = 0, bn = 0, chunks = 1, cg = 0;
@@ -592,17 +597,18 @@ static inline TallPlan tall_plan(int64_t M, int64_t N, int64_t K) {
   TallPlan p;
   if (M <= 16 || M > 128 || K <= 0 || K % 64) return p;
   const int G = ceil_div(K, kGroupK);
+  const int min_tiles = G <= 4 ? kTallMinTilesShortK : kTallMinTiles;
   p.bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
   const int narrowest = p.bm == 32 ? 32 : 16;
   for (int bn : {64, 32, 16}) {
     if (bn < narrowest) break;
     p.bn = bn;
-    if (ceil_div(N, bn) >= kTallMinTiles) break;
+    if (ceil_div(N, bn) >= min_tiles) break;
   }
   const int64_t t = ceil_div(N, p.bn);
   p.cg = G;
-  if (t < kTallMinTiles && G > 1) {
-    const int want = std::min<int64_t>(G, ceil_div(kTallMinTiles, t));
+  if (t < min_tiles && G > 1) {
+    const int want = std::min<int64_t>(G, ceil_div(min_tiles, t));
     p.cg = ceil_div(G, want);
     p.chunks = ceil_div(G, p.cg);
   }
