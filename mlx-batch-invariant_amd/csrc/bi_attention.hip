@@ -34,7 +34,22 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeArgs a) {
   const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
   const int ns = (len + kSplit - 1) / kSplit;
   float M = -INFINITY, Ls = 0.0f, A = 0.0f;
-  for (int i = 0; i < ns; ++i) {
+  // Splits merge strictly left to right; their partials are loaded eight
+  // splits at a time ahead of the merges (the loads are independent).
+  int i = 0;
+  for (; i + 8 <= ns; i += 8) {
+    float pm[8], pl[8], pa[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t po = bh * a.nsplit + i + j;
+      pm[j] = a.pm[po];
+      pl[j] = a.pl[po];
+      pa[j] = a.pacc[po * D + d];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) merge_split<1>(M, Ls, &A, pm[j], pl[j], &pa[j]);
+  }
+  for (; i < ns; ++i) {
     const int64_t po = bh * a.nsplit + i;
     const float acc = a.pacc[po * D + d];
     merge_split<1>(M, Ls, &A, a.pm[po], a.pl[po], &acc);
