@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define BI_ABI_VERSION 1
+#define BI_ABI_VERSION 2
 
 enum bi_dtype { BI_F32 = 0, BI_F16 = 1, BI_BF16 = 2 };
 
@@ -129,8 +129,9 @@ int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w, const voi
  *   strides[2..4] = k  (batch, head, position)
  *   strides[5..7] = v  (batch, head, position)
  * with d contiguous. out contiguous [B, Hq, D]. kv_lens (device int32[B], may
- * be NULL = all L) gives each sequence's own key count, 1 <= len <= L; a
- * sequence's output depends only on its own first len keys. Hq % Hkv == 0,
+ * be NULL = all L) gives each sequence's own key count, clamped to [0, L]; a
+ * sequence's output depends only on its own first len keys, and a sequence of
+ * length 0 gets an all-zero output (no key: no softmax). Hq % Hkv == 0,
  * D in {64, 128}. Keys go in fixed splits of BI_SPLIT_KEYS; the workspace
  * holds per-split (m, l, acc) partials and a work-item counter
  * (bi_attn_decode_workspace_bytes); calls that overlap must not share it.
@@ -142,21 +143,22 @@ int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* k
                    const int64_t* strides, float scale, int dtype, void* ws,
                    size_t ws_bytes, void* stream);
 
-/* Paged K/V variant of bi_attn_decode: k_pages / v_pages are pools of pages of
- * page_size keys (a power of two, 1 .. 2^24); strides[2..4] / [5..7] are the
- * (page, head, position-in-page) element strides. Key p of sequence b is row
- * p mod page_size of page block_table[b * table_stride + p / page_size]
- * (device int32; table_stride >= ceil(L / page_size); every page index a
- * sequence reaches must be valid). L is the longest sequence the table can
- * hold (it sizes the workspace, as in bi_attn_decode). Same arithmetic as
- * bi_attn_decode: the output equals the contiguous call on the same keys, bit
- * for bit.
+/* Paged K/V variant of bi_attn_decode: k_pages / v_pages are pools of
+ * num_pages pages of page_size keys (a power of two, 1 .. 2^24);
+ * strides[2..4] / [5..7] are the (page, head, position-in-page) element
+ * strides. Key p of sequence b is row p mod page_size of page
+ * block_table[b * table_stride + p / page_size] (device int32; table_stride
+ * >= ceil(L / page_size)). A table entry outside [0, num_pages) is clamped
+ * into the pool, so a stale table gives wrong values but never reads outside
+ * it. L is the longest sequence the table can hold (it sizes the workspace,
+ * as in bi_attn_decode). Same arithmetic as bi_attn_decode: the output equals
+ * the contiguous call on the same keys, bit for bit.
  * Replaces: nothing in the reference (its decode reads one contiguous cache,
  * kernels/attention.py:87-147); the paged-KV item of its roadmap of adjacent
  * ops. */
 int bi_attn_decode_paged(const void* q, const void* k_pages, const void* v_pages,
                          const int32_t* block_table, int64_t table_stride, int64_t page_size,
-                         const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
+                         int64_t num_pages, const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
                          int64_t L, int64_t D, const int64_t* strides, float scale, int dtype,
                          void* ws, size_t ws_bytes, void* stream);
 
@@ -168,8 +170,9 @@ int bi_attn_decode_paged(const void* q, const void* k_pages, const void* v_pages
  * out contiguous [B, Hq, Tq, D]. With causal != 0, query t of sequence b sees
  * keys [0, len_b - Tq + t + 1) (bottom-right aligned, so a later chunk of a
  * prompt run against the whole cache is a valid prefill); otherwise all len_b.
- * len_b = kv_lens[b] (device int32[B], may be NULL = L), Tq <= len_b <= L when
- * causal. Same split order and per-split arithmetic as bi_attn_decode, so a token's
+ * len_b = kv_lens[b] (device int32[B], may be NULL = L; clamped to [0, L]);
+ * with causal != 0, Tq <= L is required, and a query row with no visible key
+ * (len_b - Tq + t + 1 <= 0) gets an all-zero output. Same split order and per-split arithmetic as bi_attn_decode, so a token's
  * output equals a later decode step's and chunked equals one-shot prefill.
  * Replaces: kernels/attention.py:368-390 (batch_invariant_prefill_attention),
  * kernels :173-254. */
@@ -178,15 +181,16 @@ int bi_attn_prefill(const void* q, const void* k, const void* v, const int32_t* 
                     int64_t D, const int64_t* strides, int causal, float scale, int dtype,
                     void* stream);
 
-/* Paged K/V variant of bi_attn_prefill (page pool, strides[3..5] / [6..8] =
- * (page, head, position-in-page), block table as in bi_attn_decode_paged): a
+/* Paged K/V variant of bi_attn_prefill (pool of num_pages pages,
+ * strides[3..5] / [6..8] = (page, head, position-in-page), block table and
+ * clamping as in bi_attn_decode_paged): a
  * prompt chunk run against a paged cache. Bit-identical to bi_attn_prefill on
  * the same keys.
  * Replaces: nothing in the reference (kernels/attention.py:173-254 reads a
  * contiguous cache); the paged-KV prefill item of its roadmap of adjacent ops. */
 int bi_attn_prefill_paged(const void* q, const void* k_pages, const void* v_pages,
                           const int32_t* block_table, int64_t table_stride, int64_t page_size,
-                          const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
+                          int64_t num_pages, const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
                           int64_t Tq, int64_t L, int64_t D, const int64_t* strides, int causal,
                           float scale, int dtype, void* stream);
 

@@ -54,7 +54,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeArgs a) {
     const float acc = a.pacc[po * D + d];
     merge_split<1>(M, Ls, &A, a.pm[po], a.pl[po], &acc);
   }
-  static_cast<T*>(a.out)[bh * D + d] = to_store<T>(A / Ls);
+  // A sequence of length 0 has no split: Ls == 0 and its output is defined as 0.
+  static_cast<T*>(a.out)[bh * D + d] = to_store<T>(Ls > 0.0f ? A / Ls : 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -194,11 +195,14 @@ extern "C" size_t bi_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t 
 namespace {
 
 // Page table of a paged call: power-of-two page size, one row of
-// table_stride >= ceil(L / page_size) page indices per sequence.
-int check_pages(const char* what, const int32_t* table, int64_t table_stride, int64_t page_size, int64_t L,
-                int* shift) {
+// table_stride >= ceil(L / page_size) page indices per sequence, a pool of
+// 1 <= num_pages < 2^31 pages (the kernels clamp every table entry into it).
+int check_pages(const char* what, const int32_t* table, int64_t table_stride, int64_t page_size, int64_t num_pages,
+                int64_t L, int* shift) {
   using namespace bi_host;
   if (!table) return fail(BI_E_INVALID_ARG, "%s: null block table", what);
+  if (num_pages <= 0 || num_pages > 0x7fffffffLL)
+    return fail(BI_E_INVALID_ARG, "%s: num_pages %lld must be in [1, 2^31)", what, (long long)num_pages);
   if (page_size <= 0 || page_size > ((int64_t)1 << 24) || (page_size & (page_size - 1)))
     return fail(BI_E_INVALID_ARG, "%s: page size %lld must be a power of two in [1, 2^24]", what,
                 (long long)page_size);
@@ -214,7 +218,7 @@ int check_pages(const char* what, const int32_t* table, int64_t table_stride, in
 int decode_impl(const char* what, const void* q, const void* k, const void* v, const int32_t* kv_lens, void* out,
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D, const int64_t* strides, float scale,
                 int dtype, void* ws, size_t ws_bytes, void* stream, const int32_t* table, int64_t table_stride,
-                int page_shift) {
+                int page_shift, int64_t num_pages) {
   using namespace bi_host;
   if (B == 0) return BI_OK;
   if (!q || !k || !v || !out || !strides)
@@ -232,7 +236,7 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
     return fail(BI_E_INVALID_ARG, "%s: q, k, v and workspace must be 16-byte aligned", what);
   bi::DecodeArgs a;
   a.q = q; a.k = k; a.v = v; a.kv_lens = kv_lens; a.out = out;
-  a.table = table; a.table_stride = table_stride; a.page_shift = page_shift;
+  a.table = table; a.table_stride = table_stride; a.page_shift = page_shift; a.num_pages = (int)num_pages;
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.L = (int)L;
   a.nsplit = (int)((L + bi::kSplit - 1) / bi::kSplit);
   const int G = (int)(Hq / Hkv);
@@ -265,7 +269,7 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
 int prefill_impl(const char* what, const void* q, const void* k, const void* v, const int32_t* kv_lens,
                  void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L, int64_t D,
                  const int64_t* strides, int causal, float scale, int dtype, void* stream, const int32_t* table,
-                 int64_t table_stride, int page_shift) {
+                 int64_t table_stride, int page_shift, int64_t num_pages) {
   using namespace bi_host;
   if (Tq <= 0) return fail(BI_E_INVALID_ARG, "%s: Tq=%lld", what, (long long)Tq);
   if (causal && Tq > L)
@@ -284,7 +288,7 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
     return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   bi::PrefillArgs a;
   a.q = q; a.k = k; a.v = v; a.kv_lens = kv_lens; a.out = out;
-  a.table = table; a.table_stride = table_stride; a.page_shift = page_shift;
+  a.table = table; a.table_stride = table_stride; a.page_shift = page_shift; a.num_pages = (int)num_pages;
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.Tq = (int)Tq; a.L = (int)L;
   a.causal = causal ? 1 : 0;
   a.q_sb = strides[0]; a.q_sh = strides[1]; a.q_st = strides[2];
@@ -312,21 +316,22 @@ extern "C" int bi_attn_decode(const void* q, const void* k, const void* v, const
   int rc = check_attn_shape("bi_attn_decode", B, Hq, Hkv, L, D);
   if (rc) return rc;
   return decode_impl("bi_attn_decode", q, k, v, kv_lens, out, B, Hq, Hkv, L, D, strides, scale, dtype, ws,
-                     ws_bytes, stream, nullptr, 0, 0);
+                     ws_bytes, stream, nullptr, 0, 0, 0);
 }
 
 extern "C" int bi_attn_decode_paged(const void* q, const void* k_pages, const void* v_pages,
                                     const int32_t* block_table, int64_t table_stride, int64_t page_size,
-                                    const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
-                                    int64_t L, int64_t D, const int64_t* strides, float scale, int dtype,
-                                    void* ws, size_t ws_bytes, void* stream) {
+                                    int64_t num_pages, const int32_t* kv_lens, void* out, int64_t B, int64_t Hq,
+                                    int64_t Hkv, int64_t L, int64_t D, const int64_t* strides, float scale,
+                                    int dtype, void* ws, size_t ws_bytes, void* stream) {
   int rc = check_attn_shape("bi_attn_decode_paged", B, Hq, Hkv, L, D);
   if (rc) return rc;
   int shift = 0;
-  if (B > 0 && (rc = check_pages("bi_attn_decode_paged", block_table, table_stride, page_size, L, &shift)))
+  if (B > 0 &&
+      (rc = check_pages("bi_attn_decode_paged", block_table, table_stride, page_size, num_pages, L, &shift)))
     return rc;
   return decode_impl("bi_attn_decode_paged", q, k_pages, v_pages, kv_lens, out, B, Hq, Hkv, L, D, strides, scale,
-                     dtype, ws, ws_bytes, stream, block_table, table_stride, shift);
+                     dtype, ws, ws_bytes, stream, block_table, table_stride, shift, num_pages);
 }
 
 extern "C" int bi_attn_prefill(const void* q, const void* k, const void* v, const int32_t* kv_lens,
@@ -336,19 +341,20 @@ extern "C" int bi_attn_prefill(const void* q, const void* k, const void* v, cons
   int rc = check_attn_shape("bi_attn_prefill", B, Hq, Hkv, L, D);
   if (rc) return rc;
   return prefill_impl("bi_attn_prefill", q, k, v, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides, causal, scale,
-                      dtype, stream, nullptr, 0, 0);
+                      dtype, stream, nullptr, 0, 0, 0);
 }
 
 extern "C" int bi_attn_prefill_paged(const void* q, const void* k_pages, const void* v_pages,
                                      const int32_t* block_table, int64_t table_stride, int64_t page_size,
-                                     const int32_t* kv_lens, void* out, int64_t B, int64_t Hq, int64_t Hkv,
-                                     int64_t Tq, int64_t L, int64_t D, const int64_t* strides, int causal,
-                                     float scale, int dtype, void* stream) {
+                                     int64_t num_pages, const int32_t* kv_lens, void* out, int64_t B, int64_t Hq,
+                                     int64_t Hkv, int64_t Tq, int64_t L, int64_t D, const int64_t* strides,
+                                     int causal, float scale, int dtype, void* stream) {
   int rc = check_attn_shape("bi_attn_prefill_paged", B, Hq, Hkv, L, D);
   if (rc) return rc;
   int shift = 0;
-  if (B > 0 && (rc = check_pages("bi_attn_prefill_paged", block_table, table_stride, page_size, L, &shift)))
+  if (B > 0 &&
+      (rc = check_pages("bi_attn_prefill_paged", block_table, table_stride, page_size, num_pages, L, &shift)))
     return rc;
   return prefill_impl("bi_attn_prefill_paged", q, k_pages, v_pages, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides,
-                      causal, scale, dtype, stream, block_table, table_stride, shift);
+                      causal, scale, dtype, stream, block_table, table_stride, shift, num_pages);
 }

@@ -59,6 +59,7 @@ struct DecodeArgs {
   const int32_t* table;
   int64_t table_stride;
   int page_shift;
+  int num_pages;  // pages in the pool; table entries are clamped to [0, num_pages)
 };
 
 struct PrefillArgs {
@@ -73,6 +74,7 @@ struct PrefillArgs {
   const int32_t* table;
   int64_t table_stride;
   int page_shift;
+  int num_pages;
 };
 
 // Element offset of key `pos` of (sequence b, kv head hk) in a K or V cache
@@ -80,12 +82,16 @@ struct PrefillArgs {
 // Paged: the cache is a pool of pages of 2^page_shift keys, sb the page
 // stride; key pos of sequence b lives in page table[b table_stride +
 // (pos >> page_shift)] at row pos mod 2^page_shift. Addressing only: the
-// arithmetic of every split is the same either way.
+// arithmetic of every split is the same either way. A table entry outside
+// [0, num_pages) is clamped into the pool, as lengths are clamped to L: a
+// stale or corrupt table gives wrong values, never a read outside the pool.
+__device__ __forceinline__ int clamp_page(int page, int num_pages) { return min(max(page, 0), num_pages - 1); }
+
 template <class Args>
 __device__ __forceinline__ int64_t kv_row_off(const Args& a, int64_t sb, int64_t sh, int64_t sl, int b, int hk,
                                               int pos) {
   if (a.table) {
-    const int page = a.table[(int64_t)b * a.table_stride + (pos >> a.page_shift)];
+    const int page = clamp_page(a.table[(int64_t)b * a.table_stride + (pos >> a.page_shift)], a.num_pages);
     return (int64_t)page * sb + (int64_t)hk * sh + (int64_t)(pos & ((1 << a.page_shift) - 1)) * sl;
   }
   return (int64_t)b * sb + (int64_t)hk * sh + (int64_t)pos * sl;
@@ -116,7 +122,8 @@ __device__ __forceinline__ const T* kv_segment(const Args& a, const T* base, int
   if constexpr (MODE == kKvContig) {
     return base + (int64_t)b * sb + (int64_t)hk * sh + (int64_t)key0 * sl;
   } else {
-    const int page = load_uniform_i32(a.table + (int64_t)b * a.table_stride + (key0 >> a.page_shift));
+    const int page =
+        clamp_page(load_uniform_i32(a.table + (int64_t)b * a.table_stride + (key0 >> a.page_shift)), a.num_pages);
     return base + (int64_t)page * sb + (int64_t)hk * sh + (int64_t)(key0 & ((1 << a.page_shift) - 1)) * sl;
   }
 }

@@ -500,8 +500,11 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
     if (pair >= npairs) continue;
     T* o = static_cast<T*>(a.out) +
            ((((int64_t)b * a.Hq + hk * G + pair % G) * a.Tq) + pair / G) * D + r;
+    // A row with no key (causal chunk longer than its sequence's kv_lens, or
+    // a length of 0) has Lsum == 0: its output is defined as 0.
+    const bool any = Lsum[i] > 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[16 * dt] = to_store<T>(A[dt][i] / Lsum[i]);
+    for (int dt = 0; dt < NDT; ++dt) o[16 * dt] = to_store<T>(any ? A[dt][i] / Lsum[i] : 0.0f);
   }
 }
 

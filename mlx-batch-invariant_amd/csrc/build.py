@@ -64,15 +64,25 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> Path:
+def _stale(src: Path, obj: Path) -> bool:
+    """An object is stale if it is missing or older than its source, any
+    header of this directory or the C ABI header, or this build script."""
+    if not obj.exists():
+        return True
+    deps = [src, Path(__file__), *HERE.glob("*.h"), *(HERE.parent.parent / "include").glob("*.h")]
+    return obj.stat().st_mtime < max(d.stat().st_mtime for d in deps)
+
+
+def build(jobs: int | None = None, verbose: bool = False, incremental: bool = False) -> Path:
+    """Compile every source (``incremental``: only stale objects) and link."""
     cc = hipcc()
     OBJ.mkdir(exist_ok=True)
     srcs = sorted(HERE.glob("*.hip"))
     objs = [OBJ / (s.stem + ".o") for s in srcs]
     jobs = jobs or min(8, os.cpu_count() or 1)
+    todo = [(s, o) for s, o in zip(srcs, objs) if not incremental or _stale(s, o)]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_run, [cc, *CFLAGS, "-c", str(s), "-o", str(o)], verbose)
-                for s, o in zip(srcs, objs)]
+        futs = [ex.submit(_run, [cc, *CFLAGS, "-c", str(s), "-o", str(o)], verbose) for s, o in todo]
         for f in futs:
             f.result()
     tmp = OUT.with_suffix(".so.tmp")
@@ -86,8 +96,9 @@ def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--jobs", type=int, default=None)
     p.add_argument("--verbose", action="store_true")
+    p.add_argument("--incremental", action="store_true", help="recompile only objects older than their inputs")
     a = p.parse_args(argv)
-    out = build(a.jobs, a.verbose)
+    out = build(a.jobs, a.verbose, a.incremental)
     print(f"built {out}")
     return 0
 

@@ -24,6 +24,7 @@ BI_F32, BI_F16, BI_BF16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: BI_F32, torch.float16: BI_F16, torch.bfloat16: BI_BF16}
 FLOAT_DTYPES = tuple(DTYPE_CODE)
 
+ABI_VERSION = 2    # BI_ABI_VERSION of include/bi_kernels.h this binding matches
 GROUP_K = 256      # fixed K group of the matmul fold (contract constant)
 SPLIT_KEYS = 256   # fixed attention split size (contract constant)
 
@@ -53,11 +54,11 @@ _SIGNATURES = {
     "bi_attn_prefill": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_float,
                                        ctypes.c_int, _vp]),
-    "bi_attn_decode_paged": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64,
-                                            _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.c_float, ctypes.c_int,
-                                            _vp, ctypes.c_size_t, _vp]),
-    "bi_attn_prefill_paged": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64,
-                                             _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int,
+    "bi_attn_decode_paged": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64,
+                                            _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.c_float,
+                                            ctypes.c_int, _vp, ctypes.c_size_t, _vp]),
+    "bi_attn_prefill_paged": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64,
+                                             _c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int,
                                              ctypes.c_float, ctypes.c_int, _vp]),
 }
 
@@ -86,8 +87,8 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.bi_abi_version() != 1:
-            raise KernelLibraryError(f"{LIB_PATH}: ABI version {lib.bi_abi_version()} != 1")
+        if lib.bi_abi_version() != ABI_VERSION:
+            raise KernelLibraryError(f"{LIB_PATH}: ABI version {lib.bi_abi_version()} != {ABI_VERSION}")
         _lib = lib
         return lib
 

@@ -183,7 +183,10 @@ def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=No
     pool); ``block_table``: int32 ``[B, max_pages]``, key ``p`` of sequence ``b``
     lives at row ``p % page_size`` of page ``block_table[b, p // page_size]``;
     ``kv_lens``: int32 ``[B]`` (None: every sequence spans the whole table).
-    ``page_size`` must be a power of two. The output is bit for bit the
+    ``page_size`` must be a power of two. A table entry outside
+    ``[0, num_pages)`` is clamped into the pool by the kernels (wrong values,
+    never a read outside the pool); a sequence of length 0, and a causal query
+    row that sees no key, gets an all-zero output. The output is bit for bit the
     contiguous call on the same keys: paging changes addresses only. The
     reference reads one contiguous cache (kernels/attention.py:87-254); paged
     KV is an item of its roadmap of adjacent ops.
@@ -193,7 +196,7 @@ def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=No
     if mask is not None and mask != "causal":
         raise ValueError("batch_invariant_paged_attention: mask must be None or 'causal'")
     B, Hq, Tq, D = q.shape
-    _, Hkv, page_size, Dk = k_pages.shape
+    num_pages, Hkv, page_size, Dk = k_pages.shape
     if v_pages.shape != k_pages.shape or Dk != D or D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
         raise ValueError(f"paged attention: unsupported shapes q {tuple(q.shape)} k {tuple(k_pages.shape)} "
                          f"v {tuple(v_pages.shape)}")
@@ -208,7 +211,7 @@ def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=No
     L = table.shape[1] * page_size
     kl = _lens(kv_lens, B, L, q.device)
     causal = mask == "causal"
-    if causal and kl is None and Tq > L:
+    if causal and Tq > L:
         raise ValueError(f"causal prefill needs T_q <= L (T_q={Tq}, L={L})")
     out = torch.empty((B, Hq, Tq, D), dtype=dt, device=q.device)
     if B == 0 or Tq == 0:
@@ -222,7 +225,7 @@ def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=No
         ws = _lib.workspace(ws_bytes, q.device)
         strides = (_lib._c_i64 * 8)(q3.stride(0), q3.stride(1), *ks, *vs)
         rc = lib.bi_attn_decode_paged(q3.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), table.data_ptr(),
-                                      table.stride(0), page_size, _lib.ptr(kl), out.data_ptr(), B, Hq, Hkv, L, D,
+                                      table.stride(0), page_size, num_pages, _lib.ptr(kl), out.data_ptr(), B, Hq, Hkv, L, D,
                                       strides, float(scale), _lib.DTYPE_CODE[dt], _lib.ptr(ws), ws_bytes,
                                       _lib.stream_of(q))
         _lib.check(rc, "bi_attn_decode_paged")
@@ -230,7 +233,7 @@ def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=No
     q = _fix(q)
     strides = (_lib._c_i64 * 9)(q.stride(0), q.stride(1), q.stride(2), *ks, *vs)
     rc = lib.bi_attn_prefill_paged(q.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), table.data_ptr(),
-                                   table.stride(0), page_size, _lib.ptr(kl), out.data_ptr(), B, Hq, Hkv, Tq, L, D,
+                                   table.stride(0), page_size, num_pages, _lib.ptr(kl), out.data_ptr(), B, Hq, Hkv, Tq, L, D,
                                    strides, 1 if causal else 0, float(scale), _lib.DTYPE_CODE[dt],
                                    _lib.stream_of(q))
     _lib.check(rc, "bi_attn_prefill_paged")

@@ -137,11 +137,16 @@ def addmm(c, a, b, *, beta=1, alpha=1, out=None):
         reason = "non-2d-rhs-or-non-float"
     if reason is None and isinstance(c, torch.Tensor) and not _on_gpu(c):
         reason = "non-gpu-tensor"
+    if reason is None and isinstance(c, torch.Tensor) and c.dtype != torch.result_type(a, b):
+        reason = "dtype-mismatch"              # the stock op raises its own error for mixed dtypes
     if reason is None:
         handled["addmm"] += 1
         prod = batch_invariant_matmul(a, b)
         if alpha != 1:
             prod = prod * alpha
+        if beta == 0:                          # as torch.addmm: c is ignored, NaN/Inf in it do not propagate
+            return prod.expand(torch.broadcast_shapes(prod.shape, c.shape)).clone() if isinstance(
+                c, torch.Tensor) else prod
         return prod + (c if beta == 1 else c * beta)
     _fallback("addmm", reason)
     kw = {"beta": beta, "alpha": alpha}

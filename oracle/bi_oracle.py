@@ -373,7 +373,7 @@ def attention(q, k, v, scale: float, causal: bool, dtype: str, kv_lens=None) -> 
     G = Hq // Hkv
     out = np.zeros((B, Hq, Tq, D), np.float32)
     for b in range(B):
-        n_len = L if kv_lens is None else int(kv_lens[b])
+        n_len = L if kv_lens is None else min(max(int(kv_lens[b]), 0), L)   # clamped as the kernels do
         for hk in range(Hkv):
             heads = list(range(hk * G, hk * G + G))
             qrows = q[b, heads].reshape(G * Tq, D)                       # row = (head, token)
@@ -414,7 +414,9 @@ def attention(q, k, v, scale: float, causal: bool, dtype: str, kv_lens=None) -> 
                 Ls = np.where(touched, L_new, Ls)
                 A = np.where(touched[:, None], A_new, A)
             with np.errstate(invalid="ignore", divide="ignore"):
-                o = (A / Ls[:, None]).astype(np.float32)
+                # a row that sees no key (length 0, or a causal chunk longer
+                # than its sequence) is defined as 0 rather than 0 / 0
+                o = np.where(Ls[:, None] > 0, A / Ls[:, None], np.float32(0)).astype(np.float32)
             out[b, heads] = o.reshape(G, Tq, D)
     return round_to(out, dtype)
 
@@ -429,7 +431,7 @@ def attention_float64(q, k, v, scale: float, causal: bool, kv_lens=None) -> np.n
     G = Hq // Hkv
     out = np.zeros((B, Hq, Tq, D))
     for b in range(B):
-        n_len = L if kv_lens is None else int(kv_lens[b])
+        n_len = L if kv_lens is None else min(max(int(kv_lens[b]), 0), L)   # clamped as the kernels do
         for h in range(Hq):
             kk = k[b, h // G, :n_len]
             vv = v[b, h // G, :n_len]
@@ -438,9 +440,13 @@ def attention_float64(q, k, v, scale: float, causal: bool, kv_lens=None) -> np.n
                 t = np.arange(Tq)[:, None]
                 j = np.arange(n_len)[None, :]
                 s = np.where(j < n_len - Tq + t + 1, s, -np.inf)
-            s = s - s.max(-1, keepdims=True)
-            p = np.exp(s)
-            out[b, h] = (p / p.sum(-1, keepdims=True)) @ vv
+            if s.shape[-1] == 0:
+                continue                       # no key at all: defined as 0
+            with np.errstate(invalid="ignore"):
+                s = s - s.max(-1, keepdims=True)
+            p = np.where(np.isfinite(s), np.exp(s), 0.0)
+            tot = p.sum(-1, keepdims=True)
+            out[b, h] = np.where(tot > 0, (p / np.where(tot > 0, tot, 1.0)) @ vv, 0.0)   # rows with no key: 0
     return out
 
 

@@ -24,7 +24,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), n
     assert sorted(_lib.exported_symbols()) == names
-    assert lib.bi_abi_version() == 1
+    assert lib.bi_abi_version() == _lib.ABI_VERSION == 2
     assert lib.bi_split_m_max() == 32
 
 
@@ -77,9 +77,18 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.bi_matmul(p, 65 * 256, p, 65 * 256, p, 2, 4, 65 * 256, 2, None, 0, None) == -3
     # paged attention: the page table is checked before anything runs
     st = (ctypes.c_int64 * 8)(*([128] * 8))
-    assert lib.bi_attn_decode_paged(p, p, p, p, 4, 3, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20, None) == -1
-    assert lib.bi_attn_decode_paged(p, p, p, None, 4, 4, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20, None) == -1
-    assert lib.bi_attn_decode_paged(p, p, p, p, 2, 4, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20, None) == -1
+    assert lib.bi_attn_decode_paged(p, p, p, p, 4, 3, 9, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20, None) == -1
+    assert lib.bi_attn_decode_paged(p, p, p, None, 4, 4, 9, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20,
+                                    None) == -1
+    assert lib.bi_attn_decode_paged(p, p, p, p, 2, 4, 9, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p, 1 << 20, None) == -1
+    # the pool size bounds the clamp of every table entry: it must be >= 1
+    for num_pages in (0, -3, 1 << 31):
+        assert lib.bi_attn_decode_paged(p, p, p, p, 4, 4, num_pages, None, p, 1, 8, 2, 12, 128, st, 1.0, 2, p,
+                                        1 << 20, None) == -1
+        assert "num_pages" in _err(lib)
+        st9 = (ctypes.c_int64 * 9)(*([128] * 9))
+        assert lib.bi_attn_prefill_paged(p, p, p, p, 4, 4, num_pages, None, p, 1, 8, 2, 4, 12, 128, st9, 1, 1.0, 2,
+                                         None) == -1
     # unsupported quantization
     assert lib.bi_quantized_matmul(p, 64, p, p, p, p, 2, 4, 64, 3, 64, 2, None, 0, None) == -2
     assert lib.bi_quantized_matmul(p, 96, p, p, p, p, 2, 4, 96, 4, 64, 2, None, 0, None) == -1

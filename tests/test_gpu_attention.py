@@ -211,3 +211,47 @@ def test_strided_kv_cache_view():
     a = _bi().batch_invariant_decode_attention(q, k[:, :, :600], v[:, :, :600], scale=0.1)
     b = _bi().batch_invariant_decode_attention(q, k[:, :, :600].contiguous(), v[:, :, :600].contiguous(), scale=0.1)
     assert bits(a) == bits(b)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_zero_length_sequences_give_zeros(dt):
+    """kv_lens[b] = 0 (and negative lengths, clamped to 0) has no key and no
+    softmax: the output is defined as 0, and the other sequences of the batch
+    still equal themselves run alone."""
+    Hq, Hkv, D, L = 32, 8, 128, 600
+    q, k, v = _qkv(5, Hq, Hkv, 1, L, D, dt, seed=12)
+    lens = [0, 300, -4, 1, 600]
+    out = _bi().batch_invariant_decode_attention(q, k, v, scale=D ** -0.5,
+                                                 kv_lens=torch.tensor(lens, dtype=torch.int32).cuda())
+    assert torch.isfinite(out).all()
+    for b, n in enumerate(lens):
+        if n <= 0:
+            assert bits(out[b]) == bits(torch.zeros_like(out[b])), b
+        else:
+            alone = _bi().batch_invariant_decode_attention(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n],
+                                                           scale=D ** -0.5)
+            assert bits(out[b:b + 1]) == bits(alone), b
+
+
+def test_causal_prefill_kv_lens_shorter_than_chunk():
+    """A causal chunk of T_q tokens against a sequence with fewer than T_q
+    keys: query t sees len - T_q + t + 1 keys; rows that see none are 0 (not
+    0/0), the others equal the oracle and a decode step over their keys."""
+    Hq, Hkv, D, L, Tq = 8, 2, 64, 300, 40
+    q, k, v = _qkv(2, Hq, Hkv, Tq, L, D, "bf16", seed=13)
+    lens = [10, 300]
+    kl = torch.tensor(lens, dtype=torch.int32).cuda()
+    out = _bi().batch_invariant_prefill_attention(q, k, v, scale=0.125, causal=True, kv_lens=kl)
+    assert torch.isfinite(out).all()
+    got = to_np(out)
+    want = ora.attention(to_np(q), to_np(k), to_np(v), 0.125, True, "bf16", kv_lens=lens)
+    _tol_check(got, want, "bf16")
+    n0 = lens[0]
+    for t in range(Tq):
+        nk = n0 - Tq + t + 1
+        if nk <= 0:
+            assert not got[0, :, t].any(), t
+        else:
+            d = _bi().batch_invariant_decode_attention(q[0:1, :, t:t + 1], k[0:1, :, :nk], v[0:1, :, :nk],
+                                                       scale=0.125)
+            assert bits(d) == bits(out[0:1, :, t:t + 1]), t

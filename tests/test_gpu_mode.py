@@ -80,3 +80,27 @@ def test_causal_lower_right_is_the_kernel_causal_mask():
     stock = F.scaled_dot_product_attention(q.float(), kv.float(), kv.float(),
                                            attn_mask=causal_lower_right(5, 300), enable_gqa=True)
     assert torch.allclose(lr.float(), stock, atol=2e-2, rtol=2e-2)
+
+
+def test_addmm_beta_zero_ignores_c_and_mixed_dtype_falls_back():
+    """As stock torch.addmm: with beta = 0, c is not read (NaN / Inf in it do
+    not propagate) and the result is alpha * (a @ b) broadcast to c's shape; a
+    c whose dtype differs from the product goes to the stock op (counted),
+    which raises its own error."""
+    bi = _bi()
+    a = randn((4, 256), torch.bfloat16, gen(7))
+    b = randn((256, 96), torch.bfloat16, gen(8))
+    c = torch.full((4, 96), float("nan"), dtype=torch.bfloat16, device="cuda")
+    bi.reset_stats()
+    with bi.set_batch_invariant_mode(strict=True):
+        y = torch.addmm(c, a, b, beta=0)
+        y2 = torch.addmm(c[0], a, b, beta=0, alpha=2)
+    assert bi.stats()["handled"] == {"addmm": 2}
+    prod = bi.batch_invariant_matmul(a, b)
+    assert bits(y) == bits(prod)
+    assert bits(y2) == bits(prod * 2)
+    bi.reset_stats()
+    with bi.set_batch_invariant_mode():
+        with pytest.raises(RuntimeError):
+            torch.addmm(c.float(), a, b)
+    assert bi.stats()["fallbacks"] == {"addmm:dtype-mismatch": 1}

@@ -90,3 +90,29 @@ def test_paged_decode_batch_invariant_and_errors():
         assert bits(one) == bits(full[b:b + 1]), b
     with pytest.raises(ValueError, match="power of two"):
         bi.batch_invariant_paged_attention(q, kp[:, :, :24], vp[:, :, :24], table, lens)
+
+
+@pytest.mark.parametrize("page_size", [16, 64])
+def test_paged_table_entries_are_clamped_into_the_pool(page_size):
+    """A table entry outside [0, num_pages) is clamped into the pool by the
+    kernels (a stale table reads wrong pages, never memory outside the pool):
+    the output equals the call with the table clamped on the host."""
+    bi = _bi()
+    g = gen(40 + page_size)
+    B, Hq, Hkv, L, D = 3, 8, 2, 400, 128
+    q = randn((B, Hq, 1, D), torch.bfloat16, g)
+    k = randn((B, Hkv, L, D), torch.bfloat16, g)
+    v = randn((B, Hkv, L, D), torch.bfloat16, g)
+    kp, vp, table = _paginate(k, v, page_size, g)
+    npages = kp.shape[0]
+    bad = table.clone()
+    bad[0, 1] = -7
+    bad[1, 0] = npages + 100
+    bad[2, -1] = 2 ** 31 - 1
+    lens = torch.tensor([400, 390, 400], dtype=torch.int32).cuda()
+    clamped = bad.clamp(0, npages - 1)
+    for Tq, mask in ((1, None), (9, "causal")):
+        qq = randn((B, Hq, Tq, D), torch.bfloat16, g)
+        got = bi.batch_invariant_paged_attention(qq, kp, vp, bad, lens, scale=D ** -0.5, mask=mask)
+        want = bi.batch_invariant_paged_attention(qq, kp, vp, clamped, lens, scale=D ** -0.5, mask=mask)
+        assert bits(got) == bits(want), Tq
