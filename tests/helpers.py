@@ -26,3 +26,17 @@ def gen(seed: int) -> torch.Generator:
     g = torch.Generator()
     g.manual_seed(seed)
     return g
+
+
+def assert_bits_equal(got, want, what: str = "") -> None:
+    """Bitwise equality of two float32 arrays (values of any storage type),
+    with a report of how many elements differ and by how much."""
+    got = np.ascontiguousarray(got, np.float32)
+    want = np.ascontiguousarray(want, np.float32)
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    diff = got.view(np.uint32) != want.view(np.uint32)
+    if diff.any():
+        i = int(np.argmax(diff))
+        raise AssertionError(f"{what}: {int(diff.sum())} of {diff.size} elements differ; first at flat {i}: "
+                             f"got {got.flat[i]!r} want {want.flat[i]!r}; "
+                             f"max |diff| {float(np.abs(got.astype(np.float64) - want)[diff].max()):.3e}")
