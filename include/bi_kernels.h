@@ -143,6 +143,22 @@ int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* k
                    const int64_t* strides, float scale, int dtype, void* ws,
                    size_t ws_bytes, void* stream);
 
+/* bi_attn_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ * Same arguments, arithmetic and bits as bi_attn_decode; the per-split
+ * partials and the work-item counter live in a static device array of
+ * BI_DECODE_SCRATCH_BYTES per GPU (held from library load until the process
+ * ends), so calls with bi_attn_decode_workspace_bytes(B, Hq, L, D) above it
+ * are rejected with BI_E_WORKSPACE (64 MiB: e.g. B = 64, Hq = 32, L = 8192,
+ * D = 128 needs 34 MB). The call allocates nothing. Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (concurrent streams,
+ * threads) race and must be serialised by the caller. */
+#define BI_DECODE_SCRATCH_BYTES (64u << 20)
+int bi_attn_decode_noalloc(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                           void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                           const int64_t* strides, float scale, int dtype, void* stream);
+
 /* Paged K/V variant of bi_attn_decode: k_pages / v_pages are pools of
  * num_pages pages of page_size keys (a power of two, 1 .. 2^24);
  * strides[2..4] / [5..7] are the (page, head, position-in-page) element

@@ -17,6 +17,7 @@
 //           rows, token-major), K/V streamed through LDS in 64-key chunks,
 //           splits merged in registers.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "bi_attn_mfma.h"
@@ -357,4 +358,59 @@ extern "C" int bi_attn_prefill_paged(const void* q, const void* k_pages, const v
     return rc;
   return prefill_impl("bi_attn_prefill_paged", q, k_pages, v_pages, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides,
                       causal, scale, dtype, stream, block_table, table_stride, shift, num_pages);
+}
+
+// ---------------------------------------------------------------------------
+// Decode without a caller workspace: the partials and the item counter live in
+// one file-scope device array. Every GPU the library runs on holds its own copy
+// from module load until the process ends; its address is looked up once per
+// device (with that device current) and kept. Host code never passes the
+// array's name to a kernel: in host code it is only a stand-in for the symbol.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[BI_DECODE_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[bi::kMaxDev] = {};
+
+int scratch_of_current_device(const char* what, void** out) {
+  using namespace bi_host;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail((int)e, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= bi::kMaxDev) return fail(BI_E_UNSUPPORTED, "%s: device %d out of range", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(e != hipSuccess ? (int)e : BI_E_UNSUPPORTED, "%s: hipGetSymbolAddress(scratch) failed: %s", what,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BI_OK;
+}
+
+}  // namespace
+
+extern "C" int bi_attn_decode_noalloc(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                                      void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                                      const int64_t* strides, float scale, int dtype, void* stream) {
+  const char* what = "bi_attn_decode_noalloc";
+  int rc = check_attn_shape(what, B, Hq, Hkv, L, D);
+  if (rc) return rc;
+  if (B == 0) return BI_OK;
+  const size_t need = bi_attn_decode_workspace_bytes(B, Hq, L, D);
+  if (need > (size_t)BI_DECODE_SCRATCH_BYTES)
+    return bi_host::fail(BI_E_WORKSPACE,
+                         "%s: B=%lld Hq=%lld L=%lld D=%lld needs %zu bytes of partials; the static scratch holds "
+                         "%zu (use bi_attn_decode with a workspace)",
+                         what, (long long)B, (long long)Hq, (long long)L, (long long)D, need,
+                         (size_t)BI_DECODE_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if ((rc = scratch_of_current_device(what, &ws))) return rc;
+  return decode_impl(what, q, k, v, kv_lens, out, B, Hq, Hkv, L, D, strides, scale, dtype, ws,
+                     (size_t)BI_DECODE_SCRATCH_BYTES, stream, nullptr, 0, 0, 0);
 }

@@ -27,6 +27,7 @@ FLOAT_DTYPES = tuple(DTYPE_CODE)
 ABI_VERSION = 2    # BI_ABI_VERSION of include/bi_kernels.h this binding matches
 GROUP_K = 256      # fixed K group of the matmul fold (contract constant)
 SPLIT_KEYS = 256   # fixed attention split size (contract constant)
+DECODE_SCRATCH_BYTES = 64 << 20   # BI_DECODE_SCRATCH_BYTES: static scratch of bi_attn_decode_noalloc
 
 _c_i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
@@ -54,6 +55,8 @@ _SIGNATURES = {
     "bi_attn_prefill": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_float,
                                        ctypes.c_int, _vp]),
+    "bi_attn_decode_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                              ctypes.POINTER(_c_i64), ctypes.c_float, ctypes.c_int, _vp]),
     "bi_attn_decode_paged": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64,
                                             _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.c_float,
                                             ctypes.c_int, _vp, ctypes.c_size_t, _vp]),

@@ -101,6 +101,10 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.bi_attn_decode(p, p, p, None, p, 1, 6, 4, 10, 128, strides, 1.0, 2, p, 1 << 20, None) == -1
     assert lib.bi_attn_decode(p, p, p, None, p, 1, 4, 4, 10, 128, strides, 1.0, 2, None, 0, None) == -3
     assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 20, 10, 128, strides, 1, 1.0, 2, None) == -1
+    # the no-workspace decode rejects shapes whose partials exceed its static scratch, before any HIP call
+    assert lib.bi_attn_decode_workspace_bytes(256, 32, 8192, 128) > _lib.DECODE_SCRATCH_BYTES
+    assert lib.bi_attn_decode_noalloc(p, p, p, None, p, 256, 32, 8, 8192, 128, strides, 1.0, 2, None) == -3
+    assert "static scratch" in _err(lib)
     bad = (ctypes.c_int64 * 9)(*([3] * 9))
     assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 5, 10, 128, bad, 0, 1.0, 2, None) == -1
 
