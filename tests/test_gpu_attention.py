@@ -255,3 +255,83 @@ def test_causal_prefill_kv_lens_shorter_than_chunk():
             d = _bi().batch_invariant_decode_attention(q[0:1, :, t:t + 1], k[0:1, :, :nk], v[0:1, :, :nk],
                                                        scale=0.125)
             assert bits(d) == bits(out[0:1, :, t:t + 1]), t
+
+
+def _report(name, payload):
+    import json
+    import os
+    from pathlib import Path
+    out = Path(os.environ.get("GRAFT_REPO_ROOT", Path(__file__).resolve().parent.parent)) / "gpurun_out"
+    if out.is_dir():
+        (out / name).write_text(json.dumps(payload, indent=1))
+
+
+def _ulp_err(got, want, dt):
+    """max |got - want| in storage ulps of want, and max |got - want|."""
+    d = np.abs(got.astype(np.float64) - want)
+    return float(np.max(d / ora.ulp(want, dt))), float(d.max())
+
+
+def test_decode_config3_full_size():
+    """BASELINE config 3 at its size: B = 256 sequences with lengths drawn from
+    U{1..8192} (the bench's batch), GQA 32/8, D = 128, bf16. Sampled sequences
+    equal themselves run alone, bit for bit; three of them match the per-key
+    oracle within one bf16 ulp after the stated allowance."""
+    Hq, Hkv, D, L, B = 32, 8, 128, 8192, 256
+    lens = np.random.default_rng(B).integers(1, L + 1, size=B)
+    g = torch.Generator(device="cuda").manual_seed(77)      # 2 x 2 GiB of K/V: drawn on the device
+    q = torch.randn((B, Hq, 1, D), generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn((B, Hkv, L, D), generator=g, device="cuda", dtype=torch.bfloat16)
+    v = torch.randn((B, Hkv, L, D), generator=g, device="cuda", dtype=torch.bfloat16)
+    kl = torch.tensor(lens, dtype=torch.int32).cuda()
+    out = _bi().batch_invariant_decode_attention(q, k, v, scale=D ** -0.5, kv_lens=kl)
+    picks = sorted({0, B - 1, int(np.argmax(lens)), int(np.argmin(lens)), 17, 100, 200})
+    for b in picks:
+        n = int(lens[b])
+        alone = _bi().batch_invariant_decode_attention(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n],
+                                                       scale=D ** -0.5)
+        assert bits(out[b:b + 1]) == bits(alone), (b, n)
+    errs = {}
+    for b in (int(np.argmax(lens)), int(np.argmin(lens)), 100):
+        n = int(lens[b])
+        want = ora.attention(to_np(q[b:b + 1]), to_np(k[b:b + 1, :, :n]), to_np(v[b:b + 1, :, :n]), D ** -0.5, False,
+                             "bf16")
+        got = to_np(out[b:b + 1])
+        _tol_check(got, want, "bf16")
+        errs[int(n)] = _ulp_err(got, want, "bf16")
+    _report("attn_err_config3.json", {"max_err_vs_per_key_oracle (ulps, abs) by length": errs})
+
+
+def test_prefill_config4_tokens_equal_decode_steps():
+    """BASELINE config 4 shape (GQA 32/8, D = 128, T = 2048, bf16, causal):
+    each sampled token of a one-shot prefill equals a later single-token decode
+    step for that position, bit for bit, and the per-key oracle within one bf16
+    ulp after the stated allowance."""
+    Hq, Hkv, D, T = 32, 8, 128, 2048
+    q, k, v = _qkv(2, Hq, Hkv, T, T, D, "bf16", seed=21)
+    sc = D ** -0.5
+    full = _bi().batch_invariant_prefill_attention(q, k, v, scale=sc, causal=True)
+    errs = {}
+    for t in (0, 1, 255, 256, 511, 1023, 1500, 2047):
+        dec = _bi().batch_invariant_decode_attention(q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1], scale=sc)
+        assert bits(dec) == bits(full[:, :, t:t + 1]), t
+        want = ora.attention(to_np(q[:1, :, t:t + 1]), to_np(k[:1, :, :t + 1]), to_np(v[:1, :, :t + 1]), sc, False,
+                             "bf16")
+        got = to_np(full[:1, :, t:t + 1])
+        _tol_check(got, want, "bf16")
+        errs[t] = _ulp_err(got, want, "bf16")
+    _report("attn_err_config4.json", {"max_err_vs_per_key_oracle (ulps, abs) by token": errs})
+
+
+def test_fp32_prefill_closed_form_d128_long():
+    """fp32 at D = 128 over 2304 keys (nine splits), causal and not: within a
+    relative 1e-5 of the float64 softmax closed form (the in-split order, the
+    hardware exp2 and the split merge together)."""
+    q, k, v = _qkv(1, 8, 2, 64, 2304, 128, "f32", seed=23)
+    sc = 128 ** -0.5
+    for causal in (True, False):
+        got = to_np(_bi().batch_invariant_prefill_attention(q, k, v, scale=sc, causal=causal))
+        ref = ora.attention_float64(to_np(q), to_np(k), to_np(v), sc, causal)
+        rel = float(np.abs(got - ref).max() / np.abs(ref).max())
+        _report(f"attn_fp32_closed_form_causal{int(causal)}.json", {"max_rel_err": rel})
+        assert rel < 1e-5, (causal, rel)

@@ -110,3 +110,82 @@ def test_chunked_prefill_and_decode_match_one_shot(model):
     for (k1, v1), (k2, v2), (k3, v3) in zip(c1, c2, c3):
         assert bits(k1) == bits(k2) and bits(v1) == bits(v2)
         assert bits(k1) == bits(k3) and bits(v1) == bits(v3)
+
+
+def _np_forward(model, tokens):
+    """A numpy forward of one sequence's prefill built from the oracle
+    (rms_norm, dequantize, matmul with the quantized k-slot map, the per-key
+    attention) and torch's bf16 elementwise rounding (each elementwise op is
+    computed in fp32 and rounded once to bf16). Returns (row-0 hidden after the
+    first norm, its Q projection, the last token's logits)."""
+    import numpy as np
+    from oracle import bi_oracle as ora
+    cfg = model.cfg
+    rb = lambda a: ora.round_to(np.asarray(a, np.float32), "bf16")
+    f = lambda t: t.detach().float().cpu().numpy()
+
+    def lin(layer, x):
+        if cfg.bits is None:
+            return ora.matmul(x, f(layer.weight), "bf16")
+        W = ora.dequantize(layer.weight.cpu().numpy().view(np.uint32), f(layer.scales), f(layer.biases),
+                           layer.group_size, layer.bits, "bf16")
+        return ora.matmul(x, W, "bf16", kmap="blocked")
+
+    T = tokens.shape[0]
+    x = f(model.embed)[tokens]
+    cos, sin = (f(t) for t in model._rope_tables(0, T))
+
+    def rope(h):                                                  # h [H, T, D]
+        d2 = h.shape[-1] // 2
+        x1, x2 = h[..., :d2], h[..., d2:]
+        return np.concatenate([rb(rb(x1 * cos) - rb(x2 * sin)), rb(rb(x2 * cos) + rb(x1 * sin))], -1)
+
+    first = None
+    for blk in model.blocks:
+        hn = ora.rms_norm(x, f(blk.attn_norm.weight), cfg.eps, "bf16")
+        q = lin(blk.q, hn)
+        if first is None:
+            first = (hn, q)
+        q = rope(q.reshape(T, cfg.heads, cfg.head_dim).transpose(1, 0, 2))
+        k = rope(lin(blk.k, hn).reshape(T, cfg.kv_heads, cfg.head_dim).transpose(1, 0, 2))
+        v = lin(blk.v, hn).reshape(T, cfg.kv_heads, cfg.head_dim).transpose(1, 0, 2)
+        a = ora.attention(q[None], k[None], v[None], cfg.head_dim ** -0.5, True, "bf16")[0]
+        x = rb(x + lin(blk.o, a.transpose(1, 0, 2).reshape(T, -1)))
+        hn = ora.rms_norm(x, f(blk.mlp_norm.weight), cfg.eps, "bf16")
+        g = lin(blk.gate, hn)
+        silu = rb(g / (np.float32(1) + np.exp(-g)))
+        x = rb(x + lin(blk.down, rb(silu * lin(blk.up, hn))))
+    hl = ora.rms_norm(x[-1:], f(model.norm.weight), cfg.eps, "bf16")
+    return first, lin(model.head, hl)[0]
+
+
+@pytest.mark.parametrize("bits_", [4, None], ids=["q4g64", "bf16"])
+def test_forward_matches_numpy_oracle_forward(bits_):
+    """Oracle anchor of the model path: a 1-layer Llama-shaped decoder with
+    reduced widths (hidden 512, MLP 1536, 4 / 2 heads of 128, vocab 1000),
+    prefill of 24 tokens under the mode, against a numpy forward built from
+    the oracle's functions. The first norm and Q projection are bit-exact;
+    the logits, downstream of attention (compared to the per-key oracle at a
+    tolerance) and of torch's elementwise ops, agree within 2% of their range
+    (the fraction equal bit for bit is recorded)."""
+    import numpy as np
+    import mlx_batch_invariant_amd as bi
+    from mlx_batch_invariant_amd.llama import LlamaConfig, LlamaShaped
+    cfg = LlamaConfig(layers=1, hidden=512, ffn=1536, heads=4, kv_heads=2, head_dim=128, vocab=1000, bits=bits_)
+    model = LlamaShaped(cfg, device="cuda", dtype=torch.bfloat16, seed=5)
+    toks = torch.randint(0, cfg.vocab, (1, 24), generator=torch.Generator().manual_seed(9)).cuda()
+    with bi.set_batch_invariant_mode(strict=True):
+        logits = model(toks, model.new_cache(1, 24), 0)
+        blk = model.blocks[0]
+        hn = blk.attn_norm(model.embed[toks[0]])
+        q = blk.q(hn)
+    (hn_np, q_np), want = _np_forward(model, toks[0].cpu().numpy())
+    f = lambda t: t.detach().float().cpu().numpy()
+    assert np.array_equal(f(hn), hn_np)
+    assert np.array_equal(f(q), q_np)
+    got = f(logits)[0]
+    rel = float(np.abs(got - want).max() / np.abs(want).max())
+    exact = float(np.mean(got == want))
+    if OUT.is_dir():
+        (OUT / f"llama_oracle_anchor_{bits_ or 'bf16'}.json").write_text(json.dumps({"max_rel": rel, "exact": exact}))
+    assert rel < 0.02, rel
