@@ -29,48 +29,36 @@ import torch.nn.functional as F
 from . import nn as _bnn
 from . import ops
 
-_lock = threading.Lock()
-_depth = 0
-_saved: dict = {}
+# (owner object, attribute, replacement): every entry point the mode swaps.
+_PATCHES = (
+    (torch, "matmul", ops.matmul),
+    (torch, "mm", ops.mm),
+    (torch, "bmm", ops.bmm),
+    (torch, "addmm", ops.addmm),
+    (torch.Tensor, "__matmul__", ops.tensor_matmul),
+    (F, "linear", ops.linear),
+    (F, "rms_norm", ops.rms_norm),
+    (F, "layer_norm", ops.layer_norm),
+    (F, "scaled_dot_product_attention", ops.scaled_dot_product_attention),
+    (_bnn, "quantized_matmul", ops.quantized_matmul),
+)
+
+_lock = threading.Lock()   # guards _depth, the patch state and ops.strict
+_depth = 0                 # open `with` blocks, process-wide
+_originals: list = []      # what _PATCHES replaced, in the same order
 
 
 def _apply():
-    global _saved
-    _saved = {
-        "matmul": torch.matmul,
-        "mm": torch.mm,
-        "bmm": torch.bmm,
-        "addmm": torch.addmm,
-        "tensor_matmul": torch.Tensor.__matmul__,
-        "linear": F.linear,
-        "rms_norm": F.rms_norm,
-        "layer_norm": F.layer_norm,
-        "sdpa": F.scaled_dot_product_attention,
-        "quantized_matmul": _bnn.quantized_matmul,
-    }
-    torch.matmul = ops.matmul
-    torch.mm = ops.mm
-    torch.bmm = ops.bmm
-    torch.addmm = ops.addmm
-    torch.Tensor.__matmul__ = ops.tensor_matmul
-    F.linear = ops.linear
-    F.rms_norm = ops.rms_norm
-    F.layer_norm = ops.layer_norm
-    F.scaled_dot_product_attention = ops.scaled_dot_product_attention
-    _bnn.quantized_matmul = ops.quantized_matmul
+    """Swap every patched attribute for its wrapper, remembering the original."""
+    _originals[:] = [getattr(owner, name) for owner, name, _ in _PATCHES]
+    for owner, name, repl in _PATCHES:
+        setattr(owner, name, repl)
 
 
 def _restore():
-    torch.matmul = _saved["matmul"]
-    torch.mm = _saved["mm"]
-    torch.bmm = _saved["bmm"]
-    torch.addmm = _saved["addmm"]
-    torch.Tensor.__matmul__ = _saved["tensor_matmul"]
-    F.linear = _saved["linear"]
-    F.rms_norm = _saved["rms_norm"]
-    F.layer_norm = _saved["layer_norm"]
-    F.scaled_dot_product_attention = _saved["sdpa"]
-    _bnn.quantized_matmul = _saved["quantized_matmul"]
+    for (owner, name, _), orig in zip(_PATCHES, _originals):
+        setattr(owner, name, orig)
+    _originals.clear()
 
 
 def is_batch_invariant_mode_enabled() -> bool:
@@ -79,29 +67,32 @@ def is_batch_invariant_mode_enabled() -> bool:
 
 @contextlib.contextmanager
 def set_batch_invariant_mode(enabled: bool = True, *, strict: bool = False):
-    """Route matmul / bmm / linear / addmm / quantized matmul / rms_norm /
-    layer_norm / sdpa through
-    the batch-invariant kernels for the duration of the block.
+    """Inside the block, matmul / mm / bmm / addmm / ``@`` / linear / the
+    package's quantized matmul / rms_norm / layer_norm / sdpa resolve to the
+    batch-invariant kernels (reference: _mode.py:66-91).
 
-    ``strict=True`` raises instead of silently falling back to a stock kernel
-    for unsupported inputs. Re-entrant; process-global (torch dispatch by
-    attribute lookup is), guarded by a lock.
+    With ``strict`` an input no kernel handles raises ``RuntimeError``; without
+    it the stock op runs and the fallback is counted. Blocks nest: the swap
+    happens when the first one opens and is undone when the last one closes,
+    and each block's ``strict`` holds until it closes. ``enabled=False`` is a
+    no-op block. The swap is process-wide, since torch looks these attributes
+    up at call time; a lock serialises opening and closing.
     """
     global _depth
     if not enabled:
         yield
         return
     with _lock:
+        outer_strict = ops.strict
         if _depth == 0:
             _apply()
         _depth += 1
-        prev_strict = ops.strict
         ops.strict = strict
     try:
         yield
     finally:
         with _lock:
-            ops.strict = prev_strict
             _depth -= 1
+            ops.strict = outer_strict
             if _depth == 0:
                 _restore()

@@ -110,33 +110,44 @@ def dump(model: str | None = None, dev: str = "cuda") -> dict:
     return out
 
 
+def _mode_of(key: str) -> str:
+    """The mode a hash was taken in: the last path component ("inv" / "stock")."""
+    return key.rsplit("/", 1)[-1]
+
+
 def compare(a: dict, b: dict, file=sys.stdout) -> int:
-    """Print agreement per section and mode; 1 if an invariant hash differs."""
-    for tag, d in (("A", a), ("B", b)):
-        print(f"{tag}: torch {d.get('torch')} hip {d.get('hip')} on {d.get('device')} ({d.get('arch')}), "
+    """Hash-by-hash comparison of two dumps.
+
+    Prints each dump's platform line, then per section ("ops", "model") and
+    mode how many of the entries both dumps hold agree, which disagree, and
+    which appear in one dump only. Returns 1 when any invariant-mode entry
+    disagrees (the property that must hold across builds, ROCm versions and
+    machines); stock-mode differences are reported but not an error."""
+    for label, d in (("A", a), ("B", b)):
+        print(f"{label}: {d.get('device')} ({d.get('arch')}), torch {d.get('torch')}, HIP {d.get('hip')}, "
               f"library {d.get('library')}", file=file)
-    print(file=file)
-    rc = 0
+    status = 0
     for section in ("ops", "model"):
-        keys = sorted(set(a.get(section, {})) & set(b.get(section, {})))
-        if not keys:
+        ha, hb = a.get(section, {}), b.get(section, {})
+        if not ha and not hb:
             continue
-        same = {"stock": [0, 0], "inv": [0, 0]}
-        diff = []
-        for k in keys:
-            mode = "inv" if k.endswith("/inv") else "stock"
-            same[mode][1] += 1
-            if a[section][k] == b[section][k]:
-                same[mode][0] += 1
-            else:
-                diff.append(k)
+        tally: dict[str, tuple[int, list[str]]] = {}
+        for key in sorted(ha.keys() & hb.keys()):
+            n, bad = tally.get(_mode_of(key), (0, []))
+            if ha[key] != hb[key]:
+                bad = bad + [key]
+            tally[_mode_of(key)] = (n + 1, bad)
+        for mode, (n, bad) in sorted(tally.items()):
+            print(f"[{section}] {mode}: {n - len(bad)} of {n} hashes agree", file=file)
+            if bad:
+                print(f"    differ: {', '.join(bad)}", file=file)
                 if mode == "inv":
-                    rc = 1
-        for mode, (n, tot) in same.items():
-            print(f"{section:<6} {mode:<6} identical: {n}/{tot}", file=file)
-        if diff:
-            print("  differing: " + ", ".join(diff), file=file)
-    return rc
+                    status = 1
+        lonely = sorted(ha.keys() ^ hb.keys())
+        if lonely:
+            print(f"    in one dump only: {', '.join(lonely)}", file=file)
+    print("invariant hashes " + ("DIFFER" if status else "agree"), file=file)
+    return status
 
 
 def main(argv=None) -> int:

@@ -115,15 +115,27 @@ class LlamaShaped(torch.nn.Module):
         self.head = _linear(cfg, cfg.hidden, cfg.vocab, gen, device, dtype)
         self.device = torch.device(device)
 
-    def _rope_tables(self, pos, T):
+    def _ensure_rope(self, n: int):
+        """cos / sin tables of positions [0, n) on the device (built once, grown
+        on demand outside any graph capture; every position's entries are
+        computed from that position alone, so a slice equals a fresh table)."""
+        have = getattr(self, "_rope_cos", None)
+        if have is not None and have.shape[0] >= n:
+            return
         cfg = self.cfg
+        n = max(n, 2 * (have.shape[0] if have is not None else 0))
         inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float64) / cfg.head_dim))
-        t = torch.arange(pos, pos + T, dtype=torch.float64)
-        ang = torch.outer(t, inv)
-        return (ang.cos().to(self.dtype).to(self.device), ang.sin().to(self.dtype).to(self.device))
+        ang = torch.outer(torch.arange(0, n, dtype=torch.float64), inv)
+        self._rope_cos = ang.cos().to(self.dtype).to(self.device)
+        self._rope_sin = ang.sin().to(self.dtype).to(self.device)
+
+    def _rope_tables(self, pos, T):
+        self._ensure_rope(pos + T)
+        return self._rope_cos[pos:pos + T], self._rope_sin[pos:pos + T]
 
     def new_cache(self, B: int, max_len: int):
         cfg = self.cfg
+        self._ensure_rope(max_len)
         shape = (B, cfg.kv_heads, max_len, cfg.head_dim)
         return [(torch.zeros(shape, dtype=self.dtype, device=self.device),
                  torch.zeros(shape, dtype=self.dtype, device=self.device)) for _ in range(cfg.layers)]

@@ -21,8 +21,11 @@ def test_compare_counts_and_exit_code():
     buf = io.StringIO()
     assert db.compare(a, b, file=buf) == 0        # only a stock hash differs
     text = buf.getvalue()
-    assert "ops    inv    identical: 2/2" in text and "ops    stock  identical: 0/1" in text
-    assert "differing: matmul/bf16/stock" in text
+    assert "[ops] inv: 2 of 2 hashes agree" in text and "[ops] stock: 0 of 1 hashes agree" in text
+    assert "differ: matmul/bf16/stock" in text and "invariant hashes agree" in text
+    buf = io.StringIO()
+    assert db.compare(a, _d({"matmul/bf16/inv": "1", "extra/f16/inv": "4"}), file=buf) == 0
+    assert "in one dump only: extra/f16/inv, matmul/bf16/stock, rms_norm/fp32/inv" in buf.getvalue()
     c = _d({"matmul/bf16/inv": "7", "matmul/bf16/stock": "2", "rms_norm/fp32/inv": "3"})
     assert db.compare(a, c, file=io.StringIO()) == 1   # an invariant hash differs
 
