@@ -132,7 +132,7 @@ int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w, const voi
  * be NULL = all L) gives each sequence's own key count, clamped to [0, L]; a
  * sequence's output depends only on its own first len keys, and a sequence of
  * length 0 gets an all-zero output (no key: no softmax). Hq % Hkv == 0,
- * D in {64, 128}. Keys go in fixed splits of BI_SPLIT_KEYS; the workspace
+ * D in {32, 64, 96, 128, 192, 256}. Keys go in fixed splits of BI_SPLIT_KEYS; the workspace
  * holds per-split (m, l, acc) partials and a work-item counter
  * (bi_attn_decode_workspace_bytes); calls that overlap must not share it.
  * Replaces: kernels/attention.py:326-365 (batch_invariant_decode_attention),

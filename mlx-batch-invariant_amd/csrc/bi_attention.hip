@@ -5,7 +5,8 @@
 // split), combine :149-171 (left fold of splits, precise divide), prefill
 // :173-254 (queries share K/V rows, splits folded in registers, bottom-right
 // causal mask nkeys = L - Tq + t + 1). Per-split arithmetic: bi_attn_common.h;
-// kernels: bi_attn_mfma.h.
+// kernels: bi_attn_mfma.h; launchers: bi_attn_launch.h, instantiated per element
+// type in bi_attn_{bf16,f16,f32}.hip for head dims 32, 64, 96, 128, 192, 256.
 //
 // gfx950 launches:
 //   decode  a resident grid of 256-thread workgroups walking the active items
@@ -16,152 +17,25 @@
 //   prefill one 256-thread workgroup per (sequence, kv head, 64 (token, head)
 //           rows, token-major), K/V streamed through LDS in 64-key chunks,
 //           splits merged in registers.
-#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
-#include "bi_attn_mfma.h"
+#include "bi_attn_api.h"
 
 namespace bi {
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_combine_kernel(DecodeArgs a) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t total = (int64_t)a.B * a.Hq * D;
-  if (gid >= total) return;
-  const int64_t bh = gid / D;
-  const int d = (int)(gid % D);
-  const int b = (int)(bh / a.Hq);
-  const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
-  const int ns = (len + kSplit - 1) / kSplit;
-  float M = -INFINITY, Ls = 0.0f, A = 0.0f;
-  // Splits merge strictly left to right; their partials are loaded eight
-  // splits at a time ahead of the merges (the loads are independent).
-  int i = 0;
-  for (; i + 8 <= ns; i += 8) {
-    float pm[8], pl[8], pa[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t po = bh * a.nsplit + i + j;
-      pm[j] = a.pm[po];
-      pl[j] = a.pl[po];
-      pa[j] = a.pacc[po * D + d];
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) merge_split<1>(M, Ls, &A, pm[j], pl[j], &pa[j]);
+// Calls fn(std::integral_constant<int, D>) for a supported head dim (checked
+// by check_attn_shape before any launch).
+template <class Fn>
+static int with_head_dim(int D, Fn&& fn) {
+  switch (D) {
+    case 32: return fn(std::integral_constant<int, 32>());
+    case 64: return fn(std::integral_constant<int, 64>());
+    case 96: return fn(std::integral_constant<int, 96>());
+    case 128: return fn(std::integral_constant<int, 128>());
+    case 192: return fn(std::integral_constant<int, 192>());
+    default: return fn(std::integral_constant<int, 256>());
   }
-  for (; i < ns; ++i) {
-    const int64_t po = bh * a.nsplit + i;
-    const float acc = a.pacc[po * D + d];
-    merge_split<1>(M, Ls, &A, a.pm[po], a.pl[po], &acc);
-  }
-  // A sequence of length 0 has no split: Ls == 0 and its output is defined as 0.
-  static_cast<T*>(a.out)[bh * D + d] = to_store<T>(Ls > 0.0f ? A / Ls : 0.0f);
-}
-
-// ---------------------------------------------------------------------------
-// Host launchers
-// ---------------------------------------------------------------------------
-static int decode_gu(int G) {
-  for (int gu : {16, 8, 4, 2, 1})
-    if (G % gu == 0) return gu;
-  return 1;
-}
-
-// Workgroups of `kern` (256 threads) that the current device holds at once:
-// compute units x resident workgroups per unit, queried once per device and
-// kept in the caller's per-kernel cache.
-constexpr int kMaxDev = 64;
-template <typename K>
-static int resident_grid(K kern, int (&cache)[kMaxDev]) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
-  if (cache[dev] > 0) return cache[dev];  // benign race: every writer stores the same value
-  int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) != hipSuccess || cus <= 0 ||
-      per_cu <= 0)
-    return 0;
-  cache[dev] = cus * per_cu;
-  return cache[dev];
-}
-
-__global__ void zero_counter_kernel(unsigned* c) { *c = 0u; }
-
-// With more possible items than DYN_MIN_ROUNDS rounds of the resident grid,
-// items are handed out dynamically (one more tiny launch zeroes the counter:
-// a fill kernel, not a memset, so the call can be captured into a graph);
-// with fewer, the static order costs nothing extra.
-constexpr int kDynMinRounds = 4;
-
-// K/V addressing mode (bi_attn_common.h): contiguous, pages of >= 64 keys, or
-// smaller pages.
-template <class Args>
-static int kv_mode(const Args& a) {
-  return !a.table ? kKvContig : a.page_shift >= 6 ? kKvPaged : kKvRowPaged;
-}
-
-// Paged caches always take the dynamic item order (one instantiation each).
-template <typename T, int D, int GU, int MODE>
-static int launch_decode_paged(DecodeArgs& a, int64_t most, hipStream_t st) {
-  static int cache[kMaxDev] = {};
-  const int grid = resident_grid(attn_decode_mfma<T, D, GU, true, MODE>, cache);
-  if (grid <= 0) return bi_host::fail(BI_E_UNSUPPORTED, "bi_attn_decode: device occupancy query failed");
-  zero_counter_kernel<<<1, 1, 0, st>>>(a.ctr);
-  attn_decode_mfma<T, D, GU, true, MODE><<<(int)std::min<int64_t>(grid, most), 256, 0, st>>>(a);
-  return 0;
-}
-
-template <typename T, int D, int GU>
-static int launch_decode_gu(DecodeArgs& a, hipStream_t st) {
-  // Enough resident workgroups to fill the chip, never more than the number
-  // of possible items (every sequence at full length).
-  const int64_t most = (int64_t)a.B * a.nsplit * a.Hkv * a.nchunk;
-  const int mode = kv_mode(a);
-  if (mode == kKvPaged) return launch_decode_paged<T, D, GU, kKvPaged>(a, most, st);
-  if (mode == kKvRowPaged) return launch_decode_paged<T, D, GU, kKvRowPaged>(a, most, st);
-  static int cache[kMaxDev] = {};
-  int grid = resident_grid(attn_decode_mfma<T, D, GU, true, kKvContig>, cache);
-  if (grid <= 0) return bi_host::fail(BI_E_UNSUPPORTED, "bi_attn_decode: device occupancy query failed");
-  if (most > (int64_t)kDynMinRounds * grid) {
-    zero_counter_kernel<<<1, 1, 0, st>>>(a.ctr);
-    attn_decode_mfma<T, D, GU, true, kKvContig><<<grid, 256, 0, st>>>(a);
-  } else {
-    grid = (int)std::min<int64_t>(grid, most);
-    attn_decode_mfma<T, D, GU, false, kKvContig><<<grid, 256, 0, st>>>(a);
-  }
-  return 0;
-}
-
-template <typename T, int D>
-static int launch_decode(DecodeArgs& a, hipStream_t st) {
-  int rc0 = 0;
-  switch (a.GU) {
-    case 16: rc0 = launch_decode_gu<T, D, 16>(a, st); break;
-    case 8: rc0 = launch_decode_gu<T, D, 8>(a, st); break;
-    case 4: rc0 = launch_decode_gu<T, D, 4>(a, st); break;
-    case 2: rc0 = launch_decode_gu<T, D, 2>(a, st); break;
-    default: rc0 = launch_decode_gu<T, D, 1>(a, st); break;
-  }
-  if (rc0) return rc0;
-  int rc = bi_host::launch_status("bi_attn_decode");
-  if (rc) return rc;
-  const int64_t n = (int64_t)a.B * a.Hq * D;
-  attn_combine_kernel<T, D><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(a);
-  return bi_host::launch_status("bi_attn_decode(combine)");
-}
-
-template <typename T, int D>
-static int launch_prefill(PrefillArgs& a, hipStream_t st) {
-  const int G = a.Hq / a.Hkv;
-  const int64_t wgs = ((int64_t)a.Tq * G + 63) / 64;
-  dim3 grid((unsigned)wgs, a.Hkv, a.B);
-  switch (kv_mode(a)) {
-    case kKvPaged: attn_prefill_mfma<T, D, kKvPaged><<<grid, 256, 0, st>>>(a); break;
-    case kKvRowPaged: attn_prefill_mfma<T, D, kKvRowPaged><<<grid, 256, 0, st>>>(a); break;
-    default: attn_prefill_mfma<T, D, kKvContig><<<grid, 256, 0, st>>>(a); break;
-  }
-  return bi_host::launch_status("bi_attn_prefill");
 }
 
 }  // namespace bi
@@ -175,8 +49,9 @@ int check_attn_shape(const char* what, int64_t B, int64_t Hq, int64_t Hkv, int64
                 (long long)B, (long long)Hq, (long long)Hkv, (long long)L, (long long)D);
   if (Hq % Hkv) return fail(BI_E_INVALID_ARG, "%s: Hq=%lld not a multiple of Hkv=%lld", what,
                             (long long)Hq, (long long)Hkv);
-  if (D != 64 && D != 128)
-    return fail(BI_E_UNSUPPORTED, "%s: head dim %lld (supported: 64, 128)", what, (long long)D);
+  if (D != 32 && D != 64 && D != 96 && D != 128 && D != 192 && D != 256)
+    return fail(BI_E_UNSUPPORTED, "%s: head dim %lld (supported: 32, 64, 96, 128, 192, 256)", what,
+                (long long)D);
   if (B > 65535 || Hkv > 65535 || L > 0x7fffffffLL - bi::kSplit || Hq > 0x7fffffffLL / 16)
     return fail(BI_E_UNSUPPORTED, "%s: shape exceeds the grid limits", what);
   return BI_OK;
@@ -256,8 +131,7 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
   if ((int64_t)a.Hkv * a.nchunk > 65535 || a.nsplit > 0x7fffffff)
     return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define BI_DEC(TY)                                                         \
-  return D == 64 ? bi::launch_decode<TY, 64>(a, st) : bi::launch_decode<TY, 128>(a, st);
+#define BI_DEC(TY) return bi::with_head_dim((int)D, [&](auto dd) { return bi::launch_decode<TY, dd.value>(a, st); });
   switch (dtype) {
     case BI_BF16: BI_DEC(bi::bf16)
     case BI_F16: BI_DEC(bi::f16)
@@ -297,8 +171,7 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
   a.v_sb = strides[6]; a.v_sh = strides[7]; a.v_sl = strides[8];
   a.scale_log2 = scale * bi::kLog2e;
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define BI_PRE(TY)                                                           \
-  return D == 64 ? bi::launch_prefill<TY, 64>(a, st) : bi::launch_prefill<TY, 128>(a, st);
+#define BI_PRE(TY) return bi::with_head_dim((int)D, [&](auto dd) { return bi::launch_prefill<TY, dd.value>(a, st); });
   switch (dtype) {
     case BI_BF16: BI_PRE(bi::bf16)
     case BI_F16: BI_PRE(bi::f16)

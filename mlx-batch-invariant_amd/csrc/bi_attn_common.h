@@ -41,6 +41,7 @@
 namespace bi {
 
 constexpr float kLog2e = 1.44269504088896340736f;
+constexpr int kMaxDev = 64;  // devices the host-side per-device caches cover
 
 struct DecodeArgs {
   const void* q;

@@ -32,24 +32,33 @@ typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // LDS tile of K or V rows: row r, 16-byte chunk c at byte offset off(r, c).
+// Rows are stored back to back (D * sizeof(T) bytes); when a row holds a
+// multiple of 8 chunks, chunk c sits in slot c ^ (r & 7) (a fragment read's 16
+// rows then hit distinct bank groups), otherwise in slot c.
 template <typename T, int D>
 struct KVTile {
   static constexpr int kRowBytes = D * (int)sizeof(T);
-  static constexpr int kCPR = kRowBytes / 16;          // chunks per row (>= 8)
-  static constexpr int kRowsPerCopy = kWave / kCPR;    // rows per 1 KB copy instruction
-  static_assert(kCPR >= 8 && kWave % kCPR == 0, "KVTile: D * sizeof(T) must be 128..1024 bytes");
-  static __device__ __forceinline__ int off(int r, int c) { return r * kRowBytes + ((c ^ (r & 7)) << 4); }
-  // Copy instruction ci of a tile: rows ci * kRowsPerCopy .. + kRowsPerCopy - 1
-  // (global row index clamped by the caller). Lane l fetches the chunk that
-  // belongs in slot l % kCPR of its row, landing at tile + 1024 ci + 16 l.
-  // `row(i)` gives the first element of tile row i (0 <= i < nrows_valid).
+  static constexpr int kCPR = kRowBytes / 16;          // 16-byte chunks per row
+  static constexpr bool kSwz = kCPR % 8 == 0;
+  static_assert(kCPR % 4 == 0, "KVTile: D * sizeof(T) must be a multiple of 64 bytes");
+  static __device__ __forceinline__ int off(int r, int c) {
+    return r * kRowBytes + ((kSwz ? (c ^ (r & 7)) : c) << 4);
+  }
+  // Copy instruction ci of a tile moves its flat chunks 64 ci .. 64 ci + 63
+  // (1 KB): lane l fetches the chunk that belongs in flat slot 64 ci + l,
+  // landing at tile + 1024 ci + 16 l. `row(i)` gives the first element of
+  // tile row i (0 <= i < nrows_valid; rows past it repeat the last valid row).
   template <class RowPtr>
   static __device__ __forceinline__ void copy(char* tile, int ci, RowPtr row, int nrows_valid, int lane) {
-    const int r = ci * kRowsPerCopy + lane / kCPR;
-    const int c = (lane % kCPR) ^ (r & 7);
+    const int f = 64 * ci + lane;
+    const int r = f / kCPR;
+    const int slot = f - r * kCPR;
+    const int c = kSwz ? (slot ^ (r & 7)) : slot;
     const T* src = row(min(r, nrows_valid - 1)) + c * (16 / (int)sizeof(T));
     copy_to_lds16(src, tile + 1024 * ci);
   }
+  // Copy instructions that move `rows` whole rows.
+  static constexpr int copies(int rows) { return rows * kCPR / 64; }
   // A-operand fragment of the score MFMA: row r, dims 32 st + 8 qq .. + 7.
   static __device__ __forceinline__ typename Frag<T>::type kfrag(const char* tile, int r, int st, int qq) {
     typedef typename Frag<T>::type F;
@@ -113,16 +122,28 @@ struct KVTile {
 // also the weight sum. Writes (m, l, acc) of its split. The arithmetic of an
 // item does not depend on which workgroup runs it.
 // ---------------------------------------------------------------------------
+// V of a split is staged in LDS NVP dim slices of DV = D / NVP dims each: one
+// slice (the whole row) when the split's V fits in 128 KB, two otherwise
+// (fp32 with D > 128), the second copied after the first slice's P.V. The
+// order of every output element's P.V chain is the same either way.
+template <typename T, int D>
+constexpr int decode_v_slices() {
+  return kSplit * D * (int)sizeof(T) <= (128 << 10) ? 1 : 2;
+}
+
 template <typename T, int D, int GU, bool DYN, int MODE>
 __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   constexpr bool ROWPAGED = MODE == kKvRowPaged;
   typedef typename Frag<T>::type F;
-  typedef KVTile<T, D> KV;
+  constexpr int NVP = decode_v_slices<T, D>();
+  constexpr int DV = D / NVP;                           // dims per V slice
+  typedef KVTile<T, DV> KV;
   constexpr int KT = 4;                                 // score tiles per wave
-  constexpr int NDT = D / 16;                           // P.V dim tiles
-  constexpr int NCOPY = kSplit / KV::kRowsPerCopy;      // copy instructions per split
+  constexpr int NDTV = DV / 16;                         // P.V dim tiles per slice
+  constexpr int NCOPY = KV::copies(kSplit);             // copy instructions per slice
   constexpr int CPW = NCOPY / 4;                        // ... per wave
   static_assert(GU >= 1 && GU <= 16, "attn_decode_mfma: 1..16 heads per workgroup");
+  static_assert(DV % 16 == 0 && CPW >= 1 && CPW < 64, "attn_decode_mfma: V slice tiling");
   __shared__ __attribute__((aligned(1024))) char Vs[kSplit * KV::kRowBytes];
   __shared__ __attribute__((aligned(16))) float Ps[GU][kSplit];
   __shared__ float mxs[4][16];
@@ -176,9 +197,10 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
     if constexpr (ROWPAGED) return kbase + kv_row_off(a, a.k_sb, a.k_sh, a.k_sl, b, hk, j0 + key);
     else return kseg + (int64_t)(key - 64 * seg) * a.k_sl;
   };
+  int vdim0 = 0;                                        // first dim of the V slice being staged
   auto vrow = [&](int key) {
-    if constexpr (ROWPAGED) return vbase + kv_row_off(a, a.v_sb, a.v_sh, a.v_sl, b, hk, j0 + key);
-    else return vseg + (int64_t)(key - 64 * seg) * a.v_sl;
+    if constexpr (ROWPAGED) return vbase + kv_row_off(a, a.v_sb, a.v_sh, a.v_sl, b, hk, j0 + key) + vdim0;
+    else return vseg + (int64_t)(key - 64 * seg) * a.v_sl + vdim0;
   };
 
   // Memory requests, in this order: Q^T, this wave's K rows, its V copies.
@@ -233,43 +255,54 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   if (wave == 0 && qq == 0 && r < GU) a.pm[pbase + (int64_t)r * a.nsplit] = m;
   stage_barrier<0>();  // V landed (own copies: vmcnt; everyone's: the barrier); weights visible
 
-  // P.V over the split's 8 key steps, this wave's dim tiles; wave 0: weight sum.
-  f32x4 acc[(NDT + 3) / 4];
+  // P.V over the split's 8 key steps, this wave's dim tiles of each V slice
+  // (dims 16 dt, dt = wave, wave + 4, ...); wave 0 also the weight sum.
   f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < (NDT + 3) / 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int vp = 0; vp < NVP; ++vp) {
+    if (vp > 0) {
+      __syncthreads();                                  // every wave is done with the previous slice
+      vdim0 = vp * DV;
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) KV::copy(Vs, wave * CPW + c, vrow, n_act, lane);
+      stage_barrier<0>();
+    }
+    f32x4 acc[(NDTV + 3) / 4];
+#pragma unroll
+    for (int j = 0; j < (NDTV + 3) / 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 2
-  for (int ks = 0; ks < kSplit / 32; ++ks) {
-    float p8[8];
-    if (r < GU) {
-      const f32x4 x0 = *reinterpret_cast<const f32x4*>(&Ps[r][32 * ks + 4 * qq]);
-      const f32x4 x1 = *reinterpret_cast<const f32x4*>(&Ps[r][32 * ks + 16 + 4 * qq]);
+    for (int ks = 0; ks < kSplit / 32; ++ks) {
+      float p8[8];
+      if (r < GU) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(&Ps[r][32 * ks + 4 * qq]);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(&Ps[r][32 * ks + 16 + 4 * qq]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        p8[e] = x0[e];
-        p8[4 + e] = x1[e];
+        for (int e = 0; e < 4; ++e) {
+          p8[e] = x0[e];
+          p8[4 + e] = x1[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p8[e] = 0.f;
       }
-    } else {
+      const PFrag<T> pf = make_pfrag<T>(p8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) p8[e] = 0.f;
+      for (int j = 0; j < (NDTV + 3) / 4; ++j) {
+        const int dt = wave + 4 * j;
+        if (dt < NDTV) acc[j] = pv_step<T>(pf, KV::vfrag(Vs, 32 * ks, dt, lane), acc[j]);
+      }
+      if (vp == 0 && wave == 0) lsum = pv_step<T>(pf, ones_frag<T>(), lsum);
     }
-    const PFrag<T> pf = make_pfrag<T>(p8);
-#pragma unroll
-    for (int j = 0; j < (NDT + 3) / 4; ++j) {
-      const int dt = wave + 4 * j;
-      if (dt < NDT) acc[j] = pv_step<T>(pf, KV::vfrag(Vs, 32 * ks, dt, lane), acc[j]);
-    }
-    if (wave == 0) lsum = pv_step<T>(pf, ones_frag<T>(), lsum);
-  }
 
 #pragma unroll
-  for (int j = 0; j < (NDT + 3) / 4; ++j) {
-    const int dt = wave + 4 * j;
-    if (dt >= NDT) continue;
+    for (int j = 0; j < (NDTV + 3) / 4; ++j) {
+      const int dt = wave + 4 * j;
+      if (dt >= NDTV) continue;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = 4 * qq + i;
-      if (row < GU) a.pacc[(pbase + (int64_t)row * a.nsplit) * D + 16 * dt + r] = acc[j][i];
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * qq + i;
+        if (row < GU) a.pacc[(pbase + (int64_t)row * a.nsplit) * D + vp * DV + 16 * dt + r] = acc[j][i];
+      }
     }
   }
   if (wave == 0 && r == 0) {
@@ -301,9 +334,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   typedef typename Frag<T>::type F;
   typedef KVTile<T, D> KV;
   constexpr int CH = 64;                                // keys per chunk
-  constexpr int NBUF = 3;
   constexpr int CHB = CH * KV::kRowBytes;               // bytes per chunk
-  constexpr int CPW = CH / KV::kRowsPerCopy / 4;        // copy instructions per wave per chunk
+  constexpr int NBUF = 3 * CHB <= (144 << 10) ? 3 : 2;  // ring depth (2 for fp32 rows of 1 KB)
+  constexpr int PF = NBUF - 1;                          // chunks requested ahead of the current one
+  constexpr int CPW = KV::copies(CH) / 4;               // copy instructions per wave per chunk
   constexpr int NDT = D / 16;
   static_assert(CPW >= 1, "attn_prefill_mfma: chunk copy tiling");
   __shared__ __attribute__((aligned(1024))) char ring[NBUF * CHB];
@@ -380,9 +414,9 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
     for (int i = 0; i < CPW; ++i) KV::copy(buf, wave * CPW + i, row, len - key0, lane);
   };
   auto open_chunk = [&](int c) {
-    if (c + 1 < nchunks) stage_barrier<CPW>();  // chunk c landed; c + 1 may be in flight
+    if (PF == 2 && c + 1 < nchunks) stage_barrier<CPW>();  // chunk c landed; c + 1 may be in flight
     else stage_barrier<0>();
-    issue(c + 2);                               // every wave is past chunk c - 1: its buffer is free
+    issue(c + PF);                              // every wave is past chunk c - 1: its buffer is free
   };
 
   float M[4], Lsum[4];
@@ -396,7 +430,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   for (int dt = 0; dt < NDT; ++dt) A[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   issue(0);
-  issue(1);
+  if (PF == 2) issue(1);
   int ci = 0;
   // A split entirely below every valid row's key limit needs no per-key mask
   // (the wave's first row has the smallest limit; padding rows past npairs

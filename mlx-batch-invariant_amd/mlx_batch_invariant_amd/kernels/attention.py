@@ -41,7 +41,7 @@ import torch
 from .. import _lib
 
 SPLIT_SIZE = _lib.SPLIT_KEYS
-SUPPORTED_HEAD_DIMS = (64, 128)
+SUPPORTED_HEAD_DIMS = (32, 64, 96, 128, 192, 256)   # reference: any D % 32 == 0 (kernels/attention.py:299-310)
 
 
 def supports(q, k, v, mask, sinks=None) -> bool:

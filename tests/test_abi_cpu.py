@@ -97,7 +97,7 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.bi_rms_norm(p, 4, None, p, 2, 8, 1e-6, 2, None) == -1
     assert lib.bi_rms_norm(p, 8, None, p, 0, 8, 1e-6, 2, None) == 0     # nothing to do
     strides = (ctypes.c_int64 * 9)(*([128] * 9))
-    assert lib.bi_attn_decode(p, p, p, None, p, 1, 4, 4, 10, 96, strides, 1.0, 2, p, 1 << 20, None) == -2
+    assert lib.bi_attn_decode(p, p, p, None, p, 1, 4, 4, 10, 80, strides, 1.0, 2, p, 1 << 20, None) == -2   # D % 32 != 0
     assert lib.bi_attn_decode(p, p, p, None, p, 1, 6, 4, 10, 128, strides, 1.0, 2, p, 1 << 20, None) == -1
     assert lib.bi_attn_decode(p, p, p, None, p, 1, 4, 4, 10, 128, strides, 1.0, 2, None, 0, None) == -3
     assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 20, 10, 128, strides, 1, 1.0, 2, None) == -1

@@ -116,3 +116,19 @@ def test_paged_table_entries_are_clamped_into_the_pool(page_size):
         got = bi.batch_invariant_paged_attention(qq, kp, vp, bad, lens, scale=D ** -0.5, mask=mask)
         want = bi.batch_invariant_paged_attention(qq, kp, vp, clamped, lens, scale=D ** -0.5, mask=mask)
         assert bits(got) == bits(want), Tq
+
+
+@pytest.mark.parametrize("dt,D", [("bf16", 96), ("bf16", 256), ("f32", 256)])
+def test_paged_other_head_dims_equal_contiguous(dt, D):
+    bi = _bi()
+    g = gen(D)
+    B, Hq, Hkv, L = 3, 8, 2, 500
+    q = randn((B, Hq, 1, D), DT[dt], g)
+    k = randn((B, Hkv, L, D), DT[dt], g)
+    v = randn((B, Hkv, L, D), DT[dt], g)
+    lens = torch.tensor([500, 1, 300], dtype=torch.int32).cuda()
+    want = bi.batch_invariant_decode_attention(q, k, v, scale=D ** -0.5, kv_lens=lens)
+    for ps in (16, 128):
+        kp, vp, table = _paginate(k, v, ps, g)
+        got = bi.batch_invariant_paged_attention(q, kp, vp, table, lens, scale=D ** -0.5)
+        assert bits(got) == bits(want), ps
