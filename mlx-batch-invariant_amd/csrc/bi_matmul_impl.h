@@ -589,13 +589,45 @@ constexpr int kTallMinTiles = 200;
 // M = 64: 13.8 -> 9.3 us); with more groups they lose (4096 x 4096, M = 64:
 // 18.4 -> 21.6 us).
 constexpr int kTallMinTilesShortK = 100;
+constexpr int kTallMaxM = 128;
+// Dense large tile (bi_gemm_big.h) for 2-byte types, M > 128, K % 64 == 0:
+// fused when it has at least kBigMinTiles tiles of 256 x 128; otherwise, for
+// M <= kBigSplitMaxM and more than one K group, one workgroup per (tile,
+// group) writing raw group partials that fold_groups folds in order. A
+// function of the shape only, so the workspace query and the launch agree.
+constexpr int kBigFromM = 129;
+constexpr int kBigShortKMinTiles = 32;
+constexpr int kBigSplitMaxM = 256;
+struct BigPlan {
+  bool use = false, split = false;
+  int tiles_m = 0, tiles_n = 0;
+};
+static inline BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
+  BigPlan p;
+  if (M < kBigFromM || N <= 0 || K <= 0 || K % 64) return p;
+  p.tiles_m = ceil_div(M, kBigBM);
+  p.tiles_n = ceil_div(N, kBigBN);
+  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+  // With at most 4 groups of K a split launch's partial traffic outweighs the
+  // idle CUs of a fused one (Qwen2-0.5B [4864, 896] at M = 256: 38 tiles,
+  // fused 17.5 us, split 22.4 us); with 16 groups the split wins ([4096,
+  // 4096] at M = 256: 32 tiles, 49.8 against 39.1 us).
+  if (tiles >= kBigMinTiles || (K <= 4 * kGroupK && tiles >= kBigShortKMinTiles)) {
+    p.use = true;
+  } else if (M <= kBigSplitMaxM && K > kGroupK) {
+    p.use = true;
+    p.split = true;
+  }
+  return p;
+}
+
 struct TallPlan {
   bool use = false;
   int bm = 0, bn = 0, chunks = 1, cg = 0;
 };
 static inline TallPlan tall_plan(int64_t M, int64_t N, int64_t K) {
   TallPlan p;
-  if (M <= 16 || M > 128 || K <= 0 || K % 64) return p;
+  if (M <= 16 || M > kTallMaxM || K <= 0 || K % 64) return p;
   const int G = ceil_div(K, kGroupK);
   const int min_tiles = G <= 4 ? kTallMinTilesShortK : kTallMinTiles;
   p.bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
@@ -871,6 +903,23 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
     }
   }
   if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
+    const BigPlan bp = big_plan(M, N, K);
+    if (bp.use && lda < kBigMaxLd && bsrc.ldb < kBigMaxLd) {
+      const int work = bp.tiles_m * bp.tiles_n * (bp.split ? G : 1);
+      const int grid = ((work + 7) / 8) * 8;
+      if (bp.split) {
+        gemm_big<T, true><<<grid, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, ws, M, N, K, bp.tiles_m,
+                                                           bp.tiles_n);
+        const int rc = bi_host::launch_status(what);
+        if (rc) return rc;
+        const int64_t MN = (int64_t)M * N;
+        fold_groups<T><<<(unsigned)((MN + 255) / 256), 256, 0, st>>>(ws, out, MN, G);
+      } else {
+        gemm_big<T, false><<<grid, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, nullptr, M, N, K,
+                                                            bp.tiles_m, bp.tiles_n);
+      }
+      return bi_host::launch_status(what);
+    }
     const TallPlan tp = tall_plan(M, N, K);
     if (tp.use && lda < kBigMaxLd && bsrc.ldb < kBigMaxLd) {
       launch_tall<T>(a, lda, bsrc, out, ws, M, N, K, G, tp, st);
@@ -903,15 +952,6 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   }
   // M > 32: LDS-tiled; the largest tile that still gives the chip >= 256 tiles.
   auto tiles = [&](int bm, int bn) { return (int64_t)ceil_div(M, bm) * ceil_div(N, bn); };
-  if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
-    if (K % kGroupK == 0 && M >= kBigMinM && tiles(kBigBM, kBigBN) >= kBigMinTiles && lda < kBigMaxLd &&
-        bsrc.ldb < kBigMaxLd) {
-      const int tmm = ceil_div(M, kBigBM), tn = ceil_div(N, kBigBN);
-      const int grid = ((tmm * tn + 7) / 8) * 8;
-      gemm_big<T><<<grid, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K, tmm, tn);
-      return bi_host::launch_status(what);
-    }
-  }
   if constexpr (sizeof(T) == 4) {
     if (tiles(64, 128) >= 256) launch_lds<T, BSrc, 64, 128>(a, lda, bsrc, out, M, N, K, G, st);
     else launch_lds<T, BSrc, 64, 64>(a, lda, bsrc, out, M, N, K, G, st);
@@ -938,7 +978,8 @@ int run_quant(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
       bi::qmm_permute_a<T><<<(unsigned)((na + 255) / 256), 256, 0, st>>>(static_cast<const T*>(x), ldx, ap, M, K);
       const int tmm = ceil_div(M, bi::kBigBM), tn = ceil_div(N, bi::kBigBN);
       const int grid = ((tmm * tn + 7) / 8) * 8;
-      bi::gemm_big<T><<<grid, 64 * bi::kBigWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), M, N, K, tmm, tn);
+      bi::gemm_big<T, false><<<grid, 64 * bi::kBigWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), nullptr, M, N,
+                                                                  K, tmm, tn);
       return bi_host::launch_status("bi_quantized_matmul");
     }
   }

@@ -40,7 +40,12 @@ def test_workspace_sizes():
     assert lib.bi_matmul_workspace_bytes(64, 14336, 4096) == 0       # mid-M, enough column tiles
     assert lib.bi_matmul_workspace_bytes(64, 4096, 14336) == 0       # 16-column tiles fill the chip
     assert lib.bi_matmul_workspace_bytes(64, 1024, 4096) == 16 * 64 * 1024 * 4   # 4 chunks of 4 groups
-    assert lib.bi_matmul_workspace_bytes(129, 100, 896) == 0         # fused (LDS tiles)
+    assert lib.bi_matmul_workspace_bytes(129, 100, 896) == 4 * 129 * 100 * 4   # large tile, split per group
+    assert lib.bi_matmul_workspace_bytes(256, 4864, 896) == 0        # 38 tiles, 4 groups: fused
+    assert lib.bi_matmul_workspace_bytes(256, 4096, 4096) == 16 * 256 * 4096 * 4   # 32 tiles, 16 groups: split
+    assert lib.bi_matmul_workspace_bytes(129, 12800, 896) == 0       # large tile, >= 96 tiles: fused
+    assert lib.bi_matmul_workspace_bytes(257, 100, 896) == 0         # fused (LDS tiles)
+    assert lib.bi_matmul_workspace_bytes(200, 4864, 900) == 0        # K % 64 != 0: LDS tiles
     assert lib.bi_quantized_matmul_workspace_bytes(32, 100, 896) == 0   # quantized mid-M needs whole groups
     # quantized mid-M with too few (64-column, row block) tiles splits K: ~512 workgroups
     assert lib.bi_quantized_matmul_workspace_bytes(64, 4096, 14336) == 56 * 64 * 4096 * 4   # 8 chunks of 7

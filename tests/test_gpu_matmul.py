@@ -203,3 +203,23 @@ def test_batched_matmul_intercepted_by_mode():
     assert bi.stats()["handled"] == {"matmul": 3}
     assert bits(s1) == bits(s2) == bits(bi.batch_invariant_bmm(q, k.transpose(-1, -2)))
     assert bits(s3) == bits(s1[0])
+
+
+@pytest.mark.parametrize("M,N,K", [(200, 4864, 896), (256, 4864, 896), (160, 1024, 4096), (129, 12800, 896),
+                                   (300, 12416, 960), (256, 4096, 4096)])
+def test_matmul_large_tile_split_and_partial_groups(M, N, K):
+    """M > 128 takes the 256 x 128 tile: fused when there are >= 96 tiles,
+    otherwise one workgroup per (tile, K group) with raw partials folded in
+    order afterwards; K need not be whole groups (stages past K are zero).
+    Sampled rows equal the oracle and the same rows computed alone, bit for
+    bit (the decode launches)."""
+    g = gen(M + N + K)
+    W = randn((N, K), torch.bfloat16, g, scale=0.02)
+    x = randn((M, K), torch.bfloat16, g)
+    full = _mm(x, W.t())
+    rows = sorted({0, 1, 127, 128, M // 2, M - 1})
+    cols = np.r_[0:40, N // 2:N // 2 + 40, N - 40:N]
+    want = ora.matmul(to_np(x[rows]), to_np(W)[cols], "bf16")
+    assert_bits_equal(to_np(full)[rows][:, cols], want, f"{M}x{N}x{K}")
+    for lo, hi in ((0, 1), (M - 1, M), (5, 21), (100, 164)):
+        assert bits(_mm(x[lo:hi], W.t())) == bits(full[lo:hi]), (lo, hi)
