@@ -137,6 +137,9 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     # reads ~1 us per call slower for its first few hundred calls, then recovers.
     _sync()
     t0 = time.perf_counter()
+    if args.profile_m != 1:                # profiling aid: only the calls at that M, no report
+        _time_calls(call(args.profile_m), args.steps, args.warmup, ncopy, replays=3)
+        return {"metric": METRIC, "op": f"qmm{bits} profile run at M={args.profile_m}", "value": None}
     durs = _time_calls(call(1), args.steps, args.warmup, ncopy, replays=3)
     wall = time.perf_counter() - t0
     table = {}
@@ -532,6 +535,8 @@ def main(argv=None) -> int:
     p.add_argument("--llama-prompt", type=int, default=512)
     p.add_argument("--llama-steps", type=int, default=128)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--profile-m", type=int, default=1,
+                   help="qmm4/qmm8: run only the graph-replayed calls at this M and print no result (for profilers)")
     p.add_argument("--headline-only", action="store_true",
                    help="time only each op's headline shape (qmm M=1, rmsnorm D=4096, decode B=256, "
                         "prefill B=16, gemm M=4096) without sweeps or stock legs; for profiling")
