@@ -371,9 +371,12 @@ def bench_decode(args):
         kl = torch.tensor(lens, dtype=torch.int32).cuda()
         t = statistics.median(_time_calls(lambda i: bi.batch_invariant_decode_attention(
             q, k, v, scale=128 ** -0.5, kv_lens=kl), args.steps, args.warmup, 1))
+        tp = None if args.headline_only else statistics.median(_time_calls(
+            lambda i: bi.batch_invariant_decode_attention(q, k, v, scale=128 ** -0.5, kv_lens=kl, order="per_key"),
+            max(3, args.steps // 4), 2, 1))
         by = 4096 * int(lens.sum()) + 16384 * B
         res[B] = {"us": round(t * 1e6, 2), "GBps": round(by / t / 1e9, 1), "frac_hbm": round(by / t / PEAK_HBM, 4),
-                  "sum_len": int(lens.sum())}
+                  "sum_len": int(lens.sum()), "per_key_order_us": None if tp is None else round(tp * 1e6, 2)}
         del k, v
     return {"metric": METRIC, "op": "decode attention (config 3)", "per_b": res}
 
@@ -394,9 +397,13 @@ def bench_prefill(args):
         ts = None if args.headline_only else statistics.median(_time_calls(
             lambda i: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True),
             max(3, args.steps // 4), 2, 1))
+        tp = None if args.headline_only else statistics.median(_time_calls(
+            lambda i: bi.batch_invariant_prefill_attention(q, k, v, scale=128 ** -0.5, causal=True, order="per_key"),
+            3, 1, 1))
         fl = 4 * B * 32 * 128 * T * (T + 1) / 2
         res[B] = {"ms": round(t * 1e3, 3), "TFLOPs": round(fl / t / 1e12, 1), "frac_mfma": round(fl / t / PEAK_BF16, 4),
-                  "stock_sdpa_ms": None if ts is None else round(ts * 1e3, 3)}
+                  "stock_sdpa_ms": None if ts is None else round(ts * 1e3, 3),
+                  "per_key_order_ms": None if tp is None else round(tp * 1e3, 3)}
     return {"metric": METRIC, "op": "prefill attention (config 4)", "per_b": res}
 
 

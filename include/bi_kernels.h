@@ -210,6 +210,27 @@ int bi_attn_prefill_paged(const void* q, const void* k_pages, const void* v_page
                           int64_t Tq, int64_t L, int64_t D, const int64_t* strides, int causal,
                           float scale, int dtype, void* stream);
 
+/* ---- Attention in the reference's per-key order ----------------------------
+ * Same arguments, workspace, validation and invariance properties as
+ * bi_attn_decode / bi_attn_prefill, in the reference kernels' own order of
+ * operations instead of the matrix-core order: q pre-scaled in fp32, score =
+ * 32 lane partials of D/32 dims (fma chains) folded by an xor butterfly
+ * 16..1, the online softmax key by key inside each split (m' = max(m, s);
+ * corr = exp(m - m'); p = exp(s - m'); l = fma(l, corr, p); acc = fma(acc,
+ * corr, p v)), the same left-to-right split merge in base e, out = T(A / L).
+ * exp is fp32 rounded once from double precision. Slower (vector ALUs, one
+ * key at a time); for callers that need the reference order's values.
+ * Replaces: kernels/attention.py:87-147 + :149-171 (decode + combine) and
+ * :173-254 (prefill), order of operations :1-32, :47-85. */
+int bi_attn_decode_per_key(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                           void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                           const int64_t* strides, float scale, int dtype, void* ws,
+                           size_t ws_bytes, void* stream);
+int bi_attn_prefill_per_key(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                            void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
+                            int64_t D, const int64_t* strides, int causal, float scale, int dtype,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

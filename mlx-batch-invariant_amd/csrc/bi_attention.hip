@@ -94,7 +94,7 @@ int check_pages(const char* what, const int32_t* table, int64_t table_stride, in
 int decode_impl(const char* what, const void* q, const void* k, const void* v, const int32_t* kv_lens, void* out,
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D, const int64_t* strides, float scale,
                 int dtype, void* ws, size_t ws_bytes, void* stream, const int32_t* table, int64_t table_stride,
-                int page_shift, int64_t num_pages) {
+                int page_shift, int64_t num_pages, bool per_key = false) {
   using namespace bi_host;
   if (B == 0) return BI_OK;
   if (!q || !k || !v || !out || !strides)
@@ -116,22 +116,27 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.L = (int)L;
   a.nsplit = (int)((L + bi::kSplit - 1) / bi::kSplit);
   const int G = (int)(Hq / Hkv);
-  a.GU = bi::decode_gu(G);
+  a.GU = per_key ? bi::perkey_decode_nq(B, (int)Hq, (int)Hkv, a.nsplit) : bi::decode_gu(G);
   a.nchunk = G / a.GU;
   a.q_sb = strides[0]; a.q_sh = strides[1];
   a.k_sb = strides[2]; a.k_sh = strides[3]; a.k_sl = strides[4];
   a.v_sb = strides[5]; a.v_sh = strides[6]; a.v_sl = strides[7];
   a.scale_log2 = scale * bi::kLog2e;
+  a.scale = scale;
   const int64_t bh = B * Hq * a.nsplit;
   const int64_t up = (bh + 3) / 4 * 4;
   a.pm = static_cast<float*>(ws);
   a.pl = a.pm + up;
   a.pacc = a.pl + up;
   a.ctr = reinterpret_cast<unsigned*>(a.pacc + bh * D);
-  if ((int64_t)a.Hkv * a.nchunk > 65535 || a.nsplit > 0x7fffffff)
+  if ((int64_t)a.Hkv * a.nchunk > 65535 || a.nsplit > 0x7fffffff ||
+      (per_key && bh / a.GU > ((int64_t)1 << 27)))  // per-key: 32 threads per unit, < 2^32 threads
     return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define BI_DEC(TY) return bi::with_head_dim((int)D, [&](auto dd) { return bi::launch_decode<TY, dd.value>(a, st); });
+#define BI_DEC(TY)                                                                                          \
+  return bi::with_head_dim((int)D, [&](auto dd) {                                                         \
+    return per_key ? bi::launch_decode_perkey<TY, dd.value>(a, st) : bi::launch_decode<TY, dd.value>(a, st); \
+  });
   switch (dtype) {
     case BI_BF16: BI_DEC(bi::bf16)
     case BI_F16: BI_DEC(bi::f16)
@@ -144,7 +149,7 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
 int prefill_impl(const char* what, const void* q, const void* k, const void* v, const int32_t* kv_lens,
                  void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L, int64_t D,
                  const int64_t* strides, int causal, float scale, int dtype, void* stream, const int32_t* table,
-                 int64_t table_stride, int page_shift, int64_t num_pages) {
+                 int64_t table_stride, int page_shift, int64_t num_pages, bool per_key = false) {
   using namespace bi_host;
   if (Tq <= 0) return fail(BI_E_INVALID_ARG, "%s: Tq=%lld", what, (long long)Tq);
   if (causal && Tq > L)
@@ -159,7 +164,8 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return fail(BI_E_INVALID_ARG, "%s: q, k, v, out must be 16-byte aligned", what);
   const int64_t wgs = (Tq * (Hq / Hkv) + 63) / 64;
-  if (wgs > 0x7fffffffLL || Tq * (Hq / Hkv) > 0x7fffffffLL - 64)
+  if (wgs > 0x7fffffffLL || Tq * (Hq / Hkv) > 0x7fffffffLL - 64 ||
+      (per_key && B * Hq * ((Tq + bi::kPkQB - 1) / bi::kPkQB) > ((int64_t)1 << 27)))
     return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   bi::PrefillArgs a;
   a.q = q; a.k = k; a.v = v; a.kv_lens = kv_lens; a.out = out;
@@ -170,8 +176,12 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
   a.k_sb = strides[3]; a.k_sh = strides[4]; a.k_sl = strides[5];
   a.v_sb = strides[6]; a.v_sh = strides[7]; a.v_sl = strides[8];
   a.scale_log2 = scale * bi::kLog2e;
+  a.scale = scale;
   hipStream_t st = static_cast<hipStream_t>(stream);
-#define BI_PRE(TY) return bi::with_head_dim((int)D, [&](auto dd) { return bi::launch_prefill<TY, dd.value>(a, st); });
+#define BI_PRE(TY)                                                                                            \
+  return bi::with_head_dim((int)D, [&](auto dd) {                                                           \
+    return per_key ? bi::launch_prefill_perkey<TY, dd.value>(a, st) : bi::launch_prefill<TY, dd.value>(a, st); \
+  });
   switch (dtype) {
     case BI_BF16: BI_PRE(bi::bf16)
     case BI_F16: BI_PRE(bi::f16)
@@ -231,6 +241,28 @@ extern "C" int bi_attn_prefill_paged(const void* q, const void* k_pages, const v
     return rc;
   return prefill_impl("bi_attn_prefill_paged", q, k_pages, v_pages, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides,
                       causal, scale, dtype, stream, block_table, table_stride, shift, num_pages);
+}
+
+// The reference's per-key order (bi_attn_perkey.h): same arguments, workspace
+// and validation as bi_attn_decode / bi_attn_prefill.
+extern "C" int bi_attn_decode_per_key(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                                      void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                                      const int64_t* strides, float scale, int dtype, void* ws, size_t ws_bytes,
+                                      void* stream) {
+  int rc = check_attn_shape("bi_attn_decode_per_key", B, Hq, Hkv, L, D);
+  if (rc) return rc;
+  return decode_impl("bi_attn_decode_per_key", q, k, v, kv_lens, out, B, Hq, Hkv, L, D, strides, scale, dtype, ws,
+                     ws_bytes, stream, nullptr, 0, 0, 0, true);
+}
+
+extern "C" int bi_attn_prefill_per_key(const void* q, const void* k, const void* v, const int32_t* kv_lens,
+                                       void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
+                                       int64_t D, const int64_t* strides, int causal, float scale, int dtype,
+                                       void* stream) {
+  int rc = check_attn_shape("bi_attn_prefill_per_key", B, Hq, Hkv, L, D);
+  if (rc) return rc;
+  return prefill_impl("bi_attn_prefill_per_key", q, k, v, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides, causal,
+                      scale, dtype, stream, nullptr, 0, 0, 0, true);
 }
 
 // ---------------------------------------------------------------------------

@@ -14,9 +14,25 @@ inline int decode_gu(int G) {
   return 1;
 }
 
+constexpr int kPkQB = 4;  // queries per per-key prefill unit (reference QB)
+
+// Query heads a per-key decode unit scores together: 4, 2 or 1 (dividing G), and 1
+// while the grid has fewer than 16384 (head, split) pairs, where every unit
+// is wanted for parallelism.
+inline int perkey_decode_nq(int64_t B, int Hq, int Hkv, int nsplit) {
+  const int G = Hq / Hkv;
+  if ((int64_t)B * Hq * nsplit < 16384) return 1;
+  return G % 4 == 0 ? 4 : G % 2 == 0 ? 2 : 1;
+}
+
 template <typename T, int D>
 int launch_decode(DecodeArgs& a, hipStream_t st);
 template <typename T, int D>
 int launch_prefill(PrefillArgs& a, hipStream_t st);
+// The reference's per-key order on the vector ALUs (bi_attn_perkey.h).
+template <typename T, int D>
+int launch_decode_perkey(DecodeArgs& a, hipStream_t st);
+template <typename T, int D>
+int launch_prefill_perkey(PrefillArgs& a, hipStream_t st);
 
 }  // namespace bi

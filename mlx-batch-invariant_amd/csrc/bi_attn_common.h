@@ -56,6 +56,7 @@ struct DecodeArgs {
   int B, Hq, Hkv, L, nsplit, nchunk, GU;
   int64_t q_sb, q_sh, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
   float scale_log2;  // scale * log2(e), rounded once on the host
+  float scale;       // the caller's scale (per-key order)
   // Paged K/V (null table = contiguous): see kv_row_off.
   const int32_t* table;
   int64_t table_stride;
@@ -72,6 +73,7 @@ struct PrefillArgs {
   int B, Hq, Hkv, Tq, L, causal;
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
   float scale_log2;
+  float scale;
   const int32_t* table;
   int64_t table_stride;
   int page_shift;

@@ -10,6 +10,7 @@
 
 #include "bi_attn_api.h"
 #include "bi_attn_mfma.h"
+#include "bi_attn_perkey.h"
 
 namespace bi {
 
@@ -150,7 +151,9 @@ int launch_prefill(PrefillArgs& a, hipStream_t st) {
 
 #define BI_ATTN_INSTANTIATE_D(T, D)                                   \
   template int launch_decode<T, D>(DecodeArgs&, hipStream_t);        \
-  template int launch_prefill<T, D>(PrefillArgs&, hipStream_t);
+  template int launch_prefill<T, D>(PrefillArgs&, hipStream_t);      \
+  template int launch_decode_perkey<T, D>(DecodeArgs&, hipStream_t); \
+  template int launch_prefill_perkey<T, D>(PrefillArgs&, hipStream_t);
 #define BI_ATTN_INSTANTIATE(T)                                                                           \
   BI_ATTN_INSTANTIATE_D(T, 32) BI_ATTN_INSTANTIATE_D(T, 64) BI_ATTN_INSTANTIATE_D(T, 96)                \
   BI_ATTN_INSTANTIATE_D(T, 128) BI_ATTN_INSTANTIATE_D(T, 192) BI_ATTN_INSTANTIATE_D(T, 256)

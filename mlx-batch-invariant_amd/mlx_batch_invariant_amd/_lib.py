@@ -55,6 +55,12 @@ _SIGNATURES = {
     "bi_attn_prefill": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_float,
                                        ctypes.c_int, _vp]),
+    "bi_attn_decode_per_key": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                              ctypes.POINTER(_c_i64), ctypes.c_float, ctypes.c_int, _vp,
+                                              ctypes.c_size_t, _vp]),
+    "bi_attn_prefill_per_key": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+                                               _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_float,
+                                               ctypes.c_int, _vp]),
     "bi_attn_decode_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                               ctypes.POINTER(_c_i64), ctypes.c_float, ctypes.c_int, _vp]),
     "bi_attn_decode_paged": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64,

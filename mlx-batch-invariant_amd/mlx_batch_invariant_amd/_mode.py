@@ -66,15 +66,18 @@ def is_batch_invariant_mode_enabled() -> bool:
 
 
 @contextlib.contextmanager
-def set_batch_invariant_mode(enabled: bool = True, *, strict: bool = False):
+def set_batch_invariant_mode(enabled: bool = True, *, strict: bool = False, attention_order: str = "mfma"):
     """Inside the block, matmul / mm / bmm / addmm / ``@`` / linear / the
     package's quantized matmul / rms_norm / layer_norm / sdpa resolve to the
     batch-invariant kernels (reference: _mode.py:66-91).
 
     With ``strict`` an input no kernel handles raises ``RuntimeError``; without
-    it the stock op runs and the fallback is counted. Blocks nest: the swap
-    happens when the first one opens and is undone when the last one closes,
-    and each block's ``strict`` holds until it closes. ``enabled=False`` is a
+    it the stock op runs and the fallback is counted. ``attention_order``
+    picks the attention kernels: "mfma" (matrix cores, the default) or
+    "per_key" (the reference's own order of operations, slower). Blocks nest:
+    the swap happens when the first one opens and is undone when the last one
+    closes, and each block's ``strict`` and ``attention_order`` hold until it
+    closes. ``enabled=False`` is a
     no-op block. The swap is process-wide, since torch looks these attributes
     up at call time; a lock serialises opening and closing.
     """
@@ -82,17 +85,20 @@ def set_batch_invariant_mode(enabled: bool = True, *, strict: bool = False):
     if not enabled:
         yield
         return
+    from .kernels.attention import ORDERS
+    if attention_order not in ORDERS:
+        raise ValueError(f"attention_order must be one of {ORDERS}; got {attention_order!r}")
     with _lock:
-        outer_strict = ops.strict
+        outer = (ops.strict, ops.attention_order)
         if _depth == 0:
             _apply()
         _depth += 1
-        ops.strict = strict
+        ops.strict, ops.attention_order = strict, attention_order
     try:
         yield
     finally:
         with _lock:
             _depth -= 1
-            ops.strict = outer_strict
+            ops.strict, ops.attention_order = outer
             if _depth == 0:
                 _restore()

@@ -27,6 +27,12 @@ of a later decode step for that position, and chunked prefill equals one-shot
 prefill. Causal masking is bottom-right aligned (query t of a T_q-token chunk
 sees ``len - T_q + t + 1`` keys), as in MLX.
 
+``order="per_key"`` runs the reference's own order instead (q pre-scaled, 32
+lane partials of D/32 dims folded by an xor butterfly, the softmax recurrence
+key by key inside each split, splits merged in base e, exp rounded once from
+float64): the same invariance properties, values equal to the reference
+order's bit for bit, on the vector ALUs and so slower. Contiguous K/V only.
+
 ``kv_lens`` (int32 [B], optional) is an extension the reference does not have:
 sequence b uses only its first ``kv_lens[b]`` keys, and its output is bit-for-bit
 what it would be alone with K/V cut to that length.
@@ -41,6 +47,7 @@ import torch
 from .. import _lib
 
 SPLIT_SIZE = _lib.SPLIT_KEYS
+ORDERS = ("mfma", "per_key")
 SUPPORTED_HEAD_DIMS = (32, 64, 96, 128, 192, 256)   # reference: any D % 32 == 0 (kernels/attention.py:299-310)
 
 
@@ -99,11 +106,19 @@ def _check_split(split_size: int) -> None:
         raise ValueError(f"split_size is a contract constant ({SPLIT_SIZE}); got {split_size}")
 
 
+def _check_order(order: str) -> bool:
+    """True for the reference's per-key order, False for the matrix-core order."""
+    if order not in ORDERS:
+        raise ValueError(f"attention order must be one of {ORDERS}; got {order!r}")
+    return order == "per_key"
+
+
 def batch_invariant_decode_attention(q, k, v, *, scale: float, split_size: int = SPLIT_SIZE,
-                                     kv_lens=None) -> torch.Tensor:
+                                     kv_lens=None, order: str = "mfma") -> torch.Tensor:
     """T_q == 1. Per-split partials (the GU query heads of a kv head share each
     K/V row), then an ordered combine (reference: kernels/attention.py:326-365)."""
     _check_split(split_size)
+    per_key = _check_order(order)
     B, Hq, Tq, D = q.shape
     _, Hkv, L, _ = k.shape
     if Tq != 1:
@@ -124,18 +139,21 @@ def batch_invariant_decode_attention(q, k, v, *, scale: float, split_size: int =
     ws = _lib.workspace(ws_bytes, q.device)
     strides = (_lib._c_i64 * 8)(q3.stride(0), q3.stride(1), k.stride(0), k.stride(1), k.stride(2),
                                 v.stride(0), v.stride(1), v.stride(2))
-    rc = lib.bi_attn_decode(q3.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
+    name = "bi_attn_decode_per_key" if per_key else "bi_attn_decode"
+    rc = getattr(lib, name)(q3.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
                             B, Hq, Hkv, L, D, strides, float(scale), _lib.DTYPE_CODE[dt],
                             _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
-    _lib.check(rc, "bi_attn_decode")
+    _lib.check(rc, name)
     return out
 
 
 def batch_invariant_prefill_attention(q, k, v, *, scale: float, causal: bool,
-                                      split_size: int = SPLIT_SIZE, kv_lens=None) -> torch.Tensor:
+                                      split_size: int = SPLIT_SIZE, kv_lens=None,
+                                      order: str = "mfma") -> torch.Tensor:
     """Any T_q. Blocks of 16 (token, head) rows share each K/V row; same split
     loop and merge as decode (reference: kernels/attention.py:368-390)."""
     _check_split(split_size)
+    per_key = _check_order(order)
     B, Hq, Tq, D = q.shape
     _, Hkv, L, _ = k.shape
     if D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
@@ -154,24 +172,27 @@ def batch_invariant_prefill_attention(q, k, v, *, scale: float, causal: bool,
     lib = _lib.load()
     strides = (_lib._c_i64 * 9)(q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1),
                                 k.stride(2), v.stride(0), v.stride(1), v.stride(2))
-    rc = lib.bi_attn_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
-                             B, Hq, Hkv, Tq, L, D, strides, 1 if causal else 0, float(scale),
-                             _lib.DTYPE_CODE[dt], _lib.stream_of(q))
-    _lib.check(rc, "bi_attn_prefill")
+    name = "bi_attn_prefill_per_key" if per_key else "bi_attn_prefill"
+    rc = getattr(lib, name)(q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
+                            B, Hq, Hkv, Tq, L, D, strides, 1 if causal else 0, float(scale),
+                            _lib.DTYPE_CODE[dt], _lib.stream_of(q))
+    _lib.check(rc, name)
     return out
 
 
-def batch_invariant_attention(q, k, v, *, scale: float | None = None, mask=None, kv_lens=None) -> torch.Tensor:
+def batch_invariant_attention(q, k, v, *, scale: float | None = None, mask=None, kv_lens=None,
+                              order: str = "mfma") -> torch.Tensor:
     """Dispatch: decode path for T_q == 1, prefill otherwise (reference:
-    kernels/attention.py:393-397). ``mask`` is None or "causal"."""
+    kernels/attention.py:393-397). ``mask`` is None or "causal"; ``order`` is
+    "mfma" (matrix cores) or "per_key" (the reference's own order)."""
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     if mask is not None and mask != "causal":
         raise ValueError("batch_invariant_attention: mask must be None or 'causal'")
     if q.shape[2] == 1:
-        return batch_invariant_decode_attention(q, k, v, scale=scale, kv_lens=kv_lens)
+        return batch_invariant_decode_attention(q, k, v, scale=scale, kv_lens=kv_lens, order=order)
     return batch_invariant_prefill_attention(q, k, v, scale=scale, causal=(mask == "causal"),
-                                             kv_lens=kv_lens)
+                                             kv_lens=kv_lens, order=order)
 
 
 def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=None, *, scale: float | None = None,

@@ -58,6 +58,7 @@ _orig_sdpa = F.scaled_dot_product_attention
 handled: Counter = Counter()
 fallbacks: Counter = Counter()
 strict: bool = False
+attention_order: str = "mfma"   # "per_key": the reference's own attention order
 
 
 def _fallback(op: str, reason: str):
@@ -267,7 +268,7 @@ def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.
         if _attn.supports(q, k, v, mask):
             handled["sdpa_decode" if q.shape[2] == 1 else "sdpa_prefill"] += 1
             sc = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
-            return batch_invariant_attention(q, k, v, scale=sc, mask=mask)
+            return batch_invariant_attention(q, k, v, scale=sc, mask=mask, order=attention_order)
     if isinstance(attn_mask, torch.Tensor) and not (mask_ok and isinstance(attn_mask, _CausalBias)):
         reason = "array-mask"
     elif ok and not _on_gpu(q, k, v):

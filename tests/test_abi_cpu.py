@@ -112,6 +112,13 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert "static scratch" in _err(lib)
     bad = (ctypes.c_int64 * 9)(*([3] * 9))
     assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 5, 10, 128, bad, 0, 1.0, 2, None) == -1
+    # the per-key order entry points share the validation
+    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 80, strides, 1.0, 2, p, 1 << 20, None) == -2
+    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 128, strides, 1.0, 2, None, 0, None) == -3
+    assert "bi_attn_decode_per_key" in _err(lib)
+    assert lib.bi_attn_prefill_per_key(p, p, p, None, p, 1, 4, 4, 20, 10, 128, strides, 1, 1.0, 2, None) == -1
+    assert lib.bi_attn_prefill_per_key(p, p, p, None, p, 1, 4, 4, 5, 10, 128, bad, 0, 1.0, 2, None) == -1
+    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 0, 4, 4, 10, 128, strides, 1.0, 2, None, 0, None) == 0
 
 
 @pytest.mark.parametrize("name", ["matmul", "rmsnorm", "quantized", "attention"])

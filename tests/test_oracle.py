@@ -304,6 +304,73 @@ def test_attention_one_hot_v_gives_softmax_probabilities():
     assert np.abs(got - p / p.sum()).max() < 1e-6
 
 
+def _exp_correctly_rounded(x: float) -> np.float32:
+    """exp(x) from 40-digit decimal arithmetic, rounded to float32 by
+    comparing with the neighbours' midpoints exactly."""
+    import decimal
+    with decimal.localcontext() as ctx:
+        ctx.prec = 40
+        e = decimal.Decimal(float(x)).exp()
+        f = np.float32(float(e))
+        for cand in (np.nextafter(f, np.float32(0)), np.nextafter(f, np.float32(np.inf))):
+            if abs(decimal.Decimal(float(cand)) - e) < abs(decimal.Decimal(float(f)) - e):
+                f = cand
+        return f
+
+
+def test_exp_f32_is_correctly_rounded():
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([
+        -np.abs(rng.standard_normal(3000).astype(np.float32)) * np.float32(20),   # softmax arguments (<= 0)
+        rng.uniform(-103, 88, 1000).astype(np.float32),
+        np.float32([0.0, -0.0, 1e-8, -1e-8, -87.3, -103.0, 88.7, 0.5, -0.5, 1.0]),
+    ]).astype(np.float32)
+    got = ora.exp_f32(xs)
+    want = np.array([_exp_correctly_rounded(x) for x in xs], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert ora.exp_f32(np.float32(-np.inf)) == 0.0
+
+
+def test_attention_scores_fold_lanes_with_the_xor_butterfly():
+    """Lane partials 2^24 (lane 0) and 1 (lanes 8, 16, 24): the butterfly adds
+    lane 16 to lane 0 first (2^24 + 1 rounds to 2^24, ties to even), lanes 8 +
+    24 = 2, then 2^24 + 2 — exact. A left-to-right sum would give 2^24; the
+    exact sum is 2^24 + 3."""
+    D = 32
+    q = np.ones((1, D), np.float32)
+    k = np.zeros((1, D), np.float32)
+    k[0, 0], k[0, 8], k[0, 16], k[0, 24] = 2.0 ** 24, 1.0, 1.0, 1.0
+    assert ora._scores(q, k, 1.0)[0, 0] == np.float32(2.0 ** 24 + 2)
+
+
+def test_attention_scores_lane_owns_contiguous_dims():
+    """D = 128: lane l owns dims [4 l, 4 l + 4), accumulated by an fma chain.
+    Dims 0..3 = 2^24, 1, 1, 1 stay in lane 0 (2^24 + 1 -> 2^24 three times:
+    score 2^24); with dims strided over lanes (d -> lane d % 32) the
+    butterfly would pair them and give 2^24 + 2."""
+    D = 128
+    q = np.ones((1, D), np.float32)
+    k = np.zeros((1, D), np.float32)
+    k[0, :4] = [2.0 ** 24, 1.0, 1.0, 1.0]
+    assert ora._scores(q, k, 1.0)[0, 0] == np.float32(2.0 ** 24)
+    # the same four values placed one per lane (dims 0, 4, 8, 12 -> lanes 0..3)
+    k2 = np.zeros((1, D), np.float32)
+    k2[0, [0, 4, 8, 12]] = [2.0 ** 24, 1.0, 1.0, 1.0]
+    assert ora._scores(q, k2, 1.0)[0, 0] == np.float32(2.0 ** 24 + 2)
+
+
+def test_attention_split_merge_of_equal_scores_is_exact():
+    """All scores equal (q = 0): every exp argument is 0, so l counts keys and
+    acc sums V exactly (small integers) in every split; the merge then adds the
+    splits' counts and sums exactly, across 3 splits and a partial one."""
+    L = 3 * 256 + 17
+    q = np.zeros((1, 1, 1, 64), np.float32)
+    k = np.random.default_rng(3).standard_normal((1, 1, L, 64)).astype(np.float32)
+    v = np.random.default_rng(4).integers(-3, 4, size=(1, 1, L, 64)).astype(np.float32)
+    out = ora.attention(q, k, v, 0.7, False, "f32")
+    assert np.array_equal(out[0, 0, 0], (v[0, 0].sum(0) / np.float32(L)).astype(np.float32))
+
+
 def test_attention_kv_lens_and_causal_structure():
     q, k, v = _qkv(2, 4, 2, 5, 300, 64, 9)
     lens = [300, 120]
