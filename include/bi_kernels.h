@@ -211,25 +211,30 @@ int bi_attn_prefill_paged(const void* q, const void* k_pages, const void* v_page
                           float scale, int dtype, void* stream);
 
 /* ---- Attention in the reference's per-key order ----------------------------
- * Same arguments, workspace, validation and invariance properties as
- * bi_attn_decode / bi_attn_prefill, in the reference kernels' own order of
+ * The arguments, validation and invariance properties of bi_attn_decode /
+ * bi_attn_prefill plus split_size, in the reference kernels' own order of
  * operations instead of the matrix-core order: q pre-scaled in fp32, score =
  * 32 lane partials of D/32 dims (fma chains) folded by an xor butterfly
- * 16..1, the online softmax key by key inside each split (m' = max(m, s);
- * corr = exp(m - m'); p = exp(s - m'); l = fma(l, corr, p); acc = fma(acc,
- * corr, p v)), the same left-to-right split merge in base e, out = T(A / L).
- * exp is fp32 rounded once from double precision. Slower (vector ALUs, one
- * key at a time); for callers that need the reference order's values.
- * Replaces: kernels/attention.py:87-147 + :149-171 (decode + combine) and
- * :173-254 (prefill), order of operations :1-32, :47-85. */
+ * 16..1, the online softmax key by key inside each split of split_size keys
+ * (m' = max(m, s); corr = exp(m - m'); p = exp(s - m'); l = fma(l, corr, p);
+ * acc = fma(acc, corr, p v)), splits merged left to right in base e, out =
+ * T(A / L). exp is fp32 rounded once from double precision. split_size is any
+ * key count in [1, 2^20] (the reference's split_size; 256 is BI_SPLIT_KEYS);
+ * decode's workspace comes from bi_attn_decode_per_key_workspace_bytes.
+ * Slower (vector ALUs, one key at a time); for callers that need the
+ * reference order's values.
+ * Replaces: kernels/attention.py:326-365 (decode, split_size), :87-147 +
+ * :149-171 (kernels), :368-390 and :173-254 (prefill); order of operations
+ * :1-32, :47-85. */
+size_t bi_attn_decode_per_key_workspace_bytes(int64_t B, int64_t Hq, int64_t L, int64_t D, int64_t split_size);
 int bi_attn_decode_per_key(const void* q, const void* k, const void* v, const int32_t* kv_lens,
                            void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
-                           const int64_t* strides, float scale, int dtype, void* ws,
+                           const int64_t* strides, float scale, int64_t split_size, int dtype, void* ws,
                            size_t ws_bytes, void* stream);
 int bi_attn_prefill_per_key(const void* q, const void* k, const void* v, const int32_t* kv_lens,
                             void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
-                            int64_t D, const int64_t* strides, int causal, float scale, int dtype,
-                            void* stream);
+                            int64_t D, const int64_t* strides, int causal, float scale, int64_t split_size,
+                            int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -59,13 +59,32 @@ int check_attn_shape(const char* what, int64_t B, int64_t Hq, int64_t Hkv, int64
 
 }  // namespace
 
-extern "C" size_t bi_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t L, int64_t D) {
-  if (B <= 0 || Hq <= 0 || L <= 0 || D <= 0) return 0;
-  const int64_t ns = (L + bi::kSplit - 1) / bi::kSplit;
+namespace {
+
+// pm | pl | pacc | item counter (16 bytes), each 16-byte aligned, for splits of
+// `split` keys.
+size_t decode_ws_bytes(int64_t B, int64_t Hq, int64_t L, int64_t D, int64_t split) {
+  if (B <= 0 || Hq <= 0 || L <= 0 || D <= 0 || split <= 0) return 0;
+  const int64_t ns = (L + split - 1) / split;
   const int64_t bh = B * Hq * ns;
-  // pm | pl | pacc | item counter (16 bytes), each 16-byte aligned
   auto up = [](int64_t x) { return (x + 3) / 4 * 4; };
   return (size_t)(up(bh) * 2 + bh * D + 4) * sizeof(float);
+}
+
+// Split sizes the per-key kernels take (the reference's split_size): any
+// positive key count up to 2^20.
+constexpr int64_t kMaxSplit = (int64_t)1 << 20;
+
+}  // namespace
+
+extern "C" size_t bi_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t L, int64_t D) {
+  return decode_ws_bytes(B, Hq, L, D, bi::kSplit);
+}
+
+extern "C" size_t bi_attn_decode_per_key_workspace_bytes(int64_t B, int64_t Hq, int64_t L, int64_t D,
+                                                         int64_t split_size) {
+  if (split_size <= 0 || split_size > kMaxSplit) return 0;
+  return decode_ws_bytes(B, Hq, L, D, split_size);
 }
 
 namespace {
@@ -94,12 +113,15 @@ int check_pages(const char* what, const int32_t* table, int64_t table_stride, in
 int decode_impl(const char* what, const void* q, const void* k, const void* v, const int32_t* kv_lens, void* out,
                 int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D, const int64_t* strides, float scale,
                 int dtype, void* ws, size_t ws_bytes, void* stream, const int32_t* table, int64_t table_stride,
-                int page_shift, int64_t num_pages, bool per_key = false) {
+                int page_shift, int64_t num_pages, bool per_key = false, int64_t split = bi::kSplit) {
   using namespace bi_host;
+  if (per_key && (split <= 0 || split > kMaxSplit))
+    return fail(BI_E_INVALID_ARG, "%s: split_size %lld must be in [1, 2^20]", what, (long long)split);
+  if (L > 0x7fffffffLL - split) return fail(BI_E_UNSUPPORTED, "%s: L + split_size exceeds 2^31", what);
   if (B == 0) return BI_OK;
   if (!q || !k || !v || !out || !strides)
     return fail(BI_E_INVALID_ARG, "%s: null pointer argument", what);
-  const size_t need = bi_attn_decode_workspace_bytes(B, Hq, L, D);
+  const size_t need = decode_ws_bytes(B, Hq, L, D, split);
   if (!ws || ws_bytes < need)
     return fail(BI_E_WORKSPACE, "%s: workspace of %zu bytes required, got %zu", what, need,
                 ws ? ws_bytes : (size_t)0);
@@ -114,7 +136,8 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
   a.q = q; a.k = k; a.v = v; a.kv_lens = kv_lens; a.out = out;
   a.table = table; a.table_stride = table_stride; a.page_shift = page_shift; a.num_pages = (int)num_pages;
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.L = (int)L;
-  a.nsplit = (int)((L + bi::kSplit - 1) / bi::kSplit);
+  a.split = (int)split;
+  a.nsplit = (int)((L + split - 1) / split);
   const int G = (int)(Hq / Hkv);
   a.GU = per_key ? bi::perkey_decode_nq(B, (int)Hq, (int)Hkv, a.nsplit) : bi::decode_gu(G);
   a.nchunk = G / a.GU;
@@ -149,8 +172,12 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
 int prefill_impl(const char* what, const void* q, const void* k, const void* v, const int32_t* kv_lens,
                  void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L, int64_t D,
                  const int64_t* strides, int causal, float scale, int dtype, void* stream, const int32_t* table,
-                 int64_t table_stride, int page_shift, int64_t num_pages, bool per_key = false) {
+                 int64_t table_stride, int page_shift, int64_t num_pages, bool per_key = false,
+                 int64_t split = bi::kSplit) {
   using namespace bi_host;
+  if (per_key && (split <= 0 || split > kMaxSplit))
+    return fail(BI_E_INVALID_ARG, "%s: split_size %lld must be in [1, 2^20]", what, (long long)split);
+  if (L > 0x7fffffffLL - split) return fail(BI_E_UNSUPPORTED, "%s: L + split_size exceeds 2^31", what);
   if (Tq <= 0) return fail(BI_E_INVALID_ARG, "%s: Tq=%lld", what, (long long)Tq);
   if (causal && Tq > L)
     return fail(BI_E_INVALID_ARG, "%s: causal needs Tq (%lld) <= L (%lld)", what, (long long)Tq, (long long)L);
@@ -177,6 +204,7 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
   a.v_sb = strides[6]; a.v_sh = strides[7]; a.v_sl = strides[8];
   a.scale_log2 = scale * bi::kLog2e;
   a.scale = scale;
+  a.split = (int)split;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define BI_PRE(TY)                                                                                            \
   return bi::with_head_dim((int)D, [&](auto dd) {                                                           \
@@ -243,26 +271,26 @@ extern "C" int bi_attn_prefill_paged(const void* q, const void* k_pages, const v
                       causal, scale, dtype, stream, block_table, table_stride, shift, num_pages);
 }
 
-// The reference's per-key order (bi_attn_perkey.h): same arguments, workspace
-// and validation as bi_attn_decode / bi_attn_prefill.
+// The reference's per-key order (bi_attn_perkey.h): the arguments of
+// bi_attn_decode / bi_attn_prefill plus the split size.
 extern "C" int bi_attn_decode_per_key(const void* q, const void* k, const void* v, const int32_t* kv_lens,
                                       void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
-                                      const int64_t* strides, float scale, int dtype, void* ws, size_t ws_bytes,
-                                      void* stream) {
+                                      const int64_t* strides, float scale, int64_t split_size, int dtype, void* ws,
+                                      size_t ws_bytes, void* stream) {
   int rc = check_attn_shape("bi_attn_decode_per_key", B, Hq, Hkv, L, D);
   if (rc) return rc;
   return decode_impl("bi_attn_decode_per_key", q, k, v, kv_lens, out, B, Hq, Hkv, L, D, strides, scale, dtype, ws,
-                     ws_bytes, stream, nullptr, 0, 0, 0, true);
+                     ws_bytes, stream, nullptr, 0, 0, 0, true, split_size);
 }
 
 extern "C" int bi_attn_prefill_per_key(const void* q, const void* k, const void* v, const int32_t* kv_lens,
                                        void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
-                                       int64_t D, const int64_t* strides, int causal, float scale, int dtype,
-                                       void* stream) {
+                                       int64_t D, const int64_t* strides, int causal, float scale,
+                                       int64_t split_size, int dtype, void* stream) {
   int rc = check_attn_shape("bi_attn_prefill_per_key", B, Hq, Hkv, L, D);
   if (rc) return rc;
   return prefill_impl("bi_attn_prefill_per_key", q, k, v, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides, causal,
-                      scale, dtype, stream, nullptr, 0, 0, 0, true);
+                      scale, dtype, stream, nullptr, 0, 0, 0, true, split_size);
 }
 
 // ---------------------------------------------------------------------------

@@ -57,6 +57,7 @@ struct DecodeArgs {
   int64_t q_sb, q_sh, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
   float scale_log2;  // scale * log2(e), rounded once on the host
   float scale;       // the caller's scale (per-key order)
+  int split;         // keys per split (per-key order; the matrix-core kernels use kSplit)
   // Paged K/V (null table = contiguous): see kv_row_off.
   const int32_t* table;
   int64_t table_stride;
@@ -74,6 +75,7 @@ struct PrefillArgs {
   int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl;
   float scale_log2;
   float scale;
+  int split;
   const int32_t* table;
   int64_t table_stride;
   int page_shift;

@@ -14,7 +14,8 @@
 //   inside a split, key by key for the active keys:
 //     m' = max(m, s); corr = exp(m - m'); p = exp(s - m');
 //     l = fma(l, corr, p); acc[d] = fma(acc[d], corr, p * v[d]); m = m';
-//   splits of 256 keys merged left to right from M = -inf, L = 0, A = 0:
+//   splits of a.split keys (256 unless the caller picks another size, as the
+//   reference's split_size) merged left to right from M = -inf, L = 0, A = 0:
 //     M' = max(M, m); c_old = exp(M - M'); c_new = exp(m - M');
 //     L = fma(L, c_old, l * c_new); A[d] = fma(A[d], c_old, acc[d] * c_new);
 //   out[d] = T(A[d] / L) (IEEE division; 0 for a row that sees no key).
@@ -134,7 +135,7 @@ __global__ __launch_bounds__(256) void attn_decode_perkey(DecodeArgs a) {
   const int b = (int)(u / a.Hkv);
   const int h0 = hk * (a.Hq / a.Hkv) + chunk * NQ;
   const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
-  const int j0 = split * kSplit, j1 = min(len, j0 + kSplit);
+  const int j0 = split * a.split, j1 = min(len, j0 + a.split);
   if (j0 >= j1) return;
   float qs[NQ][DL], m[NQ], l[NQ], acc[NQ][DL];
   int nkeys[NQ];
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(256) void attn_combine_perkey(DecodeArgs a) {
   const int d = (int)(gid % D);
   const int b = (int)(bh / a.Hq);
   const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
-  const int ns = (len + kSplit - 1) / kSplit;
+  const int ns = (len + a.split - 1) / a.split;
   float M = -INFINITY, Ls = 0.0f, A = 0.0f;
   for (int i = 0; i < ns; ++i) {
     const int64_t po = bh * a.nsplit + i;
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(256) void attn_prefill_perkey(PrefillArgs a) {
 #pragma unroll
     for (int d = 0; d < DL; ++d) A[iq][d] = 0.0f;
   }
-  for (int j0 = 0; j0 < nmax; j0 += kSplit) {
+  for (int j0 = 0; j0 < nmax; j0 += a.split) {
     float m[QB], l[QB], acc[QB][DL];
 #pragma unroll
     for (int iq = 0; iq < QB; ++iq) {
@@ -224,7 +225,7 @@ __global__ __launch_bounds__(256) void attn_prefill_perkey(PrefillArgs a) {
 #pragma unroll
       for (int d = 0; d < DL; ++d) acc[iq][d] = 0.0f;
     }
-    pk_span<T, DL, QB>(a, b, hk, lane, j0, min(nmax, j0 + kSplit), qs, nkeys, m, l, acc);
+    pk_span<T, DL, QB>(a, b, hk, lane, j0, min(nmax, j0 + a.split), qs, nkeys, m, l, acc);
 #pragma unroll
     for (int iq = 0; iq < QB; ++iq)
       if (j0 < nkeys[iq]) pk_merge<DL>(M[iq], Ls[iq], A[iq], m[iq], l[iq], acc[iq]);

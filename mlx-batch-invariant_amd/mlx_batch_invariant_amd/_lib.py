@@ -55,12 +55,13 @@ _SIGNATURES = {
     "bi_attn_prefill": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                        _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_float,
                                        ctypes.c_int, _vp]),
+    "bi_attn_decode_per_key_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64, _c_i64, _c_i64]),
     "bi_attn_decode_per_key": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
-                                              ctypes.POINTER(_c_i64), ctypes.c_float, ctypes.c_int, _vp,
+                                              ctypes.POINTER(_c_i64), ctypes.c_float, _c_i64, ctypes.c_int, _vp,
                                               ctypes.c_size_t, _vp]),
     "bi_attn_prefill_per_key": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                                _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int, ctypes.c_float,
-                                               ctypes.c_int, _vp]),
+                                               _c_i64, ctypes.c_int, _vp]),
     "bi_attn_decode_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                               ctypes.POINTER(_c_i64), ctypes.c_float, ctypes.c_int, _vp]),
     "bi_attn_decode_paged": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64,

@@ -32,6 +32,9 @@ lane partials of D/32 dims folded by an xor butterfly, the softmax recurrence
 key by key inside each split, splits merged in base e, exp rounded once from
 float64): the same invariance properties, values equal to the reference
 order's bit for bit, on the vector ALUs and so slower. Contiguous K/V only.
+Those kernels take the reference's ``split_size`` keyword too (any split of
+1 .. 2^20 keys; a split size fixes the reduction order, so it is part of the
+result): ``split_size != 256`` runs them.
 
 ``kv_lens`` (int32 [B], optional) is an extension the reference does not have:
 sequence b uses only its first ``kv_lens[b]`` keys, and its output is bit-for-bit
@@ -101,24 +104,32 @@ def _lens(kv_lens, B: int, L: int, device) -> torch.Tensor | None:
     return kl
 
 
-def _check_split(split_size: int) -> None:
-    if split_size != SPLIT_SIZE:
-        raise ValueError(f"split_size is a contract constant ({SPLIT_SIZE}); got {split_size}")
+MAX_SPLIT = 1 << 20
 
 
-def _check_order(order: str) -> bool:
-    """True for the reference's per-key order, False for the matrix-core order."""
+def _per_key(order, split_size) -> bool:
+    """Which kernels run: the reference's per-key order (True) or the
+    matrix-core order (False). ``order=None`` picks the matrix-core kernels for
+    the contract split of 256 keys and the per-key kernels for any other
+    ``split_size`` (the reference's keyword, kernels/attention.py:326-327,
+    :368-370), whose splits only they take."""
+    if isinstance(split_size, bool) or not isinstance(split_size, int) or not 1 <= split_size <= MAX_SPLIT:
+        raise ValueError(f"split_size must be an int in [1, {MAX_SPLIT}]; got {split_size!r}")
+    if order is None:
+        return split_size != SPLIT_SIZE
     if order not in ORDERS:
         raise ValueError(f"attention order must be one of {ORDERS}; got {order!r}")
+    if order == "mfma" and split_size != SPLIT_SIZE:
+        raise ValueError(f"the matrix-core kernels use {SPLIT_SIZE}-key splits; split_size={split_size} "
+                         "runs with order='per_key'")
     return order == "per_key"
 
 
 def batch_invariant_decode_attention(q, k, v, *, scale: float, split_size: int = SPLIT_SIZE,
-                                     kv_lens=None, order: str = "mfma") -> torch.Tensor:
+                                     kv_lens=None, order: str | None = None) -> torch.Tensor:
     """T_q == 1. Per-split partials (the GU query heads of a kv head share each
     K/V row), then an ordered combine (reference: kernels/attention.py:326-365)."""
-    _check_split(split_size)
-    per_key = _check_order(order)
+    per_key = _per_key(order, split_size)
     B, Hq, Tq, D = q.shape
     _, Hkv, L, _ = k.shape
     if Tq != 1:
@@ -135,25 +146,31 @@ def batch_invariant_decode_attention(q, k, v, *, scale: float, split_size: int =
     if B == 0:
         return out
     lib = _lib.load()
-    ws_bytes = lib.bi_attn_decode_workspace_bytes(B, Hq, L, D)
-    ws = _lib.workspace(ws_bytes, q.device)
     strides = (_lib._c_i64 * 8)(q3.stride(0), q3.stride(1), k.stride(0), k.stride(1), k.stride(2),
                                 v.stride(0), v.stride(1), v.stride(2))
-    name = "bi_attn_decode_per_key" if per_key else "bi_attn_decode"
-    rc = getattr(lib, name)(q3.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
+    if per_key:
+        ws_bytes = lib.bi_attn_decode_per_key_workspace_bytes(B, Hq, L, D, split_size)
+        ws = _lib.workspace(ws_bytes, q.device)
+        rc = lib.bi_attn_decode_per_key(q3.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
+                                        B, Hq, Hkv, L, D, strides, float(scale), split_size, _lib.DTYPE_CODE[dt],
+                                        _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
+        _lib.check(rc, "bi_attn_decode_per_key")
+        return out
+    ws_bytes = lib.bi_attn_decode_workspace_bytes(B, Hq, L, D)
+    ws = _lib.workspace(ws_bytes, q.device)
+    rc = lib.bi_attn_decode(q3.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
                             B, Hq, Hkv, L, D, strides, float(scale), _lib.DTYPE_CODE[dt],
                             _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
-    _lib.check(rc, name)
+    _lib.check(rc, "bi_attn_decode")
     return out
 
 
 def batch_invariant_prefill_attention(q, k, v, *, scale: float, causal: bool,
                                       split_size: int = SPLIT_SIZE, kv_lens=None,
-                                      order: str = "mfma") -> torch.Tensor:
+                                      order: str | None = None) -> torch.Tensor:
     """Any T_q. Blocks of 16 (token, head) rows share each K/V row; same split
     loop and merge as decode (reference: kernels/attention.py:368-390)."""
-    _check_split(split_size)
-    per_key = _check_order(order)
+    per_key = _per_key(order, split_size)
     B, Hq, Tq, D = q.shape
     _, Hkv, L, _ = k.shape
     if D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
@@ -172,27 +189,34 @@ def batch_invariant_prefill_attention(q, k, v, *, scale: float, causal: bool,
     lib = _lib.load()
     strides = (_lib._c_i64 * 9)(q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1),
                                 k.stride(2), v.stride(0), v.stride(1), v.stride(2))
-    name = "bi_attn_prefill_per_key" if per_key else "bi_attn_prefill"
-    rc = getattr(lib, name)(q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
-                            B, Hq, Hkv, Tq, L, D, strides, 1 if causal else 0, float(scale),
-                            _lib.DTYPE_CODE[dt], _lib.stream_of(q))
-    _lib.check(rc, name)
+    if per_key:
+        rc = lib.bi_attn_prefill_per_key(q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
+                                         B, Hq, Hkv, Tq, L, D, strides, 1 if causal else 0, float(scale),
+                                         split_size, _lib.DTYPE_CODE[dt], _lib.stream_of(q))
+        _lib.check(rc, "bi_attn_prefill_per_key")
+        return out
+    rc = lib.bi_attn_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
+                             B, Hq, Hkv, Tq, L, D, strides, 1 if causal else 0, float(scale),
+                             _lib.DTYPE_CODE[dt], _lib.stream_of(q))
+    _lib.check(rc, "bi_attn_prefill")
     return out
 
 
 def batch_invariant_attention(q, k, v, *, scale: float | None = None, mask=None, kv_lens=None,
-                              order: str = "mfma") -> torch.Tensor:
+                              order: str | None = None, split_size: int = SPLIT_SIZE) -> torch.Tensor:
     """Dispatch: decode path for T_q == 1, prefill otherwise (reference:
     kernels/attention.py:393-397). ``mask`` is None or "causal"; ``order`` is
-    "mfma" (matrix cores) or "per_key" (the reference's own order)."""
+    "mfma" (matrix cores), "per_key" (the reference's own order) or None (the
+    matrix cores for split_size 256, else per-key)."""
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     if mask is not None and mask != "causal":
         raise ValueError("batch_invariant_attention: mask must be None or 'causal'")
     if q.shape[2] == 1:
-        return batch_invariant_decode_attention(q, k, v, scale=scale, kv_lens=kv_lens, order=order)
+        return batch_invariant_decode_attention(q, k, v, scale=scale, kv_lens=kv_lens, order=order,
+                                                split_size=split_size)
     return batch_invariant_prefill_attention(q, k, v, scale=scale, causal=(mask == "causal"),
-                                             kv_lens=kv_lens, order=order)
+                                             kv_lens=kv_lens, order=order, split_size=split_size)
 
 
 def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=None, *, scale: float | None = None,

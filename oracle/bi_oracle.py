@@ -487,8 +487,9 @@ def _scores(qrows, krows, scale: float) -> np.ndarray:
     return out
 
 
-def attention(q, k, v, scale: float, causal: bool, dtype: str, kv_lens=None) -> np.ndarray:
-    """q [B, Hq, Tq, D], k/v [B, Hkv, L, D] (float32 values in ``dtype``)."""
+def attention(q, k, v, scale: float, causal: bool, dtype: str, kv_lens=None, split: int = SPLIT) -> np.ndarray:
+    """q [B, Hq, Tq, D], k/v [B, Hkv, L, D] (float32 values in ``dtype``);
+    ``split`` keys per split (the reference's split_size, attention.py:326)."""
     q = np.asarray(q, np.float32)
     k = np.asarray(k, np.float32)
     v = np.asarray(v, np.float32)
@@ -508,13 +509,13 @@ def attention(q, k, v, scale: float, causal: bool, dtype: str, kv_lens=None) -> 
             Mx = np.full(R, -np.inf, np.float32)
             Ls = np.zeros(R, np.float32)
             A = np.zeros((R, D), np.float32)
-            nsplit = -(-int(nkeys.max()) // SPLIT)
+            nsplit = -(-int(nkeys.max()) // split)
             for sp in range(nsplit):
-                j0 = sp * SPLIT
+                j0 = sp * split
                 m = np.full(R, -np.inf, np.float32)
                 l = np.zeros(R, np.float32)
                 acc = np.zeros((R, D), np.float32)
-                for j in range(j0, min(j0 + SPLIT, int(nkeys.max()))):
+                for j in range(j0, min(j0 + split, int(nkeys.max()))):
                     act = j < nkeys
                     sj = s_all[:, j]
                     with np.errstate(invalid="ignore", over="ignore"):

@@ -112,16 +112,38 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert "static scratch" in _err(lib)
     bad = (ctypes.c_int64 * 9)(*([3] * 9))
     assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 5, 10, 128, bad, 0, 1.0, 2, None) == -1
-    # the per-key order entry points share the validation
-    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 80, strides, 1.0, 2, p, 1 << 20, None) == -2
-    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 128, strides, 1.0, 2, None, 0, None) == -3
+    # the per-key order entry points share the validation, plus the split size
+    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 80, strides, 1.0, 256, 2, p, 1 << 20,
+                                      None) == -2
+    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 128, strides, 1.0, 256, 2, None, 0, None) == -3
     assert "bi_attn_decode_per_key" in _err(lib)
-    assert lib.bi_attn_prefill_per_key(p, p, p, None, p, 1, 4, 4, 20, 10, 128, strides, 1, 1.0, 2, None) == -1
-    assert lib.bi_attn_prefill_per_key(p, p, p, None, p, 1, 4, 4, 5, 10, 128, bad, 0, 1.0, 2, None) == -1
-    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 0, 4, 4, 10, 128, strides, 1.0, 2, None, 0, None) == 0
+    assert lib.bi_attn_prefill_per_key(p, p, p, None, p, 1, 4, 4, 20, 10, 128, strides, 1, 1.0, 256, 2, None) == -1
+    assert lib.bi_attn_prefill_per_key(p, p, p, None, p, 1, 4, 4, 5, 10, 128, bad, 0, 1.0, 256, 2, None) == -1
+    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 0, 4, 4, 10, 128, strides, 1.0, 256, 2, None, 0, None) == 0
+    for split in (0, -1, (1 << 20) + 1):
+        assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 128, strides, 1.0, split, 2, p, 1 << 20,
+                                          None) == -1
+        assert "split_size" in _err(lib)
+        assert lib.bi_attn_prefill_per_key(p, p, p, None, p, 1, 4, 4, 5, 10, 128, strides, 0, 1.0, split, 2,
+                                           None) == -1
+        assert lib.bi_attn_decode_per_key_workspace_bytes(1, 4, 10, 128, split) == 0
+    # a workspace sized for 256-key splits is too small for 100-key splits
+    need = lib.bi_attn_decode_per_key_workspace_bytes(2, 8, 1000, 128, 100)
+    assert need > lib.bi_attn_decode_workspace_bytes(2, 8, 1000, 128)
+    assert lib.bi_attn_decode_per_key_workspace_bytes(2, 8, 1000, 128, 256) == lib.bi_attn_decode_workspace_bytes(
+        2, 8, 1000, 128)
+    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 2, 8, 2, 1000, 128, strides, 1.0, 100, 2, p, need - 16,
+                                      None) == -3
 
 
-@pytest.mark.parametrize("name", ["matmul", "rmsnorm", "quantized", "attention"])
-def test_product_modules_do_not_import_the_oracle(name):
-    src = (Path(_lib.__file__).parent / "kernels" / f"{name}.py").read_text()
-    assert "oracle" not in src.replace("oracle)", "")
+def test_split_size_routing():
+    """split_size other than 256 runs the per-key kernels (the only ones that
+    take it); asking the matrix-core kernels for it is an error."""
+    from mlx_batch_invariant_amd.kernels.attention import _per_key
+    assert _per_key(None, 256) is False
+    assert _per_key(None, 128) is True
+    assert _per_key("per_key", 256) is True
+    assert _per_key("mfma", 256) is False
+    for bad in [("mfma", 128), (None, 0), (None, 1.5), ("fast", 256), (None, True)]:
+        with pytest.raises(ValueError):
+            _per_key(*bad)

@@ -180,3 +180,31 @@ def test_matrix_core_order_within_stated_error_of_per_key_order():
                         "allowance_abs": atol}
     if OUT.is_dir():
         (OUT / "attn_mfma_vs_per_key.json").write_text(json.dumps(report))
+
+
+@pytest.mark.parametrize("split", [1, 37, 128, 512])
+def test_split_size_equals_oracle_and_keeps_invariance(split):
+    """The reference's split_size keyword (attention.py:326-327, :368-370): any
+    split size runs the per-key kernels, bitwise equal to the oracle at that
+    split, with decode == prefill and chunked == one-shot at the same split."""
+    Hq, Hkv, T, D = 8, 2, 300, 64
+    q, k, v = _qkv(2, Hq, Hkv, T, T, D, "bf16", seed=split)
+    sc = D ** -0.5
+    att = _bi().batch_invariant_attention
+    full = att(q, k, v, scale=sc, mask="causal", split_size=split)
+    want = ora.attention(to_np(q[:1, :, -24:]), to_np(k[:1]), to_np(v[:1]), sc, True, "bf16", split=split)
+    assert_bits_equal(to_np(full[:1, :, -24:]), want, f"prefill split={split}")
+    dec = _bi().batch_invariant_decode_attention(q[:, :, -1:], k, v, scale=sc, split_size=split)
+    assert bits(dec) == bits(full[:, :, -1:])
+    assert_bits_equal(to_np(dec[:1]), ora.attention(to_np(q[:1, :, -1:]), to_np(k[:1]), to_np(v[:1]), sc, False,
+                                                     "bf16", split=split), f"decode split={split}")
+    for t in (0, split - 1, split, T - 2):
+        if 0 <= t < T:
+            d = att(q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1], scale=sc, split_size=split)
+            assert bits(d) == bits(full[:, :, t:t + 1]), t
+    parts = [att(q[:, :, s:e], k[:, :, :e], v[:, :, :e], scale=sc, mask="causal", split_size=split)
+             for s, e in ((0, 90), (90, T))]
+    assert bits(torch.cat(parts, 2)) == bits(full)
+    if split != 256:
+        with pytest.raises(ValueError):
+            att(q, k, v, scale=sc, mask="causal", split_size=split, order="mfma")

@@ -159,10 +159,15 @@ def test_direct_kernel_calls_reject_cpu_tensors():
         bi.batch_invariant_rms_norm(torch.randn(2, 8), None, 1e-6)
 
 
-def test_split_size_is_a_contract_constant():
+def test_split_size_other_than_256_needs_the_per_key_order():
+    """split_size is the reference's keyword: the per-key kernels take any
+    size; the matrix-core kernels only the contract's 256, and an invalid size
+    is rejected before any device check."""
     q = torch.randn(1, 2, 1, 64)
-    with pytest.raises(ValueError, match="contract constant"):
-        bi.batch_invariant_decode_attention(q, q, q, scale=1.0, split_size=128)
+    with pytest.raises(ValueError, match="matrix-core kernels use 256-key splits"):
+        bi.batch_invariant_decode_attention(q, q, q, scale=1.0, split_size=128, order="mfma")
+    with pytest.raises(ValueError, match="split_size must be"):
+        bi.batch_invariant_prefill_attention(q, q, q, scale=1.0, causal=True, split_size=0)
 
 
 def test_causal_bias_masks_are_not_array_masks():

@@ -371,6 +371,21 @@ def test_attention_split_merge_of_equal_scores_is_exact():
     assert np.array_equal(out[0, 0, 0], (v[0, 0].sum(0) / np.float32(L)).astype(np.float32))
 
 
+@pytest.mark.parametrize("split", [1, 37, 128, 512])
+def test_attention_any_split_size_close_to_float64(split):
+    """The reference's split_size changes the order, not the quantity: every
+    split size stays within fp32 rounding of the float64 softmax, and split
+    sizes at or above the key count give the same bits as one split."""
+    q, k, v = _qkv(1, 4, 2, 3, 300, 64, split)
+    for causal in (False, True):
+        got = ora.attention(q, k, v, 0.125, causal, "f32", split=split)
+        ref = ora.attention_float64(q, k, v, 0.125, causal)
+        assert np.abs(got - ref).max() < 2e-5, (split, causal)
+    if split >= 300:
+        assert np.array_equal(ora.attention(q, k, v, 0.125, False, "f32", split=split),
+                              ora.attention(q, k, v, 0.125, False, "f32", split=300))
+
+
 def test_attention_kv_lens_and_causal_structure():
     q, k, v = _qkv(2, 4, 2, 5, 300, 64, 9)
     lens = [300, 120]
