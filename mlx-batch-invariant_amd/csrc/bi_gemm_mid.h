@@ -55,6 +55,23 @@ template <typename T, int BITS, int GS> struct MidLoads<QuantB<T, BITS, GS>> {
   static constexpr int kMin = QuantB<T, BITS, GS>::kWords / 4 + 2;
 };
 
+// The A ring lives in one __shared__ array per slot, and every access names
+// its slot by a compile-time index: a DS read of one slot then provably does
+// not alias the LDS copies still landing in the others, so the compiler waits
+// only for the counts the kernel asks for (one array indexed by a run-time
+// slot made it wait for every outstanding copy and B load before each
+// group's first read, which serialised the prefetch with the compute).
+#define BI_MID_SLOT(i, BYTES) __shared__ __attribute__((aligned(1024))) char ring##i[NA > i ? (BYTES) : 16];
+#define BI_MID_SLOTS(BYTES)                                                                              \
+  BI_MID_SLOT(0, BYTES) BI_MID_SLOT(1, BYTES) BI_MID_SLOT(2, BYTES) BI_MID_SLOT(3, BYTES)            \
+  BI_MID_SLOT(4, BYTES) BI_MID_SLOT(5, BYTES) BI_MID_SLOT(6, BYTES) BI_MID_SLOT(7, BYTES)            \
+  auto slot = [&](int s_) -> char* {                                                                     \
+    switch (s_) {                                                                                        \
+      case 0: return ring0; case 1: return ring1; case 2: return ring2; case 3: return ring3;            \
+      case 4: return ring4; case 5: return ring5; case 6: return ring6; default: return ring7;           \
+    }                                                                                                    \
+  };
+
 template <typename T, class BSrc, int MT, int PD, int NA, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bsrc, T* __restrict__ out,
                                                 float* __restrict__ part, int M, int N, int K, int G, int CG) {
@@ -69,7 +86,11 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
   // smaller count only waits longer.
   constexpr int kAfter = (NA - 2) * C::kCopiesPerWave + (PD < NA - 1 ? PD : NA - 1) * MidLoads<BSrc>::kMin;
   constexpr int kWaitA = kAfter < 63 ? kAfter : 63;
-  __shared__ __attribute__((aligned(1024))) char As[NA][C::kBufBytes];
+  // Groups run in unrolled rounds of U: slot (group mod NA) and B registers
+  // (group mod PD) are then compile-time indices.
+  constexpr int U = PD > NA ? PD : NA;
+  static_assert(NA <= 8 && U % PD == 0 && U % NA == 0, "gemm_mid: PD and NA powers of two, NA <= 8");
+  BI_MID_SLOTS(C::kBufBytes)
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -81,8 +102,8 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
   const int gb = blockIdx.z * CG;             // the chunk's first group
   const int gn = min(CG, G - gb);             // and its group count (>= 1)
 
-  auto copy_a = [&](int j) {  // chunk group min(j, gn - 1) into buffer j % NA
-    char* buf = As[j % NA];
+  auto copy_a = [&](int j, int sl) {  // chunk group min(j, gn - 1) into slot sl = j % NA
+    char* buf = slot(sl);
     const int gg = gb + min(j, gn - 1);
 #pragma unroll
     for (int i = 0; i < C::kCopiesPerWave; ++i) {
@@ -100,7 +121,7 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
   typename BSrc::Raw raw[PD];
   // Prologue: A of groups 0 .. NA - 2, then B of groups 0 .. PD - 1.
 #pragma unroll
-  for (int g = 0; g < NA - 1; ++g) copy_a(g);
+  for (int g = 0; g < NA - 1; ++g) copy_a(g, g);
   // One fence per group keeps the loads in group order: the scheduler would
   // otherwise batch all codes before all scales, leaving group 0's last, and
   // the wait counts at the loop head would collapse to zero.
@@ -111,16 +132,17 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
   }
   asm volatile("" ::: "memory");
 
-  // One chunk group l: wait for its A, request A of group l + NA - 1,
-  // compute, fold (or store the partial), request B of group l + PD into the
-  // registers it released.
-  auto group = [&](int l, int j) {
+  // One chunk group l (u = l mod U): wait for its A, request A of group
+  // l + NA - 1, compute, fold (or store the partial), request B of group
+  // l + PD into the registers it released.
+  auto group = [&](int l, int u) {
+    const int j = u % PD;
     // Group l's A landed for every wave; every wave is past group l - 1,
     // whose buffer now takes group l + NA - 1.
     stage_barrier<kWaitA>();
-    copy_a(l + NA - 1);
+    copy_a(l + NA - 1, (u + NA - 1) % NA);
     asm volatile("" ::: "memory");
-    const char* buf = As[l % NA];
+    const char* buf = slot(u % NA);
     f32x4 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -162,16 +184,16 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
     bsrc.load_full(raw[j], bl, gb + min(l + PD, gn - 1));
     asm volatile("" ::: "memory");
   };
-  // A whole number of PD-group rounds (padding groups recompute the last group
+  // A whole number of U-group rounds (padding groups recompute the last group
   // and are not folded), the first one peeled: the loop body then has no
   // branch around memory instructions and the loop is entered from a state
   // shaped like its own back edge, so the compiler's wait counts stay exact.
-  const int Gp = (gn + PD - 1) / PD * PD;
+  const int Gp = (gn + U - 1) / U * U;
 #pragma unroll
-  for (int j = 0; j < PD; ++j) group(j, j);
-  for (int l0 = PD; l0 < Gp; l0 += PD) {
+  for (int u = 0; u < U; ++u) group(u, u);
+  for (int l0 = U; l0 < Gp; l0 += U) {
 #pragma unroll
-    for (int j = 0; j < PD; ++j) group(l0 + j, j);
+    for (int u = 0; u < U; ++u) group(l0 + u, u);
   }
   // The ring's last requests (past the chunk they repeat its last group) are
   // still in flight: drain them before the workgroup's LDS can be reused.
@@ -207,9 +229,11 @@ __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc b
   // and at least min(PD, NA - 1) stages of this wave's B loads).
   constexpr int kAfter = (NA - 2) * kCopiesPerWave + (PD < NA - 1 ? PD : NA - 1) * MidLoads<BSrc>::kMin;
   constexpr int kWaitA = kAfter < 63 ? kAfter : 63;
-  __shared__ __attribute__((aligned(1024))) char As[NA][2][C::kBufBytes];
+  constexpr int U = PD > NA ? PD : NA;  // stages per unrolled round
+  static_assert(NA <= 8 && U % PD == 0 && U % NA == 0, "gemm_mid2: PD and NA powers of two, NA <= 8");
+  BI_MID_SLOTS(2 * C::kBufBytes)        // slot s: groups 2t, 2t + 1 of a stage t = s mod NA
   __shared__ __attribute__((aligned(16))) f32x4 xbuf[2][4][MT][kWave];
-  static_assert(sizeof(As) + sizeof(xbuf) <= 160 * 1024, "gemm_mid2: LDS");
+  static_assert(NA * 2 * C::kBufBytes + sizeof(xbuf) <= 160 * 1024, "gemm_mid2: LDS");
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -223,7 +247,7 @@ __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc b
   const int gn = min(CG, G - gb);           // its group count (>= 1)
   const int ns = (gn + 1) / 2;              // stages
 
-  auto copy_stage = [&](int t) {  // groups 2t, 2t + 1 (clamped to the chunk) into As[t % NA]
+  auto copy_stage = [&](int t, int sl) {  // groups 2t, 2t + 1 (clamped to the chunk) into slot sl = t % NA
 #pragma unroll
     for (int i = 0; i < kCopiesPerWave; ++i) {
       const int ci = wave * kCopiesPerWave + i;
@@ -232,7 +256,7 @@ __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc b
       const int row = cl * C::kRowsPerCopy + lane / (C::kRowBytes / 16);
       const int ch = (lane % (C::kRowBytes / 16)) ^ (row & 15);
       copy_to_lds16(a + (int64_t)min(m0 + row, M - 1) * lda + gg * kGroupK + 8 * ch,
-                    As[t % NA][h] + 1024 * cl);
+                    slot(sl) + h * C::kBufBytes + 1024 * cl);
     }
   };
 
@@ -242,7 +266,7 @@ __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc b
 
   typename BSrc::Raw raw[PD];
 #pragma unroll
-  for (int t = 0; t < NA - 1; ++t) copy_stage(t);
+  for (int t = 0; t < NA - 1; ++t) copy_stage(t, t);
 #pragma unroll
   for (int j = 0; j < PD; ++j) {
     asm volatile("" ::: "memory");
@@ -265,12 +289,13 @@ __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc b
     }
   };
 
-  auto stage = [&](int t, int j) {
+  auto stage = [&](int t, int u) {  // u = t mod U
+    const int j = u % PD;
     stage_barrier<kWaitA>();
     fold_stage(t - 1);
-    copy_stage(t + NA - 1);
+    copy_stage(t + NA - 1, (u + NA - 1) % NA);
     asm volatile("" ::: "memory");
-    const char* buf = As[t % NA][par];
+    const char* buf = slot(u % NA) + par * C::kBufBytes;
     f32x4 acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -314,12 +339,12 @@ __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc b
     bsrc.load_full(raw[j], bl, gb + min(2 * (t + PD) + par, gn - 1));
     asm volatile("" ::: "memory");
   };
-  const int Sp = (ns + PD - 1) / PD * PD;
+  const int Sp = (ns + U - 1) / U * U;
 #pragma unroll
-  for (int j = 0; j < PD; ++j) stage(j, j);
-  for (int t0 = PD; t0 < Sp; t0 += PD) {
+  for (int u = 0; u < U; ++u) stage(u, u);
+  for (int t0 = U; t0 < Sp; t0 += U) {
 #pragma unroll
-    for (int j = 0; j < PD; ++j) stage(t0 + j, j);
+    for (int u = 0; u < U; ++u) stage(t0 + u, u);
   }
   wait_vm_lgkm0<0>();   // every copy landed and the odd waves' last partials are written
   __syncthreads();
@@ -338,5 +363,8 @@ __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc b
       }
   }
 }
+
+#undef BI_MID_SLOTS
+#undef BI_MID_SLOT
 
 }  // namespace bi

@@ -854,7 +854,9 @@ constexpr int kMidSplitPD = 2;
 // K-interleaved eight-wave kernel (two waves per SIMD); larger grids already
 // put several four-wave workgroups on each CU, where it measured slower.
 constexpr int kMidInterleaveMaxTiles = 320;
-constexpr int kMidInterleavePD = 4;
+// B loads 4 stages ahead, 2 for 64-row blocks (measured at the Llama MLP
+// shape, M = 64: 24.3 against 25.5 us; M = 16 / 32 prefer 4).
+template <int MT> constexpr int mid_interleave_pd() { return MT == 4 ? 2 : 4; }
 template <typename T, class BSrc, int MT, int NA_ONE, int NA_SPLIT>
 static void launch_mid2(const T* a, int64_t lda, const BSrc& bsrc, T* out, float* ws, int M, int N, int K,
                         int G, const MidPlan& p, hipStream_t st) {
@@ -862,7 +864,8 @@ static void launch_mid2(const T* a, int64_t lda, const BSrc& bsrc, T* out, float
   const dim3 grid(ceil_div(N, 64), p.mtiles, p.chunks);
   if (p.chunks == 1 && G >= 2 && (int64_t)grid.x * grid.y <= kMidInterleaveMaxTiles) {
     constexpr int NA2 = MT == 4 ? 2 : 4;
-    gemm_mid2<T, BSrc, MT, kMidInterleavePD, NA2, false><<<grid, 512, 0, st>>>(a, lda, bsrc, out, ws, M, N, K, G, G);
+    gemm_mid2<T, BSrc, MT, mid_interleave_pd<MT>(), NA2, false><<<grid, 512, 0, st>>>(a, lda, bsrc, out, ws, M, N,
+                                                                                      K, G, G);
     return;
   }
   if (p.chunks > 1) {
