@@ -122,12 +122,36 @@ def check(rc: int, what: str) -> None:
         raise kind(f"{what} failed (code {rc}): {msg}")
 
 
+# The current stream of a device as a raw hipStream_t, without building a
+# torch.cuda.Stream object per call (a few microseconds of host time on every
+# eager launch); the public API is the fallback.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+_ws_cache: dict = {}
+
+
+def ws_bytes(query: str, *shape) -> int:
+    """A `bi_*_workspace_bytes` answer, remembered per (query, shape): the
+    sizes are pure functions of the shape, and a dict lookup is cheaper than
+    the foreign call on every eager launch."""
+    key = (query,) + shape
+    n = _ws_cache.get(key)
+    if n is None:
+        if len(_ws_cache) > 4096:
+            _ws_cache.clear()
+        n = _ws_cache[key] = int(getattr(load(), query)(*shape))
+    return n
 
 
 def workspace(nbytes: int, device) -> torch.Tensor | None:

@@ -87,8 +87,9 @@ def _prep(q, k, v):
 
 def _aligned(t: torch.Tensor) -> bool:
     es = t.element_size()
-    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
-            and all((t.stride(i) * es) % 16 == 0 and t.stride(i) >= 0 for i in range(t.ndim - 1)))
+    st = t.stride()
+    return (st[-1] == 1 and t.data_ptr() % 16 == 0
+            and all((s * es) % 16 == 0 and s >= 0 for s in st[:-1]))
 
 
 def _fix(t: torch.Tensor) -> torch.Tensor:
@@ -149,14 +150,14 @@ def batch_invariant_decode_attention(q, k, v, *, scale: float, split_size: int =
     strides = (_lib._c_i64 * 8)(q3.stride(0), q3.stride(1), k.stride(0), k.stride(1), k.stride(2),
                                 v.stride(0), v.stride(1), v.stride(2))
     if per_key:
-        ws_bytes = lib.bi_attn_decode_per_key_workspace_bytes(B, Hq, L, D, split_size)
+        ws_bytes = _lib.ws_bytes("bi_attn_decode_per_key_workspace_bytes", B, Hq, L, D, split_size)
         ws = _lib.workspace(ws_bytes, q.device)
         rc = lib.bi_attn_decode_per_key(q3.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
                                         B, Hq, Hkv, L, D, strides, float(scale), split_size, _lib.DTYPE_CODE[dt],
                                         _lib.ptr(ws), ws_bytes, _lib.stream_of(q))
         _lib.check(rc, "bi_attn_decode_per_key")
         return out
-    ws_bytes = lib.bi_attn_decode_workspace_bytes(B, Hq, L, D)
+    ws_bytes = _lib.ws_bytes("bi_attn_decode_workspace_bytes", B, Hq, L, D)
     ws = _lib.workspace(ws_bytes, q.device)
     rc = lib.bi_attn_decode(q3.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.ptr(kl), out.data_ptr(),
                             B, Hq, Hkv, L, D, strides, float(scale), _lib.DTYPE_CODE[dt],
@@ -266,7 +267,7 @@ def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=No
     vs = (v_pages.stride(0), v_pages.stride(1), v_pages.stride(2))
     if Tq == 1:
         q3 = _fix(q[:, :, 0, :])
-        ws_bytes = lib.bi_attn_decode_workspace_bytes(B, Hq, L, D)
+        ws_bytes = _lib.ws_bytes("bi_attn_decode_workspace_bytes", B, Hq, L, D)
         ws = _lib.workspace(ws_bytes, q.device)
         strides = (_lib._c_i64 * 8)(q3.stride(0), q3.stride(1), *ks, *vs)
         rc = lib.bi_attn_decode_paged(q3.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), table.data_ptr(),

@@ -60,7 +60,7 @@ def matmul_bt(a2: torch.Tensor, bt: torch.Tensor) -> torch.Tensor:
     a2 = _prep_rows(a2, K8)
     bt = _prep_rows(bt, K8)
     lib = _lib.load()
-    ws_bytes = lib.bi_matmul_workspace_bytes(M, N, K8)
+    ws_bytes = _lib.ws_bytes("bi_matmul_workspace_bytes", M, N, K8)
     ws = _lib.workspace(ws_bytes, a2.device)
     rc = lib.bi_matmul(a2.data_ptr(), a2.stride(0), bt.data_ptr(), bt.stride(0), out.data_ptr(),
                        M, N, K8, _lib.DTYPE_CODE[a2.dtype], _lib.ptr(ws), ws_bytes,
@@ -147,7 +147,7 @@ def batch_invariant_bmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     a3 = _prep_batched(a3, K8)
     bt3 = _prep_batched(bt3, K8)
     lib = _lib.load()
-    ws_bytes = lib.bi_matmul_workspace_bytes(M, N, K8)
+    ws_bytes = _lib.ws_bytes("bi_matmul_workspace_bytes", M, N, K8)
     ws = _lib.workspace(ws_bytes, a.device)
     o3 = out.view(Bt, M, N)
     rc = lib.bi_matmul_batched(a3.data_ptr(), a3.stride(0), a3.stride(1), bt3.data_ptr(), bt3.stride(0),

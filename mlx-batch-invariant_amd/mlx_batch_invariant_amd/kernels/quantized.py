@@ -68,17 +68,20 @@ def batch_invariant_quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: t
     if K % group_size or w.shape[1] * (32 // bits) != K:
         raise ValueError(f"shape mismatch: x {tuple(x.shape)}, w {tuple(w.shape)} at {bits} bits")
     dt = x.dtype
-    scales = scales.to(dt).contiguous()
-    biases = biases.to(dt).contiguous()
+    if scales.dtype != dt or not scales.is_contiguous():
+        scales = scales.to(dt).contiguous()
+    if biases.dtype != dt or not biases.is_contiguous():
+        biases = biases.to(dt).contiguous()
     if tuple(scales.shape) != (N, K // group_size) or scales.shape != biases.shape:
         raise ValueError("batch_invariant_quantized_matmul: scales/biases must be [N, K / group_size]")
-    w = w.contiguous()
+    if not w.is_contiguous():
+        w = w.contiguous()
     x2 = _prep_rows(x.reshape(-1, K), K)
     M = x2.shape[0]
     out = torch.empty((M, N), dtype=dt, device=x.device)
     if M > 0:
         lib = _lib.load()
-        ws_bytes = lib.bi_quantized_matmul_workspace_bytes(M, N, K)
+        ws_bytes = _lib.ws_bytes("bi_quantized_matmul_workspace_bytes", M, N, K)
         ws = _lib.workspace(ws_bytes, x.device)
         rc = lib.bi_quantized_matmul(x2.data_ptr(), x2.stride(0), w.data_ptr(), scales.data_ptr(),
                                      biases.data_ptr(), out.data_ptr(), M, N, K, bits, group_size,
