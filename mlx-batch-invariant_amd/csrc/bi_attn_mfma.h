@@ -319,23 +319,34 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
 // ---------------------------------------------------------------------------
 // Prefill: one 256-thread workgroup per (sequence, kv head, 64 (token, head)
 // rows, token-major); wave w owns the 16 rows 16 w .. 16 w + 15 of them (the
-// columns of its score tiles). K and V stream through a ring of three LDS
-// buffers of 64 keys, shared by the four waves: per split, the K chunks (each
-// wave scores its rows against the chunk's 64 keys, scores kept in
-// registers), the split maximum and weights (in registers), then the V
-// chunks (P.V and the weight sum), then the in-register merge. Chunk c + 2 is
-// requested right after the barrier that opens chunk c. Only the chunks the
+// columns of its score tiles). K and V stream through a ring of NBUF LDS
+// buffers of 64 keys (prefill_ring), shared by the four waves: per split, the
+// K chunks (each wave scores its rows against the chunk's 64 keys, scores kept
+// in registers), the split maximum and weights (in registers), then the V
+// chunks (P.V and the weight sum), then the in-register merge. Chunk
+// c + NBUF - 1 is requested right after the barrier that opens chunk c. Only the chunks the
 // workgroup's rows need are loaded (the last split may be short); rows past
 // a row's causal or kv_lens limit are masked.
 // ---------------------------------------------------------------------------
-template <typename T, int D, int MODE>
+// Ring depth of the prefill kernel: 2 chunk buffers (one chunk requested
+// ahead of the one being computed). Measured at the config-4 shape (bf16,
+// D = 128, causal T = 2048), B = 1 / 4 / 16: 0.133 / 0.412 / 1.497 ms with 2
+// buffers against 0.141 / 0.440 / 1.520 with 3 and 0.138 / 0.424 / 1.521 with
+// 5: the smaller ring leaves LDS for more workgroups per CU, and the other
+// resident workgroups hide a chunk's copy better than a deeper ring does.
+template <typename T, int D>
+constexpr int prefill_ring() {
+  return 2;
+}
+
+template <typename T, int D, int MODE, int NBUF = prefill_ring<T, D>()>
 __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   constexpr bool ROWPAGED = MODE == kKvRowPaged;
   typedef typename Frag<T>::type F;
   typedef KVTile<T, D> KV;
   constexpr int CH = 64;                                // keys per chunk
   constexpr int CHB = CH * KV::kRowBytes;               // bytes per chunk
-  constexpr int NBUF = 3 * CHB <= (144 << 10) ? 3 : 2;  // ring depth (2 for fp32 rows of 1 KB)
+  static_assert(NBUF >= 2 && NBUF <= 5 && NBUF * CHB <= (160 << 10), "attn_prefill_mfma: ring depth");
   constexpr int PF = NBUF - 1;                          // chunks requested ahead of the current one
   constexpr int CPW = KV::copies(CH) / 4;               // copy instructions per wave per chunk
   constexpr int NDT = D / 16;
@@ -414,7 +425,12 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
     for (int i = 0; i < CPW; ++i) KV::copy(buf, wave * CPW + i, row, len - key0, lane);
   };
   auto open_chunk = [&](int c) {
-    if (PF == 2 && c + 1 < nchunks) stage_barrier<CPW>();  // chunk c landed; c + 1 may be in flight
+    // Chunk c landed; the min(PF - 1, nchunks - 1 - c) chunks requested after
+    // it may still be in flight (copies complete in issue order).
+    const int ahead = min(PF - 1, nchunks - 1 - c);
+    if (PF >= 4 && ahead >= 3) stage_barrier<3 * CPW>();
+    else if (PF >= 3 && ahead >= 2) stage_barrier<2 * CPW>();
+    else if (PF >= 2 && ahead >= 1) stage_barrier<CPW>();
     else stage_barrier<0>();
     issue(c + PF);                              // every wave is past chunk c - 1: its buffer is free
   };
@@ -429,8 +445,8 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) A[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  issue(0);
-  if (PF == 2) issue(1);
+#pragma unroll
+  for (int c = 0; c < PF; ++c) issue(c);
   int ci = 0;
   // A split entirely below every valid row's key limit needs no per-key mask
   // (the wave's first row has the smallest limit; padding rows past npairs
