@@ -8,7 +8,7 @@ Each function restates one canonical reduction order of the reference,
 mlx-batch-invariant (files cited per function), in the concrete form the
 gfx950 kernels commit to. All arithmetic is float32 unless stated;
 ``fma(a, b, c)`` is emulated exactly (``fma32``: float64 evaluation, with
-the rare float32-midpoint results re-rounded from the exact rational).
+float32-midpoint sums re-rounded by their exact float64 rounding error).
 
 Pinning (how each function is checked, tests/test_oracle.py):
 
@@ -102,30 +102,29 @@ def fma32(a, b, c) -> np.ndarray:
     """fmaf on float32 operands, correctly rounded. a * b of two float32 values
     is exact in float64; adding c rounds once in float64 and the cast to
     float32 rounds again. That second rounding differs from a single one only
-    when the float64 result sits exactly on a float32 rounding midpoint; those
-    (rare) elements are re-rounded from the exact rational value."""
+    when the float64 sum sits exactly on a float32 rounding midpoint: there the
+    float64 rounding error of the sum (recovered exactly by TwoSum) says on
+    which side of the midpoint the exact value lies (zero: an exact tie, which
+    the cast already broke to the even significand)."""
     a = np.asarray(a, np.float32)
     b = np.asarray(b, np.float32)
     c = np.asarray(c, np.float32)
-    r = a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)
+    p = a.astype(np.float64) * b.astype(np.float64)          # exact
+    c64 = c.astype(np.float64)
+    r = p + c64
     f = r.astype(np.float32)
     f64 = f.astype(np.float64)
-    other = np.where(r >= f64, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf)))
-    tie = np.isfinite(r) & (r != f64) & (2 * r == f64 + other.astype(np.float64))
+    with np.errstate(invalid="ignore", over="ignore"):
+        other = np.where(r >= f64, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf)))
+        tie = np.isfinite(r) & (r != f64) & (2 * r == f64 + other.astype(np.float64))
     if np.any(tie):
-        from fractions import Fraction
-        a, b, c = np.broadcast_arrays(a, b, c)
-        f = np.array(f, np.float32, copy=True)
-        other = np.broadcast_to(other, f.shape)
-        for idx in zip(*np.nonzero(np.broadcast_to(tie, f.shape))):
-            exact = Fraction(float(a[idx])) * Fraction(float(b[idx])) + Fraction(float(c[idx]))
-            lo, hi = sorted((float(f[idx]), float(other[idx])))
-            dl, dh = exact - Fraction(lo), Fraction(hi) - exact
-            if dl != dh:
-                f[idx] = np.float32(lo if dl < dh else hi)
-            else:   # exact tie: the even significand
-                even = lo if (np.float32(lo).view(np.uint32) & 1) == 0 else hi
-                f[idx] = np.float32(even)
+        with np.errstate(invalid="ignore", over="ignore"):
+            bp = r - p
+            e = (p - (r - bp)) + (c64 - bp)                   # p + c == r + e exactly (TwoSum)
+        hi = np.maximum(f, other)
+        lo = np.minimum(f, other)
+        fix = np.where(e > 0, hi, lo)
+        f = np.where(tie & (e != 0), fix, f).astype(np.float32)
     return f
 
 

@@ -142,6 +142,29 @@ def test_fma32_matches_exact_rational_rounding():
         assert got[i] == best, i
 
 
+def test_fma32_on_float32_midpoints_matches_exact_rational_rounding():
+    """fp16-valued products land on float32 rounding midpoints often (about 4%
+    here); every such element, and a random sample of the rest, equals the
+    exact rational value rounded to nearest, ties to even."""
+    rng = np.random.default_rng(6)
+    n = 50000
+    a = rng.standard_normal(n).astype(np.float16).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float16).astype(np.float32)
+    c = (rng.standard_normal(n) * 2.0 ** rng.integers(-30, 30, n)).astype(np.float32)
+    got = ora.fma32(a, b, c)
+    r = a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)
+    f = r.astype(np.float32)
+    nb = np.where(r >= f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf)))
+    mid = np.nonzero((r != f.astype(np.float64)) & (2 * r == f.astype(np.float64) + nb.astype(np.float64)))[0]
+    assert len(mid) > 500
+    for i in list(mid[:1500]) + list(rng.integers(0, n, 500)):
+        e = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        g = np.float32(float(e))
+        cands = [g, np.nextafter(g, np.float32(np.inf)), np.nextafter(g, np.float32(-np.inf))]
+        best = min(cands, key=lambda v: (abs(Fraction(float(v)) - e), int(np.float32(v).view(np.uint32) & 1)))
+        assert got[i] == best, i
+
+
 # ---- layer_norm -----------------------------------------------------------------
 
 def _ln_rel(got, ref):
