@@ -89,6 +89,12 @@ int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out
               int64_t M, int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes,
               void* stream);
 
+/* Diagnostic, no counterpart in the reference: the mid- and large-M launch
+ * the policy picks for a 2-byte dense call of this shape (aligned operands):
+ * "big", "tall <BM>x<BN> k<SK> r<ring> c<K chunks>", or "other" (the small-M
+ * and LDS-tile launches). Host only; launch shape never changes bits. */
+const char* bi_matmul_launch(int64_t M, int64_t N, int64_t K);
+
 /* Strided batch of dense matmuls (a [batch][M, K], bt [batch][N, K],
  * out [batch][M, N]; batch strides in elements, 0 broadcasts a or bt): slice i
  * is exactly bi_matmul on the slice's pointers, so its bits equal a 2-D call

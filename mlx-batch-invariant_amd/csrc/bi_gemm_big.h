@@ -47,12 +47,6 @@
 // through the empty resource, i.e. computed with exact-zero fragments, so the
 // last group still runs its eight steps.
 //
-// SPLIT: with too few tiles to fill the chip, workgroup (tile, group g) runs
-// group g alone and writes its raw fp32 partial (0 + acc, which adds nothing:
-// the fold starts from +0) to part[g][m][n]; fold_groups folds the groups in
-// order afterwards. Workgroups of one group sit next to each other in an XCD's
-// run, so they share A rows in its L2.
-//
 // Requirements (checked by the host policy): 2-byte T, K % 64 == 0, rows of
 // A and B 16-byte aligned (lda, ldb % 8 == 0), lda, ldb < 2^22 (a tile's
 // rows are addressed with 32-bit byte offsets).
@@ -77,11 +71,11 @@ constexpr int64_t kBigMaxLd = (int64_t)1 << 22;
 constexpr int kBigMinM = 256;
 constexpr int kBigMinTiles = 96;
 
-template <typename T, bool SPLIT>
+template <typename T>
 __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__ a, int64_t lda,
                                                            const T* __restrict__ bt, int64_t ldb,
-                                                           T* __restrict__ out, float* __restrict__ part,
-                                                           int M, int N, int K, int tiles_m, int tiles_n) {
+                                                           T* __restrict__ out, int M, int N, int K, int tiles_m,
+                                                           int tiles_n) {
   static_assert(sizeof(T) == 2, "gemm_big: 2-byte element types only");
   typedef typename Frag<T>::type F;
   constexpr int TI = kBigTI, TJ = kBigTJ, NT = TI * TJ, NCH = NT / 2;
@@ -89,13 +83,12 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
 
   const int tiles_total = tiles_m * tiles_n;
   const int groups = (K + kGroupK - 1) / kGroupK;
-  const int work = SPLIT ? tiles_total * groups : tiles_total;
+  const int work = tiles_total;
   const int bid = blockIdx.x;
   const int per_xcd = (work + 7) / 8;
   const int w_id = (bid % 8) * per_xcd + bid / 8;
   if (w_id >= work) return;  // uniform per workgroup, before any barrier
-  const int t = SPLIT ? w_id % tiles_total : w_id;
-  const int g0 = SPLIT ? w_id / tiles_total : 0;   // first group of this workgroup
+  const int t = w_id;
   const int span = kBigGroupM * tiles_n;
   const int first_m = (t / span) * kBigGroupM;
   const int gm = min(tiles_m - first_m, kBigGroupM);
@@ -122,18 +115,17 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
   const __amdgpu_buffer_rsrc_t r_none = __builtin_amdgcn_make_buffer_rsrc((void*)a, (short)0, 0, 0x00020000);
   const unsigned voa = (unsigned)(((8 * wave + rr) * lda + 8 * ch) * 2);
   const unsigned vob = (unsigned)(((8 * wave + rr) * ldb + 8 * ch) * 2);
-  // Stage st of this workgroup is k stage kst0 + st of the matrix (64 k, 128
-  // bytes of each row); stages at or past K read as zero.
-  const int kst0 = 4 * g0, kst_valid = K / 64;
+  // Stage st is 64 k (128 bytes of each row); stages at or past K read as zero.
+  const int kst_valid = K / 64;
   auto copy_a = [&](int st, bool real, int c) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(real && kst0 + st < kst_valid ? ra : r_none,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(real && st < kst_valid ? ra : r_none,
                                              (lds_void_t*)(lds + a_row(st, 8 * (c * kBigWaves + wave))),
-                                             16, voa + (unsigned)(c * 8 * kBigWaves * lda * 2), (kst0 + st) * 128, 0, 0);
+                                             16, voa + (unsigned)(c * 8 * kBigWaves * lda * 2), st * 128, 0, 0);
   };
   auto copy_b = [&](int st, bool real, int c) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(real && kst0 + st < kst_valid ? rb : r_none,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(real && st < kst_valid ? rb : r_none,
                                              (lds_void_t*)(lds + b_row(st, 8 * (c * kBigWaves + wave))),
-                                             16, vob + (unsigned)(c * 8 * kBigWaves * ldb * 2), (kst0 + st) * 128, 0, 0);
+                                             16, vob + (unsigned)(c * 8 * kBigWaves * ldb * 2), st * 128, 0, 0);
   };
 
   // Fragment reads: row r of a 16-row block, chunk 4 s + q of step s.
@@ -156,7 +148,7 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
   auto fold = [&](int tt) { total[tt / TJ][tt % TJ] = total[tt / TJ][tt % TJ] + acc[tt / TJ][tt % TJ]; };
   constexpr int kFoldLast = NCH - 1;  // tiles 0 .. kFoldLast-1 fold during a group's last step
 
-  const int nst = SPLIT ? 4 : 4 * groups;  // 4 stages per group
+  const int nst = 4 * groups;  // 4 stages per group
 #pragma unroll
   for (int st = 0; st < 3; ++st) {
 #pragma unroll
@@ -228,10 +220,7 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + 16 * TI * wm + 16 * i + 4 * q + e;
-        if (m < M && n < N) {
-          if constexpr (SPLIT) part[((int64_t)g0 * M + m) * N + n] = total[i][j][e];
-          else out[(int64_t)m * N + n] = to_store<T>(total[i][j][e]);
-        }
+        if (m < M && n < N) out[(int64_t)m * N + n] = to_store<T>(total[i][j][e]);
       }
     }
 }

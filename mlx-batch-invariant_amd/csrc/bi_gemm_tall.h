@@ -38,7 +38,7 @@
 
 namespace bi {
 
-template <int TI, int WM, int WN, int SK>
+template <int TI, int WM, int WN, int SK, int RMAX = 12>
 struct TallCfg {
   static constexpr int kBM = 16 * TI * WM, kBN = 16 * WN;
   static constexpr int kRowElems = SK;                           // elements of a row per stage
@@ -50,7 +50,9 @@ struct TallCfg {
   static constexpr int kCopies = kCopiesA + kCopiesB;            // per wave per stage
   static constexpr int kRowsAlloc = kSlotRows * kCopies;         // B slots past BN land in padding rows
   static constexpr int kStageBytes = kRowsAlloc * SK * 2;
-  static constexpr int kRing = (160 * 1024 / kStageBytes) < 12 ? (160 * 1024 / kStageBytes) : 12;
+  // As deep as LDS allows, capped at RMAX (a smaller ring leaves room for
+  // more resident workgroups per CU).
+  static constexpr int kRing = (160 * 1024 / kStageBytes) < RMAX ? (160 * 1024 / kStageBytes) : RMAX;
   static constexpr int kStagesPerGroup = kGroupK / SK;
   static_assert(SK == 64 || SK == 128, "gemm_tall: 64- or 128-k stages");
   static_assert(WM * WN == 4, "gemm_tall: 4 waves");
@@ -62,12 +64,12 @@ struct TallCfg {
   static __device__ __forceinline__ int slot(int r, int c) { return c ^ (r & (kChunks - 1)); }
 };
 
-template <typename T, int TI, int WM, int WN, int SK, bool SPLIT>
+template <typename T, int TI, int WM, int WN, int SK, bool SPLIT, int RMAX = 12>
 __global__ __launch_bounds__(256) void gemm_tall(const T* __restrict__ a, int64_t lda, const T* __restrict__ bt,
                                                  int64_t ldb, T* __restrict__ out, float* __restrict__ part,
                                                  int M, int N, int K, int G, int CG) {
   static_assert(sizeof(T) == 2, "gemm_tall: 2-byte element types only");
-  typedef TallCfg<TI, WM, WN, SK> C;
+  typedef TallCfg<TI, WM, WN, SK, RMAX> C;
   constexpr int SPG = C::kStagesPerGroup;
   typedef typename Frag<T>::type F;
   constexpr int R = C::kRing;

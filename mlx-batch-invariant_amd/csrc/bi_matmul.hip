@@ -8,17 +8,15 @@
 namespace {
 
 // Group partials [G, M, N] fp32 of the small-M split launch, and of the
-// mid-M launches when they split K (the dense tall tile and large tile, the
-// quantized mid tile; 2-byte types: the query has no dtype and reports the
-// need of either).
+// mid-M launches when they split K (the dense tall tile, the quantized mid
+// tile; 2-byte types: the query has no dtype and reports the need of either).
 size_t split_ws_bytes(int64_t M, int64_t N, int64_t K, bool dense) {
   const int64_t G = (K + bi::kGroupK - 1) / bi::kGroupK;
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const bool small_split = bi::use_split(M, (int)G) && !bi::use_wg(M, (int)G);
   const bool tall_split = dense && bi::tall_plan(M, N, K).chunks > 1;
-  const bool big_split = dense && bi::big_plan(M, N, K).split;
   const bool mid_split = !dense && bi::mid_plan(M, N, K).chunks > 1;
-  if (!small_split && !tall_split && !mid_split && !big_split) return 0;
+  if (!small_split && !tall_split && !mid_split) return 0;
   return (size_t)(G * M * N) * sizeof(float);
 }
 
@@ -60,6 +58,17 @@ static size_t quant_ws_bytes(int64_t M, int64_t N, int64_t K) {
 
 extern "C" size_t bi_quantized_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   return quant_ws_bytes(M, N, K);
+}
+
+extern "C" const char* bi_matmul_launch(int64_t M, int64_t N, int64_t K) {
+  thread_local char name[64];
+  if (M <= 0 || N <= 0 || K <= 0 || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL) return "other";
+  if (bi::big_plan(M, N, K).use) return "big";
+  const bi::TallPlan p = bi::tall_plan(M, N, K);
+  if (!p.use) return "other";
+  const bi::TallShape& t = bi::kTallShapes[p.tile];
+  snprintf(name, sizeof name, "tall %dx%d k%d r%d c%d", t.bm, t.bn, t.sk, t.ring, p.chunks);
+  return name;
 }
 
 extern "C" int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out,

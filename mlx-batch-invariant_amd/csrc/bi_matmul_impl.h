@@ -578,28 +578,18 @@ static inline bool use_split(int64_t M, int G) { return M <= kSplitMMax && G > 1
 // 16-row tile); up to 64 KB of it. Larger K takes the split + fold launch.
 static inline bool use_wg(int64_t M, int G) { return M <= kSplitMMax && G * (M <= 16 ? 1 : 2) <= 64; }
 
-// Dense mid-M launch (bi_gemm_tall.h) for 2-byte types: 16 < M <= 128,
-// K % 64 == 0. The widest column tile that still gives kTallMinTiles
-// workgroups; with too few even at the narrowest, K is split into chunks of
-// groups whose raw partials fold_groups folds. A function of the shape only,
-// so the workspace query and the launch agree.
-constexpr int kTallMinTiles = 200;
-// With at most 4 groups of K a workgroup's fixed costs and the A tile it
-// re-reads dominate: wider column tiles win (Qwen2-0.5B linear [4864, 896],
-// M = 64: 13.8 -> 9.3 us); with more groups they lose (4096 x 4096, M = 64:
-// 18.4 -> 21.6 us).
-constexpr int kTallMinTilesShortK = 100;
-constexpr int kTallMaxM = 128;
 // Dense large tile (bi_gemm_big.h) for 2-byte types, M > 128, K % 64 == 0:
-// fused when it has at least kBigMinTiles tiles of 256 x 128; otherwise, for
-// M <= kBigSplitMaxM and more than one K group, one workgroup per (tile,
-// group) writing raw group partials that fold_groups folds in order. A
+// M > 256 with at least kBigMinTiles tiles of 256 x 128, or at least
+// kBigShortKMinTiles with at most 4 groups of K; 128 < M <= 256 only with
+// kBigMinTiles tiles (fewer take the tall tile, measured faster at every
+// such shape: Qwen2-0.5B [4864, 896] M = 256 12.1 against 16.9 us, [4096,
+// 4096] M = 256 29.8 against 38.6 us with the large tile's K split). A
 // function of the shape only, so the workspace query and the launch agree.
 constexpr int kBigFromM = 129;
 constexpr int kBigShortKMinTiles = 32;
-constexpr int kBigSplitMaxM = 256;
+constexpr int kTallMaxM = 256;
 struct BigPlan {
-  bool use = false, split = false;
+  bool use = false;
   int tiles_m = 0, tiles_n = 0;
 };
 static inline BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
@@ -608,80 +598,130 @@ static inline BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
   p.tiles_m = ceil_div(M, kBigBM);
   p.tiles_n = ceil_div(N, kBigBN);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-  // With at most 4 groups of K a split launch's partial traffic outweighs the
-  // idle CUs of a fused one (Qwen2-0.5B [4864, 896] at M = 256: 38 tiles,
-  // fused 17.5 us, split 22.4 us); with 16 groups the split wins ([4096,
-  // 4096] at M = 256: 32 tiles, 49.8 against 39.1 us).
-  if (tiles >= kBigMinTiles || (K <= 4 * kGroupK && tiles >= kBigShortKMinTiles)) {
-    p.use = true;
-  } else if (M <= kBigSplitMaxM && K > kGroupK) {
-    p.use = true;
-    p.split = true;
-  }
+  p.use = tiles >= kBigMinTiles || (M > kTallMaxM && K <= 4 * kGroupK && tiles >= kBigShortKMinTiles);
   return p;
+}
+
+// Dense mid-M launch (bi_gemm_tall.h) for 2-byte types: 16 < M <= 256,
+// K % 64 == 0, where the large tile is not used. Tile configurations (rows
+// x columns, k per stage, ring cap): a ring of 3-6 stages leaves LDS for 1-3
+// workgroups per CU, which measured faster than one workgroup with the
+// deepest ring at every shape tried (4 waves per workgroup; more workgroups
+// per CU overlap one's waits with another's MFMAs).
+enum TallTile { kT64x64s64, kT64x32, kT64x32s64, kT32x64, kT32x32, kT32x64s64, kT32x32s64, kTallTiles };
+struct TallShape {
+  int bm, bn, sk, ring;
+};
+constexpr TallShape kTallShapes[kTallTiles] = {
+    {64, 64, 64, 4}, {64, 32, 128, 3}, {64, 32, 64, 4}, {32, 64, 128, 4},
+    {32, 32, 128, 4}, {32, 64, 64, 5}, {32, 32, 64, 6}};
+// Workgroups of a configuration one CU holds at once (LDS-bound: the ring of
+// stages of BM + BN rows, A rows in whole copy slots of 4 waves).
+constexpr int tall_occupancy(const TallShape& t) {
+  const int slot_rows = 4 * (64 / (t.sk / 8));
+  const int rows = (t.bm / slot_rows + (t.bn + slot_rows - 1) / slot_rows) * slot_rows;
+  const int per_cu = 160 * 1024 / (t.ring * rows * t.sk * 2);
+  return per_cu < 8 ? per_cu : 8;
 }
 
 struct TallPlan {
   bool use = false;
-  int bm = 0, bn = 0, chunks = 1, cg = 0;
+  int tile = 0, chunks = 1, cg = 0;
 };
+// The choice (a function of the shape only, so the workspace query and the
+// launch agree):
+//   * M <= 32: 32-row tiles, the widest column tile (64, else 32) that gives
+//     kTallMinTiles workgroups (kTallMinTilesShortK for at most 4 groups of
+//     K); with too few even at 32 columns, K is split into chunks of groups.
+//   * 32 < M <= 256: the configuration that comes closest to filling the
+//     chip's workgroup slots (256 CUs x its occupancy) without needing a
+//     second round; ties go to the higher occupancy. When even the best one
+//     fills less than half the slots and K has at least 8 groups, K is split
+//     into 2 or 4 chunks by the same measure.
+// Measured over Llama-3-8B and Qwen2-0.5B dense shapes (M = 32..256): within
+// 2% of the best configuration tried on average, 10-30% faster than one
+// workgroup per CU with the deepest ring.
+constexpr int kTallMinTiles = 200;
+constexpr int kTallMinTilesShortK = 100;
 static inline TallPlan tall_plan(int64_t M, int64_t N, int64_t K) {
   TallPlan p;
-  if (M <= 16 || M > kTallMaxM || K <= 0 || K % 64) return p;
+  if (M <= 16 || M > kTallMaxM || N <= 0 || K <= 0 || K % 64) return p;
+  if (big_plan(M, N, K).use) return p;
   const int G = ceil_div(K, kGroupK);
-  const int min_tiles = G <= 4 ? kTallMinTilesShortK : kTallMinTiles;
-  p.bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
-  const int narrowest = p.bm == 32 ? 32 : 16;
-  for (int bn : {64, 32, 16}) {
-    if (bn < narrowest) break;
-    p.bn = bn;
-    if (ceil_div(N, bn) >= min_tiles) break;
-  }
-  const int64_t t = ceil_div(N, p.bn);
-  p.cg = G;
-  if (t < min_tiles && G > 1) {
-    const int want = std::min<int64_t>(G, ceil_div(min_tiles, t));
+  const bool k128 = K % 128 == 0;
+  auto split = [&](int want) {
     p.cg = ceil_div(G, want);
     p.chunks = ceil_div(G, p.cg);
-  }
+  };
   p.use = true;
+  p.cg = G;
+  if (M <= 32) {
+    const int min_tiles = G <= 4 ? kTallMinTilesShortK : kTallMinTiles;
+    const bool wide = ceil_div(N, 64) >= min_tiles;
+    p.tile = wide ? (k128 ? kT32x64 : kT32x64s64) : (k128 ? kT32x32 : kT32x32s64);
+    const int64_t t = ceil_div(N, wide ? 64 : 32);
+    if (t < min_tiles && G > 1) split((int)std::min<int64_t>(G, ceil_div(min_tiles, t)));
+    return p;
+  }
+  // Fill of a configuration: workgroups / (256 x occupancy); best = the
+  // largest fill <= 1, else the smallest fill above 1; ties: occupancy, then
+  // table order, then fewer chunks.
+  double best_f = -1.0;
+  int best_t = -1, best_c = 1;
+  auto better = [&](double f, int t) {
+    if (best_t < 0) return true;
+    const bool in = f <= 1.0, bin = best_f <= 1.0;
+    if (in != bin) return in;
+    if (f != best_f) return in ? f > best_f : f < best_f;
+    const int occ = tall_occupancy(kTallShapes[t]), bocc = tall_occupancy(kTallShapes[best_t]);
+    if (occ != bocc) return occ > bocc;
+    return t < best_t;
+  };
+  for (int chunks : {1, 2, 4}) {
+    // K is split only when no unsplit configuration fills half the slots.
+    if (chunks > 1 && (G < 8 || G < 2 * chunks || (best_c == 1 && best_f >= 0.5))) break;
+    for (int t = 0; t < kTallTiles; ++t) {
+      const TallShape& s = kTallShapes[t];
+      if (K % s.sk || (s.sk == 64 && k128 && s.bm == 32)) continue;  // 32-row tiles: 64-k stages only for K % 128 != 0
+      const double f = (double)(ceil_div(M, s.bm) * ceil_div(N, s.bn) * chunks) / (256.0 * tall_occupancy(s));
+      if (better(f, t)) {
+        best_f = f;
+        best_t = t;
+        best_c = chunks;
+      }
+    }
+  }
+  p.tile = best_t;
+  if (best_c > 1) split(best_c);
   return p;
 }
 
-template <typename T, int TI, int WM, int WN, int SK>
+template <typename T, int TI, int WM, int WN, int SK, int R>
 static void launch_tall2(const T* a, int64_t lda, const DenseB<T>& b, T* out, float* ws, int M, int N, int K,
                          int G, const TallPlan& p, hipStream_t st) {
   dim3 grid(ceil_div(N, 16 * WN), ceil_div(M, 16 * TI * WM), p.chunks);
   if (p.chunks > 1) {
-    gemm_tall<T, TI, WM, WN, SK, true><<<grid, 256, 0, st>>>(a, lda, b.bt, b.ldb, out, ws, M, N, K, G, p.cg);
+    gemm_tall<T, TI, WM, WN, SK, true, R><<<grid, 256, 0, st>>>(a, lda, b.bt, b.ldb, out, ws, M, N, K, G, p.cg);
     const int64_t MN = (int64_t)M * N;
     fold_groups<T><<<(unsigned)((MN + 255) / 256), 256, 0, st>>>(ws, out, MN, G);
   } else {
-    gemm_tall<T, TI, WM, WN, SK, false><<<grid, 256, 0, st>>>(a, lda, b.bt, b.ldb, out, ws, M, N, K, G, G);
+    gemm_tall<T, TI, WM, WN, SK, false, R><<<grid, 256, 0, st>>>(a, lda, b.bt, b.ldb, out, ws, M, N, K, G, G);
   }
-}
-
-// 128-k stages (256-byte row pieces) when K allows, else 64-k.
-template <typename T, int TI, int WM, int WN>
-static void launch_tall1(const T* a, int64_t lda, const DenseB<T>& b, T* out, float* ws, int M, int N, int K,
-                         int G, const TallPlan& p, hipStream_t st) {
-  if (K % 128 == 0) launch_tall2<T, TI, WM, WN, 128>(a, lda, b, out, ws, M, N, K, G, p, st);
-  else launch_tall2<T, TI, WM, WN, 64>(a, lda, b, out, ws, M, N, K, G, p, st);
 }
 
 template <typename T>
 static void launch_tall(const T* a, int64_t lda, const DenseB<T>& b, T* out, float* ws, int M, int N, int K,
                         int G, const TallPlan& p, hipStream_t st) {
-  const int key = p.bm * 1000 + p.bn;
-  switch (key) {
-    case 32064: launch_tall1<T, 2, 1, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
-    case 32032: launch_tall1<T, 1, 2, 2>(a, lda, b, out, ws, M, N, K, G, p, st); break;
-    case 64064: launch_tall1<T, 4, 1, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
-    case 64032: launch_tall1<T, 2, 2, 2>(a, lda, b, out, ws, M, N, K, G, p, st); break;
-    case 64016: launch_tall1<T, 1, 4, 1>(a, lda, b, out, ws, M, N, K, G, p, st); break;
-    case 128064: launch_tall1<T, 8, 1, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
-    case 128032: launch_tall1<T, 4, 2, 2>(a, lda, b, out, ws, M, N, K, G, p, st); break;
-    default: launch_tall1<T, 2, 4, 1>(a, lda, b, out, ws, M, N, K, G, p, st); break;  // 128 x 16
+  // Template arguments per configuration: TI x WM row blocks of 16, WN
+  // column blocks of 16 (4 waves), SK, ring cap (kTallShapes).
+  switch (p.tile) {
+    case kT64x64s64: launch_tall2<T, 4, 1, 4, 64, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case kT64x32: launch_tall2<T, 2, 2, 2, 128, 3>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case kT64x32s64: launch_tall2<T, 2, 2, 2, 64, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case kT32x64: launch_tall2<T, 2, 1, 4, 128, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case kT32x32: launch_tall2<T, 1, 2, 2, 128, 4>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    case kT32x64s64: launch_tall2<T, 2, 1, 4, 64, 5>(a, lda, b, out, ws, M, N, K, G, p, st); break;
+    default: launch_tall2<T, 1, 2, 2, 64, 6>(a, lda, b, out, ws, M, N, K, G, p, st); break;  // 32 x 32, 64-k
   }
 }
 
@@ -908,19 +948,9 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
     const BigPlan bp = big_plan(M, N, K);
     if (bp.use && lda < kBigMaxLd && bsrc.ldb < kBigMaxLd) {
-      const int work = bp.tiles_m * bp.tiles_n * (bp.split ? G : 1);
-      const int grid = ((work + 7) / 8) * 8;
-      if (bp.split) {
-        gemm_big<T, true><<<grid, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, ws, M, N, K, bp.tiles_m,
-                                                           bp.tiles_n);
-        const int rc = bi_host::launch_status(what);
-        if (rc) return rc;
-        const int64_t MN = (int64_t)M * N;
-        fold_groups<T><<<(unsigned)((MN + 255) / 256), 256, 0, st>>>(ws, out, MN, G);
-      } else {
-        gemm_big<T, false><<<grid, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, nullptr, M, N, K,
-                                                            bp.tiles_m, bp.tiles_n);
-      }
+      const int work = bp.tiles_m * bp.tiles_n;
+      gemm_big<T><<<((work + 7) / 8) * 8, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K,
+                                                                  bp.tiles_m, bp.tiles_n);
       return bi_host::launch_status(what);
     }
     const TallPlan tp = tall_plan(M, N, K);
@@ -981,8 +1011,7 @@ int run_quant(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
       bi::qmm_permute_a<T><<<(unsigned)((na + 255) / 256), 256, 0, st>>>(static_cast<const T*>(x), ldx, ap, M, K);
       const int tmm = ceil_div(M, bi::kBigBM), tn = ceil_div(N, bi::kBigBN);
       const int grid = ((tmm * tn + 7) / 8) * 8;
-      bi::gemm_big<T, false><<<grid, 64 * bi::kBigWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), nullptr, M, N,
-                                                                  K, tmm, tn);
+      bi::gemm_big<T><<<grid, 64 * bi::kBigWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), M, N, K, tmm, tn);
       return bi_host::launch_status("bi_quantized_matmul");
     }
   }

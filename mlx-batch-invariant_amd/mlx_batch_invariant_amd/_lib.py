@@ -41,6 +41,7 @@ _SIGNATURES = {
     "bi_layer_norm": (ctypes.c_int, [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, ctypes.c_float, ctypes.c_int,
                                      _vp]),
     "bi_matmul_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
+    "bi_matmul_launch": (ctypes.c_char_p, [_c_i64, _c_i64, _c_i64]),
     "bi_matmul": (ctypes.c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
                                  _vp, ctypes.c_size_t, _vp]),
     "bi_matmul_batched": (ctypes.c_int, [_vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64,

@@ -36,13 +36,14 @@ def test_workspace_sizes():
     assert lib.bi_matmul_workspace_bytes(32, 100, 896) == 4 * 32 * 100 * 4
     assert lib.bi_matmul_workspace_bytes(1, 100, 65 * 256) == 65 * 1 * 100 * 4   # split + fold
     assert lib.bi_matmul_workspace_bytes(20, 100, 33 * 256) == 33 * 20 * 100 * 4
-    assert lib.bi_matmul_workspace_bytes(33, 100, 896) == 4 * 33 * 100 * 4
+    assert lib.bi_matmul_workspace_bytes(33, 100, 896) == 0          # M > 32 splits only with >= 8 groups
     assert lib.bi_matmul_workspace_bytes(64, 14336, 4096) == 0       # mid-M, enough column tiles
-    assert lib.bi_matmul_workspace_bytes(64, 4096, 14336) == 0       # 16-column tiles fill the chip
+    assert lib.bi_matmul_workspace_bytes(64, 4096, 14336) == 0       # 32 x 32 tiles fill half the chip
     assert lib.bi_matmul_workspace_bytes(64, 1024, 4096) == 16 * 64 * 1024 * 4   # 4 chunks of 4 groups
-    assert lib.bi_matmul_workspace_bytes(129, 100, 896) == 4 * 129 * 100 * 4   # large tile, split per group
-    assert lib.bi_matmul_workspace_bytes(256, 4864, 896) == 0        # 38 tiles, 4 groups: fused
-    assert lib.bi_matmul_workspace_bytes(256, 4096, 4096) == 16 * 256 * 4096 * 4   # 32 tiles, 16 groups: split
+    assert lib.bi_matmul_workspace_bytes(129, 100, 896) == 0         # tall tile, 4 groups: no split
+    assert lib.bi_matmul_workspace_bytes(256, 4864, 896) == 0        # tall tile
+    assert lib.bi_matmul_workspace_bytes(256, 4096, 4096) == 0       # tall tile fills the chip
+    assert lib.bi_matmul_workspace_bytes(200, 768, 2048) == 8 * 200 * 768 * 4    # tall tile, 4 chunks
     assert lib.bi_matmul_workspace_bytes(129, 12800, 896) == 0       # large tile, >= 96 tiles: fused
     assert lib.bi_matmul_workspace_bytes(257, 100, 896) == 0         # fused (LDS tiles)
     assert lib.bi_matmul_workspace_bytes(200, 4864, 900) == 0        # K % 64 != 0: LDS tiles
@@ -66,6 +67,30 @@ def test_workspace_sizes():
     bh = 256 * 32 * ns
     # pm | pl | pacc | 16-byte item counter
     assert lib.bi_attn_decode_workspace_bytes(256, 32, 8192, 128) == (2 * ((bh + 3) // 4 * 4) + bh * 128 + 4) * 4
+
+
+def test_dense_launch_policy():
+    """The dense mid/large-M launch per shape (a diagnostic of the policy; the
+    bits never depend on it): the tall tile up to M = 256 unless the 256 x 128
+    tile has >= 96 tiles, ring-capped configurations chosen by how full they
+    leave the chip's workgroup slots, K split only for long K with too few
+    tiles."""
+    lib = _lib.load()
+    name = lambda M, N, K: lib.bi_matmul_launch(M, N, K).decode()
+    assert name(256, 4864, 896) == "tall 64x32 k64 r4 c1"      # Qwen2-0.5B linear, M = 256
+    assert name(64, 4864, 896) == "tall 32x32 k128 r4 c1"
+    assert name(32, 14336, 4096) == "tall 32x64 k128 r4 c1"     # M <= 32: widest tile with >= 200
+    assert name(32, 4096, 4096) == "tall 32x32 k128 r4 c2"
+    assert name(128, 14336, 4096) == "tall 64x64 k64 r4 c1"
+    assert name(256, 4096, 4096) == "tall 64x32 k128 r3 c1"
+    assert name(192, 896, 4864) == "tall 64x32 k128 r3 c4"
+    assert name(192, 14336, 4096) == "big"                       # 112 tiles of 256 x 128
+    assert name(300, 12416, 960) == "big"
+    assert name(256, 3328, 576) == "tall 32x64 k64 r5 c1"       # K % 128 != 0: 64-k stages
+    assert name(16, 4864, 896) == "other"                        # small-M launches
+    assert name(300, 4096, 4096) == "other"                      # M > 256 with < 96 tiles: LDS tiles
+    assert name(200, 4864, 900) == "other"                       # K % 64 != 0
+    assert name(0, 10, 10) == "other"
 
 
 def _err(lib):

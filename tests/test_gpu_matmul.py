@@ -207,12 +207,11 @@ def test_batched_matmul_intercepted_by_mode():
 
 @pytest.mark.parametrize("M,N,K", [(200, 4864, 896), (256, 4864, 896), (160, 1024, 4096), (129, 12800, 896),
                                    (300, 12416, 960), (256, 4096, 4096)])
-def test_matmul_large_tile_split_and_partial_groups(M, N, K):
-    """M > 128 takes the 256 x 128 tile: fused when there are >= 96 tiles,
-    otherwise one workgroup per (tile, K group) with raw partials folded in
-    order afterwards; K need not be whole groups (stages past K are zero).
-    Sampled rows equal the oracle and the same rows computed alone, bit for
-    bit (the decode launches)."""
+def test_matmul_m_above_128_and_partial_groups(M, N, K):
+    """M > 128: the 256 x 128 tile where it has >= 96 tiles (M > 256: also
+    >= 32 with at most 4 groups of K), the tall tile otherwise; K need not be
+    whole groups (stages past K are zero). Sampled rows equal the oracle and
+    the same rows computed alone, bit for bit (the decode launches)."""
     g = gen(M + N + K)
     W = randn((N, K), torch.bfloat16, g, scale=0.02)
     x = randn((M, K), torch.bfloat16, g)
@@ -222,4 +221,31 @@ def test_matmul_large_tile_split_and_partial_groups(M, N, K):
     want = ora.matmul(to_np(x[rows]), to_np(W)[cols], "bf16")
     assert_bits_equal(to_np(full)[rows][:, cols], want, f"{M}x{N}x{K}")
     for lo, hi in ((0, 1), (M - 1, M), (5, 21), (100, 164)):
+        assert bits(_mm(x[lo:hi], W.t())) == bits(full[lo:hi]), (lo, hi)
+
+
+TALL = [(40, 256, 640, "tall 32x32 k128 r4 c1"), (20, 256, 640, "tall 32x32 k128 r4 c3"),
+        (20, 6400, 640, "tall 32x64 k128 r4 c1"), (256, 2304, 640, "tall 64x32 k128 r3 c1"),
+        (200, 768, 2048, "tall 64x32 k128 r3 c4"), (256, 4352, 576, "tall 64x32 k64 r4 c1"),
+        (200, 1280, 1984, "tall 64x32 k64 r4 c4"), (200, 6400, 576, "tall 64x64 k64 r4 c1"),
+        (256, 3328, 576, "tall 32x64 k64 r5 c1"), (200, 1024, 1984, "tall 32x64 k64 r5 c4"),
+        (40, 256, 576, "tall 32x32 k64 r6 c1"), (20, 256, 832, "tall 32x32 k64 r6 c4")]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("M,N,K,launch", TALL, ids=[t[3].replace(" ", "_") for t in TALL])
+def test_matmul_tall_configurations(dt, M, N, K, launch):
+    """Every configuration of the dense mid-M tile (tile, k per stage, ring
+    depth; unsplit and with K in chunks + the ordered fold), picked by the
+    policy at these shapes: sampled rows equal the oracle and the same rows
+    computed alone (the decode launches), bit for bit."""
+    lib = _bi()._lib.load()
+    assert lib.bi_matmul_launch(M, N, K).decode() == launch
+    g = gen(M * 7 + N + K)
+    W = randn((N, K), DT[dt], g, scale=0.02)
+    x = randn((M, K), DT[dt], g)
+    full = _mm(x, W.t())
+    rows = sorted({0, 15, 16, 31, 32, M // 2, M - 1} & set(range(M)))
+    assert_bits_equal(to_np(full)[rows], ora.matmul(to_np(x[rows]), to_np(W), dt), f"{dt} {launch}")
+    for lo, hi in ((0, 1), (M - 1, M), (3, 19)):
         assert bits(_mm(x[lo:hi], W.t())) == bits(full[lo:hi]), (lo, hi)
