@@ -196,6 +196,8 @@ int bi_attn_decode_paged(const void* q, const void* k_pages, const void* v_pages
  * with causal != 0, Tq <= L is required, and a query row with no visible key
  * (len_b - Tq + t + 1 <= 0) gets an all-zero output. Same split order and per-split arithmetic as bi_attn_decode, so a token's
  * output equals a later decode step's and chunked equals one-shot prefill.
+ * The K and V position strides must stay below 2^24 bytes
+ * (BI_E_UNSUPPORTED otherwise; copy such a layout first).
  * Replaces: kernels/attention.py:368-390 (batch_invariant_prefill_attention),
  * kernels :173-254. */
 int bi_attn_prefill(const void* q, const void* k, const void* v, const int32_t* kv_lens,

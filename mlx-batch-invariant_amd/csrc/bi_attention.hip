@@ -190,6 +190,11 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
                   (long long)strides[i]);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
     return fail(BI_E_INVALID_ARG, "%s: q, k, v, out must be 16-byte aligned", what);
+  // The contiguous-cache kernel addresses the 64 rows of a key chunk with
+  // 32-bit byte offsets.
+  if (!table && !per_key && 64 * std::max(strides[5], strides[8]) * (int64_t)es >= ((int64_t)1 << 30))
+    return fail(BI_E_UNSUPPORTED, "%s: K/V row strides (%lld, %lld elements) must stay below 2^24 bytes", what,
+                (long long)strides[5], (long long)strides[8]);
   const int64_t wgs = (Tq * (Hq / Hkv) + 63) / 64;
   if (wgs > 0x7fffffffLL || Tq * (Hq / Hkv) > 0x7fffffffLL - 64 ||
       (per_key && B * Hq * ((Tq + bi::kPkQB - 1) / bi::kPkQB) > ((int64_t)1 << 27)))

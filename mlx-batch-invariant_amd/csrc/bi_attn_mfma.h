@@ -396,6 +396,24 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   const int last_keys = nsplit > 0 ? maxkeys - (nsplit - 1) * kSplit : 0;
   const int nkc_last = (last_keys + CH - 1) / CH;
   const int nchunks = nsplit > 0 ? 8 * (nsplit - 1) + 2 * nkc_last : 0;
+  // Contiguous cache: a chunk's copies go through a buffer resource whose
+  // base is the chunk's first row and whose range ends at the sequence's last
+  // key, with a per-lane byte offset that is the same for every chunk (the
+  // lane's row of the chunk times the row stride, plus its 16-byte piece of
+  // the row), computed once here: no per-copy address arithmetic. Rows past
+  // the sequence read as zero (their keys are masked and their weights are
+  // exactly 0). The host keeps 64 rows of either stride below 2^30 bytes.
+  int koff[CPW], voff[CPW];
+  if constexpr (MODE == kKvContig) {
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) {
+      const int f = 64 * (wave * CPW + i) + lane;
+      const int rr = f / KV::kCPR, slot = f - rr * KV::kCPR;
+      const int cc = KV::kSwz ? (slot ^ (rr & 7)) : slot;
+      koff[i] = (int)((rr * a.k_sl + cc * (16 / (int)sizeof(T))) * (int64_t)sizeof(T));
+      voff[i] = (int)((rr * a.v_sl + cc * (16 / (int)sizeof(T))) * (int64_t)sizeof(T));
+    }
+  }
   auto issue = [&](int c) {
     if (c >= nchunks) return;
     int sp, kind, kc;
@@ -407,22 +425,33 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
     }
     const int key0 = sp * kSplit + kc * CH;
     const int64_t sl = kind ? a.v_sl : a.k_sl;
-    const T* segp = nullptr;                            // chunks are aligned 64-key segments
-    if constexpr (MODE == kKvContig) {
-      segp = (kind ? vb : kb) + (int64_t)key0 * sl;
-    } else if constexpr (MODE == kKvPaged) {
-      segp = kind ? kv_segment<MODE>(a, vbase, a.v_sb, a.v_sh, sl, b, hk, key0)
-                  : kv_segment<MODE>(a, kbase, a.k_sb, a.k_sh, sl, b, hk, key0);
-    }
-    auto row = [&](int i) {
-      if constexpr (ROWPAGED)
-        return kind ? vbase + kv_row_off(a, a.v_sb, a.v_sh, sl, b, hk, key0 + i)
-                    : kbase + kv_row_off(a, a.k_sb, a.k_sh, sl, b, hk, key0 + i);
-      else return segp + (int64_t)i * sl;
-    };
     char* buf = ring + (c % NBUF) * CHB;
+    if constexpr (MODE == kKvContig) {
+      const int rows = min(CH, len - key0);             // >= 1: chunks start below maxkeys <= len
+      const auto rs = buffer_rsrc((kind ? vb : kb) + (int64_t)key0 * sl, (int)(rows * sl * (int64_t)sizeof(T)));
+      char* dst = buf + 1024 * wave * CPW;
+      if (kind) {
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) KV::copy(buf, wave * CPW + i, row, len - key0, lane);
+        for (int i = 0; i < CPW; ++i) copy_to_lds16(rs, voff[i], dst + 1024 * i);
+      } else {
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) copy_to_lds16(rs, koff[i], dst + 1024 * i);
+      }
+    } else {
+      const T* segp = nullptr;                          // chunks are aligned 64-key segments
+      if constexpr (MODE == kKvPaged) {
+        segp = kind ? kv_segment<MODE>(a, vbase, a.v_sb, a.v_sh, sl, b, hk, key0)
+                    : kv_segment<MODE>(a, kbase, a.k_sb, a.k_sh, sl, b, hk, key0);
+      }
+      auto row = [&](int i) {
+        if constexpr (ROWPAGED)
+          return kind ? vbase + kv_row_off(a, a.v_sb, a.v_sh, sl, b, hk, key0 + i)
+                      : kbase + kv_row_off(a, a.k_sb, a.k_sh, sl, b, hk, key0 + i);
+        else return segp + (int64_t)i * sl;
+      };
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) KV::copy(buf, wave * CPW + i, row, len - key0, lane);
+    }
   };
   auto open_chunk = [&](int c) {
     // Chunk c landed; the min(PF - 1, nchunks - 1 - c) chunks requested after

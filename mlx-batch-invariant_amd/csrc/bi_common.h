@@ -171,6 +171,15 @@ __device__ __forceinline__ void copy_to_lds16(const void* src, void* lds_block) 
   __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)lds_block, 16, 0, 0);
 }
 
+// The same copy through a buffer resource over [base, base + bytes): lane l
+// reads base + voffset (zero past the range) and lands at lds_block + 16 l.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ void copy_to_lds16(__amdgpu_buffer_rsrc_t rs, int voffset, void* lds_block) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t*)lds_block, 16, voffset, 0, 0, 0);
+}
+
 // s_waitcnt vmcnt(N) lgkmcnt(0); the empty asm statements keep the compiler
 // from moving memory accesses across it.
 template <int N>

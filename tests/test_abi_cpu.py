@@ -137,6 +137,10 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert "static scratch" in _err(lib)
     bad = (ctypes.c_int64 * 9)(*([3] * 9))
     assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 5, 10, 128, bad, 0, 1.0, 2, None) == -1
+    # K position stride of 2^24 bytes: the contiguous prefill kernel's 32-bit chunk offsets cannot hold it
+    huge = (ctypes.c_int64 * 9)(*([128] * 5 + [1 << 23] + [128] * 3))
+    assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 5, 10, 128, huge, 0, 1.0, 2, None) == -2
+    assert "2^24 bytes" in _err(lib)
     # the per-key order entry points share the validation, plus the split size
     assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 80, strides, 1.0, 256, 2, p, 1 << 20,
                                       None) == -2
