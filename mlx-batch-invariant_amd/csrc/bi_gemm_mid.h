@@ -72,6 +72,30 @@ template <typename T, int BITS, int GS> struct MidLoads<QuantB<T, BITS, GS>> {
     }                                                                                                    \
   };
 
+// The eight MFMA steps of one group for the MT row blocks: the B fragment of
+// step s dequantized from the raw registers, the A fragments read from LDS one
+// step ahead of their MFMAs, so the reads of step s + 1 are in flight while
+// step s multiplies (Llama MLP shape, 4-bit g64, M = 64: 24.2 -> 22.7 us).
+template <class C, int MT, bool FAST, class BSrc>
+__device__ __forceinline__ void mid_group_steps(const BSrc& bsrc, const typename BSrc::Raw& raw, const char* buf,
+                                                int gc, int q, int kq, int r, f32x4 (&acc)[MT]) {
+  typedef typename BSrc::F F;
+  F af[2][MT];
+  auto read_a = [&](int s, F (&dst)[MT]) {
+    const int ch = (BSrc::a_k(gc, q, s) - gc * kGroupK) / 8;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) dst[i] = *reinterpret_cast<const F*>(buf + C::off(16 * i + r, ch));
+  };
+  read_a(0, af[0]);
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const F bf = bsrc.template frag<true, FAST>(raw, s, kq);
+    if (s + 1 < kSteps) read_a(s + 1, af[(s + 1) & 1]);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[i] = mfma_step(af[s & 1][i], bf, acc[i]);
+  }
+}
+
 template <typename T, class BSrc, int MT, int PD, int NA, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bsrc, T* __restrict__ out,
                                                 float* __restrict__ part, int M, int N, int K, int G, int CG) {
@@ -149,16 +173,7 @@ __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bs
     const int gc = gb + min(l, gn - 1);
     const int kq = BSrc::kbase(gc, q);
     auto steps = [&](auto fast) {
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        const int ch = (BSrc::a_k(gc, q, s) - gc * kGroupK) / 8;
-        const F bf = bsrc.template frag<true, decltype(fast)::value>(raw[j], s, kq);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          const F af = *reinterpret_cast<const F*>(buf + C::off(16 * i + r, ch));
-          acc[i] = mfma_step(af, bf, acc[i]);
-        }
-      }
+      mid_group_steps<C, MT, decltype(fast)::value>(bsrc, raw[j], buf, gc, q, kq, r, acc);
     };
     if (!__any(bsrc.huge_scale(raw[j]))) steps(std::true_type());
     else steps(std::false_type());
@@ -303,16 +318,7 @@ __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc b
     const int gc = gb + gl;
     const int kq = BSrc::kbase(gc, q);
     auto steps = [&](auto fast) {
-#pragma unroll
-      for (int s = 0; s < kSteps; ++s) {
-        const int ch = (BSrc::a_k(gc, q, s) - gc * kGroupK) / 8;
-        const F bf = bsrc.template frag<true, decltype(fast)::value>(raw[j], s, kq);
-#pragma unroll
-        for (int i = 0; i < MT; ++i) {
-          const F af = *reinterpret_cast<const F*>(buf + C::off(16 * i + r, ch));
-          acc[i] = mfma_step(af, bf, acc[i]);
-        }
-      }
+      mid_group_steps<C, MT, decltype(fast)::value>(bsrc, raw[j], buf, gc, q, kq, r, acc);
     };
     if (!__any(bsrc.huge_scale(raw[j]))) steps(std::true_type());
     else steps(std::false_type());
