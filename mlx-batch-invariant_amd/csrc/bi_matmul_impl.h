@@ -765,6 +765,17 @@ static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b
   } else {
     if (G != W * NB) return false;
     typedef GemvStreamCfg<T, BITS, GS, W, NB, MR> C;
+    // More than 64 KB of dynamic LDS (8 rows of A: up to 148 KB) is allowed
+    // explicitly, once per instantiation (a failure leaves the default limit
+    // and no error state behind; the launch then reports its own status).
+    static const bool lds_raised = [] {
+      if (C::lds_bytes(16) <= 65536) return true;
+      const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream<T, BITS, GS, W, NB, MR, PD>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+      if (!ok) (void)hipGetLastError();
+      return ok;
+    }();
+    (void)lds_raised;
     gemv_stream<T, BITS, GS, W, NB, MR, PD><<<dim3(ceil_div(N, 16)), kWave * W, C::lds_bytes(G), st>>>(
         a, lda, b, out, M, N, K, G);
     return true;
