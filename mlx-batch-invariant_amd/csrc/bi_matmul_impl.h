@@ -10,10 +10,16 @@
 //                more than one K group it runs one workgroup per (column
 //                tile, group) and writes the raw fp32 group partial.
 //   fold_groups  out = T(((0 + part[0]) + part[1]) + ...), the split fold.
-//   gemm_big     dense 2-byte types, K % 256 == 0, enough 256 x 128 tiles to
-//                fill the chip: 8 waves, operands copied straight into
-//                swizzled LDS rows through buffer resources, copies and
+//   gemm_big     dense 2-byte types, M > 128, K % 64 == 0, enough 256 x 128
+//                tiles to fill the chip: 8 waves, operands copied straight
+//                into swizzled LDS rows through buffer resources, copies and
 //                fragment reads interleaved with the MFMAs (bi_gemm_big.h).
+//   gemm_tall    dense 2-byte types, 16 < M <= 256 where gemm_big is not
+//                used: one weight stream through a ring-capped LDS ring, 1-3
+//                workgroups per CU (bi_gemm_tall.h).
+//   gemv_stream, gemv_wg, gemm_mid, gemm_mid2
+//                the quantized decode and mid-M launches (bi_gemv_stream.h,
+//                bi_gemm_mid.h) and the workgroup-fold GEMV.
 //   gemm_lds     other M > 32. A BM x BN tile per 256-thread workgroup, K
 //                staged 64 at a time through double-buffered LDS (quantized B
 //                is dequantized while it is staged), all groups folded in
