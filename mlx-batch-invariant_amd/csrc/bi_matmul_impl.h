@@ -626,9 +626,13 @@ constexpr TallShape kTallShapes[kTallTiles] = {
 constexpr int tall_occupancy(const TallShape& t) {
   const int slot_rows = 4 * (64 / (t.sk / 8));
   const int rows = (t.bm / slot_rows + (t.bn + slot_rows - 1) / slot_rows) * slot_rows;
-  const int per_cu = 160 * 1024 / (t.ring * rows * t.sk * 2);
+  const int stage = rows * t.sk * 2;
+  const int ring = t.ring < 160 * 1024 / stage ? t.ring : 160 * 1024 / stage;  // as TallCfg::kRing
+  const int per_cu = 160 * 1024 / (ring * stage);
   return per_cu < 8 ? per_cu : 8;
 }
+static_assert(tall_occupancy(TallShape{64, 32, 64, 4}) == 3 && tall_occupancy(TallShape{32, 64, 128, 4}) == 1,
+              "tall_occupancy: LDS per workgroup as TallCfg lays it out");
 
 struct TallPlan {
   bool use = false;
