@@ -142,6 +142,8 @@ int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w, const voi
  * D in {32, 64, 96, 128, 192, 256}. Keys go in fixed splits of BI_SPLIT_KEYS; the workspace
  * holds per-split (m, l, acc) partials and a work-item counter
  * (bi_attn_decode_workspace_bytes); calls that overlap must not share it.
+ * The V position stride must stay below 2^23 bytes (BI_E_UNSUPPORTED
+ * otherwise; copy such a layout first).
  * Replaces: kernels/attention.py:326-365 (batch_invariant_decode_attention),
  * kernels :47-171; kv_lens is an extension the reference lacks. */
 size_t bi_attn_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t L, int64_t D);

@@ -132,6 +132,11 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
                   (long long)strides[i]);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(ws))
     return fail(BI_E_INVALID_ARG, "%s: q, k, v and workspace must be 16-byte aligned", what);
+  // The contiguous-cache kernel addresses a split's 256 V rows with 32-bit
+  // byte offsets.
+  if (!table && !per_key && strides[7] * (int64_t)es >= ((int64_t)1 << 23))
+    return fail(BI_E_UNSUPPORTED, "%s: V position stride (%lld elements) must stay below 2^23 bytes", what,
+                (long long)strides[7]);
   bi::DecodeArgs a;
   a.q = q; a.k = k; a.v = v; a.kv_lens = kv_lens; a.out = out;
   a.table = table; a.table_stride = table_stride; a.page_shift = page_shift; a.num_pages = (int)num_pages;

@@ -153,6 +153,21 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
   const int lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int per_split = a.Hkv * a.nchunk;  // items per (sequence, split)
+  // Fixed V copy offsets (see copy_v): a copy moves 64 / kCPR whole rows, so
+  // the swizzle key (row & 7) repeats every kVPeriod copies. The host keeps
+  // 256 rows of the V stride below 2^31 bytes.
+  constexpr bool kVFixed = MODE == kKvContig && (64 % KV::kCPR) == 0;
+  constexpr int kRowsPerCopy = kVFixed ? 64 / KV::kCPR : 1;
+  constexpr int kVPeriod = !KV::kSwz ? 1 : kRowsPerCopy >= 8 ? 1 : 8 / kRowsPerCopy;
+  int v_off0[kVPeriod];
+  const int v_step = kVPeriod * kRowsPerCopy * (int)(a.v_sl * (int64_t)sizeof(T));
+#pragma unroll
+  for (int c = 0; c < kVPeriod; ++c) {
+    const int f = 64 * (wave * CPW + c) + lane;
+    const int rr = f / KV::kCPR, slot = f - rr * KV::kCPR;
+    const int cc = KV::kSwz ? (slot ^ (rr & 7)) : slot;
+    v_off0[c] = (int)(rr * a.v_sl * (int64_t)sizeof(T)) + cc * 16;
+  }
   int b = 0;
   int64_t base = 0;                         // items of sequences before b
   int len = 0;
@@ -203,6 +218,26 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
     else return vseg + (int64_t)(key - 64 * seg) * a.v_sl + vdim0;
   };
 
+  // V copies of this wave (rows 64 w .. 64 w + 63 of the split's V slice).
+  // Contiguous cache with rows of a power-of-two number of 16-byte chunks: a
+  // buffer resource from the split's first row to its last active one (rows
+  // past it read as zero; their weights are exactly 0) and per-lane offsets
+  // from the kernel's start (v_off0), advanced by a wave-uniform row step per
+  // copy, instead of a 64-bit row address per copy.
+  auto copy_v = [&]() {
+    if constexpr (kVFixed) {
+      const auto rs = buffer_rsrc(vbase + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh + (int64_t)j0 * a.v_sl,
+                                  (int)(n_act * a.v_sl * (int64_t)sizeof(T)));
+      const int vbytes = vdim0 * (int)sizeof(T);
+#pragma unroll
+      for (int c = 0; c < CPW; ++c)
+        copy_to_lds16(rs, v_off0[c % kVPeriod] + (c / kVPeriod) * v_step + vbytes, Vs + 1024 * (wave * CPW + c));
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPW; ++c) KV::copy(Vs, wave * CPW + c, vrow, n_act, lane);
+    }
+  };
+
   // Memory requests, in this order: Q^T, this wave's K rows, its V copies.
   F qf[D / 32];
   {
@@ -218,8 +253,7 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
     for (int st = 0; st < D / 32; ++st) kf[t][st] = frag_load(kr + 32 * st);
   }
   asm volatile("" ::: "memory");
-#pragma unroll
-  for (int c = 0; c < CPW; ++c) KV::copy(Vs, wave * CPW + c, vrow, n_act, lane);
+  copy_v();
 
   // Scores of this wave's 64 keys; lane (r, qq) holds row r, keys 64 w + 16 t + 4 qq + i.
   float s[KT][4];
@@ -263,8 +297,7 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
     if (vp > 0) {
       __syncthreads();                                  // every wave is done with the previous slice
       vdim0 = vp * DV;
-#pragma unroll
-      for (int c = 0; c < CPW; ++c) KV::copy(Vs, wave * CPW + c, vrow, n_act, lane);
+      copy_v();
       stage_barrier<0>();
     }
     f32x4 acc[(NDTV + 3) / 4];

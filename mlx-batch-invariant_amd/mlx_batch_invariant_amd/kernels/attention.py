@@ -87,13 +87,14 @@ def _prep(q, k, v):
 
 def _aligned(t: torch.Tensor) -> bool:
     """Layouts the kernels take in place: unit last stride, 16-byte aligned
-    rows and base, and a row stride below 2^24 bytes (the prefill kernel
-    addresses 64 rows of a chunk with 32-bit offsets). Others are copied."""
+    rows and base, and a row stride below 2^23 bytes (the decode and prefill
+    kernels address a split's or chunk's rows with 32-bit offsets). Others are
+    copied."""
     es = t.element_size()
     st = t.stride()
     return (st[-1] == 1 and t.data_ptr() % 16 == 0
             and all((s * es) % 16 == 0 and s >= 0 for s in st[:-1])
-            and (t.dim() < 2 or st[-2] * es < 1 << 24))
+            and (t.dim() < 2 or st[-2] * es < 1 << 23))
 
 
 def _fix(t: torch.Tensor) -> torch.Tensor:
