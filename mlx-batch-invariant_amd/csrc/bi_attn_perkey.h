@@ -24,7 +24,7 @@
 //
 // One 32-lane half of a wave runs one unit, as one simdgroup does in the
 // reference: decode (b, kv head, chunk of NQ query heads, split), prefill (b,
-// query head, 4 queries). The halves of a wave never exchange data (shuffles
+// query head, kPkQB queries). The halves of a wave never exchange data (shuffles
 // of width 32) and each half's control flow is uniform. A unit loads the K
 // and V rows of several keys before running their updates in key order.
 #pragma once
@@ -203,7 +203,8 @@ __global__ __launch_bounds__(256) void attn_combine_perkey(DecodeArgs a) {
   static_cast<T*>(a.out)[bh * D + d] = to_store<T>(Ls > 0.0f ? A / Ls : 0.0f);
 }
 
-// Prefill: unit = (b, query head h, queries 4 blk .. 4 blk + 3), blk fastest.
+// Prefill: unit = (b, query head h, queries QB blk .. QB blk + QB - 1), blk
+// fastest (QB = kPkQB).
 // Query t sees keys [0, nkeys(t)), nkeys = len - Tq + t + 1 when causal
 // (bottom-right aligned), else len; a split merges into a query's running
 // result only if the query saw one of its keys.
