@@ -100,7 +100,6 @@ template <typename T, class BSrc, int MT, int PD, int NA, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_mid(const T* a, int64_t lda, BSrc bsrc, T* __restrict__ out,
                                                 float* __restrict__ part, int M, int N, int K, int G, int CG) {
   typedef MidCfg<T, MT, NA> C;
-  typedef typename Frag<T>::type F;
   // Outstanding vector-memory instructions that are certainly issued after
   // the copies of group g when its barrier is reached (copies of NA - 2 later
   // groups and at least min(PD, NA - 1) groups of B loads): waiting down to
@@ -237,7 +236,6 @@ template <typename T, class BSrc, int MT, int PD, int NA, bool SPLIT>
 __global__ __launch_bounds__(512) void gemm_mid2(const T* a, int64_t lda, BSrc bsrc, T* __restrict__ out,
                                                  float* __restrict__ part, int M, int N, int K, int G, int CG) {
   typedef MidCfg<T, MT, NA> C;  // one group's A buffer; a stage holds two
-  typedef typename Frag<T>::type F;
   constexpr int kCopiesPerWave = C::kCopies / 4;  // two groups' copies over eight waves
   // As in gemm_mid: vector-memory instructions certainly issued after a
   // stage's copies when its barrier is reached (copies of NA - 2 later stages
