@@ -52,9 +52,21 @@ CFLAGS = [
 # 0.381 / 1.416 -> 0.125 / 0.366 / 1.383 ms), decode 0.4-2%. The dense mid-M
 # tile measured 3-8% slower with it, so the flag stays per file; the fp32
 # attention kernels keep the default (with it one more of them spills).
+#
+# The quantized sources use the memory-clause scheduler (device pass only).
+# Its visible change in the decode GEMV is the prologue: every kernel-argument
+# load issued before the first wait, where the default waited once in between
+# (one more scalar-load round before the first weight request). Same-box A/B,
+# 4-bit g64 [14336, 4096], five alternating runs: M = 1 / 2 / 4 / 8 medians
+# 10.41 / 11.17 / 11.53 / 13.29 -> 9.89 / 10.72 / 11.03 / 12.84 us, M = 16-64
+# and large M (128 / 512 / 4096) equal. The dense source measured slower with
+# it at M = 1 and 4 (4.81 -> 5.16 us), the attention sources equal or slower.
+_CLAUSE = ["-Xarch_device", "-mllvm=-misched=gcn-max-memory-clause"]
 EXTRA_FLAGS = {
     "bi_attn_bf16": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "bi_attn_f16": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "bi_qmm_bf16": _CLAUSE,
+    "bi_qmm_f16": _CLAUSE,
 }
 
 
