@@ -16,9 +16,12 @@ namespace bi {
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeArgs a) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  // Threads past the end compute element 0 and do not store it (no early
+  // return: the kernel arguments are then read in one round).
+  const int64_t gid0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t total = (int64_t)a.B * a.Hq * D;
-  if (gid >= total) return;
+  const bool live = gid0 < total;
+  const int64_t gid = live ? gid0 : 0;
   const int64_t bh = gid / D;
   const int d = (int)(gid % D);
   const int b = (int)(bh / a.Hq);
@@ -46,7 +49,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeArgs a) {
     merge_split<1>(M, Ls, &A, a.pm[po], a.pl[po], &acc);
   }
   // A sequence of length 0 has no split: Ls == 0 and its output is defined as 0.
-  static_cast<T*>(a.out)[bh * D + d] = to_store<T>(Ls > 0.0f ? A / Ls : 0.0f);
+  if (live) static_cast<T*>(a.out)[bh * D + d] = to_store<T>(Ls > 0.0f ? A / Ls : 0.0f);
 }
 
 // ---------------------------------------------------------------------------
