@@ -65,25 +65,49 @@ __global__ __launch_bounds__(kLnThreads) void layer_norm_kernel(const T* __restr
   const int nchunks = (D + kLnVec - 1) / kLnVec;
 
   float xv[NC][8];
+  float wv[NC][8], bv[NC][8];
   float s = 0.0f;
+  if constexpr (VECTOR) {
+    // Every thread loads a chunk (past the row's end: its last chunk, then
+    // zeroed) and the weight and bias chunks with it: no branch before the
+    // first load and one memory round trip for x, w and b. The sums take the
+    // same elements in the same order.
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int chunk = t + c * kLnThreads;
+    for (int c = 0; c < NC; ++c) {
+      const int chunk = t + c * kLnThreads;
+      const int base = min(chunk, nchunks - 1) * kLnVec;
+      load8<T>(xr + base, xv[c]);
+      if (w) load8<T>(w + base, wv[c]);
+      if (b) load8<T>(b + base, bv[c]);
+      if (chunk >= nchunks) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xv[c][e] = 0.0f;
-    if (chunk < nchunks) {
-      const int base = chunk * kLnVec;
-      if constexpr (VECTOR) {
-        load8<T>(xr + base, xv[c]);
-      } else {
+        for (int e = 0; e < 8; ++e) xv[c][e] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (t + c * kLnThreads < nchunks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s = s + xv[c][e];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int chunk = t + c * kLnThreads;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[c][e] = 0.0f;
+      if (chunk < nchunks) {
+        const int base = chunk * kLnVec;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           if (base + e < D) xv[c][e] = (float)xr[base + e];
-      }
-      // Elements past D are +0 here: adding them leaves s unchanged (s starts
-      // at +0 and a round-to-nearest sum is never -0 unless both terms are).
+        // Elements past D are +0 here: adding them leaves s unchanged (s
+        // starts at +0 and a round-to-nearest sum is never -0 unless both
+        // terms are).
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s = s + xv[c][e];
+        for (int e = 0; e < 8; ++e) s = s + xv[c][e];
+      }
     }
   }
   const float mean = ln_block_sum(s, sums[0]) / (float)D;
@@ -111,14 +135,11 @@ __global__ __launch_bounds__(kLnThreads) void layer_norm_kernel(const T* __restr
       const int base = chunk * kLnVec;
       if constexpr (VECTOR) {
         float o[8];
-        float wv[8], bv[8];
-        if (w) load8<T>(w + base, wv);
-        if (b) load8<T>(b + base, bv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float y = (xv[c][e] - mean) * inv;
-          if (w) y = y * wv[e];
-          if (b) y = y + bv[e];
+          if (w) y = y * wv[c][e];
+          if (b) y = y + bv[c][e];
           o[e] = y;
         }
         store8<T>(orow + base, o);

@@ -38,23 +38,49 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(
   const int nchunks = (D + kNormVec - 1) / kNormVec;
 
   float xv[NC][8];
+  float wv[NC][8];
   float ss = 0.0f;
+  if constexpr (VECTOR) {
+    // Every thread loads a chunk (past the row's end: its last chunk, then
+    // zeroed), and the weights are requested with x: no branch before the
+    // first load and one memory round trip for x and w together. The sum
+    // takes the same elements in the same order.
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    const int chunk = t + c * kNormThreads;
+    for (int c = 0; c < NC; ++c) {
+      const int chunk = t + c * kNormThreads;
+      const int base = min(chunk, nchunks - 1) * kNormVec;
+      load8<T>(xr + base, xv[c]);
+      if (w) load8<T>(w + base, wv[c]);
+      else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xv[c][e] = 0.0f;
-    if (chunk < nchunks) {
-      const int base = chunk * kNormVec;
-      if constexpr (VECTOR) {
-        load8<T>(xr + base, xv[c]);
-      } else {
+        for (int e = 0; e < 8; ++e) wv[c][e] = 1.0f;
+      }
+      if (chunk >= nchunks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[c][e] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      if (t + c * kNormThreads < nchunks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(xv[c][e], xv[c][e], ss);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int chunk = t + c * kNormThreads;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[c][e] = 0.0f;
+      if (chunk < nchunks) {
+        const int base = chunk * kNormVec;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           if (base + e < D) xv[c][e] = (float)xr[base + e];
-      }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(xv[c][e], xv[c][e], ss);
+        for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(xv[c][e], xv[c][e], ss);
+      }
     }
   }
 
@@ -76,15 +102,8 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(
       const int base = chunk * kNormVec;
       float o[8];
       if constexpr (VECTOR) {
-        float wv[8];
-        if (w) {
-          load8<T>(w + base, wv);
-        } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) wv[e] = 1.0f;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (xv[c][e] * inv) * wv[e];
+        for (int e = 0; e < 8; ++e) o[e] = (xv[c][e] * inv) * wv[c][e];
         store8<T>(orow + base, o);
       } else {
 #pragma unroll
