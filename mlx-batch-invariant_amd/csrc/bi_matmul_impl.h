@@ -1060,11 +1060,28 @@ int dispatch_quant(int bits, int gs, const void* x, int64_t ldx, const uint32_t*
   return bi_host::fail(BI_E_UNSUPPORTED, "bi_quantized_matmul: bits=%d group_size=%d", bits, gs);
 }
 
-// Per-element-type entry points of the quantized op (bi_qmm_<dtype>.hip).
+// The same for one bit width (the 2-byte types compile their 4-bit and 8-bit
+// kernels in separate translation units, which the build compiles with
+// different scheduler options).
+template <typename T, int BITS>
+int dispatch_quant_bits(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                        const void* biases, void* out, int M, int N, int K, void* ws, hipStream_t st) {
+  if (gs == 32) return run_quant<T, BITS, 32>(x, ldx, w, scales, biases, out, M, N, K, ws, st);
+  if (gs == 64) return run_quant<T, BITS, 64>(x, ldx, w, scales, biases, out, M, N, K, ws, st);
+  if (gs == 128) return run_quant<T, BITS, 128>(x, ldx, w, scales, biases, out, M, N, K, ws, st);
+  return bi_host::fail(BI_E_UNSUPPORTED, "bi_quantized_matmul: bits=%d group_size=%d", BITS, gs);
+}
+
+// Per-element-type entry points of the quantized op (bi_qmm_<dtype>.hip; the
+// 8-bit kernels of the 2-byte types in bi_qmm8_<dtype>.hip).
 int qmm_bf16(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
              const void* biases, void* out, int M, int N, int K, void* ws, hipStream_t st);
 int qmm_f16(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
             const void* biases, void* out, int M, int N, int K, void* ws, hipStream_t st);
+int qmm8_bf16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
+              void* out, int M, int N, int K, void* ws, hipStream_t st);
+int qmm8_f16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
+             void* out, int M, int N, int K, void* ws, hipStream_t st);
 int qmm_f32(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
             const void* biases, void* out, int M, int N, int K, void* ws, hipStream_t st);
 

@@ -1,0 +1,13 @@
+// bi_qmm8_bf16.hip — the 8-bit affine-quantized matmul kernels for bf16
+// activations (the 4-bit ones are in bi_qmm_bf16.hip; the build compiles the
+// two with different scheduler options).
+#include "bi_matmul_impl.h"
+
+namespace bi {
+
+int qmm8_bf16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
+              void* out, int M, int N, int K, void* ws, hipStream_t st) {
+  return dispatch_quant_bits<bf16, 8>(gs, x, ldx, w, scales, biases, out, M, N, K, ws, st);
+}
+
+}  // namespace bi

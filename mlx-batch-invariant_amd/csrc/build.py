@@ -11,7 +11,8 @@ already loaded and shares torch's streams and allocations.
 Numerics flags are part of the batch-invariance contract and must not be
 changed per file: no fp contraction (every fma is explicit), no fast math,
 IEEE division and sqrt, denormals kept, and no packed-fp32 instructions.
-Per-file flags (EXTRA_FLAGS) only steer register allocation.
+Per-file flags (EXTRA_FLAGS) only steer register allocation and instruction
+scheduling.
 """
 
 from __future__ import annotations
@@ -53,14 +54,16 @@ CFLAGS = [
 # tile measured 3-8% slower with it, so the flag stays per file; the fp32
 # attention kernels keep the default (with it one more of them spills).
 #
-# The quantized sources use the memory-clause scheduler (device pass only).
-# Its visible change in the decode GEMV is the prologue: every kernel-argument
-# load issued before the first wait, where the default waited once in between
-# (one more scalar-load round before the first weight request). Same-box A/B,
-# 4-bit g64 [14336, 4096], five alternating runs: M = 1 / 2 / 4 / 8 medians
-# 10.41 / 11.17 / 11.53 / 13.29 -> 9.89 / 10.72 / 11.03 / 12.84 us, M = 16-64
-# and large M (128 / 512 / 4096) equal. The dense source measured slower with
-# it at M = 1 and 4 (4.81 -> 5.16 us), the attention sources equal or slower.
+# The 4-bit quantized sources use the memory-clause scheduler (device pass
+# only). Its visible change in the decode GEMV is the prologue: every
+# kernel-argument load issued before the first wait, where the default waited
+# once in between (one more scalar-load round before the first weight
+# request). Same-box A/B, 4-bit g64 [14336, 4096], five alternating runs:
+# M = 1 / 2 / 4 / 8 medians 10.41 / 11.17 / 11.53 / 13.29 -> 9.89 / 10.72 /
+# 11.03 / 12.84 us, M = 16-64 and large M (128 / 512 / 4096) equal. The 8-bit
+# kernels (bi_qmm8_*) measured slower with it (8-bit g128, M = 1 / 2: 14.35 /
+# 14.59 -> 14.69 / 15.15 us), the dense source too at M = 1 and 4 (4.81 ->
+# 5.16 us), and the attention sources equal or slower.
 _CLAUSE = ["-Xarch_device", "-mllvm=-misched=gcn-max-memory-clause"]
 EXTRA_FLAGS = {
     "bi_attn_bf16": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
