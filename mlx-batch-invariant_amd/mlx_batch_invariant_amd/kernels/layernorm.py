@@ -23,10 +23,11 @@ def _vec(t, D, dtype, name):
         return None
     if t.numel() != D:
         raise ValueError(f"batch_invariant_layer_norm: {name} has {t.numel()} elements, expected {D}")
-    t = t.reshape(D)
+    if t.ndim != 1:
+        t = t.reshape(D)
     if t.dtype != dtype:
         t = t.to(dtype)
-    return t.contiguous()
+    return t if t.is_contiguous() else t.contiguous()
 
 
 def batch_invariant_layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bias: torch.Tensor | None,
@@ -41,7 +42,7 @@ def batch_invariant_layer_norm(x: torch.Tensor, weight: torch.Tensor | None, bia
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     if rows == 0 or D == 0:
         return out
-    x2 = x.reshape(rows, D)
+    x2 = x if x.ndim == 2 else x.reshape(rows, D)
     if x2.stride(-1) != 1 or x2.stride(0) < D:
         x2 = x2.contiguous()
     lib = _lib.load()

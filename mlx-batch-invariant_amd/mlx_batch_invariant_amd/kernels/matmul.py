@@ -84,19 +84,20 @@ def batch_invariant_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     K = a.shape[-1]
     if K != b.shape[0]:
         raise ValueError(f"shape mismatch {tuple(a.shape)} @ {tuple(b.shape)}")
-    out_dtype = torch.result_type(a, b)
+    out_dtype = a.dtype if a.dtype == b.dtype else torch.result_type(a, b)
     if out_dtype not in _lib.FLOAT_DTYPES:
         raise ValueError(f"batch_invariant_matmul: unsupported dtype {out_dtype}")
     _lib.require_gpu("batch_invariant_matmul", a, b)
     lead = a.shape[:-1]
     N = b.shape[1]
-    a2 = a.reshape(-1, K)
+    flat = a.ndim == 2                         # no reshape round trip for the common 2-D call
+    a2 = a if flat else a.reshape(-1, K)
     if a2.dtype != out_dtype:
         a2 = a2.to(out_dtype)
     if b.dtype != out_dtype:
         b = b.to(out_dtype)
     out = matmul_bt(a2, b.t())
-    return out.reshape(*lead, N)
+    return out if flat else out.reshape(*lead, N)
 
 
 def _prep_batched(t: torch.Tensor, K8: int) -> torch.Tensor:
@@ -128,7 +129,7 @@ def batch_invariant_bmm(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     N = b.shape[-1]
     if K != b.shape[-2]:
         raise ValueError(f"shape mismatch {tuple(a.shape)} @ {tuple(b.shape)}")
-    out_dtype = torch.result_type(a, b)
+    out_dtype = a.dtype if a.dtype == b.dtype else torch.result_type(a, b)
     if out_dtype not in _lib.FLOAT_DTYPES:
         raise ValueError(f"batch_invariant_bmm: unsupported dtype {out_dtype}")
     _lib.require_gpu("batch_invariant_bmm", a, b)

@@ -76,7 +76,8 @@ def batch_invariant_quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: t
         raise ValueError("batch_invariant_quantized_matmul: scales/biases must be [N, K / group_size]")
     if not w.is_contiguous():
         w = w.contiguous()
-    x2 = _prep_rows(x.reshape(-1, K), K)
+    flat = x.ndim == 2                         # no reshape round trip for the common 2-D call
+    x2 = _prep_rows(x if flat else x.reshape(-1, K), K)
     M = x2.shape[0]
     out = torch.empty((M, N), dtype=dt, device=x.device)
     if M > 0:
@@ -87,7 +88,7 @@ def batch_invariant_quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: t
                                      biases.data_ptr(), out.data_ptr(), M, N, K, bits, group_size,
                                      _lib.DTYPE_CODE[dt], _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
         _lib.check(rc, "bi_quantized_matmul")
-    return out.reshape(*lead, N)
+    return out if flat else out.reshape(*lead, N)
 
 
 # ---- format helpers (host-side torch; not on the kernel path) -----------------

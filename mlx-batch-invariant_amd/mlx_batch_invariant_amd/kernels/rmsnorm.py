@@ -26,15 +26,17 @@ def batch_invariant_rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: 
     if weight is not None:
         if weight.numel() != D:
             raise ValueError(f"batch_invariant_rms_norm: weight has {weight.numel()} elements, expected {D}")
-        weight = weight.reshape(D)
+        if weight.ndim != 1:
+            weight = weight.reshape(D)
         if weight.dtype != x.dtype:
             weight = weight.to(x.dtype)
-        weight = weight.contiguous()
+        if not weight.is_contiguous():
+            weight = weight.contiguous()
     rows = x.numel() // D if D else 0
     out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
     if rows == 0 or D == 0:
         return out
-    x2 = x.reshape(rows, D)
+    x2 = x if x.ndim == 2 else x.reshape(rows, D)
     if x2.stride(-1) != 1 or x2.stride(0) < D:
         x2 = x2.contiguous()
     lib = _lib.load()
