@@ -1,4 +1,5 @@
-"""Build the gfx950 kernel library ``libbi_kernels.so`` in-tree.
+"""Build the gfx950 kernel library ``libbi_kernels.so`` in-tree (and the small
+CPython binding ``_bi_pycall`` of its hottest entry points).
 
     python mlx-batch-invariant_amd/csrc/build.py [--jobs N] [--verbose]
 
@@ -119,7 +120,25 @@ def build(jobs: int | None = None, verbose: bool = False, incremental: bool = Fa
     # -z defs: a kernel whose host stub was not emitted fails here, not at dlopen
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objs), "-o", str(tmp)], verbose)
     os.replace(tmp, OUT)
+    build_pycall(verbose)
     return OUT
+
+
+def build_pycall(verbose: bool = False) -> Path:
+    """The CPython binding of the hottest entry points (bi_pycall.c), a host-only
+    C extension next to the package; it calls the library through addresses
+    the package binds at load time, so it needs neither hipcc nor a link to
+    libbi_kernels.so."""
+    import sysconfig
+    out = PKG / ("_bi_pycall" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no C compiler for bi_pycall.c")
+    _run([cc, "-O2", "-shared", "-fPIC", "-Wall", "-I", sysconfig.get_paths()["include"], str(HERE / "bi_pycall.c"),
+          "-o", str(tmp)], verbose)
+    os.replace(tmp, out)
+    return out
 
 
 def main(argv=None) -> int:

@@ -59,12 +59,12 @@ def matmul_bt(a2: torch.Tensor, bt: torch.Tensor) -> torch.Tensor:
     K8 = (K + 7) // 8 * 8
     a2 = _prep_rows(a2, K8)
     bt = _prep_rows(bt, K8)
-    lib = _lib.load()
+    _lib.load()
     ws_bytes = _lib.ws_bytes("bi_matmul_workspace_bytes", M, N, K8)
     ws = _lib.workspace(ws_bytes, a2.device)
-    rc = lib.bi_matmul(a2.data_ptr(), a2.stride(0), bt.data_ptr(), bt.stride(0), out.data_ptr(),
-                       M, N, K8, _lib.DTYPE_CODE[a2.dtype], _lib.ptr(ws), ws_bytes,
-                       _lib.stream_of(a2))
+    rc = _lib.matmul_call(a2.data_ptr(), a2.stride(0), bt.data_ptr(), bt.stride(0), out.data_ptr(),
+                          M, N, K8, _lib.DTYPE_CODE[a2.dtype], _lib.ptr(ws), ws_bytes,
+                          _lib.stream_of(a2))
     _lib.check(rc, "bi_matmul")
     return out
 

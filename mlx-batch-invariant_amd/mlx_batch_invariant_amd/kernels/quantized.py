@@ -81,10 +81,10 @@ def batch_invariant_quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: t
     M = x2.shape[0]
     out = torch.empty((M, N), dtype=dt, device=x.device)
     if M > 0:
-        lib = _lib.load()
+        _lib.load()
         ws_bytes = _lib.ws_bytes("bi_quantized_matmul_workspace_bytes", M, N, K)
         ws = _lib.workspace(ws_bytes, x.device)
-        rc = lib.bi_quantized_matmul(x2.data_ptr(), x2.stride(0), w.data_ptr(), scales.data_ptr(),
+        rc = _lib.qmm_call(x2.data_ptr(), x2.stride(0), w.data_ptr(), scales.data_ptr(),
                                      biases.data_ptr(), out.data_ptr(), M, N, K, bits, group_size,
                                      _lib.DTYPE_CODE[dt], _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
         _lib.check(rc, "bi_quantized_matmul")

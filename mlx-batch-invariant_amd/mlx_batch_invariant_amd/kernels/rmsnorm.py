@@ -39,8 +39,8 @@ def batch_invariant_rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: 
     x2 = x if x.ndim == 2 else x.reshape(rows, D)
     if x2.stride(-1) != 1 or x2.stride(0) < D:
         x2 = x2.contiguous()
-    lib = _lib.load()
-    rc = lib.bi_rms_norm(x2.data_ptr(), x2.stride(0), _lib.ptr(weight), out.data_ptr(), rows, D,
-                         float(eps), _lib.DTYPE_CODE[x.dtype], _lib.stream_of(x))
+    _lib.load()
+    rc = _lib.rms_norm_call(x2.data_ptr(), x2.stride(0), _lib.ptr(weight), out.data_ptr(), rows, D,
+                            float(eps), _lib.DTYPE_CODE[x.dtype], _lib.stream_of(x))
     _lib.check(rc, "bi_rms_norm")
     return out

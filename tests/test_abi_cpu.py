@@ -180,3 +180,28 @@ def test_split_size_routing():
     for bad in [("mfma", 128), (None, 0), (None, 1.5), ("fast", 256), (None, True)]:
         with pytest.raises(ValueError):
             _per_key(*bad)
+
+
+def test_fast_binding_matches_ctypes():
+    """The CPython binding (_bi_pycall, built with the library) calls the same
+    C functions as ctypes: the same status for the same (rejected) arguments,
+    None as NULL, and a TypeError for a wrong argument count."""
+    lib = _lib.load()
+    from mlx_batch_invariant_amd import _bi_pycall
+    assert _lib.qmm_call is _bi_pycall.quantized_matmul
+    assert _lib.matmul_call is _bi_pycall.matmul
+    assert _lib.rms_norm_call is _bi_pycall.rms_norm
+    # null operands: rejected before any launch, by either binding
+    q = (0, 4096, 0, 0, 0, 0, 1, 14336, 4096, 4, 64, _lib.BI_BF16, None, 0, 0)
+    assert _lib.qmm_call(*q) == lib.bi_quantized_matmul(*q) == -1
+    m = (0, 8, 0, 8, 0, 1, 8, 8, _lib.BI_BF16, None, 0, 0)
+    assert _lib.matmul_call(*m) == lib.bi_matmul(*m) == -1
+    r = (0, 8, None, 0, 1, 8, 1e-6, _lib.BI_BF16, 0)
+    assert _lib.rms_norm_call(*r) == lib.bi_rms_norm(*r) == -1
+    # an unknown dtype code is rejected the same way
+    q_bad = q[:11] + (7,) + q[12:]
+    assert _lib.qmm_call(*q_bad) == lib.bi_quantized_matmul(*q_bad)
+    with pytest.raises(TypeError):
+        _lib.qmm_call(*q[:-1])
+    with pytest.raises(TypeError):
+        _lib.rms_norm_call(*r[:6], "eps", *r[7:])
