@@ -168,8 +168,8 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   for (int j = 0; j < NB; ++j)
     *reinterpret_cast<f32x4*>(regions + (size_t)wave * C::kWaveBytes + j * kWave * 16 + lane * 16) = accs[j];
   __syncthreads();
-  // Ordered fold: one thread per output element (lane l, register e of the
-  // MFMA result layout), eight LDS loads in flight, adds in group order.
+  // Ordered fold: one thread per stored output element (lane l, register e of
+  // the MFMA result layout), eight LDS loads in flight, adds in group order.
   // Partial of group g: wave g / NB's region, slot g % NB.
   auto pptr = [&](int g, int l, int e) {
     return reinterpret_cast<const float*>(regions + (size_t)(g / NB) * C::kWaveBytes + (g % NB) * kWave * 16 +
@@ -177,6 +177,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   };
   for (int idx = threadIdx.x; idx < kWave * 4; idx += kWave * W) {
     const int e = idx / kWave, l = idx % kWave;
+    if (4 * (l / 16) + e >= M) continue;        // tile rows past M are never stored
     float total = 0.f;
     int gg = 0;
     for (; gg + 8 <= G; gg += 8) {
