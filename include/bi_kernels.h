@@ -91,9 +91,10 @@ int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out
 
 /* Diagnostic, no counterpart in the reference: the mid- and large-M launch
  * the policy picks for a 2-byte dense call of this shape (aligned operands):
- * "big", "tall <BM>x<BN> k<SK> r<ring> c<K chunks>", or "other" (the small-M
- * and LDS-tile launches). Host only; launch shape never changes bits. The
- * string is valid until the calling thread's next call. */
+ * "big" (256 x 128 tiles), "big 128x128", "tall <BM>x<BN> k<SK> r<ring>
+ * c<K chunks>", or "other" (the small-M and LDS-tile launches). Host only;
+ * launch shape never changes bits. The string is valid until the calling
+ * thread's next call. */
 const char* bi_matmul_launch(int64_t M, int64_t N, int64_t K);
 
 /* Strided batch of dense matmuls (a [batch][M, K], bt [batch][N, K],

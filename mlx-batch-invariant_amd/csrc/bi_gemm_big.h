@@ -1,6 +1,9 @@
 // bi_gemm_big.h — the large-M dense tile: 256 x 128 outputs per workgroup of
 // 8 waves (4 x 2, 64 x 64 outputs each, two waves per SIMD), operands copied
-// global -> LDS by the load unit (buffer_load ... lds, no VGPR staging).
+// global -> LDS by the load unit (buffer_load ... lds, no VGPR staging). A
+// 128 x 128 form (2 x 2 waves, one per SIMD) serves shapes whose 256-row
+// tiles would leave CUs idle; everything below holds for both, with the
+// A rows and copy counts scaled.
 //
 // Same arithmetic as every other matmul launch (bi_gemm_tile.h, dense k-slot
 // map k = 256 g + 32 s + 8 q + e): per 256-k group eight MFMA steps from zero,
@@ -71,15 +74,35 @@ constexpr int64_t kBigMaxLd = (int64_t)1 << 22;
 constexpr int kBigMinM = 256;
 constexpr int kBigMinTiles = 96;
 
-template <typename T>
-__global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__ a, int64_t lda,
-                                                           const T* __restrict__ bt, int64_t ldb,
-                                                           T* __restrict__ out, int M, int N, int K, int tiles_m,
-                                                           int tiles_n) {
+// WM = waves along M: 4 for the 256 x 128 tile (8 waves, two per SIMD), 2
+// for a 128 x 128 tile (4 waves, one per SIMD, 112 KB of LDS), which puts
+// twice as many workgroups on the chip when the 256-row tiles are fewer than
+// the CUs. Same per-wave 64 x 64 tile, same steps, same bits.
+template <int WM>
+struct BigTile {
+  static constexpr int kBM = 64 * WM, kWaves = 2 * WM;
+  static constexpr int kACopies = kBM / 8 / kWaves;   // 4
+  static constexpr int kBCopies = kBigBN / 8 / kWaves;  // 2 (WM = 4) or 4 (WM = 2)
+  static constexpr int kAStage = kBM * 64;
+  static_assert(WM == 2 || WM == 4, "gemm_big: 128- or 256-row tiles");
+};
+static_assert(BigTile<4>::kBM == kBigBM && BigTile<4>::kWaves == kBigWaves && BigTile<4>::kACopies == kBigACopies &&
+                  BigTile<4>::kBCopies == kBigBCopies,
+              "gemm_big: the default tile is the 256 x 128 one");
+
+template <typename T, int WM = kBigWavesM>
+__global__ __launch_bounds__(64 * BigTile<WM>::kWaves) void gemm_big(const T* __restrict__ a, int64_t lda,
+                                                                     const T* __restrict__ bt, int64_t ldb,
+                                                                     T* __restrict__ out, int M, int N, int K,
+                                                                     int tiles_m, int tiles_n) {
   static_assert(sizeof(T) == 2, "gemm_big: 2-byte element types only");
   typedef typename Frag<T>::type F;
+  typedef BigTile<WM> BT;
+  constexpr int kBM = BT::kBM, kWavesAll = BT::kWaves, kACop = BT::kACopies, kBCop = BT::kBCopies;
+  constexpr int kAStg = BT::kAStage;
   constexpr int TI = kBigTI, TJ = kBigTJ, NT = TI * TJ, NCH = NT / 2;
-  __shared__ __attribute__((aligned(1024))) T lds[kBigABufs * kBigAStage + kBigBBufs * kBigBStage];
+  static_assert(kACop <= NCH && kBCop <= NCH, "gemm_big: one copy per MFMA chunk at most");
+  __shared__ __attribute__((aligned(1024))) T lds[kBigABufs * kAStg + kBigBBufs * kBigBStage];
 
   const int tiles_total = tiles_m * tiles_n;
   const int groups = (K + kGroupK - 1) / kGroupK;
@@ -93,7 +116,7 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
   const int first_m = (t / span) * kBigGroupM;
   const int gm = min(tiles_m - first_m, kBigGroupM);
   const int tm = first_m + (t % span) % gm, tn = (t % span) / gm;
-  const int m0 = tm * kBigBM, n0 = tn * kBigBN;
+  const int m0 = tm * kBM, n0 = tn * kBigBN;
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -101,13 +124,13 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
   const int wm = wave / kBigWavesN, wn = wave % kBigWavesN;
 
   // LDS element offset of row `row` of stage st (A rows 0..255, B rows 0..127).
-  auto a_row = [&](int st, int row) { return (st % kBigABufs) * kBigAStage + row * 64; };
-  auto b_row = [&](int st, int row) { return kBigABufs * kBigAStage + (st % kBigBBufs) * kBigBStage + row * 64; };
+  auto a_row = [&](int st, int row) { return (st % kBigABufs) * kAStg + row * 64; };
+  auto b_row = [&](int st, int row) { return kBigABufs * kAStg + (st % kBigBBufs) * kBigBStage + row * 64; };
 
   // Copy c of this wave moves the 8-row block c * 8 + wave of A (or of B):
   // lane l takes row l / 8 of the block, chunk (l % 8) ^ (l / 8).
   const int rr = lane / 8, ch = (lane % 8) ^ rr;
-  const int rows_a = min(M - m0, kBigBM), rows_b = min(N - n0, kBigBN);
+  const int rows_a = min(M - m0, kBM), rows_b = min(N - n0, kBigBN);
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a + (int64_t)m0 * lda), (short)0, (int)(rows_a * lda * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rb =
@@ -119,13 +142,13 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
   const int kst_valid = K / 64;
   auto copy_a = [&](int st, bool real, int c) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(real && st < kst_valid ? ra : r_none,
-                                             (lds_void_t*)(lds + a_row(st, 8 * (c * kBigWaves + wave))),
-                                             16, voa + (unsigned)(c * 8 * kBigWaves * lda * 2), st * 128, 0, 0);
+                                             (lds_void_t*)(lds + a_row(st, 8 * (c * kWavesAll + wave))),
+                                             16, voa + (unsigned)(c * 8 * kWavesAll * lda * 2), st * 128, 0, 0);
   };
   auto copy_b = [&](int st, bool real, int c) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(real && st < kst_valid ? rb : r_none,
-                                             (lds_void_t*)(lds + b_row(st, 8 * (c * kBigWaves + wave))),
-                                             16, vob + (unsigned)(c * 8 * kBigWaves * ldb * 2), st * 128, 0, 0);
+                                             (lds_void_t*)(lds + b_row(st, 8 * (c * kWavesAll + wave))),
+                                             16, vob + (unsigned)(c * 8 * kWavesAll * ldb * 2), st * 128, 0, 0);
   };
 
   // Fragment reads: row r of a 16-row block, chunk 4 s + q of step s.
@@ -152,11 +175,11 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
 #pragma unroll
   for (int st = 0; st < 3; ++st) {
 #pragma unroll
-    for (int c = 0; c < kBigACopies; ++c) copy_a(st, true, c);
+    for (int c = 0; c < kACop; ++c) copy_a(st, true, c);
 #pragma unroll
-    for (int c = 0; c < kBigBCopies; ++c) copy_b(st, true, c);
+    for (int c = 0; c < kBCop; ++c) copy_b(st, true, c);
   }
-  wait_vm_lgkm0<2 * (kBigACopies + kBigBCopies)>();
+  wait_vm_lgkm0<2 * (kACop + kBCop)>();
   __builtin_amdgcn_s_barrier();
   F fa[TI], fb0[TJ], fb1[TJ];
 #pragma unroll
@@ -175,8 +198,8 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
     int f = fold_mode == 1 ? 0 : kFoldLast;
 #pragma unroll
     for (int x = 0; x < NCH; ++x) {
-      if (copies == 1 && x < kBigBCopies) copy_b(cst, real, x);
-      if (copies == 2 && x < kBigACopies) copy_a(cst, real, x);
+      if (copies == 1 && x < kBCop) copy_b(cst, real, x);
+      if (copies == 2 && x < kACop) copy_a(cst, real, x);
       if (x < TJ) read_b(bn[x], rst, rs, x);
       if (fold_mode == 1) {
         if (x >= 1 && f < 2 * x && f < kFoldLast) fold(f++);  // tiles final in earlier chunks
@@ -201,7 +224,7 @@ __global__ __launch_bounds__(64 * kBigWaves) void gemm_big(const T* __restrict__
       step(fb0, fb1, st, 1, 1, st + 3, st + 3 < nst, p == 0, p == 0 ? 2 : 0);
       // stage st + 1 landed (younger: stage st + 2 and the B rows of st + 3);
       // this wave's reads of stage st are done; then every wave's are.
-      wait_vm_lgkm0<kBigACopies + 2 * kBigBCopies>();
+      wait_vm_lgkm0<kACop + 2 * kBCop>();
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);

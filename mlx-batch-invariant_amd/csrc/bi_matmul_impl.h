@@ -594,8 +594,19 @@ static inline bool use_wg(int64_t M, int G) { return M <= kSplitMMax && G * (M <
 constexpr int kBigFromM = 129;
 constexpr int kBigShortKMinTiles = 32;
 constexpr int kTallMaxM = 256;
+// When its 128 x 128 tiles fit the chip's 256 CUs in one round, the large
+// tile runs as 128 x 128 tiles (gemm_big<T, 2>: twice the workgroups, one wave
+// per SIMD). Same bits either way. Measured, bf16 [14336, 4096] M = 192 / 256:
+// 47.4-48.0 / 48.6-48.7 -> 35.1-35.6 / 36.3 us (stock hipBLASLt 43-46 at 256);
+// [12416, 960] 16.8 / 17.4 -> 13.0 / 13.5 us; with more tiles than CUs (M =
+// 384 / 512) it measured 20-35% slower, so those keep the 256-row tile.
+constexpr int kBigHalfMaxTiles = 256;
+static inline int64_t big_half_tiles(int64_t M, int64_t N) {
+  return (int64_t)ceil_div(M, (int64_t)BigTile<2>::kBM) * ceil_div(N, (int64_t)kBigBN);
+}
 struct BigPlan {
   bool use = false;
+  bool half = false;  // 128-row tiles
   int tiles_m = 0, tiles_n = 0;
 };
 static inline BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
@@ -605,6 +616,10 @@ static inline BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
   p.tiles_n = ceil_div(N, kBigBN);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
   p.use = tiles >= kBigMinTiles || (M > kTallMaxM && K <= 4 * kGroupK && tiles >= kBigShortKMinTiles);
+  if (p.use && big_half_tiles(M, N) <= kBigHalfMaxTiles) {
+    p.half = true;
+    p.tiles_m = ceil_div(M, BigTile<2>::kBM);
+  }
   return p;
 }
 
@@ -970,8 +985,12 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
     const BigPlan bp = big_plan(M, N, K);
     if (bp.use && lda < kBigMaxLd && bsrc.ldb < kBigMaxLd) {
       const int work = bp.tiles_m * bp.tiles_n;
-      gemm_big<T><<<((work + 7) / 8) * 8, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K,
-                                                                  bp.tiles_m, bp.tiles_n);
+      if (bp.half)
+        gemm_big<T, 2><<<((work + 7) / 8) * 8, 64 * BigTile<2>::kWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M,
+                                                                                N, K, bp.tiles_m, bp.tiles_n);
+      else
+        gemm_big<T><<<((work + 7) / 8) * 8, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K,
+                                                                    bp.tiles_m, bp.tiles_n);
       return bi_host::launch_status(what);
     }
     const TallPlan tp = tall_plan(M, N, K);
@@ -1030,9 +1049,17 @@ int run_quant(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
       bi::qmm_dequant_rows<T, BITS, GS><<<(unsigned)((nb + 255) / 256), 256, 0, st>>>(
           w, static_cast<const T*>(scales), static_cast<const T*>(biases), bq, N, K);
       bi::qmm_permute_a<T><<<(unsigned)((na + 255) / 256), 256, 0, st>>>(static_cast<const T*>(x), ldx, ap, M, K);
-      const int tmm = ceil_div(M, bi::kBigBM), tn = ceil_div(N, bi::kBigBN);
-      const int grid = ((tmm * tn + 7) / 8) * 8;
-      bi::gemm_big<T><<<grid, 64 * bi::kBigWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), M, N, K, tmm, tn);
+      const int tn = ceil_div(N, bi::kBigBN);
+      if (bi::big_half_tiles(M, N) <= bi::kBigHalfMaxTiles) {  // as the dense policy
+        const int tmm = ceil_div(M, bi::BigTile<2>::kBM);
+        const int grid = ((tmm * tn + 7) / 8) * 8;
+        bi::gemm_big<T, 2><<<grid, 64 * bi::BigTile<2>::kWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), M, N,
+                                                                         K, tmm, tn);
+      } else {
+        const int tmm = ceil_div(M, bi::kBigBM);
+        const int grid = ((tmm * tn + 7) / 8) * 8;
+        bi::gemm_big<T><<<grid, 64 * bi::kBigWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), M, N, K, tmm, tn);
+      }
       return bi_host::launch_status("bi_quantized_matmul");
     }
   }

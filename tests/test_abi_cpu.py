@@ -84,7 +84,8 @@ def test_dense_launch_policy():
     assert name(128, 14336, 4096) == "tall 64x64 k64 r4 c1"
     assert name(256, 4096, 4096) == "tall 64x32 k128 r3 c1"
     assert name(192, 896, 4864) == "tall 64x32 k128 r3 c4"
-    assert name(192, 14336, 4096) == "big"                       # 112 tiles of 256 x 128
+    assert name(192, 14336, 4096) == "big 128x128"               # 112 tiles of 256 x 128; 224 of 128 x 128 fit 256 CUs
+    assert name(384, 14336, 4096) == "big"                       # 336 tiles of 128 x 128: more than one round
     assert name(300, 12416, 960) == "big"
     assert name(256, 3328, 576) == "tall 32x64 k64 r5 c1"       # K % 128 != 0: 64-k stages
     assert name(16, 4864, 896) == "other"                        # small-M launches

@@ -129,6 +129,25 @@ def test_matmul_large_tiles_agree(dt, K):
     assert_bits_equal(to_np(big[rows]), ora.matmul(to_np(x[rows]), to_np(W), dt), f"{dt} K={K}")
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("K", [512, 4096])
+def test_matmul_large_half_tiles_agree(dt, K):
+    """The large tile run as 128 x 128 tiles (its 256-row tiles would leave CUs
+    idle; partial last tiles in both m and n) gives the decode launches' bits
+    for the same rows and matches the oracle on a sample of rows."""
+    from mlx_batch_invariant_amd import _lib
+    M, N = 200, 12400                      # 2 x 97 tiles of 128 x 128
+    assert _lib.load().bi_matmul_launch(M, N, K) == b"big 128x128"
+    g = gen(10)
+    W = randn((N, K), DT[dt], g, scale=0.02)
+    x = randn((M, K), DT[dt], g)
+    big = _mm(x, W.t())
+    for lo, hi in ((0, 1), (127, 128), (128, 144), (199, 200), (60, 92)):
+        assert bits(_mm(x[lo:hi], W.t())) == bits(big[lo:hi]), (lo, hi)
+    rows = [0, 1, 127, 128, 150, 199]
+    assert_bits_equal(to_np(big[rows]), ora.matmul(to_np(x[rows]), to_np(W), dt), f"{dt} K={K}")
+
+
 def test_matmul_layouts_and_leading_dims():
     g = gen(7)
     a = randn((2, 3, 200), torch.bfloat16, g)

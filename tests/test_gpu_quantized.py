@@ -161,12 +161,14 @@ def test_quantized_mid_m_split_k_matches_oracle(bits_, gs, dt):
 
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_quantized_large_m_launch_agrees(bits_, gs, dt):
+@pytest.mark.parametrize("M", [800, 256])
+def test_quantized_large_m_launch_agrees(bits_, gs, dt, M):
     """Large M takes the dequantize-once launch (weights dequantized into the
-    workspace in the dense tile's k order, then the large dense tile): its rows
+    workspace in the dense tile's k order, then the large dense tile: 4 x 112
+    tiles of 256 x 128 at M = 800, 2 x 112 of 128 x 128 at M = 256): its rows
     equal the same rows computed alone (M = 1, the GEMV launch) bit for bit,
     and the oracle bit for bit."""
-    N, K, M = 14336, 1024, 800             # 4 x 112 tiles of 256 x 128
+    N, K = 14336, 1024
     wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ + gs + 5)
     wq, s, b = wq.cuda(), s.cuda(), b.cuda()
     from mlx_batch_invariant_amd import _lib
@@ -174,7 +176,7 @@ def test_quantized_large_m_launch_agrees(bits_, gs, dt):
     x = randn((M, K), DT[dt], gen(21))
     run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
     full = run(x)
-    rows = [0, 257, M - 1]
+    rows = [0, min(257, M - 2), M - 1]
     for rr in rows:
         assert bits(full[rr:rr + 1]) == bits(run(x[rr:rr + 1])), rr
     W = ora.dequantize(wq.cpu().view(torch.int32).numpy().view(np.uint32), to_np(s.cpu()), to_np(b.cpu()),
