@@ -584,13 +584,15 @@ static inline bool use_split(int64_t M, int G) { return M <= kSplitMMax && G > 1
 // 16-row tile); up to 64 KB of it. Larger K takes the split + fold launch.
 static inline bool use_wg(int64_t M, int G) { return M <= kSplitMMax && G * (M <= 16 ? 1 : 2) <= 64; }
 
-// Dense large tile (bi_gemm_big.h) for 2-byte types, M > 128, K % 64 == 0:
-// M > 256 with at least kBigMinTiles tiles of 256 x 128, or at least
-// kBigShortKMinTiles with at most 4 groups of K; 128 < M <= 256 only with
-// kBigMinTiles tiles (fewer take the tall tile, measured faster at every
-// such shape: Qwen2-0.5B [4864, 896] M = 256 12.1 against 16.9 us, [4096,
-// 4096] M = 256 29.8 against 38.6 us with the large tile's K split). A
-// function of the shape only, so the workspace query and the launch agree.
+// Dense large tile (bi_gemm_big.h) for 2-byte types, K % 64 == 0: M > 256
+// with at least kBigMinTiles tiles of 256 x 128, or at least
+// kBigShortKMinTiles with at most 4 groups of K; 128 < M <= 256 with
+// kBigMinTiles tiles; and 64 < M <= 256 in its 128 x 128 form with
+// kBigHalfMinTiles of those (below). Other shapes take the tall tile (the
+// 256 x 128 tile measured slower there: Qwen2-0.5B [4864, 896] M = 256 16.9
+// against 12.1 us, [4096, 4096] M = 256 38.6 against 29.8 us with the large
+// tile's K split). A function of the shape only, so the workspace query and
+// the launch agree.
 constexpr int kBigFromM = 129;
 constexpr int kBigShortKMinTiles = 32;
 constexpr int kTallMaxM = 256;
@@ -601,6 +603,19 @@ constexpr int kTallMaxM = 256;
 // [12416, 960] 16.8 / 17.4 -> 13.0 / 13.5 us; with more tiles than CUs (M =
 // 384 / 512) it measured 20-35% slower, so those keep the 256-row tile.
 constexpr int kBigHalfMaxTiles = 256;
+// 64 < M <= 256 (the tall tile's range) takes the 128 x 128 tile from this
+// many tiles on: bf16 us, tall -> 128 x 128 (same box):
+//   [14336, 4096] M = 80 / 96 / 128: 53.0 / 53.0 / 54.0 -> 32.5 / 32.7 / 33.2;
+//   [11008, 4096] M = 96 / 192 / 256: 41.2 / 84.6 / 88.4 -> 32.1 / 33.9 / 34.4;
+//   [8192, 4096] M = 192 / 256: 42.2 / 55.5 -> 32.6 / 32.8;
+//   [6144, 4096] M = 192 / 256: 40.0 / 41.8 -> 32.1 / 32.6;
+//   [4096, 14336] M = 192 / 256: 98.6 / 108.5 -> 93.0 / 93.8;
+//   [4096, 4096] M = 192 / 256: 32.2 / 33.4 -> 31.1 / 31.5;
+//   [6144, 1024] M = 192 / 256: 13.1 / 13.7 -> 12.2 / 12.3;
+//   [11008, 2048] M = 192 / 256: 46.0 / 48.1 -> 20.0 / 20.4;
+//   [4864, 896] M = 256: 13.0 -> 12.1, but M = 192: 11.2 -> 12.0 (short K
+//   and a half-filled last row tile keep the tall tile).
+constexpr int kBigHalfMinTiles = 48;
 static inline int64_t big_half_tiles(int64_t M, int64_t N) {
   return (int64_t)ceil_div(M, (int64_t)BigTile<2>::kBM) * ceil_div(N, (int64_t)kBigBN);
 }
@@ -611,12 +626,19 @@ struct BigPlan {
 };
 static inline BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
   BigPlan p;
-  if (M < kBigFromM || N <= 0 || K <= 0 || K % 64) return p;
+  if (M <= 64 || N <= 0 || K <= 0 || K % 64) return p;
   p.tiles_m = ceil_div(M, kBigBM);
   p.tiles_n = ceil_div(N, kBigBN);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-  p.use = tiles >= kBigMinTiles || (M > kTallMaxM && K <= 4 * kGroupK && tiles >= kBigShortKMinTiles);
-  if (p.use && big_half_tiles(M, N) <= kBigHalfMaxTiles) {
+  p.use = M >= kBigFromM &&
+          (tiles >= kBigMinTiles || (M > kTallMaxM && K <= 4 * kGroupK && tiles >= kBigShortKMinTiles));
+  const int64_t ht = big_half_tiles(M, N);
+  // 64 < M <= 256 with enough 128 x 128 tiles: the half tile instead of the
+  // tall one, except at short K with a part-filled last row tile.
+  const bool half_mid = M > 64 && M <= kTallMaxM && ht >= kBigHalfMinTiles && K >= 768 &&
+                        !(K < 1024 && M % BigTile<2>::kBM != 0);
+  if ((p.use && ht <= kBigHalfMaxTiles) || (!p.use && half_mid)) {
+    p.use = true;
     p.half = true;
     p.tiles_m = ceil_div(M, BigTile<2>::kBM);
   }

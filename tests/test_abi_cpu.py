@@ -77,12 +77,14 @@ def test_dense_launch_policy():
     tiles."""
     lib = _lib.load()
     name = lambda M, N, K: lib.bi_matmul_launch(M, N, K).decode()
-    assert name(256, 4864, 896) == "tall 64x32 k64 r4 c1"      # Qwen2-0.5B linear, M = 256
+    assert name(256, 4864, 896) == "big 128x128"                # Qwen2-0.5B linear, M = 256: 76 tiles of 128 x 128
+    assert name(192, 4864, 896) == "tall 64x32 k128 r3 c1"      # short K, half-filled last row tile
     assert name(64, 4864, 896) == "tall 32x32 k128 r4 c1"
     assert name(32, 14336, 4096) == "tall 32x64 k128 r4 c1"     # M <= 32: widest tile with >= 200
     assert name(32, 4096, 4096) == "tall 32x32 k128 r4 c2"
-    assert name(128, 14336, 4096) == "tall 64x64 k64 r4 c1"
-    assert name(256, 4096, 4096) == "tall 64x32 k128 r3 c1"
+    assert name(128, 14336, 4096) == "big 128x128"              # 112 tiles of 128 x 128
+    assert name(128, 4096, 4096) == "tall 32x32 k128 r4 c1"     # 32 tiles of 128 x 128: too few
+    assert name(256, 4096, 4096) == "big 128x128"               # 64 tiles of 128 x 128
     assert name(192, 896, 4864) == "tall 64x32 k128 r3 c4"
     assert name(192, 14336, 4096) == "big 128x128"               # 112 tiles of 256 x 128; 224 of 128 x 128 fit 256 CUs
     assert name(384, 14336, 4096) == "big"                       # 336 tiles of 128 x 128: more than one round
