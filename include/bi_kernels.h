@@ -163,7 +163,11 @@ int bi_attn_decode(const void* q, const void* k, const void* v, const int32_t* k
  * are rejected with BI_E_WORKSPACE (64 MiB: e.g. B = 64, Hq = 32, L = 8192,
  * D = 128 needs 34 MB). The call allocates nothing. Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (concurrent streams,
- * threads) race and must be serialised by the caller. */
+ * threads) race and must be serialised by the caller. The scratch is the
+ * current device's: a non-null stream of another device is rejected with
+ * BI_E_INVALID_ARG. The first call on a device resolves the array's address
+ * and must be made outside graph capture (BI_E_UNSUPPORTED otherwise); later
+ * calls of the same shape may be captured and replayed. */
 #define BI_DECODE_SCRATCH_BYTES (64u << 20)
 int bi_attn_decode_noalloc(const void* q, const void* k, const void* v, const int32_t* kv_lens,
                            void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
@@ -247,6 +251,13 @@ int bi_attn_prefill_per_key(const void* q, const void* k, const void* v, const i
                             void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
                             int64_t D, const int64_t* strides, int causal, float scale, int64_t split_size,
                             int dtype, void* stream);
+
+/* Diagnostic, no counterpart in the reference: y[i] = the hardware base-2
+ * exponential (v_exp_f32) of x[i], n >= 0 floats, device pointers, on the
+ * stream. It is the instruction the matrix-core attention kernels compute
+ * every split weight and merge factor with, exposed so that a CPU emulation
+ * of that order can use the hardware's values. */
+int bi_exp2_f32(const float* x, float* y, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

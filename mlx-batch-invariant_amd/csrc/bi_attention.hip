@@ -317,14 +317,37 @@ namespace {
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[bi::kMaxDev] = {};
 
-int scratch_of_current_device(const char* what, void** out) {
+// The scratch address of the current device. The kernels run on `stream`, so
+// a stream of another device would have them write through this device's
+// address: rejected. The address is resolved on the first call per device,
+// which must not be under graph capture (the lookup is not a stream operation
+// and is not recorded).
+int scratch_of_current_device(const char* what, hipStream_t stream, void** out) {
   using namespace bi_host;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return fail((int)e, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
   if (dev < 0 || dev >= bi::kMaxDev) return fail(BI_E_UNSUPPORTED, "%s: device %d out of range", what, dev);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return fail((int)e, "%s: hipStreamGetDevice failed: %s", what, hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(BI_E_INVALID_ARG,
+                  "%s: the stream belongs to device %d but device %d is current (the static scratch is the "
+                  "current device's)",
+                  what, (int)sdev, dev);
+  }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return fail((int)e, "%s: hipStreamIsCapturing failed: %s", what, hipGetErrorString(e));
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(BI_E_UNSUPPORTED,
+                  "%s: the first call on device %d is under graph capture; make one call outside capture first "
+                  "(it resolves the static scratch's address)",
+                  what, dev);
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
@@ -353,7 +376,30 @@ extern "C" int bi_attn_decode_noalloc(const void* q, const void* k, const void* 
                          what, (long long)B, (long long)Hq, (long long)L, (long long)D, need,
                          (size_t)BI_DECODE_SCRATCH_BYTES);
   void* ws = nullptr;
-  if ((rc = scratch_of_current_device(what, &ws))) return rc;
+  if ((rc = scratch_of_current_device(what, static_cast<hipStream_t>(stream), &ws))) return rc;
   return decode_impl(what, q, k, v, kv_lens, out, B, Hq, Hkv, L, D, strides, scale, dtype, ws,
                      (size_t)BI_DECODE_SCRATCH_BYTES, stream, nullptr, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// The attention kernels' exponential as a standalone call (a diagnostic, no
+// counterpart in the reference): y[i] = the hardware exp2 (v_exp_f32) of x[i],
+// the instruction every split weight and merge factor above is computed with.
+// The CPU emulation of the matrix-core order takes this function's values as
+// its exp2, so the rest of that order can be checked bit for bit.
+// ---------------------------------------------------------------------------
+namespace bi {
+__global__ __launch_bounds__(256) void exp2_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] = __builtin_amdgcn_exp2f(x[i]);
+}
+}  // namespace bi
+
+extern "C" int bi_exp2_f32(const float* x, float* y, int64_t n, void* stream) {
+  using namespace bi_host;
+  if (n < 0 || n > ((int64_t)1 << 38)) return fail(BI_E_INVALID_ARG, "bi_exp2_f32: bad count %lld", (long long)n);
+  if (n == 0) return BI_OK;
+  if (!x || !y) return fail(BI_E_INVALID_ARG, "bi_exp2_f32: null pointer argument");
+  bi::exp2_kernel<<<(unsigned)((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(x, y, n);
+  return launch_status("bi_exp2_f32");
 }

@@ -9,6 +9,10 @@
  * the kernel library and calls exactly the functions ctypes would. Arguments
  * keep the C ABI's order and meaning (include/bi_kernels.h); None stands for
  * a NULL pointer. The functions return the ABI's status code.
+ *
+ * The GIL is released for the library call, as ctypes does: the call can block
+ * on host work (first-use code-object load, a full launch queue), and
+ * bi_last_error is thread-local, so the message stays with the calling thread.
  */
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -62,32 +66,40 @@ static PyObject* py_bind(PyObject* self, PyObject* args) {
 
 static PyObject* py_quantized_matmul(PyObject* self, PyObject* const* args, Py_ssize_t n) {
   int64_t v[15];
+  int rc;
   (void)self;
   if (!g_qmm) {
     PyErr_SetString(PyExc_RuntimeError, "quantized_matmul: entry points not bound");
     return NULL;
   }
   if (read_i64(args, n, 15, -1, v, "quantized_matmul")) return NULL;
-  return PyLong_FromLong(g_qmm(PTR(v[0]), v[1], (const uint32_t*)PTR(v[2]), PTR(v[3]), PTR(v[4]), PTR(v[5]), v[6],
-                               v[7], v[8], (int)v[9], (int)v[10], (int)v[11], PTR(v[12]), (size_t)v[13],
-                               PTR(v[14])));
+  Py_BEGIN_ALLOW_THREADS
+  rc = g_qmm(PTR(v[0]), v[1], (const uint32_t*)PTR(v[2]), PTR(v[3]), PTR(v[4]), PTR(v[5]), v[6], v[7], v[8],
+             (int)v[9], (int)v[10], (int)v[11], PTR(v[12]), (size_t)v[13], PTR(v[14]));
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(rc);
 }
 
 static PyObject* py_matmul(PyObject* self, PyObject* const* args, Py_ssize_t n) {
   int64_t v[12];
+  int rc;
   (void)self;
   if (!g_mm) {
     PyErr_SetString(PyExc_RuntimeError, "matmul: entry points not bound");
     return NULL;
   }
   if (read_i64(args, n, 12, -1, v, "matmul")) return NULL;
-  return PyLong_FromLong(g_mm(PTR(v[0]), v[1], PTR(v[2]), v[3], PTR(v[4]), v[5], v[6], v[7], (int)v[8], PTR(v[9]),
-                              (size_t)v[10], PTR(v[11])));
+  Py_BEGIN_ALLOW_THREADS
+  rc = g_mm(PTR(v[0]), v[1], PTR(v[2]), v[3], PTR(v[4]), v[5], v[6], v[7], (int)v[8], PTR(v[9]), (size_t)v[10],
+            PTR(v[11]));
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(rc);
 }
 
 static PyObject* py_rms_norm(PyObject* self, PyObject* const* args, Py_ssize_t n) {
   int64_t v[9];
   double eps;
+  int rc;
   (void)self;
   if (!g_rms) {
     PyErr_SetString(PyExc_RuntimeError, "rms_norm: entry points not bound");
@@ -96,7 +108,10 @@ static PyObject* py_rms_norm(PyObject* self, PyObject* const* args, Py_ssize_t n
   if (read_i64(args, n, 9, 6, v, "rms_norm")) return NULL;
   eps = PyFloat_AsDouble(args[6]);
   if (eps == -1.0 && PyErr_Occurred()) return NULL;
-  return PyLong_FromLong(g_rms(PTR(v[0]), v[1], PTR(v[2]), PTR(v[3]), v[4], v[5], (float)eps, (int)v[7], PTR(v[8])));
+  Py_BEGIN_ALLOW_THREADS
+  rc = g_rms(PTR(v[0]), v[1], PTR(v[2]), PTR(v[3]), v[4], v[5], (float)eps, (int)v[7], PTR(v[8]));
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(rc);
 }
 
 static PyMethodDef methods[] = {

@@ -71,6 +71,7 @@ _SIGNATURES = {
     "bi_attn_prefill_paged": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i64,
                                              _c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int,
                                              ctypes.c_float, ctypes.c_int, _vp]),
+    "bi_exp2_f32": (ctypes.c_int, [_vp, _vp, _c_i64, _vp]),
 }
 
 _lib = None

@@ -170,6 +170,11 @@ def test_invalid_arguments_are_rejected_before_launch():
         2, 8, 1000, 128)
     assert lib.bi_attn_decode_per_key(p, p, p, None, p, 2, 8, 2, 1000, 128, strides, 1.0, 100, 2, p, need - 16,
                                       None) == -3
+    # the exp2 diagnostic: count and pointers checked before launch, nothing to do for n = 0
+    assert lib.bi_exp2_f32(p, p, -1, None) == -1
+    assert lib.bi_exp2_f32(None, p, 4, None) == -1
+    assert lib.bi_exp2_f32(p, None, 4, None) == -1
+    assert lib.bi_exp2_f32(None, None, 0, None) == 0
 
 
 def test_split_size_routing():

@@ -69,3 +69,57 @@ def test_noalloc_decode_rejects_shapes_beyond_the_scratch():
     rc = lib.bi_attn_decode_noalloc(p, p, p, None, p, 256, 32, 8, 8192, 128, st, 0.1, lib_mod.BI_BF16, None)
     assert rc == -3, rc
     assert "static scratch" in lib.bi_last_error().decode()
+
+
+def test_noalloc_decode_captured_in_a_graph_replays_bitwise():
+    """One eager call (it resolves the scratch address), then the same call
+    captured into a HIP graph: q is refilled between replays, and every replay
+    must equal the workspace path on that q, bit for bit."""
+    lib_mod = _lib()
+    lib = lib_mod.load()
+    B, Hq, Hkv, L, D = 4, 32, 8, 1500, 128
+    g = gen(7)
+    q = randn((B, Hq, D), torch.bfloat16, g)
+    k = randn((B, Hkv, L, D), torch.bfloat16, g)
+    v = randn((B, Hkv, L, D), torch.bfloat16, g)
+    kl = torch.tensor([1500, 3, 700, 256], dtype=torch.int32).cuda()
+    st = _strides(q, k, v)
+    sc = D ** -0.5
+    code = lib_mod.BI_BF16
+    out = torch.empty((B, Hq, D), dtype=torch.bfloat16, device="cuda")
+    nbytes = lib.bi_attn_decode_workspace_bytes(B, Hq, L, D)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+
+    def noalloc():
+        lib_mod.check(lib.bi_attn_decode_noalloc(q.data_ptr(), k.data_ptr(), v.data_ptr(), kl.data_ptr(),
+                                                 out.data_ptr(), B, Hq, Hkv, L, D, st, sc, code,
+                                                 lib_mod.stream_of(q)), "bi_attn_decode_noalloc")
+
+    def with_ws():
+        ref = torch.empty_like(out)
+        lib_mod.check(lib.bi_attn_decode(q.data_ptr(), k.data_ptr(), v.data_ptr(), kl.data_ptr(), ref.data_ptr(),
+                                         B, Hq, Hkv, L, D, st, sc, code, ws.data_ptr(), nbytes,
+                                         lib_mod.stream_of(q)), "bi_attn_decode")
+        torch.cuda.synchronize()
+        return bits(ref)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        noalloc()                      # eager first call on this device's stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert bits(out) == with_ws()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        noalloc()
+    for seed in (11, 12, 13):
+        q.copy_(randn((B, Hq, D), torch.bfloat16, gen(seed)))
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = bits(out)
+        assert got == with_ws(), f"replay with q seed {seed}"
+    del graph
+
