@@ -35,36 +35,55 @@ def _h(t: torch.Tensor) -> str:
                            digest_size=8).hexdigest()
 
 
-def _ops(dt: torch.dtype, dev: str):
-    """(name, fn) pairs; every input is drawn from a fixed CPU generator."""
+# Probe shapes: matmul / addmm / quantized matmul x[1, 4096] @ W[4096, 4096]^T,
+# RMSNorm over 4096, decode attention 8 / 2 heads of 128 over 1000 keys,
+# causal prefill 48 tokens against 300 keys.
+K = N = 4096
+HQ, HKV, DH = 8, 2, 128
+L_DEC, TQ_PRE, L_PRE = 1000, 48, 300
+QUANT = (("qmatmul_4b", 4, 64), ("qmatmul_8b", 8, 32))
+
+
+def probe_inputs(dt: torch.dtype) -> dict:
+    """Every probe input, on the CPU, drawn from one fixed generator (so a CPU
+    checker can recompute the outputs from the same values)."""
     import mlx_batch_invariant_amd as bi
+    g = torch.Generator().manual_seed(0)
+    rn = lambda *s: torch.randn(s, generator=g).to(dt)
+    p = {"W": rn(N, K), "x": rn(1, K), "lin_b": rn(N)}
+    for name, bits, gs in QUANT:
+        wq, s, b = bi.quantize(p["W"].float(), group_size=gs, bits=bits, dtype=dt)
+        p[name] = (wq.view(torch.int32), s, b)
+    p["w_n"], p["x_n"] = rn(K), rn(1, K)
+    p["q"], p["k"], p["v"] = rn(1, HQ, 1, DH), rn(1, HKV, L_DEC, DH), rn(1, HKV, L_DEC, DH)
+    p["qp"], p["kp"], p["vp"] = rn(1, HQ, TQ_PRE, DH), rn(1, HKV, L_PRE, DH), rn(1, HKV, L_PRE, DH)
+    return p
+
+
+def _ops(dt: torch.dtype, dev: str):
+    """(name, fn) pairs over probe_inputs(dt) moved to ``dev``."""
     from mlx_batch_invariant_amd import nn as bnn
     F = torch.nn.functional
-    g = torch.Generator().manual_seed(0)
-    rn = lambda *s: torch.randn(s, generator=g).to(dt).to(dev)
-    K = N = 4096
-    W = rn(N, K)
-    x = rn(1, K)
-    lin_b = rn(N)
+    p = {k: (tuple(t.to(dev) for t in v) if isinstance(v, tuple) else v.to(dev)) for k, v in probe_inputs(dt).items()}
+    x, W, lin_b = p["x"], p["W"], p["lin_b"]
     out = [("matmul", lambda: torch.matmul(x, W.t())),
            ("addmm", lambda: F.linear(x, W, lin_b))]
-    for name, bits, gs in (("qmatmul_4b", 4, 64), ("qmatmul_8b", 8, 32)):
-        wq, s, b = bi.quantize(W.float().cpu(), group_size=gs, bits=bits, dtype=dt)
-        wq, s, b = wq.view(torch.int32).to(dev), s.to(dev), b.to(dev)
+    for name, bits, gs in QUANT:
+        wq, s, b = p[name]
         out.append((name, lambda wq=wq, s=s, b=b, bits=bits, gs=gs: bnn.quantized_matmul(
             x, wq, s, b, transpose=True, group_size=gs, bits=bits)))
-    D = 4096
-    w_n, x_n = rn(D), rn(1, D)
-    out.append(("rms_norm", lambda: F.rms_norm(x_n, (D,), w_n, 1e-5)))
-    Hq, Hkv, Dh = 8, 2, 128
-    q, k, v = rn(1, Hq, 1, Dh), rn(1, Hkv, 1000, Dh), rn(1, Hkv, 1000, Dh)
-    out.append(("sdpa_decode", lambda: F.scaled_dot_product_attention(q, k, v, scale=Dh ** -0.5, enable_gqa=True)))
-    Tq, L = 48, 300
-    qp, kp, vp = rn(1, Hq, Tq, Dh), rn(1, Hkv, L, Dh), rn(1, Hkv, L, Dh)
+    out.append(("rms_norm", lambda: F.rms_norm(p["x_n"], (K,), p["w_n"], 1e-5)))
+    out.append(("sdpa_decode", lambda: F.scaled_dot_product_attention(p["q"], p["k"], p["v"], scale=DH ** -0.5,
+                                                                       enable_gqa=True)))
     from torch.nn.attention.bias import causal_lower_right
     out.append(("sdpa_prefill", lambda: F.scaled_dot_product_attention(
-        qp, kp, vp, attn_mask=causal_lower_right(Tq, L), scale=Dh ** -0.5, enable_gqa=True)))
+        p["qp"], p["kp"], p["vp"], attn_mask=causal_lower_right(TQ_PRE, L_PRE), scale=DH ** -0.5, enable_gqa=True)))
     return out
+
+
+def hash_array(t: torch.Tensor) -> str:
+    """The dump's hash of a tensor's raw bytes (blake2b, 8 bytes)."""
+    return _h(t)
 
 
 def _library_hash() -> str | None:

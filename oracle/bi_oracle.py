@@ -545,6 +545,135 @@ def attention(q, k, v, scale: float, causal: bool, dtype: str, kv_lens=None, spl
     return round_to(out, dtype)
 
 
+# ---------------------------------------------------------------------------
+# Attention in the gfx950 kernels' matrix-core order (bi_attn_decode /
+# bi_attn_prefill): the same quantity as ``attention`` (reference
+# kernels/attention.py:1-32 splits of 256 keys, :77-85 merge) evaluated with
+# the split maximum first and every product on the MFMA units:
+#   s_j = fp32(MFMA-chain(k_j, q) * fp32(scale * log2 e)), d-slot map
+#         d = 32 st + 8 quarter + e (the "natural" map), from an exact zero;
+#   per split: m = max of the active s_j; p_j = exp2(s_j - m) (inactive: 0);
+#     acc[d], l = MFMA chains over 8 steps of 32 keys, step ks holding keys
+#     32 ks + PV_SLOTS in k-slot order; 16-bit types add hi(P).V then lo(P).V
+#     per step (hi = T(p), lo = T(p - hi)), fp32 adds P.V once; l uses V = 1;
+#   splits merged left to right from M = -inf, L = 0, A = 0 in base 2:
+#     M' = max(M, m); L = fmaf(L, exp2(M - M'), l * exp2(m - M'));
+#     A = fmaf(A, exp2(M - M'), acc * exp2(m - M')); out = T(A / L) (0 if L = 0).
+# ``exp2`` is the kernels' exponential, v_exp_f32. Its exact values are not
+# modelled here: the default is the correctly rounded exp2 (float64 rounded
+# once, results below 2^-126 flushed to +0 as the instruction does); the GPU
+# tests pass the hardware's own values (bi_exp2_f32), which makes the rest of
+# the order checkable bit for bit.
+# ---------------------------------------------------------------------------
+
+LOG2E = np.float32(1.44269504088896340736)
+# k-slot (quarter qq, element e) of a P.V step -> key offset within its 32 keys
+PV_SLOTS = np.array([4 * qq + e if e < 4 else 16 + 4 * qq + (e - 4) for qq in range(4) for e in range(8)])
+
+
+def exp2_f32(x) -> np.ndarray:
+    """exp2 of float32 arguments: the float64 exp2 rounded once to float32;
+    a result below the normal range (2^-126) is +0, as v_exp_f32 gives it
+    (the instruction produces no subnormals); exp2(-inf) = 0."""
+    x = np.asarray(x, np.float32)
+    with np.errstate(over="ignore", under="ignore"):
+        e = np.exp2(x.astype(np.float64))
+        return np.where(e < 2.0 ** -126, np.float32(0), e.astype(np.float32)).astype(np.float32)
+
+
+def _mfma_chain(a, b, dtype: str) -> np.ndarray:
+    """Chain of 32-wide MFMA steps over the last axis (natural slot order) from
+    an exact zero; a [..., K] and b [..., K] broadcast, K a multiple of 32."""
+    K = a.shape[-1]
+    acc = np.zeros(np.broadcast_shapes(a.shape[:-1], b.shape[:-1]), np.float32)
+    for st in range(K // 32):
+        acc = mfma_step(acc, a[..., 32 * st:32 * st + 32], b[..., 32 * st:32 * st + 32], dtype)
+    return acc
+
+
+def _mfma_rows(qrows, K, V, nkeys, sl2, dtype, exp2):
+    """One (sequence, kv head): rows [R, D] against keys K, V [Lp, D] (Lp a
+    multiple of 256, zero past the data), row r seeing keys [0, nkeys[r])."""
+    R, D = qrows.shape
+    Lp = K.shape[0]
+    nsplit = Lp // SPLIT
+    s = _mfma_chain(K[None, :, :], qrows[:, None, :], dtype)                 # [R, Lp]
+    s = (s * sl2).astype(np.float32)
+    active = np.arange(Lp)[None, :] < nkeys[:, None]
+    s = np.where(active, s, np.float32(-np.inf)).reshape(R, nsplit, SPLIT)
+    act = active.reshape(R, nsplit, SPLIT)
+    m = s.max(-1)                                                            # [R, nsplit]
+    p = np.zeros_like(s)
+    with np.errstate(invalid="ignore"):
+        p[act] = exp2((s - m[..., None])[act])
+    idx = (32 * np.arange(STEPS))[:, None] + PV_SLOTS[None, :]               # [8, 32] keys of each step
+    Ps = p[:, :, idx]                                                        # [R, ns, 8, 32]
+    Vs = V.reshape(nsplit, SPLIT, D)[:, idx, :].transpose(0, 1, 3, 2)       # [ns, 8, D, 32]
+    parts = [Ps]
+    if dtype != "f32":
+        hi = round_to(Ps, dtype)
+        parts = [hi, round_to((Ps - hi).astype(np.float32), dtype)]
+    ones = np.ones(32, np.float32)
+    acc = np.zeros((R, nsplit, D), np.float32)
+    lsum = np.zeros((R, nsplit), np.float32)
+    for ks in range(STEPS):
+        for part in parts:
+            pa = part[:, :, ks, :]
+            acc = mfma_step(acc, pa[:, :, None, :], Vs[None, :, ks], dtype)
+            lsum = mfma_step(lsum, pa, ones, dtype)
+    M = np.full(R, -np.inf, np.float32)
+    Ls = np.zeros(R, np.float32)
+    A = np.zeros((R, D), np.float32)
+    for sp in range(nsplit):
+        t = SPLIT * sp < nkeys                                               # rows with a key in this split
+        if not t.any():
+            continue
+        Mn = np.maximum(M[t], m[t, sp])
+        c_old = exp2((M[t] - Mn).astype(np.float32))
+        c_new = exp2((m[t, sp] - Mn).astype(np.float32))
+        Ls[t] = fma32(Ls[t], c_old, (lsum[t, sp] * c_new).astype(np.float32))
+        A[t] = fma32(A[t], c_old[:, None], (acc[t, sp] * c_new[:, None]).astype(np.float32))
+        M[t] = Mn
+    with np.errstate(invalid="ignore", divide="ignore"):
+        return np.where(Ls[:, None] > 0, A / Ls[:, None], np.float32(0)).astype(np.float32)
+
+
+def attention_mfma(q, k, v, scale: float, causal: bool, dtype: str, kv_lens=None, exp2=exp2_f32,
+                   rows_per_block: int = 256) -> np.ndarray:
+    """q [B, Hq, Tq, D], k/v [B, Hkv, L, D] (float32 values in ``dtype``), in
+    the matrix-core order above; causal rows see keys [0, len - Tq + t + 1).
+    ``exp2`` maps a float32 array to float32 (default ``exp2_f32``)."""
+    q = np.asarray(q, np.float32)
+    k = np.asarray(k, np.float32)
+    v = np.asarray(v, np.float32)
+    B, Hq, Tq, D = q.shape
+    Hkv, L = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    sl2 = np.float32(np.float32(scale) * LOG2E)
+    out = np.zeros((B, Hq, Tq, D), np.float32)
+    for b in range(B):
+        n_len = L if kv_lens is None else min(max(int(kv_lens[b]), 0), L)
+        for hk in range(Hkv):
+            heads = list(range(hk * G, hk * G + G))
+            qrows = q[b, heads].reshape(G * Tq, D)
+            tok = np.tile(np.arange(Tq), G)
+            nkeys = (n_len - Tq + tok + 1) if causal else np.full(G * Tq, n_len)
+            nmax = max(int(nkeys.max()), 0)
+            if nmax == 0:
+                continue
+            Lp = -(-nmax // SPLIT) * SPLIT
+            Kp = np.zeros((Lp, D), np.float32)
+            Vp = np.zeros((Lp, D), np.float32)
+            Kp[:nmax] = k[b, hk, :nmax]
+            Vp[:nmax] = v[b, hk, :nmax]
+            o = np.zeros((G * Tq, D), np.float32)
+            for r0 in range(0, G * Tq, rows_per_block):
+                rs = slice(r0, r0 + rows_per_block)
+                o[rs] = _mfma_rows(qrows[rs], Kp, Vp, nkeys[rs], sl2, dtype, exp2)
+            out[b, heads] = o.reshape(G, Tq, D)
+    return round_to(out, dtype)
+
+
 def attention_float64(q, k, v, scale: float, causal: bool, kv_lens=None) -> np.ndarray:
     """Textbook softmax(q k^T * scale) v in float64 (closed form, no splits)."""
     q = np.asarray(q, np.float64)

@@ -50,3 +50,37 @@ def test_dump_reproduces_itself(tmp_path):
     assert len(d1["ops"]) == len(names) * 3 * 2 and len(d1["model"]) == 2 * 2 * 2
     assert d1["ops"] == d2["ops"] and d1["model"] == d2["model"]
     assert db.compare(d1, d2, file=io.StringIO()) == 0
+
+
+@pytest.mark.gpu
+def test_dump_invariant_hashes_equal_the_oracles_bits():
+    """Every invariant-mode op hash of a dump equals the hash of the oracle's
+    output on the same probe inputs (the dump's own CPU draws): matmul, addmm
+    (matmul rounded, then + bias rounded), 4-bit and 8-bit quantized matmul
+    (the blocked k-slot map), RMSNorm, and decode / causal prefill attention
+    (the matrix-core emulation with the hardware exp2), in fp16, bf16, fp32."""
+    import numpy as np
+    import torch
+
+    from helpers import gpu_exp2
+    from oracle import bi_oracle as ora
+    d = db.dump()
+    names = {torch.float16: ("fp16", "f16"), torch.bfloat16: ("bf16", "bf16"), torch.float32: ("fp32", "f32")}
+    f = lambda t: t.float().numpy()
+    for dt, (tag, o) in names.items():
+        p = db.probe_inputs(dt)
+        x, W = f(p["x"]), f(p["W"])
+        mm = ora.matmul(x, W, o)
+        want = {"matmul": mm, "addmm": ora.round_to((mm + f(p["lin_b"])).astype(np.float32), o)}
+        for name, bits_, gs in db.QUANT:
+            wq, s, b = p[name]
+            Wd = ora.dequantize(wq.numpy().view(np.uint32), f(s), f(b), gs, bits_, o)
+            want[name] = ora.matmul(x, Wd, o, kmap="blocked")
+        want["rms_norm"] = ora.rms_norm(f(p["x_n"]), f(p["w_n"]), 1e-5, o)
+        want["sdpa_decode"] = ora.attention_mfma(f(p["q"]), f(p["k"]), f(p["v"]), db.DH ** -0.5, False, o,
+                                                 exp2=gpu_exp2)
+        want["sdpa_prefill"] = ora.attention_mfma(f(p["qp"]), f(p["kp"]), f(p["vp"]), db.DH ** -0.5, True, o,
+                                                  exp2=gpu_exp2)
+        for name, arr in want.items():
+            h = db.hash_array(torch.from_numpy(np.ascontiguousarray(arr, np.float32)).to(dt))
+            assert d["ops"][f"{name}/{tag}/inv"] == h, f"{name}/{tag}"

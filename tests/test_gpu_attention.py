@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import DT, bits, gen, randn, to_np
+from helpers import DT, assert_bits_equal, attn_bound_check, bits, gen, gpu_exp2, randn, to_np
 from oracle import bi_oracle as ora
 from sweep import sweep
 
@@ -26,11 +26,14 @@ def _qkv(B, Hq, Hkv, Tq, L, D, dt, seed):
             randn((B, Hkv, L, D), DT[dt], g))
 
 
-def _tol_check(got, want, dt):
-    # outputs are convex combinations of V rows (|v| ~ 1): one ulp of the
-    # output type plus a small absolute allowance for fp32 order differences.
-    atol = 2e-6 if dt == "f32" else 1e-6
-    assert ora.max_ulp_excess(got, want, dt, atol=atol) <= 1.0, ora.isclose_report(got, want)
+def _tol_check(got, want, dt, q, k, v, scale, causal, kv_lens=None):
+    """The matrix-core kernels against the per-key (reference-order) oracle:
+    element by element within half a storage ulp of each side plus the bound
+    the two orders imply (helpers.attn_bound: hi/lo weights, per-key
+    rescaling, score rounding, each scaled by sum p|v| / sum p). Returns the
+    worst ratio of difference to allowance (<= 1)."""
+    f = lambda t: to_np(t) if isinstance(t, torch.Tensor) else t
+    return attn_bound_check(got, want, f(q), f(k), f(v), scale, causal, dt, kv_lens)
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
@@ -40,7 +43,7 @@ def test_decode_matches_oracle(dt, Hq, Hkv, L, D):
     sc = 1 / math.sqrt(D)
     got = to_np(_bi().batch_invariant_decode_attention(q, k, v, scale=sc))
     want = ora.attention(to_np(q), to_np(k), to_np(v), sc, False, dt)
-    _tol_check(got, want, dt)
+    _tol_check(got, want, dt, q, k, v, sc, False)
     ref64 = ora.attention_float64(to_np(q), to_np(k), to_np(v), sc, False)
     assert np.abs(got - ref64).max() < (2e-2 if dt == "bf16" else 4e-3)
 
@@ -51,7 +54,7 @@ def test_prefill_matches_oracle(dt, causal):
     q, k, v = _qkv(2, 8, 2, 37, 300, 64, dt, seed=3)
     got = to_np(_bi().batch_invariant_prefill_attention(q, k, v, scale=0.125, causal=causal))
     want = ora.attention(to_np(q), to_np(k), to_np(v), 0.125, causal, dt)
-    _tol_check(got, want, dt)
+    _tol_check(got, want, dt, q, k, v, 0.125, causal)
 
 
 def test_prefill_matches_float64_closed_form():
@@ -191,6 +194,24 @@ def test_prefill_batch_invariant():
     assert not fails, fails
 
 
+def test_prefill_batch_invariant_config4_size():
+    """BASELINE config 4 at its size: causal T = 2048, GQA 32 / 8, D = 128,
+    bf16; the probe sequence at the first and the last position of batches
+    of 1 to 16 (the benchmarked B = 16 launch included) gives the batch-1
+    bits (fillers drawn on the device)."""
+    Hq, Hkv, T, D = 32, 8, 2048, 128
+    q0, k0, v0 = _qkv(1, Hq, Hkv, T, T, D, "bf16", seed=12)
+
+    def filler(n, g):
+        gd = torch.Generator(device="cuda").manual_seed(int(torch.randint(0, 2 ** 31, (1,), generator=g)))
+        r = lambda *s: torch.randn(s, generator=gd, device="cuda").to(torch.bfloat16)
+        return r(n, Hq, T, D), r(n, Hkv, T, D), r(n, Hkv, T, D)
+
+    run = lambda t: _bi().batch_invariant_prefill_attention(t[0], t[1], t[2], scale=D ** -0.5, causal=True)
+    fails = sweep((q0, k0, v0), filler, run, batches=[1, 2, 4, 8, 16])
+    assert not fails, fails
+
+
 def test_prefill_kv_lens_equal_alone():
     Hq, Hkv, D, L, Tq = 8, 2, 64, 700, 40
     q, k, v = _qkv(3, Hq, Hkv, Tq, L, D, "bf16", seed=9)
@@ -245,7 +266,7 @@ def test_causal_prefill_kv_lens_shorter_than_chunk():
     assert torch.isfinite(out).all()
     got = to_np(out)
     want = ora.attention(to_np(q), to_np(k), to_np(v), 0.125, True, "bf16", kv_lens=lens)
-    _tol_check(got, want, "bf16")
+    _tol_check(got, want, "bf16", q, k, v, 0.125, True, kv_lens=lens)
     n0 = lens[0]
     for t in range(Tq):
         nk = n0 - Tq + t + 1
@@ -291,15 +312,20 @@ def test_decode_config3_full_size():
         alone = _bi().batch_invariant_decode_attention(q[b:b + 1], k[b:b + 1, :, :n], v[b:b + 1, :, :n],
                                                        scale=D ** -0.5)
         assert bits(out[b:b + 1]) == bits(alone), (b, n)
-    errs = {}
+    errs, ratios = {}, {}
     for b in (int(np.argmax(lens)), int(np.argmin(lens)), 100):
         n = int(lens[b])
-        want = ora.attention(to_np(q[b:b + 1]), to_np(k[b:b + 1, :, :n]), to_np(v[b:b + 1, :, :n]), D ** -0.5, False,
-                             "bf16")
+        qb, kb, vb = to_np(q[b:b + 1]), to_np(k[b:b + 1, :, :n]), to_np(v[b:b + 1, :, :n])
         got = to_np(out[b:b + 1])
-        _tol_check(got, want, "bf16")
-        errs[int(n)] = _ulp_err(got, want, "bf16")
-    _report("attn_err_config3.json", {"max_err_vs_per_key_oracle (ulps, abs) by length": errs})
+        # bit for bit against the emulation of the kernels' own order (hardware exp2)
+        assert_bits_equal(got, ora.attention_mfma(qb, kb, vb, D ** -0.5, False, "bf16", exp2=gpu_exp2),
+                          f"config 3, sequence {b} (len {n})")
+        want = ora.attention(qb, kb, vb, D ** -0.5, False, "bf16")
+        ratios[n] = _tol_check(got, want, "bf16", qb, kb, vb, D ** -0.5, False)
+        errs[n] = _ulp_err(got, want, "bf16")
+    _report("attn_err_config3.json", {"max_err_vs_per_key_oracle (ulps, abs) by length": errs,
+                                      "worst ratio to the stated bound by length": ratios,
+                                      "bitwise_vs_matrix_core_emulation": True})
 
 
 def test_prefill_config4_tokens_equal_decode_steps():
@@ -311,16 +337,19 @@ def test_prefill_config4_tokens_equal_decode_steps():
     q, k, v = _qkv(2, Hq, Hkv, T, T, D, "bf16", seed=21)
     sc = D ** -0.5
     full = _bi().batch_invariant_prefill_attention(q, k, v, scale=sc, causal=True)
-    errs = {}
+    errs, ratios = {}, {}
     for t in (0, 1, 255, 256, 511, 1023, 1500, 2047):
         dec = _bi().batch_invariant_decode_attention(q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1], scale=sc)
         assert bits(dec) == bits(full[:, :, t:t + 1]), t
-        want = ora.attention(to_np(q[:1, :, t:t + 1]), to_np(k[:1, :, :t + 1]), to_np(v[:1, :, :t + 1]), sc, False,
-                             "bf16")
+        qt, kt, vt = to_np(q[:1, :, t:t + 1]), to_np(k[:1, :, :t + 1]), to_np(v[:1, :, :t + 1])
         got = to_np(full[:1, :, t:t + 1])
-        _tol_check(got, want, "bf16")
+        assert_bits_equal(got, ora.attention_mfma(qt, kt, vt, sc, False, "bf16", exp2=gpu_exp2), f"config 4, token {t}")
+        want = ora.attention(qt, kt, vt, sc, False, "bf16")
+        ratios[t] = _tol_check(got, want, "bf16", qt, kt, vt, sc, False)
         errs[t] = _ulp_err(got, want, "bf16")
-    _report("attn_err_config4.json", {"max_err_vs_per_key_oracle (ulps, abs) by token": errs})
+    _report("attn_err_config4.json", {"max_err_vs_per_key_oracle (ulps, abs) by token": errs,
+                                      "worst ratio to the stated bound by token": ratios,
+                                      "bitwise_vs_matrix_core_emulation": True})
 
 
 def test_fp32_prefill_closed_form_d128_long():
@@ -352,7 +381,10 @@ def test_every_head_dim_matches_oracle_and_decode_equals_prefill(dt, D):
     att = _bi().batch_invariant_attention
     full = att(q, k, v, scale=sc, mask="causal")
     want = ora.attention(to_np(q[:1, :, -40:]), to_np(k[:1]), to_np(v[:1]), sc, True, dt)
-    _tol_check(to_np(full[:1, :, -40:]), want, dt)
+    _tol_check(to_np(full[:1, :, -40:]), want, dt, q[:1, :, -40:], k[:1], v[:1], sc, True)
+    assert_bits_equal(to_np(full[:1, :, -40:]),
+                      ora.attention_mfma(to_np(q[:1, :, -40:]), to_np(k[:1]), to_np(v[:1]), sc, True, dt, exp2=gpu_exp2),
+                      f"{dt} D={D}")
     for t in (0, 255, 256, T - 1):
         dec = att(q[:, :, t:t + 1], k[:, :, :t + 1], v[:, :, :t + 1], scale=sc)
         assert bits(dec) == bits(full[:, :, t:t + 1]), t

@@ -327,6 +327,131 @@ def test_attention_one_hot_v_gives_softmax_probabilities():
     assert np.abs(got - p / p.sum()).max() < 1e-6
 
 
+# ---- attention in the matrix-core order (attention_mfma) --------------------------
+
+# A scale whose score factor scale * log2(e) rounds to exactly 1 in fp32, so
+# crafted raw scores q.k are the base-2 exponents of the weights.
+_UNIT = float(np.float32(1 / np.float64(ora.LOG2E)))
+
+
+def _crafted(raw, vals, D=32):
+    """One row, keys with raw scores ``raw`` (q = e0, k_j = raw_j e0) and V
+    dim 0 = ``vals`` (other dims 0)."""
+    L = len(raw)
+    q = np.zeros((1, 1, 1, D), np.float32)
+    q[0, 0, 0, 0] = 1
+    k = np.zeros((1, 1, L, D), np.float32)
+    k[0, 0, :, 0] = raw
+    v = np.zeros((1, 1, L, D), np.float32)
+    v[0, 0, :, 0] = vals
+    return q, k, v
+
+
+def test_attention_mfma_unit_scale_factor():
+    assert np.float32(np.float32(_UNIT) * ora.LOG2E) == np.float32(1.0)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_attention_mfma_single_key_is_v(dt):
+    q, k, v = _qkv(2, 4, 2, 1, 1, 64, 0)
+    out = ora.attention_mfma(q, k, v, 0.3, False, dt)
+    assert np.array_equal(out, np.repeat(v, 2, axis=1))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_attention_mfma_zero_scale_is_mean_of_v(dt):
+    """Equal scores: every weight is exp2(0) = 1 exactly, l counts the keys,
+    and small-integer V sums exactly: out = mean of V (512 keys, two splits)."""
+    q, k, _ = _qkv(1, 2, 1, 1, 512, 32, 1)
+    v = np.random.default_rng(1).integers(-4, 5, size=(1, 1, 512, 32)).astype(np.float32)
+    out = ora.attention_mfma(q, k, v, 0.0, False, dt)
+    assert np.array_equal(out[0, 0, 0], ora.round_to(v[0, 0].sum(0) / np.float32(512), dt))
+
+
+@pytest.mark.parametrize("L", [1, 255, 256, 257, 513, 1000])
+def test_attention_mfma_close_to_float64_softmax(L):
+    q, k, v = _qkv(1, 4, 2, 3, L, 64, L)
+    for causal in ((False, True) if L >= 3 else (False,)):
+        got = ora.attention_mfma(q, k, v, 0.125, causal, "f32")
+        ref = ora.attention_float64(q, k, v, 0.125, causal)
+        assert np.abs(got - ref).max() < 2e-5, (L, causal)
+        # 16-bit P is kept to 16 significant bits (hi + lo): far inside one bf16 output ulp
+        got16 = ora.attention_mfma(q, k, v, 0.125, causal, "bf16")
+        assert ora.max_ulp_excess(got16, ora.round_to(ref.astype(np.float32), "bf16"), "bf16") <= 1.0, (L, causal)
+
+
+def test_attention_mfma_pv_slot_map_is_observable():
+    """Keys 0 and 1 (weight 1, V = +1 / -1) cancel in the first k-block of the
+    P.V step; keys 4..7 (weight 2^-25, V = 1) sit in the second block under
+    the kernels' slot map (4 qq + e, 16 + 4 qq + e), so their 4 * 2^-25 survive.
+    In one block with keys 0, 1 (the natural map 0..7) the matrix core would
+    truncate them to zero and the output would be 0. l = 2 (the tiny weights
+    round away against it): out = 2^-23 / 2 = 2^-24 exactly."""
+    raw = np.full(32, -200.0)
+    vals = np.zeros(32)
+    raw[[0, 1]] = 0.0
+    vals[[0, 1]] = [1.0, -1.0]
+    raw[[4, 5, 6, 7]] = -25.0
+    vals[[4, 5, 6, 7]] = 1.0
+    q, k, v = _crafted(raw, vals)
+    assert ora.attention_mfma(q, k, v, _UNIT, False, "bf16")[0, 0, 0, 0] == np.float32(2.0 ** -24)
+
+
+def test_attention_mfma_keeps_the_low_half_of_p():
+    """p0 = exp2(-0.3) is not a bf16 value: hi(p0) = 0.8125 and lo(p0) =
+    bf16(p0 - 0.8125) != 0. Key 2 (weight 1/2, V = -1.625) cancels hi(p0) * 1
+    exactly in the first P.V step, so the output is lo(p0) / l with
+    l = fp32(2.3125 + lo(p0)): nonzero only if the second (lo) step runs."""
+    raw = np.full(32, -200.0)
+    vals = np.zeros(32)
+    raw[0], vals[0] = -0.3, 1.0
+    raw[1], vals[1] = 0.0, 0.0
+    raw[2], vals[2] = -1.0, -1.625
+    q, k, v = _crafted(raw, vals)
+    p0 = ora.exp2_f32(np.float32(-0.3))
+    hi = ora.round_to(p0, "bf16")
+    assert hi == np.float32(0.8125)
+    lo = ora.round_to(np.float32(p0 - hi), "bf16")
+    assert lo != 0
+    l = np.float32(2.3125 + np.float64(lo))
+    got = ora.attention_mfma(q, k, v, _UNIT, False, "bf16")[0, 0, 0, 0]
+    assert got == ora.round_to(np.float32(lo / l), "bf16") and got != 0
+
+
+def test_attention_mfma_merge_is_base_2_and_left_to_right():
+    """Two splits whose maxima differ by 3: the first split's state is scaled
+    by exp2(-3) = 1/8 exactly. Split 0: one key, weight 1, V = 8; split 1:
+    one key 3 units higher, V = 0. out = (8/8) / (1/8 + 1) = 8/9 (rounded);
+    a natural-exp merge factor would give e^-3-weighted values instead."""
+    raw = np.full(257, -200.0)
+    vals = np.zeros(257)
+    raw[0], vals[0] = 0.0, 8.0
+    raw[256], vals[256] = 3.0, 0.0
+    q, k, v = _crafted(raw, vals)
+    got = ora.attention_mfma(q, k, v, _UNIT, False, "f32")[0, 0, 0, 0]
+    assert got == np.float32(1.0) / np.float32(1.125)
+
+
+def test_attention_mfma_custom_exp2_is_used():
+    """The exp2 argument replaces every weight and merge factor: a constant
+    exp2 of 1 makes every active key weigh the same (the mean of V)."""
+    q, k, v = _qkv(1, 2, 1, 1, 300, 64, 3)
+    ones = lambda x: np.ones_like(np.asarray(x, np.float32))
+    got = ora.attention_mfma(q, k, v, 0.125, False, "f32", exp2=ones)
+    assert np.abs(got[0, 0, 0] - v[0, 0].astype(np.float64).mean(0)).max() < 1e-5
+
+
+def test_attention_mfma_kv_lens_and_causal_structure():
+    q, k, v = _qkv(2, 4, 2, 5, 300, 64, 9)
+    lens = [300, 120]
+    full = ora.attention_mfma(q, k, v, 0.1, True, "bf16", kv_lens=lens)
+    alone = ora.attention_mfma(q[1:], k[1:, :, :120], v[1:, :, :120], 0.1, True, "bf16")
+    assert np.array_equal(full[1:], alone)
+    dec = ora.attention_mfma(q[:, :, -1:], k, v, 0.1, False, "bf16", kv_lens=lens)
+    assert np.array_equal(full[:, :, -1:], dec)
+    assert np.array_equal(ora.attention_mfma(q, k, v, 0.1, False, "bf16", kv_lens=[0, 5])[0], np.zeros_like(q[0]))
+
+
 def _exp_correctly_rounded(x: float) -> np.float32:
     """exp(x) from 40-digit decimal arithmetic, rounded to float32 by
     comparing with the neighbours' midpoints exactly."""
@@ -527,3 +652,17 @@ def test_max_ulp_excess_known_answers():
     assert ora.max_ulp_excess(w + [0, 0, -3 * 2.0 ** -5], w, "bf16") == 3.0      # ulp(-4) = 2^-5
     assert ora.max_ulp_excess(w + [2.0 ** -7, 0, 0], w, "bf16", atol=2.0 ** -8) == 0.5
     assert ora.max_ulp_excess(np.array([]), np.array([]), "f32") == 0.0
+
+
+def test_exp2_f32_known_answers():
+    """Powers of two exactly; results below the normal range flushed to +0;
+    elsewhere within half an ulp of the float64 value (one rounding)."""
+    x = np.array([0.0, -1.0, 3.0, -126.0, -126.5, -127.0, -149.0, -np.inf, 0.5], np.float32)
+    got = ora.exp2_f32(x)
+    assert list(got[:4]) == [1.0, 0.5, 8.0, 2.0 ** -126]
+    assert not got[4:8].any()
+    assert got[8] == np.float32(np.sqrt(2.0))
+    rng = np.random.default_rng(2)
+    y = rng.uniform(-100, 100, 10000).astype(np.float32)
+    e = np.exp2(y.astype(np.float64))
+    assert (np.abs(ora.exp2_f32(y) - e) <= 0.5 * ora.ulp(e, "f32")).all()
