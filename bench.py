@@ -9,7 +9,7 @@ of distinct copies so every step streams them from HBM (the 256 MB Infinity
 Cache would otherwise hold them). Time is measured with HIP events on the
 stream the kernels run on.
 
-    python bench.py [--steps K] [--warmup W] [--op qmm4|qmm8|linear|rmsnorm|decode|prefill|gemm|llama|all]
+    python bench.py [--steps K] [--warmup W] [--op qmm4|qmm8|linear|rmsnorm|decode|prefill|gemm|llama|sweep|all]
 
 Prints one JSON line per op (the default op only, unless --op is given).
 `value` is the achieved fraction of the op's roofline in percent (HBM 8 TB/s,
@@ -206,6 +206,37 @@ def cpu_threads() -> int:
     return max(1, min(n, int(cap))) if cap and cap.isdigit() else n
 
 
+def _cpu_median(fn, warmup=3, runs=20):
+    """Median wall time of fn() on the host after warm-ups (the reference's
+    harness/bench.py:19-27 protocol: 3 warm-ups, 20 timed runs)."""
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+class _CpuThreads:
+    """torch on every host core the job may use, restored on exit."""
+
+    def __enter__(self):
+        import torch
+        self.old = torch.get_num_threads()
+        self.n = cpu_threads()
+        torch.set_num_threads(self.n)
+        return self.n
+
+    def __exit__(self, *exc):
+        import torch
+        torch.set_num_threads(self.old)
+
+
+CPU_KIND = "substitute: torch CPU (MLX unavailable)"
+
+
 def cpu_baseline_qmm(bits, gs, warmup=3, runs=20):
     """Stock MLX's CPU backend is the planned CPU baseline; MLX does not exist
     for this platform, so the same op runs in PyTorch on the host cores: the
@@ -300,7 +331,23 @@ def bench_linear(args):
         out[M] = {"rmsnorm_us": round(tn * 1e6, 2), "rmsnorm_GBps": round(by_n / tn / 1e9, 1),
                   "linear_us": round(tl * 1e6, 2), "linear_GBps": round(by_l / tl / 1e9, 1),
                   "linear_frac_hbm": round(by_l / tl / PEAK_HBM, 4), "stock_linear_us": round(ts * 1e6, 2)}
-    return {"metric": METRIC, "op": "rmsnorm+linear (config 1)", "per_m": out}
+    cpu = None
+    if not args.no_cpu:
+        with _CpuThreads() as nth:
+            gc = torch.Generator().manual_seed(0)
+            Wc = (0.02 * torch.randn((N, K), generator=gc)).to(torch.bfloat16)
+            gc_ = (1 + 0.1 * torch.randn(K, generator=gc)).to(torch.bfloat16)
+            per_m = {}
+            for M in (1, 4, 16, 64, 256):
+                xc = torch.randn((M, K), generator=gc).to(torch.bfloat16)
+                t = _cpu_median(lambda: torch.nn.functional.linear(
+                    torch.nn.functional.rms_norm(xc, (K,), gc_, 1e-6), Wc))
+                by = per + 2 * M * (K + N) + 4 * M * K + 2 * K
+                per_m[M] = {"us": round(t * 1e6, 1), "GBps": round(by / t / 1e9, 2)}
+        cpu = {"value": per_m[1]["GBps"], "unit": "GB/s (algorithmic bytes, M=1)", "cores": nth, "kind": CPU_KIND,
+               "sample": f"full config-1 call (rms_norm then linear, bf16) at each M on {nth} threads, median of 20 "
+                         "after 3 warm-ups", "per_m": per_m}
+    return {"metric": METRIC, "op": "rmsnorm+linear (config 1)", "per_m": out, "cpu_baseline": cpu}
 
 
 def bench_rmsnorm(args):
@@ -378,7 +425,26 @@ def bench_decode(args):
         res[B] = {"us": round(t * 1e6, 2), "GBps": round(by / t / 1e9, 1), "frac_hbm": round(by / t / PEAK_HBM, 4),
                   "sum_len": int(lens.sum()), "per_key_order_us": None if tp is None else round(tp * 1e6, 2)}
         del k, v
-    return {"metric": METRIC, "op": "decode attention (config 3)", "per_b": res}
+    cpu = None
+    if not args.no_cpu:
+        # bounded sample: the first sequences of the B = 256 batch's lengths, one at a time
+        lens = np.random.default_rng(256).integers(1, 8193, size=256)[:4]
+        gc = torch.Generator().manual_seed(0)
+        with _CpuThreads() as nth:
+            tot_t, tot_b = 0.0, 0
+            for n in lens:
+                n = int(n)
+                qc = torch.randn((1, 32, 1, 128), generator=gc).to(torch.bfloat16)
+                kc = torch.randn((1, 8, n, 128), generator=gc).to(torch.bfloat16)
+                vc = torch.randn((1, 8, n, 128), generator=gc).to(torch.bfloat16)
+                tot_t += _cpu_median(lambda: torch.nn.functional.scaled_dot_product_attention(
+                    qc, kc, vc, scale=128 ** -0.5, enable_gqa=True))
+                tot_b += 4096 * n + 16384
+        cpu = {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s (algorithmic bytes)", "cores": nth,
+               "kind": CPU_KIND, "sample": f"sdpa decode (GQA 32/8, D 128, bf16) of the first 4 sequences of the "
+                                           f"B = 256 batch (lengths {[int(x) for x in lens]}), one call each, median "
+                                           f"of 20 after 3 warm-ups, summed: {tot_t * 1e3:.2f} ms"}
+    return {"metric": METRIC, "op": "decode attention (config 3)", "per_b": res, "cpu_baseline": cpu}
 
 
 def bench_prefill(args):
@@ -404,7 +470,20 @@ def bench_prefill(args):
         res[B] = {"ms": round(t * 1e3, 3), "TFLOPs": round(fl / t / 1e12, 1), "frac_mfma": round(fl / t / PEAK_BF16, 4),
                   "stock_sdpa_ms": None if ts is None else round(ts * 1e3, 3),
                   "per_key_order_ms": None if tp is None else round(tp * 1e3, 3)}
-    return {"metric": METRIC, "op": "prefill attention (config 4)", "per_b": res}
+    cpu = None
+    if not args.no_cpu:
+        gc = torch.Generator().manual_seed(0)
+        with _CpuThreads() as nth:
+            qc = torch.randn((1, 32, T, 128), generator=gc).to(torch.bfloat16)
+            kc = torch.randn((1, 8, T, 128), generator=gc).to(torch.bfloat16)
+            vc = torch.randn((1, 8, T, 128), generator=gc).to(torch.bfloat16)
+            t = _cpu_median(lambda: torch.nn.functional.scaled_dot_product_attention(
+                qc, kc, vc, is_causal=True, enable_gqa=True), warmup=1, runs=5)
+        fl = 4 * 32 * 128 * T * (T + 1) / 2
+        cpu = {"value": round(fl / t / 1e12, 3), "unit": "TFLOP/s (causal half)", "cores": nth, "kind": CPU_KIND,
+               "sample": f"sdpa causal prefill of one sequence (B = 1, T = {T}, GQA 32/8, D 128, bf16), median of "
+                         f"5 after 1 warm-up: {t * 1e3:.1f} ms"}
+    return {"metric": METRIC, "op": "prefill attention (config 4)", "per_b": res, "cpu_baseline": cpu}
 
 
 def bench_gemm(args):
@@ -472,6 +551,76 @@ def _llama_generate(model, prompt, steps):
     return ev[0].elapsed_time(ev[1]) * 1e-3, ev[2].elapsed_time(ev[3]) * 1e-3, out
 
 
+def _dequantized_copy(model):
+    """The stock 4-bit baseline as a serving stack runs it: every
+    QuantizedLinear's weight dequantized once into a plain bf16 nn.Linear
+    (hipBLASLt / rocBLAS per call), sharing everything else with ``model``."""
+    import copy
+
+    import torch
+    import mlx_batch_invariant_amd as bi
+    from mlx_batch_invariant_amd.nn import QuantizedLinear
+    m = copy.copy(model)
+    m._modules = dict(model._modules)
+
+    def swap(mod):
+        for name, child in list(mod._modules.items()):
+            if isinstance(child, QuantizedLinear):
+                lin = torch.nn.Linear(child.in_features, child.out_features, bias=child.bias is not None,
+                                      device="meta", dtype=child.scales.dtype)
+                W = bi.dequantize(child.weight, child.scales, child.biases, child.group_size, child.bits,
+                                  dtype=child.scales.dtype)
+                lin.weight = torch.nn.Parameter(W, requires_grad=False)
+                if child.bias is not None:
+                    lin.bias = torch.nn.Parameter(child.bias.detach(), requires_grad=False)
+                mod._modules[name] = lin
+            elif child is not None:
+                c = copy.copy(child)
+                c._modules = dict(child._modules)
+                mod._modules[name] = c
+                swap(c)
+
+    swap(m)
+    return m
+
+
+def cpu_baseline_llama(layers=2, T=512, steps=4):
+    """Bounded CPU sample of config 5: the bf16 Llama-3-8B-shape decoder with
+    ``layers`` of its 32 layers (embedding, final norm and the 128256-row head
+    included) in torch on the host cores: prefill of T random tokens at B = 1,
+    then ``steps`` greedy decode steps. Also the per-token time scaled to 32
+    layers from the measured per-layer cost (head and embedding once)."""
+    import torch
+    from mlx_batch_invariant_amd.llama import LlamaConfig, LlamaShaped
+    with _CpuThreads() as nth:
+        res = {}
+        for L in (1, layers):
+            cfg = LlamaConfig(layers=L, bits=None)
+            m = LlamaShaped(cfg, device="cpu", dtype=torch.bfloat16, seed=0)
+            prompt = torch.randint(0, cfg.vocab, (1, T), generator=torch.Generator().manual_seed(0))
+            cache = m.new_cache(1, T + steps)
+            t0 = time.perf_counter()
+            lg = m(prompt, cache, 0)
+            tp = time.perf_counter() - t0
+            tok = lg.argmax(-1, keepdim=True)
+            t0 = time.perf_counter()
+            for st in range(steps):
+                tok = m(tok, cache, T + st).argmax(-1, keepdim=True)
+            td = (time.perf_counter() - t0) / steps
+            res[L] = (tp, td)
+            del m, cache
+    (p1, d1), (pL, dL) = res[1], res[layers]
+    per_p, per_d = (pL - p1) / (layers - 1), (dL - d1) / (layers - 1)
+    p32, d32 = p1 + 31 * per_p, d1 + 31 * per_d
+    return {"value": round(1 / d32, 3), "unit": "decode tok/s at B=1 (32 layers, from the per-layer cost)",
+            "cores": nth, "kind": CPU_KIND,
+            "sample": f"bf16 decoder with 1 and {layers} layers (+ embedding, norm, head) on {nth} threads: prefill "
+                      f"{T} tokens {res[layers][0]:.2f} s, {steps} decode steps {res[layers][1] * 1e3:.0f} ms each "
+                      f"at {layers} layers; scaled to 32 layers: prefill {T / p32:.1f} tok/s, decode {1 / d32:.2f} "
+                      "tok/s",
+            "prefill_tok_s_32_layers": round(T / p32, 2)}
+
+
 def bench_llama(args):
     """random-init Llama-3-8B-shape decoder (32 layers),
     prefill of 512 random tokens then 128 greedy decode steps at batch 1, 4,
@@ -489,6 +638,7 @@ def bench_llama(args):
         model = LlamaShaped(cfg, device="cuda", dtype=torch.bfloat16, seed=0)
         g = torch.Generator().manual_seed(0)
         row0 = torch.randint(0, cfg.vocab, (1, T), generator=g)
+        stock_model = _dequantized_copy(model) if bits else model
         per_b, ref = {}, {}
         for B in batches:
             fill = torch.randint(0, cfg.vocab, (B - 1, T), generator=torch.Generator().manual_seed(B))
@@ -496,9 +646,10 @@ def bench_llama(args):
             entry = {}
             for label, on in (("invariant", True), ("stock", False)):
                 bi.reset_stats()
+                mdl = model if on else stock_model
                 with bi.set_batch_invariant_mode(enabled=on, strict=on):
-                    _llama_generate(model, prompt[:, :16], 2)          # warm-up
-                    tp, td, lg = _llama_generate(model, prompt, steps)
+                    _llama_generate(mdl, prompt[:, :16], 2)            # warm-up
+                    tp, td, lg = _llama_generate(mdl, prompt, steps)
                 ref.setdefault(label, lg)
                 entry[label] = {"prefill_tok_s": round(B * T / tp, 1), "decode_tok_s": round(B * steps / td, 1),
                                 "prefill_s": round(tp, 3), "decode_s": round(td, 3),
@@ -508,10 +659,14 @@ def bench_llama(args):
                 print(f"# llama {tag} B={B} {label}: {entry[label]}", file=sys.stderr, flush=True)
             per_b[B] = entry
         res[tag] = {"per_b": per_b,
-                    "bitwise_invariant_all_b": all(e["invariant"]["row0_logits_equal_B1"] for e in per_b.values())}
-        del model
+                    "bitwise_invariant_all_b": all(e["invariant"]["row0_logits_equal_B1"] for e in per_b.values()),
+                    "stock": "torch bf16 linears (hipBLASLt / rocBLAS)" + (
+                        " on weights dequantized once from the same 4-bit codes" if bits else "")
+                    + ", F.rms_norm, F.scaled_dot_product_attention; not batch invariant"}
+        del model, stock_model
         torch.cuda.empty_cache()
-    return {"metric": METRIC, "op": "Llama-3-8B-shape forward (config 5)",
+    cpu = None if args.no_cpu else cpu_baseline_llama()
+    return {"metric": METRIC, "op": "Llama-3-8B-shape forward (config 5)", "cpu_baseline": cpu,
             "config": {"workload": f"{args.llama_layers}-layer Llama-3-8B-shape decoder, prefill {T} tokens + "
                                    f"{steps} greedy decode steps, batch 1/4/16/64", "dtype": "bf16 activations"},
             "models": res}
@@ -531,13 +686,28 @@ def bench_copycal(args):
             "us": round(t * 1e6, 2), "GBps": round(2 * n / t / 1e9, 1)}
 
 
+def bench_sweep(args):
+    """Batch-sweep conformance (mlx_batch_invariant_amd.conformance, the
+    reference's harness/sweep.py): per op x dtype, stock torch and the
+    invariant mode, first diverging batch and max|diff|. The table goes to
+    stderr; the JSON line summarises it."""
+    from mlx_batch_invariant_amd import conformance
+    rep = conformance.run(file=sys.stderr)
+    stock = {f"{r['op']}/{r['dtype']}": (None if r["passed"] else {"first_fail_B": r["first_fail"],
+                                                                   "max_diff": r["max_diff"]})
+             for r in rep["rows"] if r["mode"] == "STOCK"}
+    return {"metric": METRIC, "op": "conformance sweep (stock vs invariant, batch 1-256)",
+            "invariant_all_pass": rep["invariant_all_pass"], "stock_divergence": stock,
+            "structure": rep["structure"], "batches": rep["batches"]}
+
+
 def main(argv=None) -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--op", default="qmm4", choices=["qmm4", "qmm8", "linear", "rmsnorm", "layernorm", "decode", "prefill", "gemm", "llama",
-                                                     "copycal", "all"])
+                                                     "copycal", "sweep", "all"])
     p.add_argument("--llama-layers", type=int, default=32)
     p.add_argument("--llama-prompt", type=int, default=512)
     p.add_argument("--llama-steps", type=int, default=128)
@@ -580,6 +750,8 @@ def main(argv=None) -> int:
             r = bench_llama(a)
         elif op == "copycal":
             r = bench_copycal(a)
+        elif op == "sweep":
+            r = bench_sweep(a)
         else:
             r = bench_gemm(a)
         r.setdefault("n_gpus", 1)
