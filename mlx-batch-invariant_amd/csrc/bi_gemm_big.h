@@ -77,32 +77,42 @@ constexpr int kBigMinTiles = 96;
 // WM = waves along M: 4 for the 256 x 128 tile (8 waves, two per SIMD), 2
 // for a 128 x 128 tile (4 waves, one per SIMD, 112 KB of LDS), which puts
 // twice as many workgroups on the chip when the 256-row tiles are fewer than
-// the CUs. Same per-wave 64 x 64 tile, same steps, same bits.
-template <int WM>
+// the CUs. BN = tile columns: 128 (64 x 64 per wave) or 64 (128 x 64 tiles,
+// 64 x 32 per wave, 80 KB of LDS: two workgroups per CU), which puts twice as
+// many workgroups again on the chip for mid-size M. Same steps per output
+// element, same bits.
+template <int WM, int BN = kBigBN>
 struct BigTile {
-  static constexpr int kBM = 64 * WM, kWaves = 2 * WM;
+  static constexpr int kBM = 64 * WM, kBN = BN, kWaves = 2 * WM;
+  static constexpr int kTJ = BN / 16 / kBigWavesN;     // column blocks of 16 per wave: 4 or 2
   static constexpr int kACopies = kBM / 8 / kWaves;   // 4
-  static constexpr int kBCopies = kBigBN / 8 / kWaves;  // 2 (WM = 4) or 4 (WM = 2)
+  static constexpr int kBCopies = BN / 8 / kWaves;     // 2 (WM = 4) or 4 (WM = 2, BN = 128) or 2 (BN = 64)
   static constexpr int kAStage = kBM * 64;
+  static constexpr int kBStage = BN * 64;
+  static constexpr int kLdsElems = kBigABufs * kAStage + kBigBBufs * kBStage;
   static_assert(WM == 2 || WM == 4, "gemm_big: 128- or 256-row tiles");
+  static_assert(BN == 128 || (BN == 64 && WM == 2), "gemm_big: 128 columns, or 64 with 128 rows");
 };
 static_assert(BigTile<4>::kBM == kBigBM && BigTile<4>::kWaves == kBigWaves && BigTile<4>::kACopies == kBigACopies &&
                   BigTile<4>::kBCopies == kBigBCopies,
               "gemm_big: the default tile is the 256 x 128 one");
 
-template <typename T, int WM = kBigWavesM>
-__global__ __launch_bounds__(64 * BigTile<WM>::kWaves) void gemm_big(const T* __restrict__ a, int64_t lda,
+template <int WM, int BN>
+constexpr int big_threads() { return 64 * BigTile<WM, BN>::kWaves; }
+
+template <typename T, int WM = kBigWavesM, int BN = kBigBN>
+__global__ __launch_bounds__((big_threads<WM, BN>())) void gemm_big(const T* __restrict__ a, int64_t lda,
                                                                      const T* __restrict__ bt, int64_t ldb,
                                                                      T* __restrict__ out, int M, int N, int K,
                                                                      int tiles_m, int tiles_n) {
   static_assert(sizeof(T) == 2, "gemm_big: 2-byte element types only");
   typedef typename Frag<T>::type F;
-  typedef BigTile<WM> BT;
+  typedef BigTile<WM, BN> BT;
   constexpr int kBM = BT::kBM, kWavesAll = BT::kWaves, kACop = BT::kACopies, kBCop = BT::kBCopies;
-  constexpr int kAStg = BT::kAStage;
-  constexpr int TI = kBigTI, TJ = kBigTJ, NT = TI * TJ, NCH = NT / 2;
+  constexpr int kAStg = BT::kAStage, kBStg = BT::kBStage;
+  constexpr int TI = kBigTI, TJ = BT::kTJ, NT = TI * TJ, NCH = NT / 2;
   static_assert(kACop <= NCH && kBCop <= NCH, "gemm_big: one copy per MFMA chunk at most");
-  __shared__ __attribute__((aligned(1024))) T lds[kBigABufs * kAStg + kBigBBufs * kBigBStage];
+  __shared__ __attribute__((aligned(1024))) T lds[BT::kLdsElems];
 
   const int tiles_total = tiles_m * tiles_n;
   const int groups = (K + kGroupK - 1) / kGroupK;
@@ -116,7 +126,7 @@ __global__ __launch_bounds__(64 * BigTile<WM>::kWaves) void gemm_big(const T* __
   const int first_m = (t / span) * kBigGroupM;
   const int gm = min(tiles_m - first_m, kBigGroupM);
   const int tm = first_m + (t % span) % gm, tn = (t % span) / gm;
-  const int m0 = tm * kBM, n0 = tn * kBigBN;
+  const int m0 = tm * kBM, n0 = tn * BN;
 
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -125,12 +135,12 @@ __global__ __launch_bounds__(64 * BigTile<WM>::kWaves) void gemm_big(const T* __
 
   // LDS element offset of row `row` of stage st (A rows 0..255, B rows 0..127).
   auto a_row = [&](int st, int row) { return (st % kBigABufs) * kAStg + row * 64; };
-  auto b_row = [&](int st, int row) { return kBigABufs * kAStg + (st % kBigBBufs) * kBigBStage + row * 64; };
+  auto b_row = [&](int st, int row) { return kBigABufs * kAStg + (st % kBigBBufs) * kBStg + row * 64; };
 
   // Copy c of this wave moves the 8-row block c * 8 + wave of A (or of B):
   // lane l takes row l / 8 of the block, chunk (l % 8) ^ (l / 8).
   const int rr = lane / 8, ch = (lane % 8) ^ rr;
-  const int rows_a = min(M - m0, kBM), rows_b = min(N - n0, kBigBN);
+  const int rows_a = min(M - m0, kBM), rows_b = min(N - n0, BN);
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a + (int64_t)m0 * lda), (short)0, (int)(rows_a * lda * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rb =

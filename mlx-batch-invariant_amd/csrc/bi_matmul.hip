@@ -64,7 +64,7 @@ extern "C" const char* bi_matmul_launch(int64_t M, int64_t N, int64_t K) {
   thread_local char name[64];
   if (M <= 0 || N <= 0 || K <= 0 || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL) return "other";
   const bi::BigPlan bp = bi::big_plan(M, N, K);
-  if (bp.use) return bp.half ? "big 128x128" : "big";
+  if (bp.use) return bp.form == bi::kBig128x64 ? "big 128x64" : bp.form == bi::kBig128x128 ? "big 128x128" : "big";
   const bi::TallPlan p = bi::tall_plan(M, N, K);
   if (!p.use) return "other";
   const bi::TallShape& t = bi::kTallShapes[p.tile];

@@ -584,68 +584,87 @@ static inline bool use_split(int64_t M, int G) { return M <= kSplitMMax && G > 1
 // 16-row tile); up to 64 KB of it. Larger K takes the split + fold launch.
 static inline bool use_wg(int64_t M, int G) { return M <= kSplitMMax && G * (M <= 16 ? 1 : 2) <= 64; }
 
-// Dense large tile (bi_gemm_big.h) for 2-byte types, K % 64 == 0: M > 256
-// with at least kBigMinTiles tiles of 256 x 128, or at least
-// kBigShortKMinTiles with at most 4 groups of K; 128 < M <= 256 with
-// kBigMinTiles tiles; and 64 < M <= 256 in its 128 x 128 form with
-// kBigHalfMinTiles of those (below). Other shapes take the tall tile (the
-// 256 x 128 tile measured slower there: Qwen2-0.5B [4864, 896] M = 256 16.9
-// against 12.1 us, [4096, 4096] M = 256 38.6 against 29.8 us with the large
-// tile's K split). A function of the shape only, so the workspace query and
-// the launch agree.
+// Dense large tile (bi_gemm_big.h) for 2-byte types, K % 64 == 0, M > 64, in
+// three forms: 256 x 128 (8 waves), 128 x 128 (4 waves, one per SIMD) and
+// 128 x 64 (4 waves, two workgroups per CU). The policy, a function of the
+// shape only (so the workspace query and the launch agree; bits never depend
+// on it):
+//   1. 128 x 64 when it has kBigNarrowMinTiles..kBigFitTiles tiles (at most one
+//      per CU) and K >= 768;
+//   2. else 128 x 128 when its tiles fit one per CU and either the 256 x 128
+//      rule below holds or 64 < M <= 256 with kBigHalfMinTiles tiles (K >=
+//      768, and not K < 1024 with a part-filled last row tile);
+//   3. else 256 x 128 from M = 129 with kBigMinTiles tiles, or M > 256 with
+//      kBigShortKMinTiles tiles and at most 4 groups of K.
+// Other shapes take the tall tile or the small-M launches. A tile's time is
+// nearly flat in the number of tiles up to one per CU, so the smallest form
+// that still fits the chip in one round wins. Measured on one MI355X, bf16
+// us, old policy -> this one (stock hipBLASLt):
+//   [4096, 4096]  M = 192 / 256 / 512 / 1024: 33.2 / 37.2 / 90.0 / 39.6 ->
+//                 25.7 / 27.1 / 27.5 / 38.1 (- / - / 31.4 / 41.6);
+//   [4096, 14336] M = 192 / 512 / 1024: 109.3 / 310.1 / 139.5 -> 82.2 / 94.7 /
+//                 135.2 (- / 89.0 / 130.4);
+//   [14336, 4096] M = 80 / 128 / 256: 38.5 / 44.0 / 43.7 -> 30.6 / 32.6 / 42.9;
+//   [6144, 4096]  M = 128 / 256 / 512: 38.7 / 38.0 / 39.4 -> 27.9 / 27.8 / 38.6;
+//   [4864, 896]   M = 128 / 192 / 256: 10.3 / 10.8 / 13.6 -> 9.3 / 8.9 / 9.4;
+//   [1024, 4096]  M = 768 / 1024 / 2048: 68.6 / 68.6 / 88.2 -> 26.1 / 25.7 / 26.5
+//                 (20.5 / 21.1 / -).
+// With 64 tiles of 128 x 64 or fewer the tall tile (with K chunks) is faster
+// ([4096, 4096] M = 128: 25.0 against 27.0; [1024, 4096] M = 384: 23.5
+// against 25.9), and a 128 x 64 tiling with more tiles than CUs is slower than
+// the 128 x 128 one ([14336, 4096] M = 192: 47.8 against 40.8).
 constexpr int kBigFromM = 129;
 constexpr int kBigShortKMinTiles = 32;
 constexpr int kTallMaxM = 256;
-// When its 128 x 128 tiles fit the chip's 256 CUs in one round, the large
-// tile runs as 128 x 128 tiles (gemm_big<T, 2>: twice the workgroups, one wave
-// per SIMD). Same bits either way. Measured, bf16 [14336, 4096] M = 192 / 256:
-// 47.4-48.0 / 48.6-48.7 -> 35.1-35.6 / 36.3 us (stock hipBLASLt 43-46 at 256);
-// [12416, 960] 16.8 / 17.4 -> 13.0 / 13.5 us; with more tiles than CUs (M =
-// 384 / 512) it measured 20-35% slower, so those keep the 256-row tile.
-constexpr int kBigHalfMaxTiles = 256;
-// 64 < M <= 256 (the tall tile's range) takes the 128 x 128 tile from this
-// many tiles on: bf16 us, tall -> 128 x 128 (same box):
-//   [14336, 4096] M = 80 / 96 / 128: 53.0 / 53.0 / 54.0 -> 32.5 / 32.7 / 33.2;
-//   [11008, 4096] M = 96 / 192 / 256: 41.2 / 84.6 / 88.4 -> 32.1 / 33.9 / 34.4;
-//   [8192, 4096] M = 192 / 256: 42.2 / 55.5 -> 32.6 / 32.8;
-//   [6144, 4096] M = 192 / 256: 40.0 / 41.8 -> 32.1 / 32.6;
-//   [4096, 14336] M = 192 / 256: 98.6 / 108.5 -> 93.0 / 93.8;
-//   [4096, 4096] M = 192 / 256: 32.2 / 33.4 -> 31.1 / 31.5;
-//   [6144, 1024] M = 192 / 256: 13.1 / 13.7 -> 12.2 / 12.3;
-//   [11008, 2048] M = 192 / 256: 46.0 / 48.1 -> 20.0 / 20.4;
-//   [4864, 896] M = 256: 13.0 -> 12.1, but M = 192: 11.2 -> 12.0 (short K
-//   and a half-filled last row tile keep the tall tile).
+constexpr int kBigFitTiles = 256;
+constexpr int kBigNarrowMinTiles = 72;
 constexpr int kBigHalfMinTiles = 48;
-static inline int64_t big_half_tiles(int64_t M, int64_t N) {
-  return (int64_t)ceil_div(M, (int64_t)BigTile<2>::kBM) * ceil_div(N, (int64_t)kBigBN);
+enum BigForm { kBig256x128 = 0, kBig128x128 = 1, kBig128x64 = 2 };
+constexpr int kBigFormRows[3] = {256, 128, 128};
+constexpr int kBigFormCols[3] = {128, 128, 64};
+static inline int64_t big_form_tiles(int64_t M, int64_t N, int form) {
+  return (int64_t)ceil_div(M, kBigFormRows[form]) * ceil_div(N, kBigFormCols[form]);
 }
 struct BigPlan {
   bool use = false;
-  bool half = false;  // 128-row tiles
+  int form = kBig256x128;
   int tiles_m = 0, tiles_n = 0;
 };
 static inline BigPlan big_plan(int64_t M, int64_t N, int64_t K) {
   BigPlan p;
   if (M <= 64 || N <= 0 || K <= 0 || K % 64) return p;
-  p.tiles_m = ceil_div(M, kBigBM);
-  p.tiles_n = ceil_div(N, kBigBN);
-  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-  p.use = M >= kBigFromM &&
-          (tiles >= kBigMinTiles || (M > kTallMaxM && K <= 4 * kGroupK && tiles >= kBigShortKMinTiles));
-  const int64_t ht = big_half_tiles(M, N);
-  // 64 < M <= 256 with enough 128 x 128 tiles: the half tile instead of the
-  // tall one, except at short K with a part-filled last row tile.
-  const bool half_mid = M > 64 && M <= kTallMaxM && ht >= kBigHalfMinTiles && K >= 768 &&
-                        !(K < 1024 && M % BigTile<2>::kBM != 0);
-  if ((p.use && ht <= kBigHalfMaxTiles) || (!p.use && half_mid)) {
-    p.use = true;
-    p.half = true;
-    p.tiles_m = ceil_div(M, BigTile<2>::kBM);
-  }
+  const int64_t t256 = big_form_tiles(M, N, kBig256x128), t128 = big_form_tiles(M, N, kBig128x128),
+                t64 = big_form_tiles(M, N, kBig128x64);
+  const bool full = M >= kBigFromM &&
+                    (t256 >= kBigMinTiles || (M > kTallMaxM && K <= 4 * kGroupK && t256 >= kBigShortKMinTiles));
+  const bool half_mid = M <= kTallMaxM && t128 >= kBigHalfMinTiles && K >= 768 &&
+                        !(K < 1024 && M % kBigFormRows[kBig128x128] != 0);
+  if (t64 >= kBigNarrowMinTiles && t64 <= kBigFitTiles && K >= 768) p.form = kBig128x64;
+  else if (t128 <= kBigFitTiles && (full || half_mid)) p.form = kBig128x128;
+  else if (full) p.form = kBig256x128;
+  else return p;
+  p.use = true;
+  p.tiles_m = ceil_div(M, kBigFormRows[p.form]);
+  p.tiles_n = ceil_div(N, kBigFormCols[p.form]);
   return p;
 }
 
-// Dense mid-M launch (bi_gemm_tall.h) for 2-byte types: 16 < M <= 256,
+// Launch of a planned large-tile call (tile index order: bi_gemm_big.h).
+template <typename T>
+static void launch_big(const BigPlan& bp, const T* a, int64_t lda, const T* bt, int64_t ldb, T* out, int M, int N,
+                       int K, hipStream_t st) {
+  const int work = bp.tiles_m * bp.tiles_n, grid = ((work + 7) / 8) * 8;
+  if (bp.form == kBig128x64)
+    gemm_big<T, 2, 64><<<grid, big_threads<2, 64>(), 0, st>>>(a, lda, bt, ldb, out, M, N, K, bp.tiles_m,
+                                                              bp.tiles_n);
+  else if (bp.form == kBig128x128)
+    gemm_big<T, 2><<<grid, big_threads<2, kBigBN>(), 0, st>>>(a, lda, bt, ldb, out, M, N, K, bp.tiles_m,
+                                                              bp.tiles_n);
+  else
+    gemm_big<T><<<grid, big_threads<4, kBigBN>(), 0, st>>>(a, lda, bt, ldb, out, M, N, K, bp.tiles_m, bp.tiles_n);
+}
+
+// Dense mid-M launch (bi_gemm_tall.h) for 2-byte types: 16 < M <= 1024,
 // K % 64 == 0, where the large tile is not used. Tile configurations (rows
 // x columns, k per stage, ring cap): a ring of 3-6 stages leaves LDS for 1-3
 // workgroups per CU, which measured faster than one workgroup with the
@@ -689,10 +708,14 @@ struct TallPlan {
 // 2% of the best configuration tried on average, 10-30% faster than one
 // workgroup per CU with the deepest ring.
 constexpr int kTallMinTiles = 200;
+// Up to this M the tall tile also serves the shapes the large tile leaves out
+// (few output columns: [1024, 4096] M = 384 / 512 23.5 / 24.9 us, [896, 4864]
+// 24.8 / 29.1 us, where the generic LDS tile took 68-80 us).
+constexpr int kTallPlanMaxM = 1024;
 constexpr int kTallMinTilesShortK = 100;
 static inline TallPlan tall_plan(int64_t M, int64_t N, int64_t K) {
   TallPlan p;
-  if (M <= 16 || M > kTallMaxM || N <= 0 || K <= 0 || K % 64) return p;
+  if (M <= 16 || M > kTallPlanMaxM || N <= 0 || K <= 0 || K % 64) return p;
   if (big_plan(M, N, K).use) return p;
   const int G = ceil_div(K, kGroupK);
   const bool k128 = K % 128 == 0;
@@ -1006,13 +1029,7 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   if constexpr (sizeof(T) == 2 && std::is_same<BSrc, DenseB<T>>::value) {
     const BigPlan bp = big_plan(M, N, K);
     if (bp.use && lda < kBigMaxLd && bsrc.ldb < kBigMaxLd) {
-      const int work = bp.tiles_m * bp.tiles_n;
-      if (bp.half)
-        gemm_big<T, 2><<<((work + 7) / 8) * 8, 64 * BigTile<2>::kWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M,
-                                                                                N, K, bp.tiles_m, bp.tiles_n);
-      else
-        gemm_big<T><<<((work + 7) / 8) * 8, 64 * kBigWaves, 0, st>>>(a, lda, bsrc.bt, bsrc.ldb, out, M, N, K,
-                                                                    bp.tiles_m, bp.tiles_n);
+      launch_big<T>(bp, a, lda, bsrc.bt, bsrc.ldb, out, M, N, K, st);
       return bi_host::launch_status(what);
     }
     const TallPlan tp = tall_plan(M, N, K);
@@ -1071,17 +1088,7 @@ int run_quant(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
       bi::qmm_dequant_rows<T, BITS, GS><<<(unsigned)((nb + 255) / 256), 256, 0, st>>>(
           w, static_cast<const T*>(scales), static_cast<const T*>(biases), bq, N, K);
       bi::qmm_permute_a<T><<<(unsigned)((na + 255) / 256), 256, 0, st>>>(static_cast<const T*>(x), ldx, ap, M, K);
-      const int tn = ceil_div(N, bi::kBigBN);
-      if (bi::big_half_tiles(M, N) <= bi::kBigHalfMaxTiles) {  // as the dense policy
-        const int tmm = ceil_div(M, bi::BigTile<2>::kBM);
-        const int grid = ((tmm * tn + 7) / 8) * 8;
-        bi::gemm_big<T, 2><<<grid, 64 * bi::BigTile<2>::kWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), M, N,
-                                                                         K, tmm, tn);
-      } else {
-        const int tmm = ceil_div(M, bi::kBigBM);
-        const int grid = ((tmm * tn + 7) / 8) * 8;
-        bi::gemm_big<T><<<grid, 64 * bi::kBigWaves, 0, st>>>(ap, K, bq, K, static_cast<T*>(out), M, N, K, tmm, tn);
-      }
+      bi::launch_big<T>(bi::big_plan(M, N, K), ap, K, bq, K, static_cast<T*>(out), M, N, K, st);  // as the dense policy
       return bi_host::launch_status("bi_quantized_matmul");
     }
   }

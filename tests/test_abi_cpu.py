@@ -71,28 +71,35 @@ def test_workspace_sizes():
 
 def test_dense_launch_policy():
     """The dense mid/large-M launch per shape (a diagnostic of the policy; the
-    bits never depend on it): the tall tile up to M = 256 unless the 256 x 128
-    tile has >= 96 tiles, ring-capped configurations chosen by how full they
-    leave the chip's workgroup slots, K split only for long K with too few
-    tiles."""
+    bits never depend on it): the smallest large-tile form whose tiles fit one
+    per CU (128 x 64 from 72 tiles, then 128 x 128, then 256 x 128), the tall
+    tile below that (up to M = 1024) with ring-capped configurations chosen by
+    how full they leave the chip's workgroup slots, K split only for long K
+    with too few tiles."""
     lib = _lib.load()
     name = lambda M, N, K: lib.bi_matmul_launch(M, N, K).decode()
-    assert name(256, 4864, 896) == "big 128x128"                # Qwen2-0.5B linear, M = 256: 76 tiles of 128 x 128
-    assert name(192, 4864, 896) == "tall 64x32 k128 r3 c1"      # short K, half-filled last row tile
-    assert name(64, 4864, 896) == "tall 32x32 k128 r4 c1"
+    assert name(256, 4864, 896) == "big 128x64"                 # Qwen2-0.5B linear, M = 256: 152 tiles of 128 x 64
+    assert name(192, 4864, 896) == "big 128x64"
+    assert name(64, 4864, 896) == "tall 32x32 k128 r4 c1"       # M <= 64: never the large tile
     assert name(32, 14336, 4096) == "tall 32x64 k128 r4 c1"     # M <= 32: widest tile with >= 200
     assert name(32, 4096, 4096) == "tall 32x32 k128 r4 c2"
-    assert name(128, 14336, 4096) == "big 128x128"              # 112 tiles of 128 x 128
-    assert name(128, 4096, 4096) == "tall 32x32 k128 r4 c1"     # 32 tiles of 128 x 128: too few
-    assert name(256, 4096, 4096) == "big 128x128"               # 64 tiles of 128 x 128
+    assert name(128, 14336, 4096) == "big 128x64"               # 224 tiles of 128 x 64
+    assert name(128, 4096, 4096) == "tall 32x32 k128 r4 c1"     # 64 tiles of 128 x 64: too few
+    assert name(256, 4096, 4096) == "big 128x64"                # 128 tiles of 128 x 64
+    assert name(512, 4096, 4096) == "big 128x64"                # config-5 prefill at B = 1: 256 tiles
+    assert name(512, 4096, 14336) == "big 128x64"
+    assert name(768, 4096, 4096) == "big 128x128"               # 384 tiles of 128 x 64 > 256; 192 of 128 x 128
+    assert name(2048, 4096, 4096) == "big"                      # 512 tiles of 128 x 128: more than one round
     assert name(192, 896, 4864) == "tall 64x32 k128 r3 c4"
-    assert name(192, 14336, 4096) == "big 128x128"               # 112 tiles of 256 x 128; 224 of 128 x 128 fit 256 CUs
-    assert name(384, 14336, 4096) == "big"                       # 336 tiles of 128 x 128: more than one round
+    assert name(192, 14336, 4096) == "big 128x128"              # 448 tiles of 128 x 64; 224 of 128 x 128
+    assert name(384, 14336, 4096) == "big"                      # 336 tiles of 128 x 128: more than one round
     assert name(300, 12416, 960) == "big"
-    assert name(256, 3328, 576) == "tall 32x64 k64 r5 c1"       # K % 128 != 0: 64-k stages
-    assert name(16, 4864, 896) == "other"                        # small-M launches
-    assert name(300, 4096, 4096) == "other"                      # M > 256 with < 96 tiles: LDS tiles
-    assert name(200, 4864, 900) == "other"                       # K % 64 != 0
+    assert name(256, 3328, 576) == "tall 32x64 k64 r5 c1"       # K % 128 != 0: 64-k stages; K < 768: no large tile
+    assert name(512, 1024, 4096) == "tall 32x32 k128 r4 c1"     # 64 tiles of 128 x 64: the tall tile up to M = 1024
+    assert name(768, 1024, 4096) == "big 128x64"                # 96 tiles of 128 x 64
+    assert name(16, 4864, 896) == "other"                       # small-M launches
+    assert name(2048, 128, 512) == "other"                      # M > 1024 with few tiles: LDS tiles
+    assert name(200, 4864, 900) == "other"                      # K % 64 != 0
     assert name(0, 10, 10) == "other"
 
 

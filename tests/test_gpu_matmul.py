@@ -148,6 +148,32 @@ def test_matmul_large_half_tiles_agree(dt, K):
     assert_bits_equal(to_np(big[rows]), ora.matmul(to_np(x[rows]), to_np(W), dt), f"{dt} K={K}")
 
 
+@pytest.mark.parametrize("M,N,K,launch", [(80, 14336, 4096, "big 128x64"), (128, 14336, 4096, "big 128x64"),
+                                          (128, 4864, 896, "big 128x64"), (512, 4096, 4096, "big 128x64"),
+                                          (512, 4096, 14336, "big 128x64"), (768, 4096, 4096, "big 128x128"),
+                                          (768, 1024, 4096, "big 128x64"), (512, 1024, 4096, "tall 32x32 k128 r4 c1"),
+                                          (384, 896, 4864, "tall 32x32 k128 r4 c1")])
+def test_matmul_mid_m_large_tile_forms(M, N, K, launch):
+    """The 128 x 64 and 128 x 128 large-tile forms and the tall tile above
+    M = 256 at the Llama / Qwen2 shapes that select them (config-5 prefill at
+    B = 1 is M = 512): sampled rows (first, last, both sides of the 128-row
+    tile edge) equal the same rows computed alone (the decode launches) and
+    the oracle on a column sample, bit for bit."""
+    lib = _bi()._lib.load()
+    assert lib.bi_matmul_launch(M, N, K).decode() == launch
+    g = gen(M + N + 3 * K)
+    W = randn((N, K), torch.bfloat16, g, scale=0.02)
+    x = randn((M, K), torch.bfloat16, g)
+    full = _mm(x, W.t())
+    rows = sorted(r for r in {0, 1, 63, 64, 127, 128, M // 2, M - 1} if r < M)   # in range for every M
+    cols = np.r_[0:32, 60:70, N // 2:N // 2 + 32, N - 32:N]
+    want = ora.matmul(to_np(x[rows]), to_np(W)[cols], "bf16")
+    assert_bits_equal(to_np(full)[rows][:, cols], want, launch)
+    for r in rows:
+        assert bits(_mm(x[r:r + 1], W.t())) == bits(full[r:r + 1]), r
+    assert bits(_mm(x[M - 40:], W.t())) == bits(full[M - 40:])
+
+
 def test_matmul_layouts_and_leading_dims():
     g = gen(7)
     a = randn((2, 3, 200), torch.bfloat16, g)
