@@ -74,18 +74,6 @@ __device__ __forceinline__ float pk_score(const float (&qs)[DL], const float (&k
 }
 
 template <int DL>
-__device__ __forceinline__ void pk_key_update(float s, const float (&v)[DL], float& m, float& l,
-                                              float (&acc)[DL]) {
-  const float m_new = fmaxf(m, s);
-  const float corr = exp_cr(m - m_new);
-  const float p = exp_cr(s - m_new);
-  l = __builtin_fmaf(l, corr, p);
-#pragma unroll
-  for (int d = 0; d < DL; ++d) acc[d] = __builtin_fmaf(acc[d], corr, p * v[d]);
-  m = m_new;
-}
-
-template <int DL>
 __device__ __forceinline__ void pk_merge(float& M, float& L, float* A, float m, float l, const float* acc) {
   const float M_new = fmaxf(M, m);
   const float c_old = exp_cr(M - M_new);
@@ -112,11 +100,25 @@ __device__ __forceinline__ void pk_load_q(const T* row, float scale, float (&qs)
 // Keys [j0, j1) of (sequence b, kv head hk) for NQ queries; query iq takes
 // key j only if j < nkeys[iq] (its score is still computed: every lane of
 // the half-wave takes part in the butterfly).
+//
+// A block of AH keys is evaluated in three passes with the recurrence's own
+// values and order:
+//   1. the scores of every (key, query) (each lane ends up with all of them);
+//   2. per query, key by key: m' = max(m, s) for its active keys, and the two
+//      exp arguments m - m' and s - m' (the maxima depend on the scores only);
+//   3. every exp of the block once, one argument per lane of the half-wave
+//      (all 32 lanes hold the same arguments), then back to every lane by a
+//      shuffle, and the updates l = fma(l, corr, p), acc = fma(acc, corr, p v)
+//      in key order.
+// The same numbers as evaluating the recurrence key by key on every lane
+// (which computed each exp 32 times).
 template <typename T, int DL, int NQ, class Args>
 __device__ __forceinline__ void pk_span(const Args& a, int b, int hk, int lane, int j0, int j1,
                                         const float (&qs)[NQ][DL], const int (&nkeys)[NQ], float (&m)[NQ],
                                         float (&l)[NQ], float (&acc)[NQ][DL]) {
   constexpr int AH = pk_ahead<DL>();
+  constexpr int NE = 2 * AH * NQ;              // exp arguments per block: (corr, p) per (key, query)
+  constexpr int ROUNDS = (NE + 31) / 32;       // exps per lane per block
   const T* kbase = static_cast<const T*>(a.k) + lane * DL;
   const T* vbase = static_cast<const T*>(a.v) + lane * DL;
   for (int j = j0; j < j1; j += AH) {
@@ -127,13 +129,42 @@ __device__ __forceinline__ void pk_span(const Args& a, int b, int hk, int lane, 
       pk_load<T, DL>(kbase + kv_row_off(a, a.k_sb, a.k_sh, a.k_sl, b, hk, jj), kr[u]);
       pk_load<T, DL>(vbase + kv_row_off(a, a.v_sb, a.v_sh, a.v_sl, b, hk, jj), vr[u]);
     }
+    // Passes 1 and 2: scores, running maxima, and this lane's exp arguments
+    // (argument 2 (u NQ + iq) is corr, + 1 is p; lane i of round r takes
+    // argument 32 r + i).
+    float ein[ROUNDS];
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) ein[r] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < AH; ++u) {
+#pragma unroll
+      for (int iq = 0; iq < NQ; ++iq) {
+        const float s = pk_score<DL>(qs[iq], kr[u]);
+        const bool act = j + u < j1 && j + u < nkeys[iq];
+        const float m_new = act ? fmaxf(m[iq], s) : m[iq];
+        const int i = 2 * (u * NQ + iq);
+        if (lane == i % 32) ein[i / 32] = m[iq] - m_new;
+        if (lane == (i + 1) % 32) ein[(i + 1) / 32] = s - m_new;
+        m[iq] = m_new;
+      }
+    }
+    float e[ROUNDS];
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) e[r] = exp_cr(ein[r]);
+    // Pass 3: the updates in key order.
 #pragma unroll
     for (int u = 0; u < AH; ++u) {
       if (j + u >= j1) break;
 #pragma unroll
       for (int iq = 0; iq < NQ; ++iq) {
-        const float s = pk_score<DL>(qs[iq], kr[u]);
-        if (j + u < nkeys[iq]) pk_key_update<DL>(s, vr[u], m[iq], l[iq], acc[iq]);
+        const int i = 2 * (u * NQ + iq);
+        const float corr = __shfl(e[i / 32], i % 32, 32);
+        const float p = __shfl(e[(i + 1) / 32], (i + 1) % 32, 32);
+        if (j + u < nkeys[iq]) {
+          l[iq] = __builtin_fmaf(l[iq], corr, p);
+#pragma unroll
+          for (int d = 0; d < DL; ++d) acc[iq][d] = __builtin_fmaf(acc[iq][d], corr, p * vr[u][d]);
+        }
       }
     }
   }

@@ -70,12 +70,8 @@ __global__ __launch_bounds__(256) void qmm_permute_a(const T* __restrict__ a, in
       *reinterpret_cast<const u32x4*>(a + (int64_t)m * lda + g * kGroupK + 8 * blocked_chunk(cn));
 }
 
-// Large-M quantized launch: the same shapes as the dense large tile
-// (K % 256 == 0, M >= kBigMinM, >= kBigMinTiles tiles), 2-byte T.
-inline bool qmm_use_big(int64_t M, int64_t N, int64_t K, int elem_bytes) {
-  const int64_t tiles = ((M + kBigBM - 1) / kBigBM) * ((N + kBigBN - 1) / kBigBN);
-  return elem_bytes == 2 && M >= kBigMinM && K % kGroupK == 0 && tiles >= kBigMinTiles && K < kBigMaxLd;
-}
+// The shapes that take this launch (qmm_use_big) are defined with the dense
+// policy in bi_matmul_impl.h.
 
 inline size_t qmm_big_ws_bytes(int64_t M, int64_t N, int64_t K) { return (size_t)((N + M) * K) * 2; }
 

@@ -59,9 +59,10 @@ def test_workspace_sizes():
     assert lib.bi_quantized_matmul_workspace_bytes(800, 14336, 1024) == (14336 + 800) * 1024 * 2
     assert lib.bi_quantized_matmul_workspace_bytes(2048, 4096, 4096) == (4096 + 2048) * 4096 * 2
     assert lib.bi_quantized_matmul_workspace_bytes(300, 14336, 4096) == (14336 + 300) * 4096 * 2
-    # below the large-tile threshold (M < 256, or < 96 tiles of 256 x 128) or K not whole groups: none
+    assert lib.bi_quantized_matmul_workspace_bytes(300, 4096, 4096) == (4096 + 300) * 4096 * 2   # 128 x 64 form
+    assert lib.bi_quantized_matmul_workspace_bytes(512, 1024, 4096) == (1024 + 512) * 4096 * 2   # unsplit tall
+    # below M = 256 (the mid-M launches) or K not whole groups: none
     assert lib.bi_quantized_matmul_workspace_bytes(200, 14336, 4096) == 0
-    assert lib.bi_quantized_matmul_workspace_bytes(300, 4096, 4096) == 0
     assert lib.bi_quantized_matmul_workspace_bytes(2048, 4096, 4000) == 0
     ns = (8192 + 255) // 256
     bh = 256 * 32 * ns

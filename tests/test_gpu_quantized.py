@@ -186,6 +186,32 @@ def test_quantized_large_m_launch_agrees(bits_, gs, dt, M):
     assert_bits_equal(to_np(full)[rows][:, cols], want, f"{dt} large M")
 
 
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128)])
+@pytest.mark.parametrize("N,K", [(4096, 4096), (1024, 4096), (4096, 14336)])
+def test_quantized_prefill_m512_launch_agrees(bits_, gs, N, K):
+    """Config-5 prefill at B = 1 (M = 512) at the Llama projection shapes:
+    the weight dequantized once into the workspace, then the dense policy's
+    launch (the 128 x 64 large tile for N = 4096, the unsplit tall tile for
+    N = 1024). Sampled rows equal the same rows computed alone (the GEMV) and
+    the oracle, bit for bit."""
+    M = 512
+    from mlx_batch_invariant_amd import _lib
+    assert _lib.load().bi_quantized_matmul_workspace_bytes(M, N, K) == (N + M) * K * 2
+    wq, s, b = _qweights(N, K, bits_, gs, "bf16", seed=bits_ + N + K)
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    x = randn((M, K), torch.bfloat16, gen(N + K))
+    run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+    got = run(x)
+    W = ora.dequantize(wq.cpu().view(torch.int32).numpy().view(np.uint32), to_np(s.cpu()), to_np(b.cpu()),
+                       gs, bits_, "bf16")
+    rows = [0, 127, 128, 300, 511]
+    cols = np.r_[0:24, N // 2:N // 2 + 24, N - 24:N]
+    want = ora.matmul(to_np(x[rows]), W[cols], "bf16", kmap="blocked")
+    assert_bits_equal(to_np(got)[rows][:, cols], want, f"M=512 N={N} K={K}")
+    for r in rows:
+        assert bits(got[r:r + 1]) == bits(run(x[r:r + 1])), r
+
+
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
 def test_quantized_batch_invariant_llama_mlp(bits_, gs):
     """W [14336, 4096], x [M, 4096], M in 1..64 (and beyond)."""
