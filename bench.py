@@ -38,7 +38,7 @@ PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 # on a 256 MiB device copy (bench.py --op copycal): read x 2.000, write x 1.000.
 # Source: profiles/qmatmul4_g64_llama_mlp_m1.txt. Re-measure after changing
 # the kernel.
-MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 16210.5, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
+MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 16213.0, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
 PEAK_BF16 = 2.5e15         # FLOP/s, dense bf16 MFMA
 METRIC = "% of HBM/MFMA roofline per op at batch 1–256, with bitwise batch invariance"
 ROTATE_BYTES = 512 << 20
@@ -168,6 +168,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     achieved = by1 / t_med
     cpu = None if args.no_cpu else cpu_baseline_qmm(bits, gs)
     cpu_oracle = None if args.no_cpu else cpu_oracle_qmm(bits, gs)
+    achievable = None if args.headline_only else stream_read_rate(per, args)
     traffic = None
     if bits == 4 and gs == 64:
         mt = MEASURED_TRAFFIC_QMM4_M1
@@ -187,7 +188,13 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
                      "traffic_source": None if traffic is None else
                      "rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch x copy-kernel scale (bytes per launch)",
-                     "algorithmic_bytes": by1, "kernel": HEADLINE_KERNEL[(bits, gs)]},
+                     "algorithmic_bytes": by1, "kernel": HEADLINE_KERNEL[(bits, gs)],
+                     "achievable": None if achievable is None else {
+                         "value": round(achievable / 1e9, 1), "unit": "GB/s",
+                         "frac_of_peak": round(achievable / PEAK_HBM, 4),
+                         "frac_achieved_of_achievable": round(by1 / t_med / achievable, 4),
+                         "kernel": "bi_stream_read: a plain read of the same bytes in one launch (1 KB per wave "
+                                   "instruction), graph-replayed over the same rotation"}},
         "per_m": table,
         "bitwise_invariant_M1_vs_all": inv,
         "stock_gpu": {"dequant_plus_matmul_us": None if stock_deq is None else round(stock_deq * 1e6, 2),
@@ -196,6 +203,27 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
         "cpu_baseline": cpu,
         "cpu_oracle": cpu_oracle,
     }
+
+
+def stream_read_rate(nbytes, args):
+    """Achievable HBM read rate for one launch over `nbytes`: bi_stream_read
+    (a plain read, 1 KB per wave instruction) graph-replayed like the op,
+    over enough distinct buffers (>= 512 MB) that every launch reads HBM."""
+    import torch
+    from mlx_batch_invariant_amd import _lib
+    lib = _lib.load()
+    nbytes = nbytes // 16 * 16
+    ncopy = max(1, math.ceil(ROTATE_BYTES / nbytes))
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device="cuda") for _ in range(ncopy)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+
+    def call(i):
+        _lib.check(lib.bi_stream_read(bufs[i].data_ptr(), nbytes, sink.data_ptr(), 0x9E3779B9,
+                                      _lib.stream_of(sink)), "bi_stream_read")
+
+    t = statistics.median(_time_calls(call, args.steps, args.warmup, ncopy))
+    del bufs
+    return nbytes / t
 
 
 def cpu_threads() -> int:
@@ -503,7 +531,16 @@ def bench_gemm(args):
         res[M] = {"ms": round(t * 1e3, 3), "TFLOPs": round(fl / t / 1e12, 1), "frac_mfma": round(fl / t / PEAK_BF16, 4),
                   "stock_ms": None if ts is None else round(ts * 1e3, 3),
                   "stock_TFLOPs": None if ts is None else round(fl / ts / 1e12, 1)}
-    return {"metric": METRIC, "op": "bf16 GEMM (large M)", "per_m": res}
+    achievable = None
+    if not args.headline_only:
+        n = 8192
+        a = torch.randn((n, n), generator=g).to(torch.bfloat16).cuda()
+        b = torch.randn((n, n), generator=g).to(torch.bfloat16).cuda()
+        t = statistics.median(_time_calls(lambda i: torch.matmul(a, b), 5, 2, 1))
+        achievable = {"value": round(2 * n ** 3 / t / 1e12, 1), "unit": "TFLOP/s",
+                      "frac_of_peak": round(2 * n ** 3 / t / PEAK_BF16, 4),
+                      "kernel": "torch.matmul (hipBLASLt) bf16 8192 x 8192 x 8192, the achievable dense MFMA rate"}
+    return {"metric": METRIC, "op": "bf16 GEMM (large M)", "per_m": res, "achievable": achievable}
 
 
 def _llama_generate(model, prompt, steps):

@@ -259,6 +259,13 @@ int bi_attn_prefill_per_key(const void* q, const void* k, const void* v, const i
  * of that order can use the hardware's values. */
 int bi_exp2_f32(const float* x, float* y, int64_t n, void* stream);
 
+/* Diagnostic, no counterpart in the reference: one pass over `bytes` (a
+ * multiple of 16, 16-byte aligned) of device memory at src in one launch,
+ * every wave reading whole 1 KB chunks; writes sink[0] only in the unlikely
+ * case that a thread's xor of its data equals magic. The achievable-bandwidth
+ * reference for the HBM-bound kernels (same bytes, one launch). */
+int bi_stream_read(const void* src, int64_t bytes, uint32_t* sink, uint32_t magic, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

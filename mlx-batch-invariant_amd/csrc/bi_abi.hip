@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+
 #include "bi_common.h"
 
 namespace {
@@ -39,3 +41,48 @@ int launch_status(const char* what) {
 
 extern "C" int bi_abi_version(void) { return BI_ABI_VERSION; }
 extern "C" const char* bi_last_error(void) { return g_last_error; }
+
+// ---------------------------------------------------------------------------
+// Achievable-bandwidth probe (a diagnostic, no counterpart in the reference):
+// one pass over `bytes` of device memory, each wave reading whole 1 KB chunks
+// (lane l: bytes 16 l .. 16 l + 15 of the chunk), up to kReadAhead chunks per
+// wave requested before any is used. Nothing is written unless the xor of a
+// thread's data equals `magic` (a value the caller picks), so the loads cannot
+// be elided and the pass costs the reads alone.
+// ---------------------------------------------------------------------------
+namespace bi {
+constexpr int kReadAhead = 8;
+__global__ __launch_bounds__(512) void stream_read_kernel(const u32x4* __restrict__ src, int64_t n16,
+                                                          uint32_t* __restrict__ sink, uint32_t magic) {
+  const int64_t nwaves = (int64_t)gridDim.x * 8;
+  const int64_t wave = (int64_t)blockIdx.x * 8 + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  uint32_t acc = 0;
+  for (int64_t c0 = wave; c0 * 64 < n16; c0 += kReadAhead * nwaves) {
+    u32x4 v[kReadAhead];
+#pragma unroll
+    for (int k = 0; k < kReadAhead; ++k) {
+      const int64_t i = (c0 + k * nwaves) * 64 + lane;
+      v[k] = src[i < n16 ? i : 0];
+    }
+#pragma unroll
+    for (int k = 0; k < kReadAhead; ++k) acc ^= v[k][0] ^ v[k][1] ^ v[k][2] ^ v[k][3];
+  }
+  if (acc == magic) sink[0] = acc;
+}
+}  // namespace bi
+
+extern "C" int bi_stream_read(const void* src, int64_t bytes, uint32_t* sink, uint32_t magic, void* stream) {
+  using namespace bi_host;
+  if (bytes < 0 || bytes % 16 || bytes > ((int64_t)1 << 40))
+    return fail(BI_E_INVALID_ARG, "bi_stream_read: bytes (%lld) must be a multiple of 16 in [0, 2^40]", (long long)bytes);
+  if (bytes == 0) return BI_OK;
+  if (!src || !sink || !aligned16(src)) return fail(BI_E_INVALID_ARG, "bi_stream_read: null or unaligned pointer");
+  const int64_t chunks = (bytes / 16 + 63) / 64;
+  // about four chunks per wave: every wave resident at once for the sizes of
+  // one weight matrix (33 MB: 1,010 workgroups of 8 waves)
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(65535, (chunks + 31) / 32));
+  bi::stream_read_kernel<<<(unsigned)blocks, 512, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const bi::u32x4*>(src), bytes / 16, sink, magic);
+  return launch_status("bi_stream_read");
+}

@@ -72,6 +72,7 @@ _SIGNATURES = {
                                              _c_i64, _c_i64, _c_i64, _c_i64, ctypes.POINTER(_c_i64), ctypes.c_int,
                                              ctypes.c_float, ctypes.c_int, _vp]),
     "bi_exp2_f32": (ctypes.c_int, [_vp, _vp, _c_i64, _vp]),
+    "bi_stream_read": (ctypes.c_int, [_vp, _c_i64, _vp, ctypes.c_uint32, _vp]),
 }
 
 _lib = None

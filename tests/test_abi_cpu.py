@@ -183,6 +183,9 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.bi_exp2_f32(None, p, 4, None) == -1
     assert lib.bi_exp2_f32(p, None, 4, None) == -1
     assert lib.bi_exp2_f32(None, None, 0, None) == 0
+    assert lib.bi_stream_read(p, 24, p, 0, None) == -1          # not whole 16-byte pieces
+    assert lib.bi_stream_read(None, 32, p, 0, None) == -1
+    assert lib.bi_stream_read(None, 0, None, 0, None) == 0
 
 
 def test_split_size_routing():
