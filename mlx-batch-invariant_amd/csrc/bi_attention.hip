@@ -38,20 +38,43 @@ static int with_head_dim(int D, Fn&& fn) {
   }
 }
 
+// The per-key kernels take every head dim D % 32 == 0 up to 512 (the
+// reference's kernels accept any multiple of 32, kernels/attention.py:299-310);
+// the six of with_head_dim, plus these.
+template <class Fn>
+static int with_head_dim_per_key(int D, Fn&& fn) {
+  switch (D) {
+    case 160: return fn(std::integral_constant<int, 160>());
+    case 224: return fn(std::integral_constant<int, 224>());
+    case 288: return fn(std::integral_constant<int, 288>());
+    case 320: return fn(std::integral_constant<int, 320>());
+    case 352: return fn(std::integral_constant<int, 352>());
+    case 384: return fn(std::integral_constant<int, 384>());
+    case 416: return fn(std::integral_constant<int, 416>());
+    case 448: return fn(std::integral_constant<int, 448>());
+    case 480: return fn(std::integral_constant<int, 480>());
+    case 512: return fn(std::integral_constant<int, 512>());
+    default: return with_head_dim(D, fn);
+  }
+}
+
 }  // namespace bi
 
 namespace {
 
-int check_attn_shape(const char* what, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D) {
+int check_attn_shape(const char* what, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
+                     bool per_key = false) {
   using namespace bi_host;
   if (B < 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || D <= 0)
     return fail(BI_E_INVALID_ARG, "%s: bad shape B=%lld Hq=%lld Hkv=%lld L=%lld D=%lld", what,
                 (long long)B, (long long)Hq, (long long)Hkv, (long long)L, (long long)D);
   if (Hq % Hkv) return fail(BI_E_INVALID_ARG, "%s: Hq=%lld not a multiple of Hkv=%lld", what,
                             (long long)Hq, (long long)Hkv);
-  if (D != 32 && D != 64 && D != 96 && D != 128 && D != 192 && D != 256)
-    return fail(BI_E_UNSUPPORTED, "%s: head dim %lld (supported: 32, 64, 96, 128, 192, 256)", what,
-                (long long)D);
+  if (per_key && (D % 32 || D > 512))
+    return fail(BI_E_UNSUPPORTED, "%s: head dim %lld (supported: multiples of 32 up to 512)", what, (long long)D);
+  if (!per_key && D != 32 && D != 64 && D != 96 && D != 128 && D != 192 && D != 256)
+    return fail(BI_E_UNSUPPORTED, "%s: head dim %lld (supported: 32, 64, 96, 128, 192, 256; any multiple of 32 "
+                "up to 512 in the per-key order)", what, (long long)D);
   if (B > 65535 || Hkv > 65535 || L > 0x7fffffffLL - bi::kSplit || Hq > 0x7fffffffLL / 16)
     return fail(BI_E_UNSUPPORTED, "%s: shape exceeds the grid limits", what);
   return BI_OK;
@@ -162,9 +185,9 @@ int decode_impl(const char* what, const void* q, const void* k, const void* v, c
     return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define BI_DEC(TY)                                                                                          \
-  return bi::with_head_dim((int)D, [&](auto dd) {                                                         \
-    return per_key ? bi::launch_decode_perkey<TY, dd.value>(a, st) : bi::launch_decode<TY, dd.value>(a, st); \
-  });
+  if (per_key)                                                                                              \
+    return bi::with_head_dim_per_key((int)D, [&](auto dd) { return bi::launch_decode_perkey<TY, dd.value>(a, st); }); \
+  return bi::with_head_dim((int)D, [&](auto dd) { return bi::launch_decode<TY, dd.value>(a, st); });
   switch (dtype) {
     case BI_BF16: BI_DEC(bi::bf16)
     case BI_F16: BI_DEC(bi::f16)
@@ -217,9 +240,9 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
   a.split = (int)split;
   hipStream_t st = static_cast<hipStream_t>(stream);
 #define BI_PRE(TY)                                                                                            \
-  return bi::with_head_dim((int)D, [&](auto dd) {                                                           \
-    return per_key ? bi::launch_prefill_perkey<TY, dd.value>(a, st) : bi::launch_prefill<TY, dd.value>(a, st); \
-  });
+  if (per_key)                                                                                                \
+    return bi::with_head_dim_per_key((int)D, [&](auto dd) { return bi::launch_prefill_perkey<TY, dd.value>(a, st); }); \
+  return bi::with_head_dim((int)D, [&](auto dd) { return bi::launch_prefill<TY, dd.value>(a, st); });
   switch (dtype) {
     case BI_BF16: BI_PRE(bi::bf16)
     case BI_F16: BI_PRE(bi::f16)
@@ -287,7 +310,7 @@ extern "C" int bi_attn_decode_per_key(const void* q, const void* k, const void* 
                                       void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D,
                                       const int64_t* strides, float scale, int64_t split_size, int dtype, void* ws,
                                       size_t ws_bytes, void* stream) {
-  int rc = check_attn_shape("bi_attn_decode_per_key", B, Hq, Hkv, L, D);
+  int rc = check_attn_shape("bi_attn_decode_per_key", B, Hq, Hkv, L, D, true);
   if (rc) return rc;
   return decode_impl("bi_attn_decode_per_key", q, k, v, kv_lens, out, B, Hq, Hkv, L, D, strides, scale, dtype, ws,
                      ws_bytes, stream, nullptr, 0, 0, 0, true, split_size);
@@ -297,7 +320,7 @@ extern "C" int bi_attn_prefill_per_key(const void* q, const void* k, const void*
                                        void* out, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq, int64_t L,
                                        int64_t D, const int64_t* strides, int causal, float scale,
                                        int64_t split_size, int dtype, void* stream) {
-  int rc = check_attn_shape("bi_attn_prefill_per_key", B, Hq, Hkv, L, D);
+  int rc = check_attn_shape("bi_attn_prefill_per_key", B, Hq, Hkv, L, D, true);
   if (rc) return rc;
   return prefill_impl("bi_attn_prefill_per_key", q, k, v, kv_lens, out, B, Hq, Hkv, Tq, L, D, strides, causal,
                       scale, dtype, stream, nullptr, 0, 0, 0, true, split_size);

@@ -157,6 +157,16 @@ int launch_prefill(PrefillArgs& a, hipStream_t st) {
   template int launch_prefill<T, D>(PrefillArgs&, hipStream_t);      \
   template int launch_decode_perkey<T, D>(DecodeArgs&, hipStream_t); \
   template int launch_prefill_perkey<T, D>(PrefillArgs&, hipStream_t);
+#define BI_ATTN_PERKEY_INSTANTIATE_D(T, D)                            \
+  template int launch_decode_perkey<T, D>(DecodeArgs&, hipStream_t); \
+  template int launch_prefill_perkey<T, D>(PrefillArgs&, hipStream_t);
+// Head dims of the per-key kernels only (every multiple of 32 up to 512).
+#define BI_ATTN_PERKEY_EXTRA(T)                                                                          \
+  BI_ATTN_PERKEY_INSTANTIATE_D(T, 160) BI_ATTN_PERKEY_INSTANTIATE_D(T, 224)                             \
+  BI_ATTN_PERKEY_INSTANTIATE_D(T, 288) BI_ATTN_PERKEY_INSTANTIATE_D(T, 320)                             \
+  BI_ATTN_PERKEY_INSTANTIATE_D(T, 352) BI_ATTN_PERKEY_INSTANTIATE_D(T, 384)                             \
+  BI_ATTN_PERKEY_INSTANTIATE_D(T, 416) BI_ATTN_PERKEY_INSTANTIATE_D(T, 448)                             \
+  BI_ATTN_PERKEY_INSTANTIATE_D(T, 480) BI_ATTN_PERKEY_INSTANTIATE_D(T, 512)
 #define BI_ATTN_INSTANTIATE(T)                                                                           \
   BI_ATTN_INSTANTIATE_D(T, 32) BI_ATTN_INSTANTIATE_D(T, 64) BI_ATTN_INSTANTIATE_D(T, 96)                \
   BI_ATTN_INSTANTIATE_D(T, 128) BI_ATTN_INSTANTIATE_D(T, 192) BI_ATTN_INSTANTIATE_D(T, 256)

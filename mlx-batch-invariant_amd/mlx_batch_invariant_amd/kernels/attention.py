@@ -51,7 +51,12 @@ from .. import _lib
 
 SPLIT_SIZE = _lib.SPLIT_KEYS
 ORDERS = ("mfma", "per_key")
-SUPPORTED_HEAD_DIMS = (32, 64, 96, 128, 192, 256)   # reference: any D % 32 == 0 (kernels/attention.py:299-310)
+# Head dims: the matrix-core kernels take these six; the per-key kernels every
+# multiple of 32 up to 512 (the reference: any D % 32 == 0,
+# kernels/attention.py:299-310). order=None runs the per-key kernels for a
+# head dim only they take.
+MFMA_HEAD_DIMS = (32, 64, 96, 128, 192, 256)
+SUPPORTED_HEAD_DIMS = tuple(range(32, 513, 32))
 
 
 def supports(q, k, v, mask, sinks=None) -> bool:
@@ -113,21 +118,24 @@ def _lens(kv_lens, B: int, L: int, device) -> torch.Tensor | None:
 MAX_SPLIT = 1 << 20
 
 
-def _per_key(order, split_size) -> bool:
+def _per_key(order, split_size, head_dim: int = 128) -> bool:
     """Which kernels run: the reference's per-key order (True) or the
     matrix-core order (False). ``order=None`` picks the matrix-core kernels for
-    the contract split of 256 keys and the per-key kernels for any other
-    ``split_size`` (the reference's keyword, kernels/attention.py:326-327,
-    :368-370), whose splits only they take."""
+    the contract split of 256 keys at their head dims, and the per-key kernels
+    for any other ``split_size`` (the reference's keyword,
+    kernels/attention.py:326-327, :368-370) or head dim, which only they take."""
     if isinstance(split_size, bool) or not isinstance(split_size, int) or not 1 <= split_size <= MAX_SPLIT:
         raise ValueError(f"split_size must be an int in [1, {MAX_SPLIT}]; got {split_size!r}")
     if order is None:
-        return split_size != SPLIT_SIZE
+        return split_size != SPLIT_SIZE or head_dim not in MFMA_HEAD_DIMS
     if order not in ORDERS:
         raise ValueError(f"attention order must be one of {ORDERS}; got {order!r}")
     if order == "mfma" and split_size != SPLIT_SIZE:
         raise ValueError(f"the matrix-core kernels use {SPLIT_SIZE}-key splits; split_size={split_size} "
                          "runs with order='per_key'")
+    if order == "mfma" and head_dim not in MFMA_HEAD_DIMS:
+        raise ValueError(f"the matrix-core kernels take head dims {MFMA_HEAD_DIMS}; D={head_dim} runs with "
+                         "order='per_key'")
     return order == "per_key"
 
 
@@ -135,9 +143,9 @@ def batch_invariant_decode_attention(q, k, v, *, scale: float, split_size: int =
                                      kv_lens=None, order: str | None = None) -> torch.Tensor:
     """T_q == 1. Per-split partials (the GU query heads of a kv head share each
     K/V row), then an ordered combine (reference: kernels/attention.py:326-365)."""
-    per_key = _per_key(order, split_size)
     B, Hq, Tq, D = q.shape
     _, Hkv, L, _ = k.shape
+    per_key = _per_key(order, split_size, D)
     if Tq != 1:
         raise ValueError(f"decode attention needs T_q == 1, got {Tq}")
     if D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
@@ -176,9 +184,9 @@ def batch_invariant_prefill_attention(q, k, v, *, scale: float, causal: bool,
                                       order: str | None = None) -> torch.Tensor:
     """Any T_q. Blocks of 16 (token, head) rows share each K/V row; same split
     loop and merge as decode (reference: kernels/attention.py:368-390)."""
-    per_key = _per_key(order, split_size)
     B, Hq, Tq, D = q.shape
     _, Hkv, L, _ = k.shape
+    per_key = _per_key(order, split_size, D)
     if D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
         raise ValueError(f"prefill attention: unsupported shape q {tuple(q.shape)} k {tuple(k.shape)}")
     if causal and Tq > L:
@@ -248,7 +256,7 @@ def batch_invariant_paged_attention(q, k_pages, v_pages, block_table, kv_lens=No
         raise ValueError("batch_invariant_paged_attention: mask must be None or 'causal'")
     B, Hq, Tq, D = q.shape
     num_pages, Hkv, page_size, Dk = k_pages.shape
-    if v_pages.shape != k_pages.shape or Dk != D or D not in SUPPORTED_HEAD_DIMS or Hq % Hkv:
+    if v_pages.shape != k_pages.shape or Dk != D or D not in MFMA_HEAD_DIMS or Hq % Hkv:
         raise ValueError(f"paged attention: unsupported shapes q {tuple(q.shape)} k {tuple(k_pages.shape)} "
                          f"v {tuple(v_pages.shape)}")
     if page_size & (page_size - 1):

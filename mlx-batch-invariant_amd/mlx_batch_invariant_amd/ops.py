@@ -268,7 +268,9 @@ def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.
         if _attn.supports(q, k, v, mask):
             handled["sdpa_decode" if q.shape[2] == 1 else "sdpa_prefill"] += 1
             sc = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
-            return batch_invariant_attention(q, k, v, scale=sc, mask=mask, order=attention_order)
+            # head dims only the per-key kernels take run there whatever the mode's order
+            order = attention_order if q.shape[-1] in _attn.MFMA_HEAD_DIMS else "per_key"
+            return batch_invariant_attention(q, k, v, scale=sc, mask=mask, order=order)
     if isinstance(attn_mask, torch.Tensor) and not (mask_ok and isinstance(attn_mask, _CausalBias)):
         reason = "array-mask"
     elif ok and not _on_gpu(q, k, v):

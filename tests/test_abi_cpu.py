@@ -178,6 +178,12 @@ def test_invalid_arguments_are_rejected_before_launch():
         2, 8, 1000, 128)
     assert lib.bi_attn_decode_per_key(p, p, p, None, p, 2, 8, 2, 1000, 128, strides, 1.0, 100, 2, p, need - 16,
                                       None) == -3
+    # head dims: the per-key entry points take multiples of 32 up to 512, the matrix-core ones six of them
+    assert lib.bi_attn_decode_per_key(p, p, p, None, p, 1, 4, 4, 10, 544, strides, 1.0, 256, 2, p, 1 << 20,
+                                      None) == -2
+    assert lib.bi_attn_prefill_per_key(p, p, p, None, p, 1, 4, 4, 5, 10, 176, strides, 0, 1.0, 256, 2, None) == -2
+    assert lib.bi_attn_decode(p, p, p, None, p, 1, 4, 4, 10, 160, strides, 1.0, 2, p, 1 << 20, None) == -2
+    assert "per-key" in _err(lib)
     # the exp2 diagnostic: count and pointers checked before launch, nothing to do for n = 0
     assert lib.bi_exp2_f32(p, p, -1, None) == -1
     assert lib.bi_exp2_f32(None, p, 4, None) == -1
@@ -196,7 +202,9 @@ def test_split_size_routing():
     assert _per_key(None, 128) is True
     assert _per_key("per_key", 256) is True
     assert _per_key("mfma", 256) is False
-    for bad in [("mfma", 128), (None, 0), (None, 1.5), ("fast", 256), (None, True)]:
+    assert _per_key(None, 256, 160) is True          # a head dim only the per-key kernels take
+    assert _per_key(None, 256, 192) is False
+    for bad in [("mfma", 128), (None, 0), (None, 1.5), ("fast", 256), (None, True), ("mfma", 256, 160)]:
         with pytest.raises(ValueError):
             _per_key(*bad)
 

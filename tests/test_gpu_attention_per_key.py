@@ -207,3 +207,33 @@ def test_split_size_equals_oracle_and_keeps_invariance(split):
     if split != 256:
         with pytest.raises(ValueError):
             att(q, k, v, scale=sc, mask="causal", split_size=split, order="mfma")
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("D", [160, 224, 320, 512])
+def test_per_key_head_dims_beyond_the_matrix_core_set(dt, D):
+    """Head dims only the per-key kernels take (any multiple of 32 up to 512,
+    as the reference accepts): decode and causal prefill bitwise equal to the
+    oracle, decode == prefill, ragged lengths equal alone; order=None and the
+    mode pick these kernels for such a head dim."""
+    bi = _bi()
+    Hq, Hkv, T = 4, 2, 300
+    g = gen(D + len(dt))
+    q, k, v = (randn((2, Hq, T, D), DT[dt], g), randn((2, Hkv, T, D), DT[dt], g), randn((2, Hkv, T, D), DT[dt], g))
+    sc = D ** -0.5
+    full = bi.batch_invariant_prefill_attention(q, k, v, scale=sc, causal=True)        # order=None: per-key
+    want = ora.attention(to_np(q[:1, :, -24:]), to_np(k[:1]), to_np(v[:1]), sc, True, dt)
+    assert_bits_equal(to_np(full[:1, :, -24:]), want, f"prefill D={D}")
+    dec = bi.batch_invariant_decode_attention(q[:, :, -1:], k, v, scale=sc)
+    assert bits(dec) == bits(full[:, :, -1:])
+    lens = torch.tensor([T, 45], dtype=torch.int32).cuda()
+    rag = bi.batch_invariant_decode_attention(q[:, :, -1:], k, v, scale=sc, kv_lens=lens)
+    alone = bi.batch_invariant_decode_attention(q[1:, :, -1:], k[1:, :, :45], v[1:, :, :45], scale=sc)
+    assert bits(rag[1:]) == bits(alone)
+    with pytest.raises(ValueError):
+        bi.batch_invariant_decode_attention(q[:, :, -1:], k, v, scale=sc, order="mfma")
+    bi.reset_stats()
+    with bi.set_batch_invariant_mode(strict=True):
+        y = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, scale=sc, enable_gqa=True)
+    assert bi.stats()["handled"] == {"sdpa_prefill": 1}
+    assert bits(y) == bits(full)
