@@ -49,13 +49,14 @@ def _sync():
     torch.cuda.synchronize()
 
 
-def _time_calls(fn, n, warmup, rotate, graph=True, replays=3):
+def _time_calls(fn, n, warmup, rotate, graph=True, replays=3, warm_replays=1):
     """Per-call device time (s) of fn(i), i cycling over `rotate` weight copies.
 
     graph=True: the n calls are captured into one HIP graph (so the host's
     per-call launch cost cannot leave the GPU idle between kernels), the graph
-    is replayed, and each replay is bracketed by HIP events on the stream the
-    kernels run on; the result is replay time / n, once per replay.
+    is replayed `warm_replays` times untimed and then `replays` times, each
+    timed replay bracketed by HIP events on the stream the kernels run on; the
+    result is replay time / n, once per timed replay.
     graph=False: events around each eagerly launched call."""
     import torch
     for i in range(warmup):
@@ -72,7 +73,8 @@ def _time_calls(fn, n, warmup, rotate, graph=True, replays=3):
         with torch.cuda.graph(g):
             for i in range(n):
                 fn(i % rotate)
-        g.replay()
+        for _ in range(warm_replays):
+            g.replay()
         _sync()
         out = []
         for _ in range(replays):
@@ -131,8 +133,8 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     def call(M):
         return lambda i: bi.batch_invariant_quantized_matmul(xs[:M], *copies[i], group_size=gs, bits=bits)
 
-    # headline M = 1: `steps` calls captured in one graph, replayed three times
-    # (each replay times exactly `steps` calls; the median replay is reported).
+    # headline M = 1: `steps` calls captured in one graph, replayed (each
+    # timed replay times exactly `steps` calls; the median replay is reported).
     # Timed before the M sweep: after the larger-M launches the same M = 1 graph
     # reads ~1 us per call slower for its first few hundred calls, then recovers.
     _sync()
@@ -140,7 +142,9 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     if args.profile_m != 1:                # profiling aid: only the calls at that M, no report
         _time_calls(call(args.profile_m), args.steps, args.warmup, ncopy, replays=3)
         return {"metric": METRIC, "op": f"qmm{bits} profile run at M={args.profile_m}", "value": None}
-    durs = _time_calls(call(1), args.steps, args.warmup, ncopy, replays=3)
+    # 9 timed replays after 3 untimed ones: single replays of a short graph
+    # spread by several percent on one box.
+    durs = _time_calls(call(1), args.steps, args.warmup, ncopy, replays=9, warm_replays=3)
     wall = time.perf_counter() - t0
     table = {}
     for M in (() if args.headline_only else Ms):
