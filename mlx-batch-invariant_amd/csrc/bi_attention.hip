@@ -225,7 +225,7 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
                 (long long)strides[5], (long long)strides[8]);
   const int64_t wgs = (Tq * (Hq / Hkv) + 63) / 64;
   if (wgs > 0x7fffffffLL || Tq * (Hq / Hkv) > 0x7fffffffLL - 64 ||
-      (per_key && B * Hq * ((Tq + bi::kPkQB - 1) / bi::kPkQB) > ((int64_t)1 << 27)))
+      (per_key && B * Hq * ((Tq + bi::pk_prefill_qb(D) - 1) / bi::pk_prefill_qb(D)) > ((int64_t)1 << 27)))
     return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   bi::PrefillArgs a;
   a.q = q; a.k = k; a.v = v; a.kv_lens = kv_lens; a.out = out;

@@ -14,12 +14,11 @@ inline int decode_gu(int G) {
   return 1;
 }
 
-// Queries per per-key prefill unit. Each query's arithmetic does not depend
-// on it (a query takes only its own keys and splits); one query per unit
-// measured fastest (config-4 B = 1 / 4 / 16: 5.4 / 19.5 / 76.7 ms, against
-// 5.7 / 20.0 / 77.5 with 2, 7.0 / 24.1 / 92.3 with 4 and 9.6 / 36.0 / 140.5
-// with 8: fewer registers, more units in flight).
-constexpr int kPkQB = 1;
+// Queries per per-key prefill unit: 4 up to D = 128, 2 up to 256, else 1 (a
+// unit's rows and accumulators grow with D). A query's arithmetic does not
+// depend on it (a query takes only its own keys and splits); the K / V rows
+// of a key block are loaded and converted once for the unit's queries.
+__host__ __device__ constexpr int pk_prefill_qb(int64_t D) { return D <= 128 ? 4 : D <= 256 ? 2 : 1; }
 
 // Query heads a per-key decode unit scores together: 4, 2 or 1 (dividing G), and 1
 // while the grid has fewer than 16384 (head, split) pairs, where every unit

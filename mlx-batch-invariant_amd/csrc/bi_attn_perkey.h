@@ -22,12 +22,16 @@
 // exp is the fp32 exponential rounded from double precision, exp_cr below
 // (the reference asks for metal::precise::exp; this build fixes the rounding).
 //
-// One 32-lane half of a wave runs one unit, as one simdgroup does in the
-// reference: decode (b, kv head, chunk of NQ query heads, split), prefill (b,
-// query head, kPkQB queries). The halves of a wave never exchange data (shuffles
-// of width 32) and each half's control flow is uniform. A unit loads the K
-// and V rows of several keys before running their updates in key order.
+// One 32-lane half of a wave runs one unit: decode (b, kv head, chunk of NQ
+// query heads, split), prefill (b, query head, pk_prefill_qb(D) queries). The
+// halves of a wave never exchange data (shuffles of width 32) and each half's
+// control flow is uniform. The reference evaluates a key's score on 32 lanes
+// (one per partial) and its butterfly on every lane; here the lanes compute
+// the partials of a block of keys, then each lane folds one (query, key)'s 32
+// partials by the butterfly's own tree (pk_span): the same sums, once.
 #pragma once
+
+#include <type_traits>
 
 #include "bi_attn_api.h"
 
@@ -41,37 +45,6 @@ __device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x);
 // Keys whose K/V rows a unit holds at once (about 64 registers of rows).
 template <int DL>
 constexpr int pk_ahead() { return DL >= 4 ? 32 / DL : 8; }
-
-// The xor butterfly 16, 8, 4, 2, 1 within each 32-lane half, each step
-// part + part[lane ^ off], without LDS-routed shuffles: xor 16 and 4 by
-// ds_swizzle (bitmask mode: and 0x1f, xor off, within 32 lanes), xor 8 by a
-// DPP row rotation of 8 (in a 16-lane row, i + 8 mod 16 == i ^ 8), xor 2 and
-// 1 by DPP quad permutations. The same pairs as __shfl_xor(part, off, 32), so
-// the same sums (measured 7% faster per-key decode than the shuffles).
-__device__ __forceinline__ float pk_swizzle_xor16(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (16 << 10)));
-}
-__device__ __forceinline__ float pk_swizzle_xor4(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (4 << 10)));
-}
-template <int CTRL>
-__device__ __forceinline__ float pk_dpp(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kDppRowRor8 = 0x128, kDppQuadXor2 = 0x4E, kDppQuadXor1 = 0xB1;  // quad_perm [2,3,0,1] / [1,0,3,2]
-
-template <int DL>
-__device__ __forceinline__ float pk_score(const float (&qs)[DL], const float (&k)[DL]) {
-  float part = 0.0f;
-#pragma unroll
-  for (int d = 0; d < DL; ++d) part = __builtin_fmaf(qs[d], k[d], part);
-  part = part + pk_swizzle_xor16(part);
-  part = part + pk_dpp<kDppRowRor8>(part);
-  part = part + pk_swizzle_xor4(part);
-  part = part + pk_dpp<kDppQuadXor2>(part);
-  part = part + pk_dpp<kDppQuadXor1>(part);
-  return part;
-}
 
 template <int DL>
 __device__ __forceinline__ void pk_merge(float& M, float& L, float* A, float m, float l, const float* acc) {
@@ -97,77 +70,177 @@ __device__ __forceinline__ void pk_load_q(const T* row, float scale, float (&qs)
   for (int d = 0; d < DL; ++d) qs[d] = qs[d] * scale;
 }
 
+// A unit's LDS: the lane partials of a key block (32 keys x 32 lanes for one
+// query, KB = 32 / NQ keys x 32 lanes x NQ queries in general) and the
+// block's (corr, p) pairs, per query and key.
+constexpr int kPkTable = 32 * 32;
+constexpr int kPkPairs = 2 * 32;
+constexpr int kPkUnitFloats = kPkTable + kPkPairs;
+
+// Keys per block of a unit scoring NQ queries: one (query, key) score per lane.
+template <int NQ>
+constexpr int pk_block() { return 32 / NQ; }
+
+constexpr int pk_pow2_floor(int n) { return n >= 16 ? 16 : n >= 8 ? 8 : n >= 4 ? 4 : n >= 2 ? 2 : 1; }
+
+// NQ floats stored as one LDS write.
+template <int NQ> struct PkVec { typedef float type __attribute__((ext_vector_type(NQ))); };
+template <> struct PkVec<1> {
+  struct type {
+    float x;
+    __device__ float& operator[](int) { return x; }
+  };
+};
+
+// The xor butterfly 16, 8, 4, 2, 1 of 32 lane partials, evaluated by one lane:
+// level k adds the value of lane i + h to that of lane i (h = 16, 8, 4, 2, 1),
+// which is what lane 0 of the butterfly computes (every lane of it computes
+// the same sums in the other operand order, and the adds commute).
+__device__ __forceinline__ float pk_tree(float (&v)[32]) {
+#pragma unroll
+  for (int h = 16; h >= 1; h >>= 1)
+#pragma unroll
+    for (int i = 0; i < h; ++i) v[i] = v[i] + v[i + h];
+  return v[0];
+}
+
+// Inclusive prefix maximum over the G consecutive lanes of a group (G = 8, 16
+// or 32 within a 32-lane half; lanes of a group are the keys of one query in
+// key order). The maximum is exact and order-free (v_max_f32 treats -0 < +0;
+// NaN operands are dropped as by fmaxf), so the scan equals the key-by-key
+// running maximum.
+template <int G>
+__device__ __forceinline__ float pk_scan_max(float x, int jl) {
+#pragma unroll
+  for (int off = 1; off < G; off <<= 1) {
+    const float y = __shfl_up(x, off, G);
+    x = jl >= off ? fmaxf(x, y) : x;
+  }
+  return x;
+}
+
 // Keys [j0, j1) of (sequence b, kv head hk) for NQ queries; query iq takes
-// key j only if j < nkeys[iq] (its score is still computed: every lane of
-// the half-wave takes part in the butterfly).
+// key j only if j < nkeys[iq]. tb / cp: the unit's LDS (kPkTable / kPkPairs
+// floats, written and read back by this half-wave only: DS operations of one
+// wave complete in order).
 //
-// A block of AH keys is evaluated in three passes with the recurrence's own
+// Blocks of KB = 32 / NQ keys, in three phases with the recurrence's own
 // values and order:
-//   1. the scores of every (key, query) (each lane ends up with all of them);
-//   2. per query, key by key: m' = max(m, s) for its active keys, and the two
-//      exp arguments m - m' and s - m' (the maxima depend on the scores only);
-//   3. every exp of the block once, one argument per lane of the half-wave
-//      (all 32 lanes hold the same arguments), then back to every lane by a
-//      shuffle, and the updates l = fma(l, corr, p), acc = fma(acc, corr, p v)
-//      in key order.
-// The same numbers as evaluating the recurrence key by key on every lane
-// (which computed each exp 32 times).
+//   1. lanes own dims: lane l's score partials of every (key, query) of the
+//      block (fma chains over its DL dims from 0), written to LDS;
+//   2. lanes own (query q, key j): the 32 partials of (q, j) read back and
+//      folded by the butterfly's tree (pk_tree), the running maximum of the
+//      query's active keys by an exact prefix-maximum scan, and the key's
+//      corr = exp(m_prev - m') (1 when the maximum did not move: exp(0) = 1)
+//      and p = exp(s - m'), each evaluated once;
+//   3. lanes own dims again: l = fma(l, corr, p), acc = fma(acc, corr, p v)
+//      for every query in key order, (corr, p) read from LDS.
+// The same numbers as evaluating the recurrence key by key with the
+// butterfly on every lane; the K / V rows of a block are converted once for
+// all NQ queries. Blocks whose keys every query takes (FULL) run without
+// per-key checks and address row jb + u as the block's row pointer plus u
+// row strides. The cache is contiguous (the per-key entry points take no
+// page table).
 template <typename T, int DL, int NQ, class Args>
 __device__ __forceinline__ void pk_span(const Args& a, int b, int hk, int lane, int j0, int j1,
-                                        const float (&qs)[NQ][DL], const int (&nkeys)[NQ], float (&m)[NQ],
-                                        float (&l)[NQ], float (&acc)[NQ][DL]) {
-  constexpr int AH = pk_ahead<DL>();
-  constexpr int NE = 2 * AH * NQ;              // exp arguments per block: (corr, p) per (key, query)
-  constexpr int ROUNDS = (NE + 31) / 32;       // exps per lane per block
-  const T* kbase = static_cast<const T*>(a.k) + lane * DL;
-  const T* vbase = static_cast<const T*>(a.v) + lane * DL;
-  for (int j = j0; j < j1; j += AH) {
-    float kr[AH][DL], vr[AH][DL];
+                                             const float (&qs)[NQ][DL], const int (&nkeys)[NQ], float (&m)[NQ],
+                                             float (&l)[NQ], float (&acc)[NQ][DL], float* __restrict__ tb,
+                                             float* __restrict__ cp) {
+  constexpr int KB = pk_block<NQ>();
+  constexpr int AH = pk_pow2_floor(pk_ahead<DL>() < KB ? pk_ahead<DL>() : KB);   // rows held at once
+  static_assert(KB % AH == 0, "pk_span: whole row batches per block");
+  typedef typename PkVec<NQ>::type qvec;
+  const int jl = lane % KB, ql = lane / KB;    // phase 2: key jl of the block, query ql
+  int kend[NQ];
+  int kend_q = 0, kmin = j1;
+  float mq = m[0];
 #pragma unroll
-    for (int u = 0; u < AH; ++u) {
-      const int jj = min(j + u, j1 - 1);
-      pk_load<T, DL>(kbase + kv_row_off(a, a.k_sb, a.k_sh, a.k_sl, b, hk, jj), kr[u]);
-      pk_load<T, DL>(vbase + kv_row_off(a, a.v_sb, a.v_sh, a.v_sl, b, hk, jj), vr[u]);
+  for (int iq = 0; iq < NQ; ++iq) {
+    kend[iq] = min(j1, nkeys[iq]);
+    kmin = min(kmin, kend[iq]);
+    if (ql == iq) {
+      kend_q = kend[iq];
+      mq = m[iq];
     }
-    // Passes 1 and 2: scores, running maxima, and this lane's exp arguments
-    // (argument 2 (u NQ + iq) is corr, + 1 is p; lane i of round r takes
-    // argument 32 r + i).
-    float ein[ROUNDS];
+  }
+  // The lane's elements of row 0 of (b, hk).
+  const T* kbase = static_cast<const T*>(a.k) + lane * DL + (int64_t)b * a.k_sb + (int64_t)hk * a.k_sh;
+  const T* vbase = static_cast<const T*>(a.v) + lane * DL + (int64_t)b * a.v_sb + (int64_t)hk * a.v_sh;
+  auto krow = [&](int j) -> const T* { return kbase + (int64_t)j * a.k_sl; };
+  auto vrow = [&](int j) -> const T* { return vbase + (int64_t)j * a.v_sl; };
+
+  auto block = [&](int jb, auto full_t) {
+    constexpr bool FULL = decltype(full_t)::value;
+    // Row u0 + u of the block: row jb + u0 + u, or (partial blocks) the last
+    // row of the span in place of rows past it.
+    auto rowp = [&](auto rowf, int64_t sl, int u) -> const T* {
+      if constexpr (FULL) return rowf(jb) + (int64_t)u * sl;
+      else return rowf(min(jb + u, j1 - 1));
+    };
+    // Phase 1: partial of lane l for (key u, query iq) at tb[(u 32 + (l ^ u)) NQ + iq]
+    // (the xor spreads the 32 readers of phase 2 over distinct banks).
+#pragma unroll 1
+    for (int u0 = 0; u0 < KB; u0 += AH) {
+      float kr[AH][DL];
 #pragma unroll
-    for (int r = 0; r < ROUNDS; ++r) ein[r] = 0.0f;
+      for (int u = 0; u < AH; ++u) pk_load<T, DL>(rowp(krow, a.k_sl, u0 + u), kr[u]);
 #pragma unroll
-    for (int u = 0; u < AH; ++u) {
+      for (int u = 0; u < AH; ++u) {
+        qvec pq;
 #pragma unroll
-      for (int iq = 0; iq < NQ; ++iq) {
-        const float s = pk_score<DL>(qs[iq], kr[u]);
-        const bool act = j + u < j1 && j + u < nkeys[iq];
-        const float m_new = act ? fmaxf(m[iq], s) : m[iq];
-        const int i = 2 * (u * NQ + iq);
-        if (lane == i % 32) ein[i / 32] = m[iq] - m_new;
-        if (lane == (i + 1) % 32) ein[(i + 1) / 32] = s - m_new;
-        m[iq] = m_new;
+        for (int iq = 0; iq < NQ; ++iq) {
+          float part = 0.0f;
+#pragma unroll
+          for (int d = 0; d < DL; ++d) part = __builtin_fmaf(qs[iq][d], kr[u][d], part);
+          pq[iq] = part;
+        }
+        *reinterpret_cast<qvec*>(tb + ((u0 + u) * 32 + (lane ^ (u0 + u))) * NQ) = pq;
       }
     }
-    float e[ROUNDS];
+    asm volatile("" ::: "memory");
+    // Phase 2.
+    float v[32];
 #pragma unroll
-    for (int r = 0; r < ROUNDS; ++r) e[r] = exp_cr(ein[r]);
-    // Pass 3: the updates in key order.
+    for (int i = 0; i < 32; ++i) v[i] = tb[(jl * 32 + (i ^ jl)) * NQ + ql];
+    const float s = pk_tree(v);
+    const bool act = FULL || jb + jl < kend_q;
+    const float mj = fmaxf(mq, pk_scan_max<KB>(act ? s : -INFINITY, jl));
+    float mp = __shfl_up(mj, 1, KB);
+    mp = jl == 0 ? mq : mp;
+    mq = __shfl(mj, ql * KB + KB - 1, 32);
+    const float carg = mp - mj;
+    float corr = 1.0f;
+    if (carg != 0.0f) corr = exp_cr(carg);
+    const float p = exp_cr(s - mj);
+    *reinterpret_cast<float2*>(cp + 2 * (ql * KB + jl)) = float2{corr, p};
+    asm volatile("" ::: "memory");
+    // Phase 3.
+#pragma unroll 1
+    for (int u0 = 0; u0 < KB; u0 += AH) {
+      float vr[AH][DL];
 #pragma unroll
-    for (int u = 0; u < AH; ++u) {
-      if (j + u >= j1) break;
+      for (int u = 0; u < AH; ++u) pk_load<T, DL>(rowp(vrow, a.v_sl, u0 + u), vr[u]);
 #pragma unroll
-      for (int iq = 0; iq < NQ; ++iq) {
-        const int i = 2 * (u * NQ + iq);
-        const float corr = __shfl(e[i / 32], i % 32, 32);
-        const float p = __shfl(e[(i + 1) / 32], (i + 1) % 32, 32);
-        if (j + u < nkeys[iq]) {
-          l[iq] = __builtin_fmaf(l[iq], corr, p);
+      for (int u = 0; u < AH; ++u) {
+        const int key = jb + u0 + u;
 #pragma unroll
-          for (int d = 0; d < DL; ++d) acc[iq][d] = __builtin_fmaf(acc[iq][d], corr, p * vr[u][d]);
+        for (int iq = 0; iq < NQ; ++iq) {
+          if (FULL || key < kend[iq]) {
+            const float2 e = *reinterpret_cast<const float2*>(cp + 2 * (iq * KB + u0 + u));
+            l[iq] = __builtin_fmaf(l[iq], e.x, e.y);
+#pragma unroll
+            for (int d = 0; d < DL; ++d) acc[iq][d] = __builtin_fmaf(acc[iq][d], e.x, e.y * vr[u][d]);
+          }
         }
       }
     }
-  }
+    asm volatile("" ::: "memory");
+  };
+  int jb = j0;
+  for (; jb + KB <= kmin; jb += KB) block(jb, std::true_type());
+  for (; jb < j1; jb += KB) block(jb, std::false_type());
+#pragma unroll
+  for (int iq = 0; iq < NQ; ++iq) m[iq] = __shfl(mq, iq * KB, 32);
 }
 
 // Decode: unit = (b, kv head hk, chunk of NQ query heads, split), split
@@ -176,7 +249,9 @@ __device__ __forceinline__ void pk_span(const Args& a, int b, int hk, int lane, 
 template <typename T, int D, int NQ>
 __global__ __launch_bounds__(256) void attn_decode_perkey(DecodeArgs a) {
   constexpr int DL = D / 32;
+  __shared__ __attribute__((aligned(16))) float lds[8][kPkUnitFloats];
   const int lane = threadIdx.x % 32;
+  float* tb = lds[threadIdx.x / 32];
   int64_t u = (int64_t)blockIdx.x * 8 + threadIdx.x / 32;
   if (u >= (int64_t)a.B * a.Hkv * a.nchunk * a.nsplit) return;
   const int split = (int)(u % a.nsplit);
@@ -201,7 +276,7 @@ __global__ __launch_bounds__(256) void attn_decode_perkey(DecodeArgs a) {
 #pragma unroll
     for (int d = 0; d < DL; ++d) acc[iq][d] = 0.0f;
   }
-  pk_span<T, DL, NQ>(a, b, hk, lane, j0, j1, qs, nkeys, m, l, acc);
+  pk_span<T, DL, NQ>(a, b, hk, lane, j0, j1, qs, nkeys, m, l, acc, tb, tb + kPkTable);
 #pragma unroll
   for (int iq = 0; iq < NQ; ++iq) {
     const int64_t po = ((int64_t)b * a.Hq + h0 + iq) * a.nsplit + split;
@@ -235,14 +310,16 @@ __global__ __launch_bounds__(256) void attn_combine_perkey(DecodeArgs a) {
 }
 
 // Prefill: unit = (b, query head h, queries QB blk .. QB blk + QB - 1), blk
-// fastest (QB = kPkQB).
+// fastest (QB = pk_prefill_qb(D)).
 // Query t sees keys [0, nkeys(t)), nkeys = len - Tq + t + 1 when causal
 // (bottom-right aligned), else len; a split merges into a query's running
 // result only if the query saw one of its keys.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_prefill_perkey(PrefillArgs a) {
-  constexpr int DL = D / 32, QB = kPkQB;
+  constexpr int DL = D / 32, QB = pk_prefill_qb(D);
+  __shared__ __attribute__((aligned(16))) float lds[8][kPkUnitFloats];
   const int lane = threadIdx.x % 32;
+  float* tb = lds[threadIdx.x / 32];
   const int nblk = (a.Tq + QB - 1) / QB;
   int64_t u = (int64_t)blockIdx.x * 8 + threadIdx.x / 32;
   if (u >= (int64_t)a.B * a.Hq * nblk) return;
@@ -278,7 +355,7 @@ __global__ __launch_bounds__(256) void attn_prefill_perkey(PrefillArgs a) {
 #pragma unroll
       for (int d = 0; d < DL; ++d) acc[iq][d] = 0.0f;
     }
-    pk_span<T, DL, QB>(a, b, hk, lane, j0, min(nmax, j0 + a.split), qs, nkeys, m, l, acc);
+    pk_span<T, DL, QB>(a, b, hk, lane, j0, min(nmax, j0 + a.split), qs, nkeys, m, l, acc, tb, tb + kPkTable);
 #pragma unroll
     for (int iq = 0; iq < QB; ++iq)
       if (j0 < nkeys[iq]) pk_merge<DL>(M[iq], Ls[iq], A[iq], m[iq], l[iq], acc[iq]);
@@ -313,7 +390,8 @@ int launch_decode_perkey(DecodeArgs& a, hipStream_t st) {
 
 template <typename T, int D>
 int launch_prefill_perkey(PrefillArgs& a, hipStream_t st) {
-  const int64_t units = (int64_t)a.B * a.Hq * ((a.Tq + kPkQB - 1) / kPkQB);
+  constexpr int QB = pk_prefill_qb(D);
+  const int64_t units = (int64_t)a.B * a.Hq * ((a.Tq + QB - 1) / QB);
   attn_prefill_perkey<T, D><<<(unsigned)((units + 7) / 8), 256, 0, st>>>(a);
   return bi_host::launch_status("bi_attn_prefill_per_key");
 }
