@@ -39,18 +39,19 @@
 
 namespace bi {
 
-template <typename T, int BITS, int GS, int W, int NB, int MR>
+template <typename T, int BITS, int GS, int W, int NB, int MR, int CT = 1>
 struct GemvStreamCfg {
   static constexpr int kCE = 16 / (int)sizeof(T);            // elements per 16-byte load
   static constexpr int kSPR = NB * kGroupK / GS;              // scales per row per wave
+  static constexpr int kRows = 16 * CT;                       // weight rows (output columns) per workgroup
   static constexpr int kAElems = MR * NB * kGroupK;           // A elements per wave
   static constexpr int kALoads = kAElems / kCE / kWave;       // A loads per lane
-  static constexpr int kMChunks = 2 * 16 * kSPR / kCE;        // meta chunks per wave
+  static constexpr int kMChunks = 2 * kRows * kSPR / kCE;     // meta chunks per wave
   static constexpr int kMLoads = (kMChunks + kWave - 1) / kWave;
-  static constexpr int kWaveElems = kAElems + 2 * 16 * kSPR;  // A + metadata elements per wave
-  // Bytes per wave region: A and metadata, or later the NB partials.
-  static constexpr int kWaveBytes = (kWaveElems * (int)sizeof(T) > NB * kWave * 16)
-                                        ? kWaveElems * (int)sizeof(T) : NB * kWave * 16;
+  static constexpr int kWaveElems = kAElems + 2 * kRows * kSPR;  // A + metadata elements per wave
+  // Bytes per wave region: A and metadata, or later the NB x CT partials.
+  static constexpr int kWaveBytes = (kWaveElems * (int)sizeof(T) > NB * CT * kWave * 16)
+                                        ? kWaveElems * (int)sizeof(T) : NB * CT * kWave * 16;
   static constexpr int kRowElems = NB * kGroupK;               // A row of the wave's slice
   // LDS element offset of A element k (0 <= k < kRowElems) of slice row ar.
   static __device__ __forceinline__ int a_off(int ar, int k) {
@@ -62,12 +63,12 @@ struct GemvStreamCfg {
   static size_t lds_bytes(int /*G*/) { return (size_t)W * kWaveBytes; }
 };
 
-template <typename T, int BITS, int GS, int W, int NB, int MR, int PD>
+template <typename T, int BITS, int GS, int W, int NB, int MR, int PD, int CT = 1>
 __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
                                                         QuantB<T, BITS, GS> bsrc,
                                                         T* __restrict__ out, int M, int N, int K,
                                                         int G) {
-  typedef GemvStreamCfg<T, BITS, GS, W, NB, MR> C;
+  typedef GemvStreamCfg<T, BITS, GS, W, NB, MR, CT> C;
   typedef QuantB<T, BITS, GS> QB;
   typedef typename Frag<T>::type F;
   extern __shared__ __attribute__((aligned(16))) f32x4 smem[];
@@ -75,10 +76,9 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   T* As = reinterpret_cast<T*>(regions + (size_t)wave * C::kWaveBytes);
-  T* Ms = As + C::kAElems;                                          // [2][16][SPR]
+  T* Ms = As + C::kAElems;                                          // [2][kRows][SPR]
   const int r = lane % 16, q = lane / 16;
-  const int n_base = blockIdx.x * 16;
-  const int n = min(n_base + r, N - 1);          // clamped: padding columns are not stored
+  const int n_base = blockIdx.x * C::kRows;
   const int g0 = wave * NB;                      // G == W * NB (checked on the host)
 
   // 1. A slice: row ar, elements [g0 * 256 + ac, +kCE) of the wave's slice.
@@ -89,26 +89,37 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     const int ar = c / (NB * kGroupK / C::kCE), ac = (c % (NB * kGroupK / C::kCE)) * C::kCE;
     av[i] = frag_load(a + (int64_t)min(ar, M - 1) * lda + g0 * kGroupK + ac);
   }
-  // 2. Scales then biases of rows n_base .. n_base + 15 for the wave's groups.
+  // 2. Scales then biases of rows n_base .. n_base + kRows - 1 for the wave's groups.
   F mv[C::kMLoads];
   const int gpr = (int)bsrc.groups_per_row;
 #pragma unroll
   for (int i = 0; i < C::kMLoads; ++i) {
     const int c0 = lane + kWave * i;
     const int c = c0 < C::kMChunks ? c0 : 0;
-    const int kind = c / (16 * C::kSPR / C::kCE);
-    const int within = c % (16 * C::kSPR / C::kCE);
+    const int kind = c / (C::kRows * C::kSPR / C::kCE);
+    const int within = c % (C::kRows * C::kSPR / C::kCE);
     const int row = within / (C::kSPR / C::kCE), col = (within % (C::kSPR / C::kCE)) * C::kCE;
     const T* base = kind ? bsrc.biases : bsrc.scales;
     mv[i] = frag_load(base + (int64_t)min(n_base + row, N - 1) * gpr + g0 * (kGroupK / GS) + col);
   }
-  // 3. Codes of the wave's first PD groups, after everything above in issue
-  // order; group j + PD is requested when group j starts.
+  // 3. Codes of the wave's first PD groups (CT column tiles: weight rows
+  // n_base + 16 c + r, clamped; padding columns are not stored), after
+  // everything above in issue order; group j + PD is requested when group j
+  // starts.
   asm volatile("" ::: "memory");
-  typename QB::Raw braw[NB];
-  const typename QB::Lane bl = bsrc.lane(n, q);
+  typename QB::Raw braw[NB][CT];
+  typename QB::Lane bl[CT];
+  int rt[CT];                                     // the lanes' rows of the staged metadata
 #pragma unroll
-  for (int j = 0; j < PD && j < NB; ++j) bsrc.load_codes(braw[j], bl, g0 + j);
+  for (int c = 0; c < CT; ++c) {
+    const int n = min(n_base + 16 * c + r, N - 1);
+    bl[c] = bsrc.lane(n, q);
+    rt[c] = n - n_base;
+  }
+#pragma unroll
+  for (int j = 0; j < PD && j < NB; ++j)
+#pragma unroll
+    for (int c = 0; c < CT; ++c) bsrc.load_codes(braw[j][c], bl[c], g0 + j);
   // Wave-private LDS: written and read back by this wave only.
 #pragma unroll
   for (int i = 0; i < C::kALoads; ++i) {
@@ -123,22 +134,27 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   }
   asm volatile("" ::: "memory");
 
-  const int rt = n - n_base;                      // this lane's row of the tile (clamped)
   const int arow = min(r, MR - 1);                // A rows past MR alias a loaded row (never stored)
-  f32x4 accs[NB];
+  f32x4 accs[NB][CT];
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int g = g0 + j;
     if (j + PD < NB) {
       asm volatile("" ::: "memory");
-      bsrc.load_codes(braw[j + PD], bl, g0 + j + PD);
+#pragma unroll
+      for (int c = 0; c < CT; ++c) bsrc.load_codes(braw[j + PD][c], bl[c], g0 + j + PD);
       asm volatile("" ::: "memory");
     }
+    bool huge = false;
 #pragma unroll
-    for (int i = 0; i < QB::kScales; ++i) {
-      const int v = j * (kGroupK / GS) + (64 * q) / GS + i;
-      braw[j].scale[i] = Ms[rt * C::kSPR + v];
-      braw[j].bias[i] = Ms[16 * C::kSPR + rt * C::kSPR + v];
+    for (int c = 0; c < CT; ++c) {
+#pragma unroll
+      for (int i = 0; i < QB::kScales; ++i) {
+        const int v = j * (kGroupK / GS) + (64 * q) / GS + i;
+        braw[j][c].scale[i] = Ms[rt[c] * C::kSPR + v];
+        braw[j][c].bias[i] = Ms[C::kRows * C::kSPR + rt[c] * C::kSPR + v];
+      }
+      huge |= bsrc.huge_scale(braw[j][c]);
     }
     // A fragments are read from LDS one step ahead of their MFMA (not all
     // eight up front): 24 fewer live registers, which lets a CU hold every
@@ -146,51 +162,61 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     auto afrag = [&](int s) {
       return *reinterpret_cast<const F*>(As + C::a_off(arow, j * kGroupK + 64 * q + 8 * s));
     };
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto steps = [&](auto fast) {
       F a_cur = afrag(0);
 #pragma unroll
       for (int s = 0; s < kSteps; ++s) {
         const F a_nxt = afrag(s + 1 < kSteps ? s + 1 : s);
-        const F bf = bsrc.template frag<true, decltype(fast)::value>(braw[j], s, QB::kbase(g, q));
-        acc = mfma_step(a_cur, bf, acc);
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+          const F bf = bsrc.template frag<true, decltype(fast)::value>(braw[j][c], s, QB::kbase(g, q));
+          acc[c] = mfma_step(a_cur, bf, acc[c]);
+        }
         a_cur = a_nxt;
       }
     };
-    if (!__any(bsrc.huge_scale(braw[j]))) steps(std::true_type());
+    if (!__any(huge)) steps(std::true_type());
     else steps(std::false_type());
-    accs[j] = acc;
+#pragma unroll
+    for (int c = 0; c < CT; ++c) accs[j][c] = acc[c];
   }
   // The wave's A and metadata are dead now (its DS reads complete in order):
-  // its partials take their place.
+  // its partials take their place, slot j CT + c.
   asm volatile("" ::: "memory");
 #pragma unroll
   for (int j = 0; j < NB; ++j)
-    *reinterpret_cast<f32x4*>(regions + (size_t)wave * C::kWaveBytes + j * kWave * 16 + lane * 16) = accs[j];
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+      *reinterpret_cast<f32x4*>(regions + (size_t)wave * C::kWaveBytes + (j * CT + c) * kWave * 16 + lane * 16) =
+          accs[j][c];
   __syncthreads();
-  // Ordered fold: one thread per stored output element (lane l, register e of
-  // the MFMA result layout), eight LDS loads in flight, adds in group order.
-  // Partial of group g: wave g / NB's region, slot g % NB.
-  auto pptr = [&](int g, int l, int e) {
-    return reinterpret_cast<const float*>(regions + (size_t)(g / NB) * C::kWaveBytes + (g % NB) * kWave * 16 +
-                                          l * 16) + e;
+  // Ordered fold: one thread per stored output element (column tile c, lane
+  // l, register e of the MFMA result layout), eight LDS loads in flight, adds
+  // in group order. Partial of group g: wave g / NB's region, slot
+  // (g % NB) CT + c.
+  auto pptr = [&](int g, int c, int l, int e) {
+    return reinterpret_cast<const float*>(regions + (size_t)(g / NB) * C::kWaveBytes +
+                                          ((g % NB) * CT + c) * kWave * 16 + l * 16) + e;
   };
-  for (int idx = threadIdx.x; idx < kWave * 4; idx += kWave * W) {
-    const int e = idx / kWave, l = idx % kWave;
-    if (4 * (l / 16) + e >= M) continue;        // tile rows past M are never stored
+  for (int idx = threadIdx.x; idx < CT * kWave * 4; idx += kWave * W) {
+    const int c = idx / (kWave * 4), e = (idx / kWave) % 4, l = idx % kWave;
+    const int m = 4 * (l / 16) + e;
+    const int col = n_base + 16 * c + l % 16;
+    if (m >= M || col >= N) continue;           // tile rows past M, columns past N are never stored
     float total = 0.f;
     int gg = 0;
     for (; gg + 8 <= G; gg += 8) {
       float v[8];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) v[jj] = *pptr(gg + jj, l, e);
+      for (int jj = 0; jj < 8; ++jj) v[jj] = *pptr(gg + jj, c, l, e);
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) total = total + v[jj];
     }
-    for (; gg < G; ++gg) total = total + *pptr(gg, l, e);
-    const int col = n_base + l % 16;
-    const int m = 4 * (l / 16) + e;
-    if (m < M && col < N) out[(int64_t)m * N + col] = to_store<T>(total);
+    for (; gg < G; ++gg) total = total + *pptr(gg, c, l, e);
+    out[(int64_t)m * N + col] = to_store<T>(total);
   }
 }
 

@@ -43,7 +43,7 @@
 namespace bi {
 
 constexpr int kSplitMMax = 32;
-constexpr int kStreamMMax = 8;    // rows of x the streaming GEMV takes (9..16 measured faster on gemm_mid2)
+constexpr int kStreamMMax = 16;   // rows of x the streaming GEMV takes (4-bit; 8-bit codes: 8)
 // gemv_wg with A staged in LDS: at most kGemvAChunks / W 16-byte chunks of A
 // per thread (M * K <= kGemvAChunks * 64 * 8).
 constexpr int kGemvAChunks = 32;
@@ -834,9 +834,10 @@ static void launch_wg_alds(const T* a, int64_t lda, const BSrc& bsrc, T* out, in
 }
 
 // The barrier-free decode GEMV for a quantized B (bi_gemv_stream.h): W waves
-// of NB = G / W consecutive groups (G in {4, 8, 16}), M <= 4, code loads PD
-// groups ahead. Returns false when the shape does not qualify.
-template <typename T, int BITS, int GS, int W, int NB, int MR, int PD>
+// of NB = G / W consecutive groups (G in {4, 8, 16}), M <= MR rows of A staged
+// per wave, CT column tiles per wave, code loads PD groups ahead. Returns
+// false when the shape does not qualify.
+template <typename T, int BITS, int GS, int W, int NB, int MR, int PD, int CT = 1>
 static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
                            int K, int G, hipStream_t st) {
   constexpr int kCE = 16 / (int)sizeof(T);
@@ -845,23 +846,40 @@ static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b
   if constexpr (sizeof(T) != 2 || (NB * kGroupK / GS) % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0) {
     return false;
   } else {
-    if (G != W * NB) return false;
-    typedef GemvStreamCfg<T, BITS, GS, W, NB, MR> C;
-    // More than 64 KB of dynamic LDS (8 rows of A: up to 148 KB) is allowed
+    typedef GemvStreamCfg<T, BITS, GS, W, NB, MR, CT> C;
+    if (G != W * NB || C::lds_bytes(G) > 160 * 1024) return false;
+    // More than 64 KB of dynamic LDS (8 or 16 rows of A) is allowed
     // explicitly, once per instantiation (a failure leaves the default limit
     // and no error state behind; the launch then reports its own status).
     static const bool lds_raised = [] {
       if (C::lds_bytes(16) <= 65536) return true;
-      const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream<T, BITS, GS, W, NB, MR, PD>),
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+      const bool ok =
+          hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream<T, BITS, GS, W, NB, MR, PD, CT>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
       if (!ok) (void)hipGetLastError();
       return ok;
     }();
     (void)lds_raised;
-    gemv_stream<T, BITS, GS, W, NB, MR, PD><<<dim3(ceil_div(N, 16)), kWave * W, C::lds_bytes(G), st>>>(
+    gemv_stream<T, BITS, GS, W, NB, MR, PD, CT><<<dim3(ceil_div(N, 16 * CT)), kWave * W, C::lds_bytes(G), st>>>(
         a, lda, b, out, M, N, K, G);
     return true;
   }
+}
+
+// Column tiles per wave of the streaming GEMV: the fewest (1, 2, 4) that bring
+// the grid within one round of resident workgroups (LDS: four per CU at MR <= 4,
+// two at MR = 8, one at MR = 16: A's MR rows x K of every workgroup sit in
+// LDS). Each further tile reuses every A fragment the wave reads. Measured,
+// 4-bit g64 [14336, 4096] (896 column tiles): M = 5 / 8 11.2 / 12.1 ->
+// 10.1 / 10.5 us at MR = 8, CT = 2; M = 12 / 16 16.7 / 16.9 (the mid-M
+// launch) -> 12.3 / 12.9 us at MR = 16, CT = 4; M = 1 keeps CT = 1 (9.2
+// against 10.3 us).
+constexpr int kStreamCUs = 256;   // MI355X compute units
+inline int stream_ct(int MR, int N) {
+  const int64_t cap = (int64_t)kStreamCUs * (MR >= 16 ? 1 : MR >= 8 ? 2 : 4);
+  int ct = 1;
+  while (ct < 4 && ceil_div(N, 16 * ct) > cap) ct *= 2;
+  return ct;
 }
 
 template <typename T, int BITS, int GS, int W, int NB, int PD>
@@ -869,7 +887,22 @@ static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& 
                             int K, int G, hipStream_t st) {
   if (M == 1) return launch_stream1<T, BITS, GS, W, NB, 1, PD>(a, lda, b, out, M, N, K, G, st);
   if (M <= 4) return launch_stream1<T, BITS, GS, W, NB, 4, PD>(a, lda, b, out, M, N, K, G, st);
-  return launch_stream1<T, BITS, GS, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
+  if constexpr (BITS == 4) {
+    // Column tiles only for 4-bit codes (8-bit codes of four tiles do not fit
+    // the register file next to A).
+    if (M <= 8) {
+      if (stream_ct(8, N) > 1) return launch_stream1<T, BITS, GS, W, NB, 8, PD, 2>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream1<T, BITS, GS, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
+    }
+    switch (stream_ct(16, N)) {
+      case 4: return launch_stream1<T, BITS, GS, W, NB, 16, PD, 4>(a, lda, b, out, M, N, K, G, st);
+      case 2: return launch_stream1<T, BITS, GS, W, NB, 16, PD, 2>(a, lda, b, out, M, N, K, G, st);
+      default: return launch_stream1<T, BITS, GS, W, NB, 16, PD>(a, lda, b, out, M, N, K, G, st);
+    }
+  } else {
+    if (M > 8) return false;
+    return launch_stream1<T, BITS, GS, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
+  }
 }
 
 // Launch shapes in order of preference (measured, Llama MLP shape, M = 1):
@@ -880,7 +913,7 @@ static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& 
 template <typename T, int BITS, int GS>
 static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N, int K,
                           int G, hipStream_t st) {
-  if (M > kStreamMMax || K % kGroupK || (G != 4 && G != 8 && G != 16)) return false;
+  if (M > (BITS == 4 ? kStreamMMax : 8) || K % kGroupK || (G != 4 && G != 8 && G != 16)) return false;
   if (b.groups_per_row % (16 / (int)sizeof(T)) || !bi_host::aligned16(b.scales) || !bi_host::aligned16(b.biases) ||
       lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a))
     return false;

@@ -109,11 +109,13 @@ def test_quantized_mid_m_launch_matches_oracle(bits_, gs, dt):
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 def test_quantized_stream_launch_up_to_16_rows(bits_, gs, dt):
-    """M <= 8 with >= 512 tiles of 16 columns and 8 or 16 groups takes the
-    streaming GEMV for 2-byte types (one 16-row MFMA tile, A rows past M
-    clamped), 9 <= M <= 16 the mid-M launch, fp32 the workgroup-fold GEMV:
-    rows equal the oracle bit for bit and the same rows computed
-    alone, bit for bit."""
+    """M <= 16 (4-bit; 8-bit: M <= 8) with >= 512 tiles of 16 columns and 8
+    or 16 groups takes the streaming GEMV for 2-byte types (one 16-row MFMA
+    tile, A rows past M clamped; 515 tiles: two column tiles per wave at
+    M = 5..8, four at M = 9..16, the last workgroup's tiles partly or wholly
+    past N), 8-bit at 9 <= M <= 16 the mid-M launch, fp32 the workgroup-fold
+    GEMV: rows equal the oracle bit for bit and the same rows computed alone,
+    bit for bit."""
     N, K = 8192 + 40, 4096     # 515 column tiles, the last one partial; G = 16
     wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 3 + gs)
     wq, s, b = wq.cuda(), s.cuda(), b.cuda()
@@ -122,7 +124,7 @@ def test_quantized_stream_launch_up_to_16_rows(bits_, gs, dt):
     W = ora.dequantize(wq.cpu().view(torch.int32).numpy().view(np.uint32), to_np(s.cpu()), to_np(b.cpu()),
                        gs, bits_, dt)
     cols = np.r_[0:24, 4100:4124, N - 24:N]
-    for M in (1, 4, 5, 8, 9, 16):
+    for M in (1, 4, 5, 8, 9, 12, 16):
         got = run(x[:M])
         rows = sorted({0, M // 2, M - 1})
         want = ora.matmul(to_np(x[rows]), W[cols], dt, kmap="blocked")
