@@ -266,6 +266,19 @@ int bi_exp2_f32(const float* x, float* y, int64_t n, void* stream);
  * reference for the HBM-bound kernels (same bytes, one launch). */
 int bi_stream_read(const void* src, int64_t bytes, uint32_t* sink, uint32_t magic, void* stream);
 
+/* Diagnostic, no counterpart in the reference: one matrix-core step of the
+ * matmul kernels per block, on caller-chosen operands and accumulator. Block
+ * i: a, b [16][32] elements of dtype (row r, k-slot j; slot 8 q + e is what
+ * lane quarter q holds as its element e), c, d [16][16] fp32 (row, column):
+ *   d = c + A B^T by one v_mfma_f32_16x16x32_{bf16,f16}, or for fp32 by the
+ *   kernels' eight v_mfma_f32_16x16x4_f32 (element e of every quarter in
+ *   sub-step e).
+ * nblocks in [0, 2^24]; a and b 16-byte aligned; device pointers, on the
+ * stream. It isolates the instruction whose accumulation the oracle models,
+ * independent of any matmul kernel's data movement. */
+int bi_mfma_step_probe(const void* a, const void* b, const float* c, float* d, int64_t nblocks, int dtype,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,6 +72,51 @@ __global__ __launch_bounds__(512) void stream_read_kernel(const u32x4* __restric
 }
 }  // namespace bi
 
+namespace bi {
+// One matrix-core step per block of the probe: lane (r, q) holds A row r and
+// B row r (an output column) at k-slots 8 q .. 8 q + 7, and accumulator rows
+// 4 q .. 4 q + 3 of column r, as in every matmul kernel of this library.
+template <typename T>
+__global__ __launch_bounds__(64) void mfma_step_probe_kernel(const T* __restrict__ a, const T* __restrict__ b,
+                                                            const float* __restrict__ c, float* __restrict__ d) {
+  const int64_t blk = blockIdx.x;
+  const int lane = threadIdx.x, r = lane % 16, q = lane / 16;
+  const typename Frag<T>::type af = frag_load(a + blk * 512 + r * 32 + 8 * q);
+  const typename Frag<T>::type bf = frag_load(b + blk * 512 + r * 32 + 8 * q);
+  f32x4 acc;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc[e] = c[blk * 256 + (4 * q + e) * 16 + r];
+  acc = mfma_step(af, bf, acc);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) d[blk * 256 + (4 * q + e) * 16 + r] = acc[e];
+}
+}  // namespace bi
+
+extern "C" int bi_mfma_step_probe(const void* a, const void* b, const float* c, float* d, int64_t nblocks,
+                                  int dtype, void* stream) {
+  using namespace bi_host;
+  if (nblocks < 0 || nblocks > ((int64_t)1 << 24))
+    return fail(BI_E_INVALID_ARG, "bi_mfma_step_probe: block count %lld outside [0, 2^24]", (long long)nblocks);
+  if (dtype != BI_BF16 && dtype != BI_F16 && dtype != BI_F32)
+    return fail(BI_E_UNSUPPORTED, "bi_mfma_step_probe: unknown dtype %d", dtype);
+  if (nblocks == 0) return BI_OK;
+  if (!a || !b || !c || !d || !aligned16(a) || !aligned16(b))
+    return fail(BI_E_INVALID_ARG, "bi_mfma_step_probe: null pointer, or a / b not 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned g = (unsigned)nblocks;
+  const float* cf = c;
+  if (dtype == BI_BF16)
+    bi::mfma_step_probe_kernel<bi::bf16><<<g, 64, 0, st>>>(static_cast<const bi::bf16*>(a),
+                                                            static_cast<const bi::bf16*>(b), cf, d);
+  else if (dtype == BI_F16)
+    bi::mfma_step_probe_kernel<bi::f16><<<g, 64, 0, st>>>(static_cast<const bi::f16*>(a),
+                                                          static_cast<const bi::f16*>(b), cf, d);
+  else
+    bi::mfma_step_probe_kernel<float><<<g, 64, 0, st>>>(static_cast<const float*>(a), static_cast<const float*>(b),
+                                                        cf, d);
+  return launch_status("bi_mfma_step_probe");
+}
+
 extern "C" int bi_stream_read(const void* src, int64_t bytes, uint32_t* sink, uint32_t magic, void* stream) {
   using namespace bi_host;
   if (bytes < 0 || bytes % 16 || bytes > ((int64_t)1 << 40))

@@ -192,6 +192,13 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.bi_stream_read(p, 24, p, 0, None) == -1          # not whole 16-byte pieces
     assert lib.bi_stream_read(None, 32, p, 0, None) == -1
     assert lib.bi_stream_read(None, 0, None, 0, None) == 0
+    # the single-step MFMA probe: count, dtype and pointers checked before launch
+    assert lib.bi_mfma_step_probe(p, p, p, p, -1, 2, None) == -1
+    assert lib.bi_mfma_step_probe(p, p, p, p, (1 << 24) + 1, 2, None) == -1
+    assert lib.bi_mfma_step_probe(p, p, p, p, 1, 9, None) == -2
+    assert lib.bi_mfma_step_probe(None, p, p, p, 1, 2, None) == -1
+    assert lib.bi_mfma_step_probe(ctypes.c_void_p(24), p, p, p, 1, 2, None) == -1   # a not 16-byte aligned
+    assert lib.bi_mfma_step_probe(None, None, None, None, 0, 2, None) == 0
 
 
 def test_split_size_routing():

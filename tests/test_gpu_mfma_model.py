@@ -56,3 +56,36 @@ def test_committed_fixture_reproduces_on_this_gpu():
             a, bt = mg.operands(dt, kind, seed=mg.FIXTURE_SEED)
             _, part = mg.split_partials(torch.from_numpy(a).to(DT[dt]).cuda(), torch.from_numpy(bt).to(DT[dt]).cuda())
             assert_bits_equal(mg.sample(part), fx[f"{dt}_{kind}"], f"{dt} {kind}")
+
+
+# ---------------------------------------------------------------------------
+# One matrix-core step on its own (bi_mfma_step_probe): the same model,
+# pinned through the instruction alone, with live accumulators.
+# ---------------------------------------------------------------------------
+import make_mfma_step_golden as sg  # noqa: E402
+
+
+@pytest.mark.parametrize("dt", sg.DTYPES)
+@pytest.mark.parametrize("kind", sg.KINDS)
+def test_single_step_equals_the_mfma_model(dt, kind):
+    """d = c + A B^T by the instruction (no matmul kernel involved) equals the
+    oracle's mfma_step bit for bit on fresh operands of every kind: large and
+    cancelling accumulators, sparse and empty quarters, subnormal operands."""
+    a, b, c = sg.step_operands(dt, kind, seed=77, blocks=64)
+    d = sg.probe(a, b, c, dt)
+    want = sg.model(a, b, c, dt)
+    exact = float(np.mean(d.view(np.uint32) == want.view(np.uint32)))
+    if OUT.is_dir():
+        (OUT / f"mfma_step_{dt}_{kind}.json").write_text(json.dumps({"dtype": dt, "kind": kind, "exact": exact}))
+    assert_bits_equal(d, want, f"{dt} {kind}")
+
+
+def test_committed_step_fixture_reproduces_on_this_gpu():
+    """The single-step vectors in tests/golden/mfma_step_gfx950.npz come back
+    bit for bit from this GPU (the CPU suite checks the oracle against the
+    same file)."""
+    fx = np.load(sg.FIXTURE)
+    for dt in sg.DTYPES:
+        for kind in sg.KINDS:
+            a, b, c = sg.step_operands(dt, kind, sg.FIXTURE_SEED)
+            assert_bits_equal(sg.probe(a, b, c, dt), fx[f"{dt}_{kind}"], f"{dt} {kind}")
