@@ -556,9 +556,14 @@ def _llama_generate(model, prompt, steps):
     memory pool and replay in capture order); the graph also takes the argmax
     into the static token buffer the next step reads. The timed decode region
     replays the 128 graphs back to back, so tokens/s measure the kernels, not
-    Python's per-layer launch cost. Prefill runs eagerly."""
+    Python's per-layer launch cost. Prefill runs eagerly, once untimed on a
+    throwaway cache first (the first call of a shape loads its kernels and
+    grows the allocator's pool)."""
     import torch
     B, T = prompt.shape
+    warm = model.new_cache(B, T)
+    model(prompt, warm, 0)
+    del warm
     cache = model.new_cache(B, T + steps)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     _sync()
