@@ -60,7 +60,8 @@ struct GemvStreamCfg {
   static_assert(sizeof(T) == 2, "gemv_stream: 2-byte element types only (16-byte pieces = one fragment)");
   static_assert(kAElems % (kCE * kWave) == 0, "A slice must be whole 16-byte loads per lane");
   static_assert(kSPR % kCE == 0, "scale rows must be whole 16-byte chunks");
-  static size_t lds_bytes(int /*G*/) { return (size_t)W * kWaveBytes; }
+  static constexpr size_t kLdsBytes = (size_t)W * kWaveBytes;
+  static size_t lds_bytes(int /*G*/) { return kLdsBytes; }
 };
 
 template <typename T, int BITS, int GS, int W, int NB, int MR, int PD, int CT = 1>

@@ -44,6 +44,7 @@ namespace bi {
 
 constexpr int kSplitMMax = 32;
 constexpr int kStreamMMax = 16;   // rows of x the streaming GEMV takes (4-bit; 8-bit codes: 8)
+constexpr int kStreamMinTiles = 128;  // 16-column tiles below which the streaming GEMV is not used
 // gemv_wg with A staged in LDS: at most kGemvAChunks / W 16-byte chunks of A
 // per thread (M * K <= kGemvAChunks * 64 * 8).
 constexpr int kGemvAChunks = 32;
@@ -843,11 +844,18 @@ static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b
   constexpr int kCE = 16 / (int)sizeof(T);
   // 2-byte T only: the kernel's 16-byte staging pieces are whole 8-element
   // fragments only there.
-  if constexpr (sizeof(T) != 2 || (NB * kGroupK / GS) % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0) {
+  // LDS of the configuration (GemvStreamCfg::kLdsBytes, computed here so an
+  // unsupported configuration is never instantiated): MR rows x K of A do not
+  // fit for every shape; the caller then falls back.
+  constexpr size_t kElemBytes = (size_t)(MR * NB * kGroupK + 2 * 16 * CT * (NB * kGroupK / GS)) * sizeof(T);
+  constexpr size_t kLds = (size_t)W * std::max<size_t>(kElemBytes, (size_t)NB * CT * kWave * 16);
+  if constexpr (sizeof(T) != 2 || (NB * kGroupK / GS) % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0 ||
+                kLds > 160 * 1024) {
     return false;
   } else {
     typedef GemvStreamCfg<T, BITS, GS, W, NB, MR, CT> C;
-    if (G != W * NB || C::lds_bytes(G) > 160 * 1024) return false;
+    static_assert(C::kLdsBytes == kLds, "launch_stream1: LDS size");
+    if (G != W * NB) return false;
     // More than 64 KB of dynamic LDS (8 or 16 rows of A) is allowed
     // explicitly, once per instantiation (a failure leaves the default limit
     // and no error state behind; the launch then reports its own status).
@@ -910,10 +918,14 @@ static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& 
 // computed, else four groups per wave one ahead (8-bit g128, whose two-group
 // scale slice is not a whole 16-byte load: 13.7 us against 14.1 two ahead). A
 // shape whose scale slice or A slice is not whole 16-byte loads is skipped.
+// 32 and 56 groups (K = 8192, 14336) run 8 and 14 waves of four groups:
+// [4096, 8192] M = 1 / 4 / 8 8.7 / 10.7 / 11.4 -> 6.6 / 7.2 / 8.1 us, the
+// Llama MLP down projection [4096, 14336] M = 1 / 4 16.7 / 17.5 -> 9.7 /
+// 11.0 us (A's rows x K must fit in LDS: M <= 8 and M <= 4 there).
 template <typename T, int BITS, int GS>
 static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N, int K,
                           int G, hipStream_t st) {
-  if (M > (BITS == 4 ? kStreamMMax : 8) || K % kGroupK || (G != 4 && G != 8 && G != 16)) return false;
+  if (M > (BITS == 4 ? kStreamMMax : 8) || K % kGroupK) return false;
   if (b.groups_per_row % (16 / (int)sizeof(T)) || !bi_host::aligned16(b.scales) || !bi_host::aligned16(b.biases) ||
       lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a))
     return false;
@@ -924,19 +936,22 @@ static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b,
     case 8:
       return launch_stream_m<T, BITS, GS, 4, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
              launch_stream_m<T, BITS, GS, 2, 4, 2>(a, lda, b, out, M, N, K, G, st);
-    default:
+    case 4:
       return launch_stream_m<T, BITS, GS, 4, 1, 1>(a, lda, b, out, M, N, K, G, st) ||
              launch_stream_m<T, BITS, GS, 2, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
              launch_stream_m<T, BITS, GS, 1, 4, 2>(a, lda, b, out, M, N, K, G, st);
+    case 32:
+      return launch_stream_m<T, BITS, GS, 8, 4, 1>(a, lda, b, out, M, N, K, G, st);
+    case 56:
+      return launch_stream_m<T, BITS, GS, 14, 4, 1>(a, lda, b, out, M, N, K, G, st);
+    default:
+      return false;
   }
 }
 
 template <typename T, class BSrc, int W>
 static void launch_wg(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, int N, int K, int G,
                       hipStream_t st) {
-  if constexpr (BSrc::kMeta) {
-    if (W == 4 && launch_stream<T, BSrc::kBits, BSrc::kGS>(a, lda, bsrc, out, M, N, K, G, st)) return;
-  }
   dim3 grid(ceil_div(N, 16), 1, 1);
   const int mt = M <= 16 ? 1 : 2;
   const size_t part_bytes = (size_t)G * mt * kWave * sizeof(f32x4);
@@ -1060,7 +1075,13 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   const int G = ceil_div(K, kGroupK);
   constexpr int WAVES = 4;
   if constexpr (BSrc::kMeta) {
-    if (M > 4 && ceil_div(N, 16) >= 512 && G >= 8 &&
+    // The streaming GEMV wherever it takes the shape (M <= 16, 4-bit; M <= 8,
+    // 8-bit; 4 < M only with 8 or more groups) and there are at least 128
+    // column tiles. Measured against the workgroup-fold GEMV and the mid-M
+    // launch it replaces below 512 tiles (4-bit g64, K = 4096): N = 4096 M =
+    // 1 / 4 / 8 / 16 5.7 / 5.9 / 6.8 / 8.0 -> 4.5 / 4.8 / 5.3 / 6.0 us; N =
+    // 2048 (128 tiles) 5.0 / 5.2 / 6.6 / 7.8 -> 4.1 / 4.4 / 4.8 / 5.5 us.
+    if (ceil_div(N, 16) >= kStreamMinTiles && (M <= 4 || G >= 8) &&
         launch_stream<T, BSrc::kBits, BSrc::kGS>(a, lda, bsrc, out, M, N, K, G, st))
       return bi_host::launch_status(what);
   }

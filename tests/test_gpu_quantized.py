@@ -133,6 +133,31 @@ def test_quantized_stream_launch_up_to_16_rows(bits_, gs, dt):
             assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
 
 
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (4, 128)])
+@pytest.mark.parametrize("N,K", [(2048 + 40, 4096), (4096 + 24, 8192), (4096 + 8, 14336)])
+def test_quantized_stream_launch_fewer_tiles_and_longer_k(bits_, gs, N, K):
+    """The streaming GEMV below 512 column tiles (131 and 258 tiles, the last
+    one partial) and at 32 and 56 groups (eight and fourteen waves of four
+    groups): M <= 16 (4-bit) / 8 (8-bit) where A's rows fit in LDS, the
+    mid-M launch past that (56 groups: M > 4). Rows equal the oracle and the
+    same rows computed alone, bit for bit."""
+    dt = "bf16"
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 11 + gs + K % 977)
+    cols = np.r_[0:24, N // 2:N // 2 + 16, N - 24:N]
+    W = ora.dequantize(wq[cols].view(torch.int32).numpy().view(np.uint32), to_np(s[cols]), to_np(b[cols]),
+                       gs, bits_, dt)
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    x = randn((16, K), DT[dt], gen(19))
+    run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+    for M in (1, 3, 5, 8, 12, 16):
+        got = run(x[:M])
+        rows = sorted({0, M // 2, M - 1})
+        want = ora.matmul(to_np(x[rows]), W, dt, kmap="blocked")
+        assert_bits_equal(to_np(got)[rows][:, cols], want, f"N={N} K={K} M={M}")
+        for rr in rows:
+            assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
+
+
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_quantized_mid_m_split_k_matches_oracle(bits_, gs, dt):
