@@ -353,8 +353,9 @@ __global__ __launch_bounds__(256) void attn_decode_mfma(DecodeArgs a) {
 // Prefill: one 256-thread workgroup per (sequence, kv head, 64 (token, head)
 // rows, token-major); wave w owns the 16 rows 16 w .. 16 w + 15 of them (the
 // columns of its score tiles). K and V stream through a ring of NBUF LDS
-// buffers of 64 keys (prefill_ring), shared by the four waves: per split, the
-// K chunks (each wave scores its rows against the chunk's 64 keys, scores kept
+// buffers of CH keys (prefill_ring, prefill_chunk), shared by the four waves:
+// per split, the K chunks (each wave scores its rows against the chunk's keys,
+// scores kept
 // in registers), the split maximum and weights (in registers), then the V
 // chunks (P.V and the weight sum), then the in-register merge. Chunk
 // c + NBUF - 1 is requested right after the barrier that opens chunk c. Only the chunks the
@@ -372,12 +373,23 @@ constexpr int prefill_ring() {
   return 2;
 }
 
-template <typename T, int D, int MODE, int NBUF = prefill_ring<T, D>()>
+// Keys per ring chunk: 128 for contiguous caches whose rows are at most 256
+// bytes (16-bit D <= 128), else 64 (paged caches address 64-key segments).
+// A chunk costs a barrier and its copy issue; 128-key chunks halve both per
+// split.
+template <typename T, int D, int MODE>
+constexpr int prefill_chunk() {
+  return MODE == kKvContig && D * (int)sizeof(T) <= 256 ? 128 : 64;
+}
+
+template <typename T, int D, int MODE, int NBUF = prefill_ring<T, D>(), int CH = prefill_chunk<T, D, MODE>()>
 __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   constexpr bool ROWPAGED = MODE == kKvRowPaged;
   typedef typename Frag<T>::type F;
   typedef KVTile<T, D> KV;
-  constexpr int CH = 64;                                // keys per chunk
+  static_assert(CH == 64 || (CH == 128 && MODE == kKvContig), "attn_prefill_mfma: chunk size");
+  constexpr int KC = kSplit / CH;                       // chunks per split (of K, then of V)
+  constexpr int TPC = CH / 16;                          // 16-key score tiles per chunk
   constexpr int CHB = CH * KV::kRowBytes;               // bytes per chunk
   static_assert(NBUF >= 2 && NBUF <= 5 && NBUF * CHB <= (160 << 10), "attn_prefill_mfma: ring depth");
   constexpr int PF = NBUF - 1;                          // chunks requested ahead of the current one
@@ -423,12 +435,12 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
     for (int st = 0; st < D / 32; ++st) qf[st] = ok ? frag_load(qrow + 32 * st + 8 * qq) : frag_zero<F>();
   }
 
-  // Chunk schedule: split sp has nkc(sp) = 4 chunks of 64 keys (the last
+  // Chunk schedule: split sp has nkc(sp) = KC chunks of CH keys (the last
   // split: enough for maxkeys), K chunks then V chunks.
   const int nsplit = maxkeys > 0 ? (maxkeys + kSplit - 1) / kSplit : 0;
   const int last_keys = nsplit > 0 ? maxkeys - (nsplit - 1) * kSplit : 0;
   const int nkc_last = (last_keys + CH - 1) / CH;
-  const int nchunks = nsplit > 0 ? 8 * (nsplit - 1) + 2 * nkc_last : 0;
+  const int nchunks = nsplit > 0 ? 2 * KC * (nsplit - 1) + 2 * nkc_last : 0;
   // Contiguous cache: a chunk's copies go through a buffer resource whose
   // base is the chunk's first row and whose range ends at the sequence's last
   // key, with a per-lane byte offset that is the same for every chunk (the
@@ -450,10 +462,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   auto issue = [&](int c) {
     if (c >= nchunks) return;
     int sp, kind, kc;
-    if (c < 8 * (nsplit - 1)) {
-      sp = c / 8; kind = (c % 8) / 4; kc = c % 4;
+    if (c < 2 * KC * (nsplit - 1)) {
+      sp = c / (2 * KC); kind = (c % (2 * KC)) / KC; kc = c % KC;
     } else {
-      const int cl = c - 8 * (nsplit - 1);
+      const int cl = c - 2 * KC * (nsplit - 1);
       sp = nsplit - 1; kind = cl / nkc_last; kc = cl % nkc_last;
     }
     const int key0 = sp * kSplit + kc * CH;
@@ -518,31 +530,31 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   auto split_body = [&](const int sp, auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
     const int j0 = sp * kSplit;
-    const int nkc = sp + 1 < nsplit ? 4 : nkc_last;
+    const int nkc = sp + 1 < nsplit ? KC : nkc_last;
     // Scores of the wave's 16 rows against the split's keys (tile t: keys j0 + 16 t + ...).
     float s[16][4];
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
+    for (int kc = 0; kc < KC; ++kc) {
       if (kc < nkc) {
         open_chunk(ci);
         const char* buf = ring + (ci % NBUF) * CHB;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < TPC; ++t) {
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int st = 0; st < D / 32; ++st) acc = mfma_step(KV::kfrag(buf, 16 * t + r, st, qq), qf[st], acc);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int key = j0 + 64 * kc + 16 * t + 4 * qq + i;
-            s[4 * kc + t][i] = (!MASKED || key < my_nkeys) ? acc[i] * a.scale_log2 : -INFINITY;
+            const int key = j0 + CH * kc + 16 * t + 4 * qq + i;
+            s[TPC * kc + t][i] = (!MASKED || key < my_nkeys) ? acc[i] * a.scale_log2 : -INFINITY;
           }
         }
         ++ci;
       } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < TPC; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) s[4 * kc + t][i] = -INFINITY;
+          for (int i = 0; i < 4; ++i) s[TPC * kc + t][i] = -INFINITY;
       }
     }
     float m = -INFINITY;
@@ -563,13 +575,13 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
+    for (int kc = 0; kc < KC; ++kc) {
       if (kc < nkc) {
         open_chunk(ci);
         const char* buf = ring + (ci % NBUF) * CHB;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int t0 = 4 * kc + 2 * h;
+        for (int h = 0; h < CH / 32; ++h) {
+          const int t0 = TPC * kc + 2 * h;
           float p8[8];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
