@@ -676,6 +676,7 @@ def bench_llama(args):
     import torch
     import mlx_batch_invariant_amd as bi
     from mlx_batch_invariant_amd.llama import LlamaConfig, LlamaShaped
+    from mlx_batch_invariant_amd.nn import QuantizedLinear
     T, steps, batches = args.llama_prompt, args.llama_steps, (1, 4, 16, 64)
     res = {}
     for bits in (4, None):
@@ -690,13 +691,26 @@ def bench_llama(args):
             fill = torch.randint(0, cfg.vocab, (B - 1, T), generator=torch.Generator().manual_seed(B))
             prompt = torch.cat([row0, fill]).cuda()
             entry = {}
-            for label, on in (("invariant", True), ("stock", False)):
+            # 4-bit also runs with every weight dequantized once next to its codes
+            # (QuantizedLinear.cache_dequantized): prefill (M >= 256) then skips the
+            # per-call dequantization, same bits; decode reads the codes either way.
+            runs = [("invariant", True, False), ("stock", False, False)]
+            if bits:
+                runs.append(("invariant_dequantized_once", True, True))
+            for label, on, cached in runs:
                 bi.reset_stats()
                 mdl = model if on else stock_model
+                qlins = [m for m in mdl.modules() if isinstance(m, QuantizedLinear)] if cached else []
+                for m in qlins:
+                    m.cache_dequantized()
                 with bi.set_batch_invariant_mode(enabled=on, strict=on):
                     _llama_generate(mdl, prompt[:, :16], 2)            # warm-up
                     tp, td, lg = _llama_generate(mdl, prompt, steps)
+                for m in qlins:
+                    bi.drop_dequantized(m.weight)
                 ref.setdefault(label, lg)
+                if cached:
+                    entry[label + "_bits_equal_invariant"] = lg == ref["invariant"]
                 entry[label] = {"prefill_tok_s": round(B * T / tp, 1), "decode_tok_s": round(B * steps / td, 1),
                                 "prefill_s": round(tp, 3), "decode_s": round(td, 3),
                                 "row0_logits_equal_B1": lg == ref[label]}

@@ -131,6 +131,25 @@ int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w, const voi
                         int bits, int group_size, int dtype, void* ws, size_t ws_bytes,
                         void* stream);
 
+/* The quantized op on a weight dequantized once. bi_quantized_dequantize
+ * writes bq [N, K] (dtype elements): W dequantized as above, its 8-element
+ * chunks permuted within each 256-k group into the order the dense kernels
+ * read (the large-M launch's own copy of the weight). bi_quantized_matmul_-
+ * dequantized computes out[M, N] from x and bq, bit for bit equal to
+ * bi_quantized_matmul on the same x and weight at every M (the dense kernels
+ * on the permuted operands put the quantized order's products in every
+ * matrix-core slot); workspace from bi_quantized_matmul_dequantized_-
+ * workspace_bytes (x reordered, plus the dense launch's partials).
+ * bf16 / fp16, K % 256 == 0, ldx % 8 == 0, x and bq 16-byte aligned.
+ * No counterpart in the reference (MLX dequantizes inside its kernels): for
+ * callers that keep a dequantized copy next to the codes, so that prefill
+ * (large M) skips the per-call dequantization. */
+int bi_quantized_dequantize(const uint32_t* w, const void* scales, const void* biases, void* bq, int64_t N,
+                            int64_t K, int bits, int group_size, int dtype, void* stream);
+size_t bi_quantized_matmul_dequantized_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int bi_quantized_matmul_dequantized(const void* x, int64_t ldx, const void* bq, void* out, int64_t M, int64_t N,
+                                    int64_t K, int dtype, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- Split-KV decode attention (one query token per sequence) -------------
  * q [B, Hq, D], k/v [B, Hkv, L, D] addressed through element strides
  *   strides[0..1] = q  (batch, head)

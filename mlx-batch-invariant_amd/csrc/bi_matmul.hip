@@ -170,3 +170,97 @@ extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w
     default: return fail(BI_E_UNSUPPORTED, "bi_quantized_matmul: unknown dtype %d", dtype);
   }
 }
+
+// ---------------------------------------------------------------------------
+// The quantized op on a weight dequantized once (the large-M launch's B': the
+// dequantized weight in the dense tile's k order, bi_qmm_big.h). With A
+// reordered the same way, every dense launch puts in each MFMA slot exactly
+// the product the quantized launches put there, so the result equals
+// bi_quantized_matmul's bit for bit at every M; a caller that keeps B' skips
+// the per-call dequantization of the large-M launch.
+// ---------------------------------------------------------------------------
+namespace {
+
+template <typename T, int BITS>
+int dequantize_bits(int gs, const uint32_t* w, const void* scales, const void* biases, void* bq, int N, int K,
+                    hipStream_t st) {
+  const int64_t nb = (int64_t)N * (K / 8);
+  const unsigned grid = (unsigned)((nb + 255) / 256);
+  const T* sc = static_cast<const T*>(scales);
+  const T* bs = static_cast<const T*>(biases);
+  T* out = static_cast<T*>(bq);
+  if (gs == 32) bi::qmm_dequant_rows<T, BITS, 32><<<grid, 256, 0, st>>>(w, sc, bs, out, N, K);
+  else if (gs == 64) bi::qmm_dequant_rows<T, BITS, 64><<<grid, 256, 0, st>>>(w, sc, bs, out, N, K);
+  else bi::qmm_dequant_rows<T, BITS, 128><<<grid, 256, 0, st>>>(w, sc, bs, out, N, K);
+  return bi_host::launch_status("bi_quantized_dequantize");
+}
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+}  // namespace
+
+extern "C" int bi_quantized_dequantize(const uint32_t* w, const void* scales, const void* biases, void* bq,
+                                       int64_t N, int64_t K, int bits, int group_size, int dtype, void* stream) {
+  using namespace bi_host;
+  if ((bits != 4 && bits != 8) || (group_size != 32 && group_size != 64 && group_size != 128))
+    return fail(BI_E_UNSUPPORTED, "bi_quantized_dequantize: bits=%d group_size=%d not in {4,8}x{32,64,128}", bits,
+                group_size);
+  if (dtype != BI_BF16 && dtype != BI_F16)
+    return fail(BI_E_UNSUPPORTED, "bi_quantized_dequantize: dtype %d (bf16 and fp16 only)", dtype);
+  if (N < 0 || K < 0 || N > 0x7fffffffLL || K > 0x7fffffffLL || K % bi::kGroupK || N * (K / 8) > ((int64_t)1 << 40))
+    return fail(BI_E_INVALID_ARG, "bi_quantized_dequantize: N=%lld K=%lld (K a multiple of 256)", (long long)N,
+                (long long)K);
+  if (N == 0 || K == 0) return BI_OK;
+  if (!w || !scales || !biases || !bq || !aligned16(bq))
+    return fail(BI_E_INVALID_ARG, "bi_quantized_dequantize: null pointer, or bq not 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Ni = (int)N, Ki = (int)K;
+  if (dtype == BI_BF16)
+    return bits == 4 ? dequantize_bits<bi::bf16, 4>(group_size, w, scales, biases, bq, Ni, Ki, st)
+                     : dequantize_bits<bi::bf16, 8>(group_size, w, scales, biases, bq, Ni, Ki, st);
+  return bits == 4 ? dequantize_bits<bi::f16, 4>(group_size, w, scales, biases, bq, Ni, Ki, st)
+                   : dequantize_bits<bi::f16, 8>(group_size, w, scales, biases, bq, Ni, Ki, st);
+}
+
+extern "C" size_t bi_quantized_matmul_dequantized_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return align256((size_t)M * (size_t)K * 2) + split_ws_bytes(M, N, K, true);
+}
+
+extern "C" int bi_quantized_matmul_dequantized(const void* x, int64_t ldx, const void* bq, void* out, int64_t M,
+                                               int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes,
+                                               void* stream) {
+  using namespace bi_host;
+  if (dtype != BI_BF16 && dtype != BI_F16)
+    return fail(BI_E_UNSUPPORTED, "bi_quantized_matmul_dequantized: dtype %d (bf16 and fp16 only)", dtype);
+  if (M < 0 || N < 0 || K < 0 || M > 0x7fffffffLL || N > 0x7fffffffLL || K > 0x7fffffffLL || K % bi::kGroupK)
+    return fail(BI_E_INVALID_ARG, "bi_quantized_matmul_dequantized: M=%lld N=%lld K=%lld (K a multiple of 256)",
+                (long long)M, (long long)N, (long long)K);
+  if (M == 0 || N == 0) return BI_OK;
+  if (K == 0) return fail(BI_E_INVALID_ARG, "bi_quantized_matmul_dequantized: K = 0");
+  if (!x || !bq || !out || ldx % 8 || ldx < K || !aligned16(x) || !aligned16(bq))
+    return fail(BI_E_INVALID_ARG,
+                "bi_quantized_matmul_dequantized: needs ldx %% 8 == 0, ldx >= K, 16-byte aligned x and bq");
+  const size_t a_bytes = align256((size_t)M * (size_t)K * 2);
+  const size_t need = bi_quantized_matmul_dequantized_workspace_bytes(M, N, K);
+  if (!ws || ws_bytes < need || !aligned16(ws))
+    return fail(BI_E_WORKSPACE,
+                "bi_quantized_matmul_dequantized: 16-byte aligned workspace of %zu bytes required, got %zu", need,
+                ws ? ws_bytes : (size_t)0);
+  int rc = check_common("bi_quantized_matmul_dequantized", M, N, K, out, static_cast<char*>(ws) + a_bytes,
+                        ws_bytes - a_bytes, true);
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+  float* wsd = reinterpret_cast<float*>(static_cast<char*>(ws) + a_bytes);
+  const int64_t na = (int64_t)M * (K / 8);
+  auto go = [&](auto tag) {
+    typedef decltype(tag) T;
+    T* ap = static_cast<T*>(ws);
+    bi::qmm_permute_a<T><<<(unsigned)((na + 255) / 256), 256, 0, st>>>(static_cast<const T*>(x), ldx, ap, Mi, Ki);
+    bi::DenseB<T> db{static_cast<const T*>(bq), K, Ni, Ki};
+    return bi::run_gemm<T, bi::DenseB<T>>(ap, K, db, static_cast<T*>(out), Mi, Ni, Ki, wsd, st,
+                                          "bi_quantized_matmul_dequantized");
+  };
+  return dtype == BI_BF16 ? go(bi::bf16{}) : go(bi::f16{});
+}

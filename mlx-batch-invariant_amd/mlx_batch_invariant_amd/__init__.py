@@ -22,7 +22,7 @@ from .kernels import (
     batch_invariant_quantized_matmul,
     batch_invariant_rms_norm,
 )
-from .kernels.quantized import quantize, dequantize, pack, unpack
+from .kernels.quantized import quantize, dequantize, pack, unpack, cache_dequantized, drop_dequantized
 from . import library  # registers torch.ops.mlx_bi.*
 
 __all__ = [
@@ -41,6 +41,8 @@ __all__ = [
     "batch_invariant_paged_attention",
     "quantize",
     "dequantize",
+    "cache_dequantized",
+    "drop_dequantized",
     "pack",
     "unpack",
 ]

@@ -73,6 +73,11 @@ _SIGNATURES = {
                                              ctypes.c_float, ctypes.c_int, _vp]),
     "bi_exp2_f32": (ctypes.c_int, [_vp, _vp, _c_i64, _vp]),
     "bi_stream_read": (ctypes.c_int, [_vp, _c_i64, _vp, ctypes.c_uint32, _vp]),
+    "bi_quantized_dequantize": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int, _vp]),
+    "bi_quantized_matmul_dequantized_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
+    "bi_quantized_matmul_dequantized": (ctypes.c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
+                                                       _vp, ctypes.c_size_t, _vp]),
     "bi_mfma_step_probe": (ctypes.c_int, [_vp, _vp, _vp, _vp, _c_i64, ctypes.c_int, _vp]),
 }
 

@@ -21,6 +21,8 @@ and are cast to the input dtype, as in the reference (quantized.py:116-119).
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from .. import _lib
@@ -80,7 +82,16 @@ def batch_invariant_quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: t
     x2 = _prep_rows(x if flat else x.reshape(-1, K), K)
     M = x2.shape[0]
     out = torch.empty((M, N), dtype=dt, device=x.device)
-    if M > 0:
+    bq = _dequantized_for(w, scales, biases, group_size, bits, dt) if M >= DEQUANTIZED_MIN_M else None
+    if bq is not None:
+        _lib.load()
+        ws_bytes = _lib.ws_bytes("bi_quantized_matmul_dequantized_workspace_bytes", M, N, K)
+        ws = _lib.workspace(ws_bytes, x.device)
+        rc = _lib.load().bi_quantized_matmul_dequantized(x2.data_ptr(), x2.stride(0), bq.data_ptr(), out.data_ptr(),
+                                                         M, N, K, _lib.DTYPE_CODE[dt], _lib.ptr(ws), ws_bytes,
+                                                         _lib.stream_of(x))
+        _lib.check(rc, "bi_quantized_matmul_dequantized")
+    elif M > 0:
         _lib.load()
         ws_bytes = _lib.ws_bytes("bi_quantized_matmul_workspace_bytes", M, N, K)
         ws = _lib.workspace(ws_bytes, x.device)
@@ -89,6 +100,71 @@ def batch_invariant_quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: t
                                      _lib.DTYPE_CODE[dt], _lib.ptr(ws), ws_bytes, _lib.stream_of(x))
         _lib.check(rc, "bi_quantized_matmul")
     return out if flat else out.reshape(*lead, N)
+
+
+# ---- weights dequantized once (large-M calls) ----------------------------------
+
+# Rows of x from which a cached dequantized weight is used: the large-M launch
+# of bi_quantized_matmul dequantizes its weight on every call from here on.
+DEQUANTIZED_MIN_M = 256
+# id(w) -> (weakref to w, w's / scales' / biases' data pointers, group size, bits,
+# dtype, the copy); an entry goes when w is collected (tensors compare
+# elementwise, so they cannot key a WeakKeyDictionary).
+_DEQUANTIZED: dict = {}
+
+
+def cache_dequantized(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, group_size: int,
+                      bits: int) -> torch.Tensor:
+    """Keep a dequantized copy of the packed weight ``w`` (``bi_quantized_dequantize``:
+    ``[N, K]`` in scales' dtype, bf16 or fp16, its chunks in the dense kernels'
+    k order) for as long as ``w`` lives. Calls of
+    ``batch_invariant_quantized_matmul`` with at least ``DEQUANTIZED_MIN_M`` rows,
+    this ``w`` (the same tensor object) and these scales / biases then run
+    ``bi_quantized_matmul_dequantized`` on it: the same bits, without the
+    per-call dequantization. The copy holds N * K * 2 bytes (the size of the
+    weight dequantized once, as a stock serving path keeps it). Call again after
+    changing the weight's values in place; ``drop_dequantized`` releases it."""
+    if bits not in SUPPORTED_BITS or group_size not in SUPPORTED_GROUPS:
+        raise ValueError(f"cache_dequantized: bits={bits} group_size={group_size}")
+    dt = scales.dtype
+    if dt not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"cache_dequantized: scales dtype {dt} (bf16 or fp16)")
+    if w.dtype not in _WORD_DTYPES or w.ndim != 2 or not w.is_contiguous():
+        raise ValueError("cache_dequantized: w must be a contiguous 2-D uint32 tensor")
+    _lib.require_gpu("cache_dequantized", w, scales, biases)
+    N, K = w.shape[0], w.shape[1] * (32 // bits)
+    if K % 256:
+        raise ValueError(f"cache_dequantized: K={K} must be a multiple of 256")
+    if tuple(scales.shape) != (N, K // group_size) or scales.shape != biases.shape or biases.dtype != dt \
+            or not scales.is_contiguous() or not biases.is_contiguous():
+        raise ValueError("cache_dequantized: scales/biases must be contiguous [N, K / group_size] of one dtype")
+    bq = torch.empty((N, K), dtype=dt, device=w.device)
+    rc = _lib.load().bi_quantized_dequantize(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), bq.data_ptr(), N, K,
+                                             bits, group_size, _lib.DTYPE_CODE[dt], _lib.stream_of(w))
+    _lib.check(rc, "bi_quantized_dequantize")
+    key = id(w)
+    ref = weakref.ref(w, lambda _r, k=key: _DEQUANTIZED.pop(k, None) if _DEQUANTIZED.get(k, (None,))[0] is _r else None)
+    _DEQUANTIZED[key] = (ref, w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size, bits, dt, bq)
+    return bq
+
+
+def drop_dequantized(w: torch.Tensor) -> None:
+    """Release the dequantized copy ``cache_dequantized`` keeps for ``w``."""
+    e = _DEQUANTIZED.get(id(w))
+    if e is not None and e[0]() is w:
+        del _DEQUANTIZED[id(w)]
+
+
+def _dequantized_for(w, scales, biases, group_size, bits, dt):
+    """The cached copy for exactly this call (same tensor and storage, same
+    scales / biases, format and dtype), else None."""
+    e = _DEQUANTIZED.get(id(w)) if _DEQUANTIZED else None
+    if e is None or e[0]() is not w:
+        return None
+    if (e[1], e[2], e[3], e[4], e[5], e[6]) != (w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size,
+                                                bits, dt):
+        return None
+    return e[7]
 
 
 # ---- format helpers (host-side torch; not on the kernel path) -----------------

@@ -59,6 +59,14 @@ class QuantizedLinear(torch.nn.Module):
         q.bias = None if lin.bias is None else torch.nn.Parameter(lin.bias.detach().clone())
         return q
 
+    def cache_dequantized(self):
+        """Keep the weight dequantized once (``kernels.quantized.cache_dequantized``):
+        under the mode, calls with at least ``DEQUANTIZED_MIN_M`` rows (prefill)
+        then skip the per-call dequantization, with the same bits. Costs
+        out_features * in_features * 2 bytes of device memory."""
+        _quant.cache_dequantized(self.weight, self.scales, self.biases, group_size=self.group_size, bits=self.bits)
+        return self
+
     def forward(self, x):
         y = _this.quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
                                    group_size=self.group_size, bits=self.bits)

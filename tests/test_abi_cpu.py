@@ -199,6 +199,19 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.bi_mfma_step_probe(None, p, p, p, 1, 2, None) == -1
     assert lib.bi_mfma_step_probe(ctypes.c_void_p(24), p, p, p, 1, 2, None) == -1   # a not 16-byte aligned
     assert lib.bi_mfma_step_probe(None, None, None, None, 0, 2, None) == 0
+    # the dequantize-once pair: formats, dtypes, shapes, pointers and workspace checked before launch
+    assert lib.bi_quantized_dequantize(p, p, p, p, 16, 256, 3, 64, 2, None) == -2        # bits
+    assert lib.bi_quantized_dequantize(p, p, p, p, 16, 256, 4, 64, 3, None) == -2        # fp32
+    assert lib.bi_quantized_dequantize(p, p, p, p, 16, 320, 4, 64, 2, None) == -1        # K % 256
+    assert lib.bi_quantized_dequantize(None, p, p, p, 16, 256, 4, 64, 2, None) == -1
+    assert lib.bi_quantized_dequantize(None, None, None, None, 0, 256, 4, 64, 2, None) == 0
+    need = lib.bi_quantized_matmul_dequantized_workspace_bytes(512, 4096, 4096)
+    assert need >= 512 * 4096 * 2
+    assert lib.bi_quantized_matmul_dequantized(p, 4096, p, p, 512, 4096, 4096, 2, p, need - 16, None) == -3
+    assert lib.bi_quantized_matmul_dequantized(p, 4096, p, p, 512, 4096, 4096, 3, p, need, None) == -2
+    assert lib.bi_quantized_matmul_dequantized(p, 4096, p, p, 512, 4096, 4000, 2, p, need, None) == -1
+    assert lib.bi_quantized_matmul_dequantized(p, 4095, p, p, 512, 4096, 4096, 2, p, need, None) == -1
+    assert lib.bi_quantized_matmul_dequantized(None, 0, None, None, 0, 4096, 4096, 2, None, 0, None) == 0
 
 
 def test_split_size_routing():

@@ -261,3 +261,64 @@ def test_quantized_errors():
         bi.batch_invariant_quantized_matmul(x, w, s, s, group_size=64, bits=3)
     with pytest.raises(ValueError):
         bi.batch_invariant_quantized_matmul(x[:, :32], w, s, s, group_size=64, bits=4)
+
+
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_dequantized_once_equals_the_quantized_op(bits_, gs, dt):
+    """bi_quantized_matmul_dequantized on the weight dequantized once
+    (bi_quantized_dequantize) equals bi_quantized_matmul bit for bit at every M
+    (the GEMV, mid-M and large-M launches of the quantized op against the
+    dense launches on the reordered operands); the cache that
+    batch_invariant_quantized_matmul uses from DEQUANTIZED_MIN_M rows gives the
+    same bits, follows only the cached tensors, and is released by
+    drop_dequantized."""
+    from mlx_batch_invariant_amd import _lib
+    from mlx_batch_invariant_amd.kernels import quantized as kq
+    bi = _bi()
+    N, K = 1000, 768
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 13 + gs)
+    wq, s, b = wq.view(torch.int32).cuda(), s.cuda(), b.cuda()
+    x = randn((300, K), DT[dt], gen(23))
+    lib = _lib.load()
+    bq = torch.empty((N, K), dtype=DT[dt], device="cuda")
+    _lib.check(lib.bi_quantized_dequantize(wq.data_ptr(), s.data_ptr(), b.data_ptr(), bq.data_ptr(), N, K, bits_, gs,
+                                           _lib.DTYPE_CODE[DT[dt]], None), "bi_quantized_dequantize")
+    for M in (1, 5, 16, 64, 255, 256, 300):
+        want = bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=gs, bits=bits_)
+        need = lib.bi_quantized_matmul_dequantized_workspace_bytes(M, N, K)
+        ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+        got = torch.empty((M, N), dtype=DT[dt], device="cuda")
+        _lib.check(lib.bi_quantized_matmul_dequantized(x.data_ptr(), x.stride(0), bq.data_ptr(), got.data_ptr(), M, N,
+                                                       K, _lib.DTYPE_CODE[DT[dt]], ws.data_ptr(), need, None),
+                   "bi_quantized_matmul_dequantized")
+        torch.cuda.synchronize()
+        assert bits(got) == bits(want), M
+    # the cache inside batch_invariant_quantized_matmul
+    plain = bi.batch_invariant_quantized_matmul(x, wq, s, b, group_size=gs, bits=bits_)
+    cached = bi.cache_dequantized(wq, s, b, group_size=gs, bits=bits_)
+    assert bits(cached) == bits(bq)
+    assert kq._dequantized_for(wq, s, b, gs, bits_, DT[dt]) is not None
+    assert kq._dequantized_for(wq, s.clone(), b, gs, bits_, DT[dt]) is None      # other scales: not this copy
+    assert bits(bi.batch_invariant_quantized_matmul(x, wq, s, b, group_size=gs, bits=bits_)) == bits(plain)
+    assert bits(bi.batch_invariant_quantized_matmul(x[:16], wq, s, b, group_size=gs, bits=bits_)) == bits(plain[:16])
+    bi.drop_dequantized(wq)
+    assert kq._dequantized_for(wq, s, b, gs, bits_, DT[dt]) is None
+
+
+def test_quantized_linear_cache_under_the_mode():
+    """QuantizedLinear.cache_dequantized: the module's prefill-sized call under
+    the mode gives the same bits with and without the cached copy."""
+    bi = _bi()
+    from mlx_batch_invariant_amd.nn import QuantizedLinear
+    lin = torch.nn.Linear(1024, 2048, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn((2048, 1024), generator=gen(29)) * 0.02)
+    q = QuantizedLinear.from_linear(lin.to(torch.bfloat16), group_size=64, bits=4).cuda()
+    x = randn((2, 300, 1024), torch.bfloat16, gen(31))
+    with bi.set_batch_invariant_mode(strict=True):
+        plain = q(x)
+        q.cache_dequantized()
+        cached = q(x)
+    assert bits(cached) == bits(plain)
+    bi.drop_dequantized(q.weight)

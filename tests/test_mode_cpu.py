@@ -192,3 +192,32 @@ def test_causal_bias_masks_are_not_array_masks():
     assert ops._causal_variant(None, True, 3, 7) == (True, "upper_left")
     assert ops._causal_variant(lr, True, 3, 7) == (False, None)
     assert ops._causal_variant(causal_lower_right(3, 6), False, 3, 7) == (False, None)
+
+
+def test_dequantized_cache_follows_the_weight_tensor():
+    """The dequantize-once cache entry matches only its own weight tensor and
+    the scales / biases it was made from, goes with drop_dequantized, and goes
+    when the weight tensor is collected (bookkeeping only: no GPU call)."""
+    import gc
+    import weakref
+    from mlx_batch_invariant_amd.kernels import quantized as kq
+    w = torch.zeros((4, 32), dtype=torch.int32)
+    s, b = torch.zeros((4, 4)), torch.zeros((4, 4))
+    key = id(w)
+
+    def put():
+        ref = weakref.ref(w, lambda _r, k=key: kq._DEQUANTIZED.pop(k, None)
+                          if kq._DEQUANTIZED.get(k, (None,))[0] is _r else None)
+        kq._DEQUANTIZED[key] = (ref, w.data_ptr(), s.data_ptr(), b.data_ptr(), 64, 4, torch.float32, "copy")
+
+    put()
+    assert kq._dequantized_for(w, s, b, 64, 4, torch.float32) == "copy"
+    assert kq._dequantized_for(w, s.clone(), b, 64, 4, torch.float32) is None
+    assert kq._dequantized_for(w, s, b, 32, 4, torch.float32) is None
+    assert kq._dequantized_for(w.clone(), s, b, 64, 4, torch.float32) is None
+    kq.drop_dequantized(w)
+    assert key not in kq._DEQUANTIZED
+    put()
+    del w
+    gc.collect()
+    assert key not in kq._DEQUANTIZED
