@@ -39,10 +39,14 @@
 
 namespace bi {
 
-template <typename T, int BITS, int GS, int W, int NB, int MR, int CT = 1>
+// Group size of a B source's per-group metadata; 0 for a dense B (none).
+template <class BSrc> struct StreamMeta { static constexpr int kGS = 0; };
+template <typename T, int BITS, int GS> struct StreamMeta<QuantB<T, BITS, GS>> { static constexpr int kGS = GS; };
+
+template <typename T, int GS, int W, int NB, int MR, int CT = 1>
 struct GemvStreamCfg {
   static constexpr int kCE = 16 / (int)sizeof(T);            // elements per 16-byte load
-  static constexpr int kSPR = NB * kGroupK / GS;              // scales per row per wave
+  static constexpr int kSPR = GS > 0 ? NB * kGroupK / GS : 0; // scales per row per wave (GS = 0: dense B)
   static constexpr int kRows = 16 * CT;                       // weight rows (output columns) per workgroup
   static constexpr int kAElems = MR * NB * kGroupK;           // A elements per wave
   static constexpr int kALoads = kAElems / kCE / kWave;       // A loads per lane
@@ -64,13 +68,13 @@ struct GemvStreamCfg {
   static size_t lds_bytes(int /*G*/) { return kLdsBytes; }
 };
 
-template <typename T, int BITS, int GS, int W, int NB, int MR, int PD, int CT = 1>
-__global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
-                                                        QuantB<T, BITS, GS> bsrc,
+template <typename T, class BSrc, int W, int NB, int MR, int PD, int CT = 1>
+__global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda, BSrc bsrc,
                                                         T* __restrict__ out, int M, int N, int K,
                                                         int G) {
-  typedef GemvStreamCfg<T, BITS, GS, W, NB, MR, CT> C;
-  typedef QuantB<T, BITS, GS> QB;
+  constexpr int GS = StreamMeta<BSrc>::kGS;
+  typedef GemvStreamCfg<T, GS, W, NB, MR, CT> C;
+  typedef BSrc QB;
   typedef typename Frag<T>::type F;
   extern __shared__ __attribute__((aligned(16))) f32x4 smem[];
   char* regions = reinterpret_cast<char*>(smem);                   // W x kWaveBytes
@@ -90,24 +94,33 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     const int ar = c / (NB * kGroupK / C::kCE), ac = (c % (NB * kGroupK / C::kCE)) * C::kCE;
     av[i] = frag_load(a + (int64_t)min(ar, M - 1) * lda + g0 * kGroupK + ac);
   }
-  // 2. Scales then biases of rows n_base .. n_base + kRows - 1 for the wave's groups.
-  F mv[C::kMLoads];
-  const int gpr = (int)bsrc.groups_per_row;
+  // 2. Scales then biases of rows n_base .. n_base + kRows - 1 for the wave's
+  // groups (a quantized B; a dense one has none).
+  F mv[C::kMLoads > 0 ? C::kMLoads : 1];
+  if constexpr (GS > 0) {
+    const int gpr = (int)bsrc.groups_per_row;
 #pragma unroll
-  for (int i = 0; i < C::kMLoads; ++i) {
-    const int c0 = lane + kWave * i;
-    const int c = c0 < C::kMChunks ? c0 : 0;
-    const int kind = c / (C::kRows * C::kSPR / C::kCE);
-    const int within = c % (C::kRows * C::kSPR / C::kCE);
-    const int row = within / (C::kSPR / C::kCE), col = (within % (C::kSPR / C::kCE)) * C::kCE;
-    const T* base = kind ? bsrc.biases : bsrc.scales;
-    mv[i] = frag_load(base + (int64_t)min(n_base + row, N - 1) * gpr + g0 * (kGroupK / GS) + col);
+    for (int i = 0; i < C::kMLoads; ++i) {
+      const int c0 = lane + kWave * i;
+      const int c = c0 < C::kMChunks ? c0 : 0;
+      const int kind = c / (C::kRows * C::kSPR / C::kCE);
+      const int within = c % (C::kRows * C::kSPR / C::kCE);
+      const int row = within / (C::kSPR / C::kCE), col = (within % (C::kSPR / C::kCE)) * C::kCE;
+      const T* base = kind ? bsrc.biases : bsrc.scales;
+      mv[i] = frag_load(base + (int64_t)min(n_base + row, N - 1) * gpr + g0 * (kGroupK / GS) + col);
+    }
   }
   // 3. Codes of the wave's first PD groups (CT column tiles: weight rows
   // n_base + 16 c + r, clamped; padding columns are not stored), after
   // everything above in issue order; group j + PD is requested when group j
   // starts.
   asm volatile("" ::: "memory");
+  // A group's B operand: the codes of a quantized B (its scales and biases
+  // come from LDS), all eight fragments of a dense one.
+  auto load_b = [&](typename QB::Raw& raw, const typename QB::Lane& l, int g) {
+    if constexpr (GS > 0) bsrc.load_codes(raw, l, g);
+    else bsrc.load_full(raw, l, g);
+  };
   typename QB::Raw braw[NB][CT];
   typename QB::Lane bl[CT];
   int rt[CT];                                     // the lanes' rows of the staged metadata
@@ -120,7 +133,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
 #pragma unroll
   for (int j = 0; j < PD && j < NB; ++j)
 #pragma unroll
-    for (int c = 0; c < CT; ++c) bsrc.load_codes(braw[j][c], bl[c], g0 + j);
+    for (int c = 0; c < CT; ++c) load_b(braw[j][c], bl[c], g0 + j);
   // Wave-private LDS: written and read back by this wave only.
 #pragma unroll
   for (int i = 0; i < C::kALoads; ++i) {
@@ -143,26 +156,26 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     if (j + PD < NB) {
       asm volatile("" ::: "memory");
 #pragma unroll
-      for (int c = 0; c < CT; ++c) bsrc.load_codes(braw[j + PD][c], bl[c], g0 + j + PD);
+      for (int c = 0; c < CT; ++c) load_b(braw[j + PD][c], bl[c], g0 + j + PD);
       asm volatile("" ::: "memory");
     }
     bool huge = false;
+    if constexpr (GS > 0) {
 #pragma unroll
-    for (int c = 0; c < CT; ++c) {
+      for (int c = 0; c < CT; ++c) {
 #pragma unroll
-      for (int i = 0; i < QB::kScales; ++i) {
-        const int v = j * (kGroupK / GS) + (64 * q) / GS + i;
-        braw[j][c].scale[i] = Ms[rt[c] * C::kSPR + v];
-        braw[j][c].bias[i] = Ms[C::kRows * C::kSPR + rt[c] * C::kSPR + v];
+        for (int i = 0; i < QB::kScales; ++i) {
+          const int v = j * (kGroupK / GS) + (64 * q) / GS + i;
+          braw[j][c].scale[i] = Ms[rt[c] * C::kSPR + v];
+          braw[j][c].bias[i] = Ms[C::kRows * C::kSPR + rt[c] * C::kSPR + v];
+        }
+        huge |= bsrc.huge_scale(braw[j][c]);
       }
-      huge |= bsrc.huge_scale(braw[j][c]);
     }
     // A fragments are read from LDS one step ahead of their MFMA (not all
     // eight up front): 24 fewer live registers, which lets a CU hold every
     // workgroup of the decode grid at once.
-    auto afrag = [&](int s) {
-      return *reinterpret_cast<const F*>(As + C::a_off(arow, j * kGroupK + 64 * q + 8 * s));
-    };
+    auto afrag = [&](int s) { return *reinterpret_cast<const F*>(As + C::a_off(arow, QB::a_k(j, q, s))); };
     f32x4 acc[CT];
 #pragma unroll
     for (int c = 0; c < CT; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};

@@ -834,26 +834,28 @@ static void launch_wg_alds(const T* a, int64_t lda, const BSrc& bsrc, T* out, in
   else launch_wg1<T, BSrc, W, 4, true, META, AC>(a, lda, bsrc, out, M, N, K, G, lds, st);
 }
 
-// The barrier-free decode GEMV for a quantized B (bi_gemv_stream.h): W waves
-// of NB = G / W consecutive groups (G in {4, 8, 16}), M <= MR rows of A staged
-// per wave, CT column tiles per wave, code loads PD groups ahead. Returns
-// false when the shape does not qualify.
-template <typename T, int BITS, int GS, int W, int NB, int MR, int PD, int CT = 1>
-static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
-                           int K, int G, hipStream_t st) {
+// The barrier-free decode GEMV (bi_gemv_stream.h) for a quantized or a dense
+// B: W waves of NB = G / W consecutive groups, M <= MR rows of A staged per
+// wave, CT column tiles per wave, B loads PD groups ahead. Returns false when
+// the shape does not qualify.
+template <typename T, class BSrc, int W, int NB, int MR, int PD, int CT = 1>
+static bool launch_stream1(const T* a, int64_t lda, const BSrc& b, T* out, int M, int N, int K, int G,
+                           hipStream_t st) {
   constexpr int kCE = 16 / (int)sizeof(T);
+  constexpr int GS = StreamMeta<BSrc>::kGS;
+  constexpr int kSPR = GS > 0 ? NB * kGroupK / GS : 0;
   // 2-byte T only: the kernel's 16-byte staging pieces are whole 8-element
   // fragments only there.
   // LDS of the configuration (GemvStreamCfg::kLdsBytes, computed here so an
   // unsupported configuration is never instantiated): MR rows x K of A do not
   // fit for every shape; the caller then falls back.
-  constexpr size_t kElemBytes = (size_t)(MR * NB * kGroupK + 2 * 16 * CT * (NB * kGroupK / GS)) * sizeof(T);
+  constexpr size_t kElemBytes = (size_t)(MR * NB * kGroupK + 2 * 16 * CT * kSPR) * sizeof(T);
   constexpr size_t kLds = (size_t)W * std::max<size_t>(kElemBytes, (size_t)NB * CT * kWave * 16);
-  if constexpr (sizeof(T) != 2 || (NB * kGroupK / GS) % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0 ||
+  if constexpr (sizeof(T) != 2 || kSPR % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0 ||
                 kLds > 160 * 1024) {
     return false;
   } else {
-    typedef GemvStreamCfg<T, BITS, GS, W, NB, MR, CT> C;
+    typedef GemvStreamCfg<T, GS, W, NB, MR, CT> C;
     static_assert(C::kLdsBytes == kLds, "launch_stream1: LDS size");
     if (G != W * NB) return false;
     // More than 64 KB of dynamic LDS (8 or 16 rows of A) is allowed
@@ -861,14 +863,13 @@ static bool launch_stream1(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b
     // and no error state behind; the launch then reports its own status).
     static const bool lds_raised = [] {
       if (C::lds_bytes(16) <= 65536) return true;
-      const bool ok =
-          hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream<T, BITS, GS, W, NB, MR, PD, CT>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+      const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream<T, BSrc, W, NB, MR, PD, CT>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
       if (!ok) (void)hipGetLastError();
       return ok;
     }();
     (void)lds_raised;
-    gemv_stream<T, BITS, GS, W, NB, MR, PD, CT><<<dim3(ceil_div(N, 16 * CT)), kWave * W, C::lds_bytes(G), st>>>(
+    gemv_stream<T, BSrc, W, NB, MR, PD, CT><<<dim3(ceil_div(N, 16 * CT)), kWave * W, C::lds_bytes(G), st>>>(
         a, lda, b, out, M, N, K, G);
     return true;
   }
@@ -893,23 +894,24 @@ inline int stream_ct(int MR, int N) {
 template <typename T, int BITS, int GS, int W, int NB, int PD>
 static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
                             int K, int G, hipStream_t st) {
-  if (M == 1) return launch_stream1<T, BITS, GS, W, NB, 1, PD>(a, lda, b, out, M, N, K, G, st);
-  if (M <= 4) return launch_stream1<T, BITS, GS, W, NB, 4, PD>(a, lda, b, out, M, N, K, G, st);
+  typedef QuantB<T, BITS, GS> QB;
+  if (M == 1) return launch_stream1<T, QB, W, NB, 1, PD>(a, lda, b, out, M, N, K, G, st);
+  if (M <= 4) return launch_stream1<T, QB, W, NB, 4, PD>(a, lda, b, out, M, N, K, G, st);
   if constexpr (BITS == 4) {
     // Column tiles only for 4-bit codes (8-bit codes of four tiles do not fit
     // the register file next to A).
     if (M <= 8) {
-      if (stream_ct(8, N) > 1) return launch_stream1<T, BITS, GS, W, NB, 8, PD, 2>(a, lda, b, out, M, N, K, G, st);
-      return launch_stream1<T, BITS, GS, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
+      if (stream_ct(8, N) > 1) return launch_stream1<T, QB, W, NB, 8, PD, 2>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream1<T, QB, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
     }
     switch (stream_ct(16, N)) {
-      case 4: return launch_stream1<T, BITS, GS, W, NB, 16, PD, 4>(a, lda, b, out, M, N, K, G, st);
-      case 2: return launch_stream1<T, BITS, GS, W, NB, 16, PD, 2>(a, lda, b, out, M, N, K, G, st);
-      default: return launch_stream1<T, BITS, GS, W, NB, 16, PD>(a, lda, b, out, M, N, K, G, st);
+      case 4: return launch_stream1<T, QB, W, NB, 16, PD, 4>(a, lda, b, out, M, N, K, G, st);
+      case 2: return launch_stream1<T, QB, W, NB, 16, PD, 2>(a, lda, b, out, M, N, K, G, st);
+      default: return launch_stream1<T, QB, W, NB, 16, PD>(a, lda, b, out, M, N, K, G, st);
     }
   } else {
     if (M > 8) return false;
-    return launch_stream1<T, BITS, GS, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
+    return launch_stream1<T, QB, W, NB, 8, PD>(a, lda, b, out, M, N, K, G, st);
   }
 }
 
@@ -946,6 +948,39 @@ static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b,
       return launch_stream_m<T, BITS, GS, 14, 4, 1>(a, lda, b, out, M, N, K, G, st);
     default:
       return false;
+  }
+}
+
+// The streaming GEMV for a dense 2-byte B, M <= 16: one column tile per wave
+// (a dense tile is eight 16-byte loads per group and lane; two tiles measured
+// slower), A's MR rows of the wave's groups staged in LDS. G = 16: 8 waves of
+// 2 groups, 8: 4 of 2, 32: 8 of 4, 56: 14 of 4. Measured against the
+// workgroup-fold GEMV it replaces (bf16, same-box probe, bits equal):
+// [14336, 4096] M = 1 / 4 / 8 / 16 22.0 / 26.8 / 29.3 / 34.6 -> 21.5 / 22.0 /
+// 23.8 / 28.6 us; [4096, 4096] 9.1 / 9.0 / 10.0 / 11.3 -> 7.7 / 8.0 / 8.3 /
+// 9.1 us; [4096, 14336] M = 1 / 4 26.9 / 28.0 -> 21.5 / 22.4 us.
+template <typename T, int W, int NB>
+static bool launch_stream_dense_m(const T* a, int64_t lda, const DenseB<T>& b, T* out, int M, int N, int K,
+                                  int G, hipStream_t st) {
+  typedef DenseB<T> DB;
+  if (M == 1) return launch_stream1<T, DB, W, NB, 1, 1>(a, lda, b, out, M, N, K, G, st);
+  if (M <= 4) return launch_stream1<T, DB, W, NB, 4, 1>(a, lda, b, out, M, N, K, G, st);
+  if (M <= 8) return launch_stream1<T, DB, W, NB, 8, 1>(a, lda, b, out, M, N, K, G, st);
+  return launch_stream1<T, DB, W, NB, 16, 1>(a, lda, b, out, M, N, K, G, st);
+}
+
+template <typename T>
+static bool launch_stream_dense(const T* a, int64_t lda, const DenseB<T>& b, T* out, int M, int N, int K, int G,
+                                hipStream_t st) {
+  if (M > kStreamMMax || K % kGroupK || b.ldb % (16 / (int)sizeof(T)) || !bi_host::aligned16(b.bt) ||
+      lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a))
+    return false;
+  switch (G) {
+    case 16: return launch_stream_dense_m<T, 8, 2>(a, lda, b, out, M, N, K, G, st);
+    case 8: return launch_stream_dense_m<T, 4, 2>(a, lda, b, out, M, N, K, G, st);
+    case 32: return launch_stream_dense_m<T, 8, 4>(a, lda, b, out, M, N, K, G, st);
+    case 56: return launch_stream_dense_m<T, 14, 4>(a, lda, b, out, M, N, K, G, st);
+    default: return false;
   }
 }
 
@@ -1083,6 +1118,9 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
     // 2048 (128 tiles) 5.0 / 5.2 / 6.6 / 7.8 -> 4.1 / 4.4 / 4.8 / 5.5 us.
     if (ceil_div(N, 16) >= kStreamMinTiles && (M <= 4 || G >= 8) &&
         launch_stream<T, BSrc::kBits, BSrc::kGS>(a, lda, bsrc, out, M, N, K, G, st))
+      return bi_host::launch_status(what);
+  } else if constexpr (sizeof(T) == 2) {
+    if (ceil_div(N, 16) >= kStreamMinTiles && launch_stream_dense<T>(a, lda, bsrc, out, M, N, K, G, st))
       return bi_host::launch_status(what);
   }
   if constexpr (BSrc::kMeta) {

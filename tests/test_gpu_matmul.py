@@ -174,6 +174,27 @@ def test_matmul_mid_m_large_tile_forms(M, N, K, launch):
     assert bits(_mm(x[M - 40:], W.t())) == bits(full[M - 40:])
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("N,K", [(2048 + 40, 4096), (4096 + 8, 14336), (4096, 2048), (8192 + 24, 8192)])
+def test_matmul_stream_launch_matches_oracle(dt, N, K):
+    """M <= 16 with at least 128 column tiles and 8 / 16 / 32 / 56 groups takes
+    the streaming GEMV for a dense B (A's rows staged per wave in LDS; the
+    last tile partial; 56 groups: M <= 4, then the workgroup-fold GEMV): rows
+    equal the oracle and the same rows computed alone, bit for bit."""
+    g = gen(N + K)
+    bt = randn((N, K), DT[dt], g)
+    x = randn((16, K), DT[dt], g)
+    cols = np.r_[0:24, N // 2:N // 2 + 16, N - 24:N]
+    W = to_np(bt[cols])
+    for M in (1, 3, 5, 8, 12, 16):
+        got = _mm(x[:M], bt.t())
+        rows = sorted({0, M // 2, M - 1})
+        want = ora.matmul(to_np(x[rows]), W, dt)
+        assert_bits_equal(to_np(got)[rows][:, cols], want, f"N={N} K={K} M={M}")
+        for rr in rows:
+            assert bits(got[rr:rr + 1]) == bits(_mm(x[rr:rr + 1], bt.t())), (M, rr)
+
+
 def test_matmul_layouts_and_leading_dims():
     g = gen(7)
     a = randn((2, 3, 200), torch.bfloat16, g)
