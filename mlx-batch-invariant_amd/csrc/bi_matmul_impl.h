@@ -44,7 +44,6 @@ namespace bi {
 
 constexpr int kSplitMMax = 32;
 constexpr int kStreamMMax = 16;   // rows of x the streaming GEMV takes (4-bit; 8-bit codes: 8)
-constexpr int kStreamMinTiles = 128;  // 16-column tiles below which the streaming GEMV is not used
 // gemv_wg with A staged in LDS: at most kGemvAChunks / W 16-byte chunks of A
 // per thread (M * K <= kGemvAChunks * 64 * 8).
 constexpr int kGemvAChunks = 32;
@@ -1111,16 +1110,24 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   constexpr int WAVES = 4;
   if constexpr (BSrc::kMeta) {
     // The streaming GEMV wherever it takes the shape (M <= 16, 4-bit; M <= 8,
-    // 8-bit; 4 < M only with 8 or more groups) and there are at least 128
-    // column tiles. Measured against the workgroup-fold GEMV and the mid-M
-    // launch it replaces below 512 tiles (4-bit g64, K = 4096): N = 4096 M =
-    // 1 / 4 / 8 / 16 5.7 / 5.9 / 6.8 / 8.0 -> 4.5 / 4.8 / 5.3 / 6.0 us; N =
-    // 2048 (128 tiles) 5.0 / 5.2 / 6.6 / 7.8 -> 4.1 / 4.4 / 4.8 / 5.5 us.
-    if (ceil_div(N, 16) >= kStreamMinTiles && (M <= 4 || G >= 8) &&
+    // 8-bit), at any number of column tiles, with 8 or more groups, or with 4
+    // groups at M <= 2 and groups of up to 64 (4 groups of 128: 2.99 -> 3.82 us
+    // at N = 256, M = 1). Measured against the workgroup-fold GEMV and the mid-M
+    // launch it replaces (4-bit g64, bits equal): K = 4096 N = 4096 M = 1 / 4 /
+    // 8 / 16 5.7 / 5.9 / 6.8 / 8.0 -> 4.5 / 4.8 / 5.3 / 6.0 us; N = 1024 (64
+    // tiles) 4.6 / 4.8 / 6.2 / 7.5 -> 3.8 / 4.1 / 4.3 / 4.9 us; N = 16 (one
+    // tile) 5.5 / 4.3 / 5.7 / 6.9 -> 3.7 / 3.7 / 3.9 / 4.3 us; K = 14336 N = 1024
+    // M = 1 / 4 15.7 / 16.1 -> 8.1 / 9.6 us; 8-bit g64 K = 2048 N = 1024 M = 1 /
+    // 8 5.6 / 5.9 -> 3.5 / 3.9 us.
+    if ((G >= 8 || (M <= 2 && BSrc::kGS <= 64)) &&
         launch_stream<T, BSrc::kBits, BSrc::kGS>(a, lda, bsrc, out, M, N, K, G, st))
       return bi_host::launch_status(what);
   } else if constexpr (sizeof(T) == 2) {
-    if (ceil_div(N, 16) >= kStreamMinTiles && launch_stream_dense<T>(a, lda, bsrc, out, M, N, K, G, st))
+    // Dense 2-byte B at any number of column tiles (bf16, bits equal): K =
+    // 4096 N = 1024 M = 1 / 8 / 16 6.1 / 8.8 / 10.5 -> 5.8 / 6.6 / 7.2 us, N =
+    // 16 M = 16 8.8 -> 6.2 us; K = 14336 N = 1024 M = 1 / 4 22.0 / 24.1 -> 15.0
+    // / 16.8 us; K = 2048 N = 1024 M = 16 5.6 -> 4.3 us.
+    if (launch_stream_dense<T>(a, lda, bsrc, out, M, N, K, G, st))
       return bi_host::launch_status(what);
   }
   if constexpr (BSrc::kMeta) {

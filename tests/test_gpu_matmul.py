@@ -100,8 +100,8 @@ def test_matmul_row_position_independence():
 
 @pytest.mark.parametrize("K", [4096, 65 * 256 + 128])
 def test_matmul_launch_shapes_agree(K):
-    """M = 1, 16 (workgroup fold, or split partials + fold kernel when K has
-    more than 64 groups), 17..32 (two m-tiles) and 33 (LDS tiles, register
+    """M = 1, 16 (the streaming GEMV at 16 groups; split partials + fold
+    kernel at 66 groups), 17..32 (two m-tiles) and 33 (LDS tiles, register
     fold) give the same bits for the same rows."""
     g = gen(6)
     N = 160
@@ -175,16 +175,19 @@ def test_matmul_mid_m_large_tile_forms(M, N, K, launch):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("N,K", [(2048 + 40, 4096), (4096 + 8, 14336), (4096, 2048), (8192 + 24, 8192)])
+@pytest.mark.parametrize("N,K", [(2048 + 40, 4096), (4096 + 8, 14336), (4096, 2048), (8192 + 24, 8192), (16, 4096),
+                                 (1000, 2048), (5, 8192), (40, 14336)])
 def test_matmul_stream_launch_matches_oracle(dt, N, K):
-    """M <= 16 with at least 128 column tiles and 8 / 16 / 32 / 56 groups takes
-    the streaming GEMV for a dense B (A's rows staged per wave in LDS; the
-    last tile partial; 56 groups: M <= 4, then the workgroup-fold GEMV): rows
-    equal the oracle and the same rows computed alone, bit for bit."""
+    """M <= 16 with 8 / 16 / 32 / 56 groups takes the streaming GEMV for a
+    dense B at any number of column tiles (one tile, a single partial tile of
+    5 columns, 63 with the last partial, up to 515; A's rows staged per wave
+    in LDS; 32 groups: M <= 8, 56 groups: M <= 4, then the workgroup-fold
+    GEMV): rows equal the oracle and the same rows computed alone, bit for
+    bit."""
     g = gen(N + K)
     bt = randn((N, K), DT[dt], g)
     x = randn((16, K), DT[dt], g)
-    cols = np.r_[0:24, N // 2:N // 2 + 16, N - 24:N]
+    cols = np.unique(np.clip(np.r_[0:24, N // 2:N // 2 + 16, N - 24:N], 0, N - 1))
     W = to_np(bt[cols])
     for M in (1, 3, 5, 8, 12, 16):
         got = _mm(x[:M], bt.t())

@@ -70,8 +70,9 @@ def test_quantized_partial_last_group(bits_, gs, K, M):
 
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
 def test_quantized_launch_shapes_agree(bits_, gs):
-    """M = 1 and 16 (one m-tile, workgroup fold), 20 and 32 (two m-tiles), 33
-    and 100 (LDS tiles, register fold) give the same bits for the same rows."""
+    """M = 1 and 16 (the streaming GEMV; 8-bit M = 16 one m-tile), 20 and 32
+    (two m-tiles), 33 and 100 (LDS tiles, register fold) give the same bits
+    for the same rows."""
     N, K = 512, 2048
     wq, s, b = _qweights(N, K, bits_, gs, "bf16", seed=9)
     wq, s, b = wq.cuda(), s.cuda(), b.cuda()
@@ -134,16 +135,18 @@ def test_quantized_stream_launch_up_to_16_rows(bits_, gs, dt):
 
 
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (4, 128)])
-@pytest.mark.parametrize("N,K", [(2048 + 40, 4096), (4096 + 24, 8192), (4096 + 8, 14336)])
+@pytest.mark.parametrize("N,K", [(2048 + 40, 4096), (4096 + 24, 8192), (4096 + 8, 14336), (16, 4096), (1000, 2048),
+                                 (200, 1024)])
 def test_quantized_stream_launch_fewer_tiles_and_longer_k(bits_, gs, N, K):
-    """The streaming GEMV below 512 column tiles (131 and 258 tiles, the last
-    one partial) and at 32 and 56 groups (eight and fourteen waves of four
-    groups): M <= 16 (4-bit) / 8 (8-bit) where A's rows fit in LDS, the
-    mid-M launch past that (56 groups: M > 4). Rows equal the oracle and the
-    same rows computed alone, bit for bit."""
+    """The streaming GEMV below 512 column tiles (131, 258 and 63 tiles, the
+    last one partial, and a single tile), at 32 and 56 groups (eight and
+    fourteen waves of four groups) and at 4 groups (M <= 2 with groups of up
+    to 64 only): M <= 16 (4-bit) / 8 (8-bit) where A's rows fit in LDS, the
+    mid-M launch or the workgroup-fold GEMV past that (56 groups: M > 4).
+    Rows equal the oracle and the same rows computed alone, bit for bit."""
     dt = "bf16"
     wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 11 + gs + K % 977)
-    cols = np.r_[0:24, N // 2:N // 2 + 16, N - 24:N]
+    cols = np.unique(np.clip(np.r_[0:24, N // 2:N // 2 + 16, N - 24:N], 0, N - 1))
     W = ora.dequantize(wq[cols].view(torch.int32).numpy().view(np.uint32), to_np(s[cols]), to_np(b[cols]),
                        gs, bits_, dt)
     wq, s, b = wq.cuda(), s.cuda(), b.cuda()
