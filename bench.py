@@ -677,15 +677,20 @@ def bench_llama(args):
     import mlx_batch_invariant_amd as bi
     from mlx_batch_invariant_amd.llama import LlamaConfig, LlamaShaped
     from mlx_batch_invariant_amd.nn import QuantizedLinear
-    T, steps, batches = args.llama_prompt, args.llama_steps, (1, 4, 16, 64)
+    T, steps = args.llama_prompt, args.llama_steps
+    batches = tuple(int(b) for b in args.llama_batches.split(","))
+    weights = [w.strip() for w in args.llama_weights.split(",")]
+    if not batches or batches[0] != 1 or any(b < 1 for b in batches) or set(weights) - {"q4", "bf16"}:
+        raise SystemExit("--llama-batches must start at 1 (row 0 is checked against B = 1); "
+                         "--llama-weights takes q4 and/or bf16")
     res = {}
-    for bits in (4, None):
+    for bits in [4 if w == "q4" else None for w in weights]:
         tag = f"q{bits}g64" if bits else "bf16"
         cfg = LlamaConfig(layers=args.llama_layers, bits=bits)
         model = LlamaShaped(cfg, device="cuda", dtype=torch.bfloat16, seed=0)
         g = torch.Generator().manual_seed(0)
         row0 = torch.randint(0, cfg.vocab, (1, T), generator=g)
-        stock_model = _dequantized_copy(model) if bits else model
+        stock_model = (_dequantized_copy(model) if bits else model) if args.llama_stock else None
         per_b, ref = {}, {}
         for B in batches:
             fill = torch.randint(0, cfg.vocab, (B - 1, T), generator=torch.Generator().manual_seed(B))
@@ -694,9 +699,11 @@ def bench_llama(args):
             # 4-bit also runs with every weight dequantized once next to its codes
             # (QuantizedLinear.cache_dequantized): prefill (M >= 256) then skips the
             # per-call dequantization, same bits; decode reads the codes either way.
-            runs = [("invariant", True, False), ("stock", False, False)]
-            if bits:
-                runs.append(("invariant_dequantized_once", True, True))
+            runs = [("invariant", True, False)]
+            if args.llama_stock:
+                runs.append(("stock", False, False))
+                if bits:
+                    runs.append(("invariant_dequantized_once", True, True))
             for label, on, cached in runs:
                 bi.reset_stats()
                 mdl = model if on else stock_model
@@ -728,7 +735,8 @@ def bench_llama(args):
     cpu = None if args.no_cpu else cpu_baseline_llama()
     return {"metric": METRIC, "op": "Llama-3-8B-shape forward (config 5)", "cpu_baseline": cpu,
             "config": {"workload": f"{args.llama_layers}-layer Llama-3-8B-shape decoder, prefill {T} tokens + "
-                                   f"{steps} greedy decode steps, batch 1/4/16/64", "dtype": "bf16 activations"},
+                                   f"{steps} greedy decode steps, batch {'/'.join(map(str, batches))}",
+                       "dtype": "bf16 activations"},
             "models": res}
 
 
@@ -771,6 +779,10 @@ def main(argv=None) -> int:
     p.add_argument("--llama-layers", type=int, default=32)
     p.add_argument("--llama-prompt", type=int, default=512)
     p.add_argument("--llama-steps", type=int, default=128)
+    p.add_argument("--llama-batches", default="1,4,16,64", help="llama: comma-separated batch sizes")
+    p.add_argument("--llama-weights", default="q4,bf16", help="llama: comma-separated subset of q4, bf16")
+    p.add_argument("--llama-stock", action=argparse.BooleanOptionalAction, default=True,
+                   help="llama: also run the stock path and the dequantized-once run (off: the invariant run only)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--profile-m", type=int, default=1,
                    help="qmm4/qmm8: run only the graph-replayed calls at this M and print no result (for profilers)")
