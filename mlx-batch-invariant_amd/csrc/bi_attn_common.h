@@ -36,6 +36,8 @@
 // every row runs this one sequence whichever kernel computes it.
 #pragma once
 
+#include <type_traits>
+
 #include "bi_common.h"
 
 namespace bi {
@@ -144,10 +146,33 @@ template <> struct PFrag<bf16> { bf16x8 hi, lo; };
 template <> struct PFrag<f16> { f16x8 hi, lo; };
 template <> struct PFrag<float> { f32x8 f; };
 
-template <typename T>
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// PAIRED (bf16): the hi halves of a pair of weights come from one packed
+// conversion; both forms round the same values the same way, so they give the
+// same bits (a kernel picks the one that fits its register budget).
+template <typename T, bool PAIRED = true>
 __device__ __forceinline__ PFrag<T> make_pfrag(const float (&p)[8]) {
   PFrag<T> r;
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (PAIRED && std::is_same_v<T, bf16>) {
+    // Per pair of weights: one packed round-to-nearest-even conversion gives
+    // both hi halves; their fp32 values are the converted bits moved to the
+    // top half (an exact widening), so the residuals p - hi are the same
+    // exact differences, rounded once by the second packed conversion.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bf16x2_t h = __builtin_convertvector(f32x2_t{p[2 * j], p[2 * j + 1]}, bf16x2_t);
+      const uint32_t hb = __builtin_bit_cast(uint32_t, h);
+      const float h0 = __builtin_bit_cast(float, hb << 16);
+      const float h1 = __builtin_bit_cast(float, hb & 0xffff0000u);
+      const bf16x2_t l = __builtin_convertvector(f32x2_t{p[2 * j] - h0, p[2 * j + 1] - h1}, bf16x2_t);
+      r.hi[2 * j] = h[0];
+      r.hi[2 * j + 1] = h[1];
+      r.lo[2 * j] = l[0];
+      r.lo[2 * j + 1] = l[1];
+    }
+  } else if constexpr (sizeof(T) == 2) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const T h = to_store<T>(p[e]);

@@ -382,8 +382,18 @@ constexpr int prefill_chunk() {
   return MODE == kKvContig && D * (int)sizeof(T) <= 256 ? 128 : 64;
 }
 
+// Workgroups per CU the prefill kernel's registers are held to: two (two
+// waves per SIMD, 256 registers each) for a contiguous cache of a 16-bit type
+// with D <= 128, which fits that budget without spilling; otherwise no bound
+// (D >= 192 needs more registers per wave; the paged forms' addressing takes
+// a few more registers and would spill under the bound).
+template <typename T, int D, int MODE>
+constexpr int prefill_min_blocks() {
+  return sizeof(T) == 2 && D <= 128 && MODE == kKvContig ? 2 : 1;
+}
+
 template <typename T, int D, int MODE, int NBUF = prefill_ring<T, D>(), int CH = prefill_chunk<T, D, MODE>()>
-__global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
+__global__ __launch_bounds__(256, (prefill_min_blocks<T, D, MODE>())) void attn_prefill_mfma(PrefillArgs a) {
   constexpr bool ROWPAGED = MODE == kKvRowPaged;
   typedef typename Frag<T>::type F;
   typedef KVTile<T, D> KV;
@@ -530,7 +540,9 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
   auto split_body = [&](const int sp, auto masked) {
     constexpr bool MASKED = decltype(masked)::value;
     const int j0 = sp * kSplit;
-    const int nkc = sp + 1 < nsplit ? KC : nkc_last;
+    // An unmasked split lies below every valid row's key limit, so it is a
+    // whole split of the workgroup too (its last split then holds 256 keys).
+    const int nkc = !MASKED || sp + 1 < nsplit ? KC : nkc_last;
     // Scores of the wave's 16 rows against the split's keys (tile t: keys j0 + 16 t + ...).
     float s[16][4];
 #pragma unroll
@@ -588,7 +600,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
             p8[e] = s[t0][e];
             p8[4 + e] = s[t0 + 1][e];
           }
-          const PFrag<T> pf = make_pfrag<T>(p8);
+          const PFrag<T> pf = make_pfrag<T, !ROWPAGED>(p8);
 #pragma unroll
           for (int dt = 0; dt < NDT; ++dt) acc[dt] = pv_step<T>(pf, KV::vfrag(buf, 32 * h, dt, lane), acc[dt]);
           lsum = pv_step<T>(pf, ones_frag<T>(), lsum);
@@ -596,11 +608,13 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma(PrefillArgs a) {
         ++ci;
       }
     }
-    // Merge into the running state (accumulator layout: rows 4 qq + i).
+    // Merge into the running state (accumulator layout: rows 4 qq + i). A
+    // row whose keys end before the split skips it; in an unmasked split every
+    // valid row has keys in it (padding rows are merged too, never stored).
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float mi = __shfl(m, 4 * qq + i, kWave);
-      if (acc_nkeys[i] > j0) {
+      if (!MASKED || acc_nkeys[i] > j0) {
         float ai[NDT];
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) ai[dt] = A[dt][i];
