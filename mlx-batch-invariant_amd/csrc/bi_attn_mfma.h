@@ -550,16 +550,17 @@ __global__ __launch_bounds__(256, (prefill_min_blocks<T, D, MODE>())) void attn_
       if (kc < nkc) {
         open_chunk(ci);
         const char* buf = ring + (ci % NBUF) * CHB;
+        // Key j0 + CH kc + 16 t + 4 qq + i is below this row's limit iff
+        // 16 t + i < lim: one lane value per chunk against constants.
+        const int lim = my_nkeys - (j0 + CH * kc + 4 * qq);
 #pragma unroll
         for (int t = 0; t < TPC; ++t) {
           f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int st = 0; st < D / 32; ++st) acc = mfma_step(KV::kfrag(buf, 16 * t + r, st, qq), qf[st], acc);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = j0 + CH * kc + 16 * t + 4 * qq + i;
-            s[TPC * kc + t][i] = (!MASKED || key < my_nkeys) ? acc[i] * a.scale_log2 : -INFINITY;
-          }
+          for (int i = 0; i < 4; ++i)
+            s[TPC * kc + t][i] = (!MASKED || 16 * t + i < lim) ? acc[i] * a.scale_log2 : -INFINITY;
         }
         ++ci;
       } else {
@@ -576,10 +577,15 @@ __global__ __launch_bounds__(256, (prefill_min_blocks<T, D, MODE>())) void attn_
       for (int i = 0; i < 4; ++i) m = fmaxf(m, s[t][i]);
     m = fmaxf(m, __shfl_xor(m, 16, kWave));
     m = fmaxf(m, __shfl_xor(m, 32, kWave));
+    // Weights exp2(s - m): a masked key's score is -inf, so its weight is
+    // exactly +0 (v_exp_f32(-inf) = 0), the value an active-key select gives.
+    // A row with no active key in the split (m = -inf; such a row is not
+    // merged) subtracts 0 instead, so its weights are 0 rather than NaN.
+    const float msub = MASKED && m == -INFINITY ? 0.0f : m;
 #pragma unroll
     for (int t = 0; t < 16; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[t][i] = split_weight(s[t][i], m, !MASKED || j0 + 16 * t + 4 * qq + i < my_nkeys);
+      for (int i = 0; i < 4; ++i) s[t][i] = __builtin_amdgcn_exp2f(s[t][i] - msub);
 
     // P.V and the weight sum over the split's V chunks.
     f32x4 acc[NDT];
