@@ -224,7 +224,10 @@ int prefill_impl(const char* what, const void* q, const void* k, const void* v, 
     return fail(BI_E_UNSUPPORTED, "%s: K/V row strides (%lld, %lld elements) must stay below 2^24 bytes", what,
                 (long long)strides[5], (long long)strides[8]);
   const int64_t wgs = (Tq * (Hq / Hkv) + 63) / 64;
+  // The matrix-core kernel runs one 1-D grid over every (b, kv head, 64-pair
+  // workgroup) item, padded to a multiple of 8.
   if (wgs > 0x7fffffffLL || Tq * (Hq / Hkv) > 0x7fffffffLL - 64 ||
+      (!per_key && wgs * Hkv * B > 0x7fffffffLL - 8) ||
       (per_key && B * Hq * ((Tq + bi::pk_prefill_qb(D) - 1) / bi::pk_prefill_qb(D)) > ((int64_t)1 << 27)))
     return fail(BI_E_UNSUPPORTED, "%s: grid too large", what);
   bi::PrefillArgs a;

@@ -143,7 +143,8 @@ template <typename T, int D>
 int launch_prefill(PrefillArgs& a, hipStream_t st) {
   const int G = a.Hq / a.Hkv;
   const int64_t wgs = ((int64_t)a.Tq * G + 63) / 64;
-  dim3 grid((unsigned)wgs, a.Hkv, a.B);
+  const int64_t items = wgs * a.Hkv * a.B;     // the kernel maps blocks to items per XCD
+  dim3 grid((unsigned)(8 * ((items + 7) / 8)));
   switch (kv_mode(a)) {
     case kKvPaged: attn_prefill_mfma<T, D, kKvPaged><<<grid, 256, 0, st>>>(a); break;
     case kKvRowPaged: attn_prefill_mfma<T, D, kKvRowPaged><<<grid, 256, 0, st>>>(a); break;

@@ -412,11 +412,23 @@ __global__ __launch_bounds__(256, (prefill_min_blocks<T, D, MODE>())) void attn_
   const int lane = tid % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int r = lane % 16, qq = lane / 16;
-  const int wg = gridDim.x - 1 - blockIdx.x;            // heaviest (latest tokens) first
-  const int hk = blockIdx.y;
-  const int b = blockIdx.z;
   const int G = a.Hq / a.Hkv;
   const int npairs = a.Tq * G;
+  // Work items (sequence b, kv head hk, workgroup wg of 64 (token, head)
+  // pairs) in that nesting order, each (b, hk)'s workgroups heaviest (latest
+  // tokens) first. The 1-D grid is padded to a multiple of 8 and block i runs
+  // item (i % 8) per_xcd + i / 8: workgroups are dispatched to the 8 XCDs
+  // round-robin, so each XCD walks its own contiguous range of items and its
+  // L2 holds the K/V of about one (b, hk) at a time rather than of every
+  // (b, hk) the whole grid has in flight.
+  const int wgs = (npairs + 63) / 64;
+  const int64_t items = (int64_t)wgs * a.Hkv * a.B;
+  const int64_t per_xcd = (items + 7) / 8;
+  const int64_t item = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (item >= items) return;  // uniform per workgroup, before any barrier
+  const int wg = wgs - 1 - (int)(item % wgs);
+  const int hk = (int)(item / wgs % a.Hkv);
+  const int b = (int)(item / wgs / a.Hkv);
   const int len = a.kv_lens ? min(max(a.kv_lens[b], 0), a.L) : a.L;
   auto nkeys_of = [&](int pair) -> int {
     if (pair >= npairs) return 0;
