@@ -1034,8 +1034,26 @@ struct MidPlan {
 static inline MidPlan mid_plan(int64_t M, int64_t N, int64_t K) {
   MidPlan p;
   if (M <= 4 || M >= kBigMinM || N <= 0 || K <= 0 || K % kGroupK) return p;
-  if (M <= 16 && ceil_div(N, 64) < 128) return p;
   const int G = (int)(K / kGroupK);
+  if (M <= 16 && ceil_div(N, 64) < 128) {
+    // Few columns and a long K (the streaming GEMV, tried first, did not
+    // take the shape): the workgroup-fold GEMV runs one workgroup per 16
+    // columns (at most 128 here, half the CUs) and reads A's rows from L2 for
+    // every group; the split launch runs chunks of 4 groups on every CU and
+    // folds the per-group partials in order. 4-bit g64, same-box probe, bits
+    // equal: [1024, 14336] M = 5 / 8 / 16 16.4 / 18.6 / 24.7 -> 11.8 / 12.2 /
+    // 12.6 us, [2048, 14336] 16.6 / 18.8 / 24.6 -> 14.7 / 15.1 / 17.0,
+    // [1024, 16384] 17.2 / 19.2 / 25.8 -> 12.3 / 12.6 / 13.0, [2048, 8192]
+    // M = 16 14.0 -> 12.0 (M <= 8 streams there). With 20 groups, or 3072
+    // columns and more, the workgroup-fold GEMV measured as fast or faster.
+    if (G < 32 || N > 2048) return p;
+    p.mt = 1;
+    p.mtiles = (int)ceil_div(M, 16);
+    p.cg = std::min(4, G);
+    p.chunks = ceil_div(G, p.cg);
+    p.use = true;
+    return p;
+  }
   // 64-row blocks only for 32 < M <= 64; larger M runs several 32-row blocks
   // (measured faster: more workgroups per CU, each a shallower register file).
   p.mt = M <= 16 ? 1 : (M <= 32 || M > 64) ? 2 : 4;

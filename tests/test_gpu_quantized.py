@@ -162,6 +162,31 @@ def test_quantized_stream_launch_fewer_tiles_and_longer_k(bits_, gs, N, K):
 
 
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
+@pytest.mark.parametrize("N,K", [(1000, 14336), (2048, 8192), (520, 16384)])
+def test_quantized_split_k_few_columns_long_k(bits_, gs, N, K):
+    """5 <= M <= 16 with at most 2048 columns and 32 or more groups where the
+    streaming GEMV does not take the shape (A's rows x K beyond LDS; 64
+    groups): K split into chunks of 4 groups, the per-group partials folded in
+    group order. Rows equal the oracle and the same rows computed alone (the
+    streaming GEMV or the workgroup-fold GEMV), bit for bit."""
+    dt = "bf16"
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 5 + gs + K % 1013)
+    cols = np.unique(np.clip(np.r_[0:16, N // 2:N // 2 + 8, N - 16:N], 0, N - 1))
+    W = ora.dequantize(wq[cols].view(torch.int32).numpy().view(np.uint32), to_np(s[cols]), to_np(b[cols]),
+                       gs, bits_, dt)
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    x = randn((16, K), DT[dt], gen(23))
+    run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+    for M in (5, 8, 12, 16):
+        got = run(x[:M])
+        rows = sorted({0, M - 1})
+        want = ora.matmul(to_np(x[rows]), W, dt, kmap="blocked")
+        assert_bits_equal(to_np(got)[rows][:, cols], want, f"N={N} K={K} M={M}")
+        for rr in rows:
+            assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
+
+
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_quantized_mid_m_split_k_matches_oracle(bits_, gs, dt):
     """Few column blocks (N = 4136: 65 blocks of 64) make the mid-M launch split
