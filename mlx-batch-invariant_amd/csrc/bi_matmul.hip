@@ -9,13 +9,14 @@ namespace {
 
 // Group partials [G, M, N] fp32 of the small-M split launch, and of the
 // mid-M launches when they split K (the dense tall tile, the quantized mid
-// tile; 2-byte types: the query has no dtype and reports the need of either).
+// tile, the mid tile on a dense B with few columns and a long K; 2-byte types:
+// the query has no dtype and reports the need of either).
 size_t split_ws_bytes(int64_t M, int64_t N, int64_t K, bool dense) {
   const int64_t G = (K + bi::kGroupK - 1) / bi::kGroupK;
   if (M <= 0 || N <= 0 || K <= 0) return 0;
   const bool small_split = bi::use_split(M, (int)G) && !bi::use_wg(M, (int)G);
   const bool tall_split = dense && bi::tall_plan(M, N, K).chunks > 1;
-  const bool mid_split = !dense && bi::mid_plan(M, N, K).chunks > 1;
+  const bool mid_split = dense ? bi::few_columns_plan(M, N, K).use : bi::mid_plan(M, N, K).chunks > 1;
   if (!small_split && !tall_split && !mid_split) return 0;
   return (size_t)(G * M * N) * sizeof(float);
 }

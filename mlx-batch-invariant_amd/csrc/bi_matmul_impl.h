@@ -1031,29 +1031,35 @@ struct MidPlan {
   bool use = false;
   int mt = 1, mtiles = 1, chunks = 1, cg = 0;
 };
+// 5 <= M <= 16 with at most 2048 columns and 32 or more groups, where the
+// streaming GEMV (tried first) does not take the shape: the workgroup-fold
+// GEMV would run one workgroup per 16 columns (at most 128, half the CUs) and
+// read A's rows from L2 for every group; the split mid-M launch runs chunks of
+// 4 groups on every CU and folds the per-group partials in order. Same-box
+// probe, bits equal: 4-bit g64 [1024, 14336] M = 5 / 8 / 16 16.4 / 18.6 /
+// 24.7 -> 11.8 / 12.2 / 12.6 us, [2048, 14336] 16.6 / 18.8 / 24.6 -> 14.7 /
+// 15.1 / 17.0, [1024, 16384] 17.2 / 19.2 / 25.8 -> 12.3 / 12.6 / 13.0,
+// [2048, 8192] M = 16 14.0 -> 12.0 (M <= 8 streams there); dense bf16
+// [1024, 14336] 24.4 / 26.5 / 31.9 -> 14.0 / 14.1 / 14.2, [2048, 14336]
+// 25.6 / 27.4 / 33.3 -> 21.0 / 21.0 / 22.3. With 20 groups, or 3072 columns
+// and more, the workgroup-fold GEMV measured as fast or faster.
+static inline MidPlan few_columns_plan(int64_t M, int64_t N, int64_t K) {
+  MidPlan p;
+  if (M <= 4 || M > 16 || N <= 0 || N > 2048 || K <= 0 || K % kGroupK || K / kGroupK < 32) return p;
+  const int G = (int)(K / kGroupK);
+  p.mt = 1;
+  p.mtiles = (int)ceil_div(M, 16);
+  p.cg = 4;
+  p.chunks = ceil_div(G, p.cg);
+  p.use = true;
+  return p;
+}
+
 static inline MidPlan mid_plan(int64_t M, int64_t N, int64_t K) {
   MidPlan p;
   if (M <= 4 || M >= kBigMinM || N <= 0 || K <= 0 || K % kGroupK) return p;
   const int G = (int)(K / kGroupK);
-  if (M <= 16 && ceil_div(N, 64) < 128) {
-    // Few columns and a long K (the streaming GEMV, tried first, did not
-    // take the shape): the workgroup-fold GEMV runs one workgroup per 16
-    // columns (at most 128 here, half the CUs) and reads A's rows from L2 for
-    // every group; the split launch runs chunks of 4 groups on every CU and
-    // folds the per-group partials in order. 4-bit g64, same-box probe, bits
-    // equal: [1024, 14336] M = 5 / 8 / 16 16.4 / 18.6 / 24.7 -> 11.8 / 12.2 /
-    // 12.6 us, [2048, 14336] 16.6 / 18.8 / 24.6 -> 14.7 / 15.1 / 17.0,
-    // [1024, 16384] 17.2 / 19.2 / 25.8 -> 12.3 / 12.6 / 13.0, [2048, 8192]
-    // M = 16 14.0 -> 12.0 (M <= 8 streams there). With 20 groups, or 3072
-    // columns and more, the workgroup-fold GEMV measured as fast or faster.
-    if (G < 32 || N > 2048) return p;
-    p.mt = 1;
-    p.mtiles = (int)ceil_div(M, 16);
-    p.cg = std::min(4, G);
-    p.chunks = ceil_div(G, p.cg);
-    p.use = true;
-    return p;
-  }
+  if (M <= 16 && ceil_div(N, 64) < 128) return few_columns_plan(M, N, K);
   // 64-row blocks only for 32 < M <= 64; larger M runs several 32-row blocks
   // (measured faster: more workgroups per CU, each a shallower register file).
   p.mt = M <= 16 ? 1 : (M <= 32 || M > 64) ? 2 : 4;
@@ -1147,6 +1153,11 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
     // / 16.8 us; K = 2048 N = 1024 M = 16 5.6 -> 4.3 us.
     if (launch_stream_dense<T>(a, lda, bsrc, out, M, N, K, G, st))
       return bi_host::launch_status(what);
+    const MidPlan fp = few_columns_plan(M, N, K);
+    if (fp.use && lda % 8 == 0 && bi_host::aligned16(a) && bsrc.ldb % 8 == 0 && bi_host::aligned16(bsrc.bt)) {
+      launch_mid2<T, BSrc, 1, 8, 4>(a, lda, bsrc, out, ws, M, N, K, G, fp, st);
+      return bi_host::launch_status(what);
+    }
   }
   if constexpr (BSrc::kMeta) {
     const MidPlan mp = mid_plan(M, N, K);

@@ -198,6 +198,28 @@ def test_matmul_stream_launch_matches_oracle(dt, N, K):
             assert bits(got[rr:rr + 1]) == bits(_mm(x[rr:rr + 1], bt.t())), (M, rr)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("N,K", [(1000, 14336), (2048, 8192), (520, 16384)])
+def test_matmul_split_k_few_columns_long_k(dt, N, K):
+    """5 <= M <= 16 with at most 2048 columns and 32 or more groups where the
+    dense streaming GEMV does not take the shape (A's rows x K beyond LDS; 64
+    groups): the mid-M tile on a dense B with K split into chunks of 4
+    groups, the per-group partials folded in group order. Rows equal the
+    oracle and the same rows computed alone, bit for bit."""
+    g = gen(N + 3 * K)
+    bt = randn((N, K), DT[dt], g)
+    x = randn((16, K), DT[dt], g)
+    cols = np.unique(np.clip(np.r_[0:16, N // 2:N // 2 + 8, N - 16:N], 0, N - 1))
+    W = to_np(bt[cols])
+    for M in (5, 8, 12, 16):
+        got = _mm(x[:M], bt.t())
+        rows = sorted({0, M - 1})
+        want = ora.matmul(to_np(x[rows]), W, dt)
+        assert_bits_equal(to_np(got)[rows][:, cols], want, f"N={N} K={K} M={M}")
+        for rr in rows:
+            assert bits(got[rr:rr + 1]) == bits(_mm(x[rr:rr + 1], bt.t())), (M, rr)
+
+
 def test_matmul_layouts_and_leading_dims():
     g = gen(7)
     a = randn((2, 3, 200), torch.bfloat16, g)
