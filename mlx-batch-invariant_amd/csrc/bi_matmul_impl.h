@@ -1014,8 +1014,19 @@ static void launch_wg(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, 
     else alds = false;
     if (alds) return;
   }
-  if (M <= 16) launch_wg1<T, BSrc, W, 2, false, false, 0>(a, lda, bsrc, out, M, N, K, G, part_bytes, st);
-  else gemv_wg<T, BSrc, 2, W, 2, false><<<grid, kWave * W, part_bytes, st>>>(a, lda, bsrc, out, M, N, K, G);
+  if (M <= 16) {
+    // A quantized B with 5..16 rows and 32 or more groups (the Llama MLP down
+    // projection at M = 5 .. 16, where A's rows x K do not fit in LDS):
+    // codes of four groups requested ahead instead of two. 4-bit g64
+    // [4096, 14336] M = 8 / 12 / 16 19.4 / 22.4 / 25.3 -> 18.4 / 20.8 / 23.3
+    // us, [4096, 8192] M = 12 / 16 13.0 / 15.0 -> 12.7 / 14.0; a dense B
+    // measured slower with it, and so did 16 waves either way.
+    if (BSrc::kMeta && M > 4 && G >= 32)
+      launch_wg1<T, BSrc, W, 4, false, false, 0>(a, lda, bsrc, out, M, N, K, G, part_bytes, st);
+    else launch_wg1<T, BSrc, W, 2, false, false, 0>(a, lda, bsrc, out, M, N, K, G, part_bytes, st);
+  } else {
+    gemv_wg<T, BSrc, 2, W, 2, false><<<grid, kWave * W, part_bytes, st>>>(a, lda, bsrc, out, M, N, K, G);
+  }
 }
 
 // Mid-M launch (bi_gemm_mid.h) for a quantized B, 2-byte T, K % 256 == 0:
