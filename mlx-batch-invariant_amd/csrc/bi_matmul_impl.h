@@ -193,9 +193,8 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* a, int64_t lda, BSr
   const int nw = gfull > wave ? (gfull - 1 - wave) / W + 1 : 0;   // this wave's full groups
   const int last = wave + (nw - 1) * W;
 
-  auto compute = [&](typename BSrc::Raw& braw, int g, f32x4 (&acc)[MT]) {
-    if constexpr (META) bsrc.meta_from_lds(braw, Ms, n - n_base, g, q);
-    F af[MT][kSteps];
+  // A fragments of group g: from LDS (ALDS) or from global memory.
+  auto load_af = [&](F (&af)[MT][kSteps], int g) {
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -206,6 +205,11 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* a, int64_t lda, BSr
         else
           af[i][s] = load_a_frag<T, true>(a, lda, rows[i], K, k0);
       }
+  };
+  auto compute = [&](typename BSrc::Raw& braw, int g, f32x4 (&acc)[MT]) {
+    if constexpr (META) bsrc.meta_from_lds(braw, Ms, n - n_base, g, q);
+    F af[MT][kSteps];
+    load_af(af, g);
     mma_group<T, BSrc, MT, true>(bsrc, braw, af, g, q, acc);
   };
   auto load_group = [&](typename BSrc::Raw& braw, const typename BSrc::Lane& bl, int g) {
@@ -291,17 +295,34 @@ __global__ __launch_bounds__(kWave* W) void gemv_wg(const T* a, int64_t lda, BSr
 #pragma unroll
     for (int j = 0; j < NB; ++j) load_group(braw[j], blane, min(wave + j * W, lastc));
   }
+  // Dense B without ALDS: the A fragments of the batch's NB groups are
+  // requested right after their rows of B (clamped group indices, as for B:
+  // every load is unconditional). bf16 [4096, 14336] M = 5 / 8 / 16 28.5 /
+  // 30.0 / 35.7 -> 26.9 / 28.3 / 34.5 us; a quantized B measured slower with
+  // it (M = 5 17.5 -> 20.6 us), so it and ALDS read A per group.
+  constexpr bool kPre = !ALDS && !BSrc::kMeta;
+  constexpr int kAB = kPre ? NB : 1;
+  F afb[kAB][MT][kSteps];
+  if constexpr (kPre) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) load_af(afb[j], min(wave + j * W, lastc));
+  }
   for (int c0 = 0; c0 < nw; c0 += NB) {
     if (c0 > 0) {
 #pragma unroll
       for (int j = 0; j < NB; ++j) load_group(braw[j], blane, min(wave + (c0 + j) * W, last));
+      if constexpr (kPre) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) load_af(afb[j], min(wave + (c0 + j) * W, last));
+      }
     }
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if (c0 + j < nw) {
         const int g = wave + (c0 + j) * W;
         f32x4 acc[MT];
-        compute(braw[j], g, acc);
+        if constexpr (kPre) mma_group<T, BSrc, MT, true>(bsrc, braw[j], afb[j], g, q, acc);
+        else compute(braw[j], g, acc);
 #pragma unroll
         for (int i = 0; i < MT; ++i) part[(g * MT + i) * kWave + lane] = acc[i];
       }
