@@ -310,7 +310,12 @@ __global__ __launch_bounds__(256) void attn_combine_perkey(DecodeArgs a) {
 }
 
 // Prefill: unit = (b, query head h, queries QB blk .. QB blk + QB - 1), blk
-// fastest (QB = pk_prefill_qb(D)).
+// fastest and latest (most keys) first (QB = pk_prefill_qb(D)); a workgroup
+// runs 8 consecutive units, one per half-wave. The 1-D grid is padded to a
+// multiple of 8 and block i runs workgroup (i mod 8) ceil(nwg / 8) + i / 8:
+// workgroups reach the 8 XCDs round-robin, so each XCD walks its own range of
+// heads and its L2 holds about one head's K/V rather than those of every head
+// in flight.
 // Query t sees keys [0, nkeys(t)), nkeys = len - Tq + t + 1 when causal
 // (bottom-right aligned), else len; a split merges into a query's running
 // result only if the query saw one of its keys.
@@ -321,9 +326,12 @@ __global__ __launch_bounds__(256) void attn_prefill_perkey(PrefillArgs a) {
   const int lane = threadIdx.x % 32;
   float* tb = lds[threadIdx.x / 32];
   const int nblk = (a.Tq + QB - 1) / QB;
-  int64_t u = (int64_t)blockIdx.x * 8 + threadIdx.x / 32;
-  if (u >= (int64_t)a.B * a.Hq * nblk) return;
-  const int blk = (int)(u % nblk);
+  const int64_t units = (int64_t)a.B * a.Hq * nblk;
+  const int64_t nwg = (units + 7) / 8;
+  const int64_t wg = (int64_t)(blockIdx.x % 8) * ((nwg + 7) / 8) + blockIdx.x / 8;
+  int64_t u = wg * 8 + threadIdx.x / 32;
+  if (wg >= nwg || u >= units) return;   // half-waves are independent: no barrier below
+  const int blk = nblk - 1 - (int)(u % nblk);
   u /= nblk;
   const int h = (int)(u % a.Hq);
   const int b = (int)(u / a.Hq);
@@ -392,7 +400,8 @@ template <typename T, int D>
 int launch_prefill_perkey(PrefillArgs& a, hipStream_t st) {
   constexpr int QB = pk_prefill_qb(D);
   const int64_t units = (int64_t)a.B * a.Hq * ((a.Tq + QB - 1) / QB);
-  attn_prefill_perkey<T, D><<<(unsigned)((units + 7) / 8), 256, 0, st>>>(a);
+  const int64_t nwg = (units + 7) / 8;
+  attn_prefill_perkey<T, D><<<(unsigned)(8 * ((nwg + 7) / 8)), 256, 0, st>>>(a);
   return bi_host::launch_status("bi_attn_prefill_per_key");
 }
 
