@@ -38,7 +38,7 @@ PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 # on a 256 MiB device copy (bench.py --op copycal): read x 2.000, write x 1.000.
 # Source: profiles/qmatmul4_g64_llama_mlp_m1.txt. Re-measure after changing
 # the kernel.
-MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 16213.0, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
+MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 16217.5, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
 PEAK_BF16 = 2.5e15         # FLOP/s, dense bf16 MFMA
 METRIC = "% of HBM/MFMA roofline per op at batch 1–256, with bitwise batch invariance"
 ROTATE_BYTES = 512 << 20
