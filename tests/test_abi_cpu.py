@@ -152,6 +152,10 @@ def test_invalid_arguments_are_rejected_before_launch():
     huge = (ctypes.c_int64 * 9)(*([128] * 5 + [1 << 23] + [128] * 3))
     assert lib.bi_attn_prefill(p, p, p, None, p, 1, 4, 4, 5, 10, 128, huge, 0, 1.0, 2, None) == -2
     assert "2^24 bytes" in _err(lib)
+    # more (sequence, kv head, 64-row workgroup) items than the prefill kernel's padded 1-D grid can hold
+    assert lib.bi_attn_prefill(p, p, p, None, p, 1000, 1024, 1024, 200000, 200000, 128, strides, 1, 1.0, 2,
+                               None) == -2
+    assert "grid too large" in _err(lib)
     # V position stride of 2^23 bytes: the contiguous decode kernel's 32-bit split offsets cannot hold it
     huge8 = (ctypes.c_int64 * 9)(*([128] * 7 + [1 << 22] + [128]))
     assert lib.bi_attn_decode(p, p, p, None, p, 1, 4, 4, 10, 128, huge8, 1.0, 2, p, 1 << 20, None) == -2
