@@ -54,6 +54,25 @@ def test_quantized_matches_oracle(bits_, gs, dt, M):
     assert_bits_equal(got, ora.matmul(to_np(x), W, dt, kmap="blocked"), f"{dt} {bits_}-bit g{gs} M={M}")
 
 
+@pytest.mark.parametrize("bits_,gs,K", [(4, 64, 8256), (8, 128, 8320)])
+def test_quantized_partial_last_group_long_k(bits_, gs, K):
+    """33 K groups, the last cut short, at 5..16 rows: the workgroup-fold GEMV
+    with four groups of codes requested ahead and the short group computed
+    from global memory. Rows equal the oracle and the same rows alone."""
+    N = 136
+    wq, s, b = _qweights(N, K, bits_, gs, "bf16", seed=K + bits_)
+    W = ora.dequantize(wq.view(torch.int32).numpy().view(np.uint32), to_np(s), to_np(b), gs, bits_, "bf16")
+    wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+    x = randn((16, K), torch.bfloat16, gen(K))
+    run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+    for M in (5, 8, 16):
+        got = run(x[:M])
+        rows = sorted({0, M - 1})
+        assert_bits_equal(to_np(got)[rows], ora.matmul(to_np(x[rows]), W, "bf16", kmap="blocked"), f"K={K} M={M}")
+        for rr in rows:
+            assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
+
+
 @pytest.mark.parametrize("bits_,gs,K", [(4, 64, 1088), (4, 32, 1056), (8, 128, 1152), (8, 32, 288)])
 @pytest.mark.parametrize("M", [1, 20, 40])
 def test_quantized_partial_last_group(bits_, gs, K, M):
