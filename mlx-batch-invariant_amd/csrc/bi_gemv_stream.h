@@ -31,6 +31,12 @@
 // chunk c of row r sits in slot c ^ (r & 15) of its row, so the 16 rows of a
 // fragment read (same chunk, row stride a multiple of 256 bytes) hit 16
 // distinct bank groups instead of one.
+//
+// AG (A from global memory): for rows x K of A too large for LDS, no A slice
+// is staged; each group's eight A fragments are loaded into registers with
+// the group's codes (PD groups ahead), so the LDS holds only the metadata and
+// the partials and several workgroups share a CU. Same values in the same
+// MFMA steps, so the same bits.
 #pragma once
 
 #include <type_traits>
@@ -43,12 +49,12 @@ namespace bi {
 template <class BSrc> struct StreamMeta { static constexpr int kGS = 0; };
 template <typename T, int BITS, int GS> struct StreamMeta<QuantB<T, BITS, GS>> { static constexpr int kGS = GS; };
 
-template <typename T, int GS, int W, int NB, int MR, int CT = 1>
+template <typename T, int GS, int W, int NB, int MR, int CT = 1, bool AG = false>
 struct GemvStreamCfg {
   static constexpr int kCE = 16 / (int)sizeof(T);            // elements per 16-byte load
   static constexpr int kSPR = GS > 0 ? NB * kGroupK / GS : 0; // scales per row per wave (GS = 0: dense B)
   static constexpr int kRows = 16 * CT;                       // weight rows (output columns) per workgroup
-  static constexpr int kAElems = MR * NB * kGroupK;           // A elements per wave
+  static constexpr int kAElems = AG ? 0 : MR * NB * kGroupK;  // A elements per wave staged in LDS
   static constexpr int kALoads = kAElems / kCE / kWave;       // A loads per lane
   static constexpr int kMChunks = 2 * kRows * kSPR / kCE;     // meta chunks per wave
   static constexpr int kMLoads = (kMChunks + kWave - 1) / kWave;
@@ -68,12 +74,12 @@ struct GemvStreamCfg {
   static size_t lds_bytes(int /*G*/) { return kLdsBytes; }
 };
 
-template <typename T, class BSrc, int W, int NB, int MR, int PD, int CT = 1>
+template <typename T, class BSrc, int W, int NB, int MR, int PD, int CT = 1, bool AG = false>
 __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda, BSrc bsrc,
                                                         T* __restrict__ out, int M, int N, int K,
                                                         int G) {
   constexpr int GS = StreamMeta<BSrc>::kGS;
-  typedef GemvStreamCfg<T, GS, W, NB, MR, CT> C;
+  typedef GemvStreamCfg<T, GS, W, NB, MR, CT, AG> C;
   typedef BSrc QB;
   typedef typename Frag<T>::type F;
   extern __shared__ __attribute__((aligned(16))) f32x4 smem[];
@@ -87,7 +93,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   const int g0 = wave * NB;                      // G == W * NB (checked on the host)
 
   // 1. A slice: row ar, elements [g0 * 256 + ac, +kCE) of the wave's slice.
-  F av[C::kALoads];
+  F av[C::kALoads > 0 ? C::kALoads : 1];
 #pragma unroll
   for (int i = 0; i < C::kALoads; ++i) {
     const int c = lane + kWave * i;
@@ -121,6 +127,18 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     if constexpr (GS > 0) bsrc.load_codes(raw, l, g);
     else bsrc.load_full(raw, l, g);
   };
+  // AG: A's fragments of a group go straight from global memory (L2) to
+  // registers, requested with the group's codes (PD groups ahead), instead of
+  // the MR rows x K of A staged in LDS.
+  constexpr int kAR = AG ? (PD < NB ? PD + 1 : NB) : 1;
+  F areg[kAR][AG ? kSteps : 1];
+  const T* arowp = a + (int64_t)min(r, M - 1) * lda;
+  auto load_a = [&](int j) {
+    if constexpr (AG) {
+#pragma unroll
+      for (int s = 0; s < kSteps; ++s) areg[j % kAR][s] = frag_load(arowp + QB::a_k(g0 + j, q, s));
+    }
+  };
   typename QB::Raw braw[NB][CT];
   typename QB::Lane bl[CT];
   int rt[CT];                                     // the lanes' rows of the staged metadata
@@ -131,9 +149,11 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     rt[c] = n - n_base;
   }
 #pragma unroll
-  for (int j = 0; j < PD && j < NB; ++j)
+  for (int j = 0; j < PD && j < NB; ++j) {
+    load_a(j);
 #pragma unroll
     for (int c = 0; c < CT; ++c) load_b(braw[j][c], bl[c], g0 + j);
+  }
   // Wave-private LDS: written and read back by this wave only.
 #pragma unroll
   for (int i = 0; i < C::kALoads; ++i) {
@@ -155,6 +175,7 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     const int g = g0 + j;
     if (j + PD < NB) {
       asm volatile("" ::: "memory");
+      load_a(j + PD);
 #pragma unroll
       for (int c = 0; c < CT; ++c) load_b(braw[j + PD][c], bl[c], g0 + j + PD);
       asm volatile("" ::: "memory");
@@ -175,7 +196,10 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
     // A fragments are read from LDS one step ahead of their MFMA (not all
     // eight up front): 24 fewer live registers, which lets a CU hold every
     // workgroup of the decode grid at once.
-    auto afrag = [&](int s) { return *reinterpret_cast<const F*>(As + C::a_off(arow, QB::a_k(j, q, s))); };
+    auto afrag = [&](int s) {
+      if constexpr (AG) return areg[j % kAR][s];
+      else return *reinterpret_cast<const F*>(As + C::a_off(arow, QB::a_k(j, q, s)));
+    };
     f32x4 acc[CT];
 #pragma unroll
     for (int c = 0; c < CT; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};

@@ -43,7 +43,7 @@
 namespace bi {
 
 constexpr int kSplitMMax = 32;
-constexpr int kStreamMMax = 16;   // rows of x the streaming GEMV takes (4-bit; 8-bit codes: 8)
+constexpr int kStreamMMax = 16;   // rows of x the streaming GEMV takes (8-bit codes: 8 with A staged in LDS)
 // gemv_wg with A staged in LDS: at most kGemvAChunks / W 16-byte chunks of A
 // per thread (M * K <= kGemvAChunks * 64 * 8).
 constexpr int kGemvAChunks = 32;
@@ -856,9 +856,10 @@ static void launch_wg_alds(const T* a, int64_t lda, const BSrc& bsrc, T* out, in
 
 // The barrier-free decode GEMV (bi_gemv_stream.h) for a quantized or a dense
 // B: W waves of NB = G / W consecutive groups, M <= MR rows of A staged per
-// wave, CT column tiles per wave, B loads PD groups ahead. Returns false when
-// the shape does not qualify.
-template <typename T, class BSrc, int W, int NB, int MR, int PD, int CT = 1>
+// wave (AG: read per group from global memory instead), CT column tiles per
+// wave, B loads PD groups ahead. Returns false when the shape does not
+// qualify.
+template <typename T, class BSrc, int W, int NB, int MR, int PD, int CT = 1, bool AG = false>
 static bool launch_stream1(const T* a, int64_t lda, const BSrc& b, T* out, int M, int N, int K, int G,
                            hipStream_t st) {
   constexpr int kCE = 16 / (int)sizeof(T);
@@ -869,13 +870,13 @@ static bool launch_stream1(const T* a, int64_t lda, const BSrc& b, T* out, int M
   // LDS of the configuration (GemvStreamCfg::kLdsBytes, computed here so an
   // unsupported configuration is never instantiated): MR rows x K of A do not
   // fit for every shape; the caller then falls back.
-  constexpr size_t kElemBytes = (size_t)(MR * NB * kGroupK + 2 * 16 * CT * kSPR) * sizeof(T);
+  constexpr size_t kElemBytes = (size_t)((AG ? 0 : MR * NB * kGroupK) + 2 * 16 * CT * kSPR) * sizeof(T);
   constexpr size_t kLds = (size_t)W * std::max<size_t>(kElemBytes, (size_t)NB * CT * kWave * 16);
   if constexpr (sizeof(T) != 2 || kSPR % kCE != 0 || (MR * NB * kGroupK) % (kCE * kWave) != 0 ||
                 kLds > 160 * 1024) {
     return false;
   } else {
-    typedef GemvStreamCfg<T, GS, W, NB, MR, CT> C;
+    typedef GemvStreamCfg<T, GS, W, NB, MR, CT, AG> C;
     static_assert(C::kLdsBytes == kLds, "launch_stream1: LDS size");
     if (G != W * NB) return false;
     // More than 64 KB of dynamic LDS (8 or 16 rows of A) is allowed
@@ -883,13 +884,13 @@ static bool launch_stream1(const T* a, int64_t lda, const BSrc& b, T* out, int M
     // and no error state behind; the launch then reports its own status).
     static const bool lds_raised = [] {
       if (C::lds_bytes(16) <= 65536) return true;
-      const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream<T, BSrc, W, NB, MR, PD, CT>),
+      const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_stream<T, BSrc, W, NB, MR, PD, CT, AG>),
                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
       if (!ok) (void)hipGetLastError();
       return ok;
     }();
     (void)lds_raised;
-    gemv_stream<T, BSrc, W, NB, MR, PD, CT><<<dim3(ceil_div(N, 16 * CT)), kWave * W, C::lds_bytes(G), st>>>(
+    gemv_stream<T, BSrc, W, NB, MR, PD, CT, AG><<<dim3(ceil_div(N, 16 * CT)), kWave * W, C::lds_bytes(G), st>>>(
         a, lda, b, out, M, N, K, G);
     return true;
   }
@@ -909,6 +910,28 @@ inline int stream_ct(int MR, int N) {
   int ct = 1;
   while (ct < 4 && ceil_div(N, 16 * ct) > cap) ct *= 2;
   return ct;
+}
+
+// The streaming GEMV with A read per group from global memory (AG), for M <=
+// 16 rows whose MR rows x K of A do not fit in LDS beside the other resident
+// workgroups (K = 8192 at M > 8, K = 14336 at M > 4), with at least one column
+// tile per CU (fewer tiles take the split-K mid-M launch). A's fragments of a
+// group then come from L2 with the group's codes: each workgroup rereads A
+// (M x K, a few hundred KB) from L2, which costs less than the workgroup-fold
+// GEMV's per-group reads. Measured against the launches they replace (same
+// box, bits equal), 4-bit g64 [4096, 14336] M = 5 / 8 / 12 / 16: 17.6 / 19.0
+// / 20.7 / 23.1 -> 13.5 / 15.1 / 17.4 / 20.7 us (7 waves of 8 groups; 14 of 4
+// equal); [4096, 8192] M = 12 / 16 12.7 / 14.0 -> 10.8 / 12.6 us, [8192,
+// 8192] 23.9 / 25.6 -> 18.8 / 22.2 (4 waves of 8); 8-bit g128 [4096, 14336]
+// M = 5 / 16 21.7 / 28.8 -> 16.7 / 23.8 us; dense bf16 [4096, 8192] M = 12 /
+// 16 19.9 / 20.4 -> 15.1 / 16.4 us (8 waves of 4), [4096, 14336] M = 5 / 8
+// 21.3 / 23.1 -> 20.6 / 22.3 us. Where A fits in LDS the staged launches are
+// faster (K = 4096 M = 16: 12.8 against 14.2 us), so they keep those shapes.
+template <typename T, class BSrc, int W, int NB>
+static bool launch_stream_ag(const T* a, int64_t lda, const BSrc& b, T* out, int M, int N, int K, int G,
+                             hipStream_t st) {
+  if (M > 16 || ceil_div(N, 16) < kStreamCUs) return false;
+  return launch_stream1<T, BSrc, W, NB, 16, 1, 1, true>(a, lda, b, out, M, N, K, G, st);
 }
 
 template <typename T, int BITS, int GS, int W, int NB, int PD>
@@ -947,7 +970,8 @@ static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& 
 template <typename T, int BITS, int GS>
 static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N, int K,
                           int G, hipStream_t st) {
-  if (M > (BITS == 4 ? kStreamMMax : 8) || K % kGroupK) return false;
+  typedef QuantB<T, BITS, GS> QB;
+  if (M > kStreamMMax || K % kGroupK) return false;
   if (b.groups_per_row % (16 / (int)sizeof(T)) || !bi_host::aligned16(b.scales) || !bi_host::aligned16(b.biases) ||
       lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a))
     return false;
@@ -963,9 +987,11 @@ static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b,
              launch_stream_m<T, BITS, GS, 2, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
              launch_stream_m<T, BITS, GS, 1, 4, 2>(a, lda, b, out, M, N, K, G, st);
     case 32:
-      return launch_stream_m<T, BITS, GS, 8, 4, 1>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream_m<T, BITS, GS, 8, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_ag<T, QB, 4, 8>(a, lda, b, out, M, N, K, G, st);
     case 56:
-      return launch_stream_m<T, BITS, GS, 14, 4, 1>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream_m<T, BITS, GS, 14, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_ag<T, QB, 7, 8>(a, lda, b, out, M, N, K, G, st);
     default:
       return false;
   }
@@ -998,8 +1024,12 @@ static bool launch_stream_dense(const T* a, int64_t lda, const DenseB<T>& b, T* 
   switch (G) {
     case 16: return launch_stream_dense_m<T, 8, 2>(a, lda, b, out, M, N, K, G, st);
     case 8: return launch_stream_dense_m<T, 4, 2>(a, lda, b, out, M, N, K, G, st);
-    case 32: return launch_stream_dense_m<T, 8, 4>(a, lda, b, out, M, N, K, G, st);
-    case 56: return launch_stream_dense_m<T, 14, 4>(a, lda, b, out, M, N, K, G, st);
+    case 32:
+      return launch_stream_dense_m<T, 8, 4>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_ag<T, DenseB<T>, 8, 4>(a, lda, b, out, M, N, K, G, st);
+    case 56:
+      return launch_stream_dense_m<T, 14, 4>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_ag<T, DenseB<T>, 7, 8>(a, lda, b, out, M, N, K, G, st);
     default: return false;
   }
 }
@@ -1166,7 +1196,8 @@ static int run_gemm(const T* a, int64_t lda, const BSrc& bsrc, T* out, int M, in
   constexpr int WAVES = 4;
   if constexpr (BSrc::kMeta) {
     // The streaming GEMV wherever it takes the shape (M <= 16, 4-bit; M <= 8,
-    // 8-bit), at any number of column tiles, with 8 or more groups, or with 4
+    // 8-bit, or up to 16 with A read from global memory at 32 or 56 groups),
+    // at any number of column tiles, with 8 or more groups, or with 4
     // groups at M <= 2 and groups of up to 64 (4 groups of 128: 2.99 -> 3.82 us
     // at N = 256, M = 1). Measured against the workgroup-fold GEMV and the mid-M
     // launch it replaces (4-bit g64, bits equal): K = 4096 N = 4096 M = 1 / 4 /

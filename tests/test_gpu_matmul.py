@@ -181,8 +181,9 @@ def test_matmul_stream_launch_matches_oracle(dt, N, K):
     """M <= 16 with 8 / 16 / 32 / 56 groups takes the streaming GEMV for a
     dense B at any number of column tiles (one tile, a single partial tile of
     5 columns, 63 with the last partial, up to 515; A's rows staged per wave
-    in LDS; 32 groups: M <= 8, 56 groups: M <= 4, then the workgroup-fold
-    GEMV): rows equal the oracle and the same rows computed alone, bit for
+    in LDS; 32 groups: M <= 8, 56 groups: M <= 4; past that A read per group
+    from global memory at 257 and 515 tiles, the workgroup-fold GEMV at
+    fewer): rows equal the oracle and the same rows computed alone, bit for
     bit."""
     g = gen(N + K)
     bt = randn((N, K), DT[dt], g)
@@ -196,6 +197,32 @@ def test_matmul_stream_launch_matches_oracle(dt, N, K):
         assert_bits_equal(to_np(got)[rows][:, cols], want, f"N={N} K={K} M={M}")
         for rr in rows:
             assert bits(got[rr:rr + 1]) == bits(_mm(x[rr:rr + 1], bt.t())), (M, rr)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_matmul_stream_a_from_global(dt):
+    """5 <= M <= 16 where A's rows x K do not fit in LDS (56 groups at M > 4,
+    32 groups at M > 8) with at least 256 column tiles: the dense streaming
+    GEMV with A's fragments read per group from global memory (7 waves of 8
+    groups at 56, 8 of 4 at 32), on exactly 256 tiles and on 257 with the
+    last one partial; 255 tiles take the launch before. x is a column slice
+    of a wider matrix (row stride K + 64). Rows equal the oracle and the same
+    rows computed alone, bit for bit."""
+    for N, K in ((4096, 14336), (4096 + 8, 8192), (4080, 14336)):
+        g = gen(N + 5 * K)
+        bt = randn((N, K), DT[dt], g)
+        xw = randn((17, K + 64), DT[dt], g)
+        cols = np.unique(np.clip(np.r_[0:16, N // 2:N // 2 + 8, N - 16:N], 0, N - 1))
+        W = to_np(bt[cols])
+        for M in (5, 9, 16):
+            x = xw[:M, 32:32 + K]
+            assert x.stride(0) == K + 64
+            got = _mm(x, bt.t())
+            rows = sorted({0, M // 2, M - 1})
+            want = ora.matmul(to_np(x[rows]), W, dt)
+            assert_bits_equal(to_np(got)[rows][:, cols], want, f"N={N} K={K} M={M}")
+            for rr in rows:
+                assert bits(got[rr:rr + 1]) == bits(_mm(x[rr:rr + 1].contiguous(), bt.t())), (N, K, M, rr)
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])

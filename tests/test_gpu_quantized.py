@@ -160,9 +160,11 @@ def test_quantized_stream_launch_fewer_tiles_and_longer_k(bits_, gs, N, K):
     """The streaming GEMV below 512 column tiles (131, 258 and 63 tiles, the
     last one partial, and a single tile), at 32 and 56 groups (eight and
     fourteen waves of four groups) and at 4 groups (M <= 2 with groups of up
-    to 64 only): M <= 16 (4-bit) / 8 (8-bit) where A's rows fit in LDS, the
-    mid-M launch or the workgroup-fold GEMV past that (56 groups: M > 4).
-    Rows equal the oracle and the same rows computed alone, bit for bit."""
+    to 64 only): M <= 16 (4-bit) / 8 (8-bit) where A's rows fit in LDS; past
+    that (32 groups: M > 8, 56 groups: M > 4) with A read per group from
+    global memory at 258 / 257 tiles, the mid-M launch or the workgroup-fold
+    GEMV at fewer. Rows equal the oracle and the same rows computed alone, bit
+    for bit."""
     dt = "bf16"
     wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 11 + gs + K % 977)
     cols = np.unique(np.clip(np.r_[0:24, N // 2:N // 2 + 16, N - 24:N], 0, N - 1))
@@ -178,6 +180,36 @@ def test_quantized_stream_launch_fewer_tiles_and_longer_k(bits_, gs, N, K):
         assert_bits_equal(to_np(got)[rows][:, cols], want, f"N={N} K={K} M={M}")
         for rr in rows:
             assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1])), (M, rr)
+
+
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32), (8, 32)])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_quantized_stream_a_from_global(bits_, gs, dt):
+    """5 <= M <= 16 where A's rows x K do not fit in LDS (56 groups at M > 4,
+    32 groups at M > 8; 8-bit codes up to 16 rows as well) with at least 256
+    column tiles: the streaming GEMV with A's fragments read per group from
+    global memory (7 waves of 8 groups at 56, 4 of 8 at 32), on exactly 256
+    tiles and on 257 with the last one partial; 255 tiles take the launch
+    before. x is a column slice of a wider matrix (row stride K + 64) whose
+    rows past M hold other values. Rows equal the oracle and the same rows
+    computed alone, bit for bit."""
+    for N, K in ((4096, 14336), (4096 + 8, 8192), (4080, 14336)):
+        wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 7 + gs + N % 97)
+        cols = np.unique(np.clip(np.r_[0:16, N // 2:N // 2 + 8, N - 16:N], 0, N - 1))
+        W = ora.dequantize(wq[cols].view(torch.int32).numpy().view(np.uint32), to_np(s[cols]), to_np(b[cols]),
+                           gs, bits_, dt)
+        wq, s, b = wq.cuda(), s.cuda(), b.cuda()
+        xw = randn((17, K + 64), DT[dt], gen(K + bits_))
+        run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
+        for M in (5, 9, 16):
+            x = xw[:M, 32:32 + K]
+            assert x.stride(0) == K + 64
+            got = run(x)
+            rows = sorted({0, M // 2, M - 1})
+            want = ora.matmul(to_np(x[rows]), W, dt, kmap="blocked")
+            assert_bits_equal(to_np(got)[rows][:, cols], want, f"N={N} K={K} M={M}")
+            for rr in rows:
+                assert bits(got[rr:rr + 1]) == bits(run(x[rr:rr + 1].contiguous())), (N, K, M, rr)
 
 
 @pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 128), (4, 32)])
