@@ -36,9 +36,11 @@ PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 # HBM traffic of the headline kernel per launch, from two rocprofv3 counter
 # passes (FETCH_SIZE, WRITE_SIZE, KiB per dispatch) scaled by the same counters
 # on a 256 MiB device copy (bench.py --op copycal): read x 2.000, write x 1.000.
-# Source: profiles/qmatmul4_g64_llama_mlp_m1.txt. Re-measure after changing
-# the kernel.
-MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 16217.5, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
+# Source: profiles/qmatmul4_g64_llama_mlp_m1.txt (the repacked copy, the
+# default) and the earlier take of the MLX-layout kernel recorded there.
+# Re-measure after changing the kernel.
+MEASURED_TRAFFIC_QMM4_M1 = {"fetch_kib": 16217.0, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
+MEASURED_TRAFFIC_QMM4_M1_MLX = {"fetch_kib": 16217.5, "fetch_scale": 2.000, "write_kib": 28, "write_scale": 1.000}
 PEAK_BF16 = 2.5e15         # FLOP/s, dense bf16 MFMA
 METRIC = "% of HBM/MFMA roofline per op at batch 1–256, with bitwise batch invariance"
 ROTATE_BYTES = 512 << 20
@@ -113,6 +115,10 @@ HEADLINE_KERNEL = {
     (4, 64): "gemv_stream<bf16,4,64,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)",
     (8, 128): "gemv_stream<bf16,8,128,W=4,NB=4,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)",
 }
+# The same launch on the repacked copy (bi_quantized_matmul_packed; group size 64).
+HEADLINE_KERNEL_PACKED = {
+    (4, 64): "gemv_stream<bf16,QuantPacked<4>,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul_packed, M <= 4: one launch)",
+}
 
 
 def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
@@ -129,6 +135,12 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     for _ in range(ncopy - 1):
         copies.append(tuple(t.clone() for t in copies[0]))
     xs = (torch.randn((max(Ms), K), generator=g)).to(torch.bfloat16).cuda()
+    # The decode layout: every copy repacked once (cache_packed), so calls of
+    # up to PACKED_MAX_M rows read the repacked codes (same bits).
+    packed = args.qmm_layout == "packed" and gs == 64
+    if packed:
+        for c in copies:
+            bi.cache_packed(*c, group_size=gs, bits=bits)
 
     def call(M):
         return lambda i: bi.batch_invariant_quantized_matmul(xs[:M], *copies[i], group_size=gs, bits=bits)
@@ -142,10 +154,24 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     if args.profile_m != 1:                # profiling aid: only the calls at that M, no report
         _time_calls(call(args.profile_m), args.steps, args.warmup, ncopy, replays=3)
         return {"metric": METRIC, "op": f"qmm{bits} profile run at M={args.profile_m}", "value": None}
-    # 9 timed replays after 3 untimed ones: single replays of a short graph
-    # spread by several percent on one box.
-    durs = _time_calls(call(1), args.steps, args.warmup, ncopy, replays=9, warm_replays=3)
+    # 9 timed replays after 20 untimed ones: single replays of a short graph
+    # spread by several percent on one box, and the first few milliseconds of
+    # replays run slower (per-step times fell 10.3 -> 9.2 us over the first
+    # nine 1 ms replays after 3 untimed ones).
+    durs = _time_calls(call(1), args.steps, args.warmup, ncopy, replays=9, warm_replays=20)
     wall = time.perf_counter() - t0
+    mlx_layout = None
+    if packed and not args.headline_only:
+        # The same M = 1 graph on the MLX-layout operands (the copies dropped,
+        # then repacked for the sweep), timed before any larger M.
+        for c in copies:
+            bi.drop_packed(c[0])
+        d_mlx = _time_calls(call(1), args.steps, args.warmup, ncopy, replays=9, warm_replays=20)
+        mlx_layout = {"us_per_step": round(statistics.median(d_mlx) * 1e6, 3),
+                      "frac": round(qmm_bytes(1, N, K, bits, gs) / statistics.median(d_mlx) / PEAK_HBM, 4),
+                      "kernel": HEADLINE_KERNEL[(bits, gs)]}
+        for c in copies:
+            bi.cache_packed(*c, group_size=gs, bits=bits)
     table = {}
     for M in (() if args.headline_only else Ms):
         t = statistics.median(_time_calls(call(M), args.steps, args.warmup, ncopy))
@@ -175,7 +201,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     achievable = None if args.headline_only else stream_read_rate(per, args)
     traffic = None
     if bits == 4 and gs == 64:
-        mt = MEASURED_TRAFFIC_QMM4_M1
+        mt = MEASURED_TRAFFIC_QMM4_M1 if packed else MEASURED_TRAFFIC_QMM4_M1_MLX
         traffic = int(1024 * (mt["fetch_kib"] * mt["fetch_scale"] + mt["write_kib"] * mt["write_scale"]))
     return {
         "metric": METRIC,
@@ -187,12 +213,16 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
         "wall_s_timed": round(wall, 4),
         "dtype": "bf16",
         "config": {"workload": f"qmatmul {bits}-bit g{gs} affine, x[M,4096] @ W[14336,4096]^T, Llama-3-8B MLP shape",
-                   "M": 1, "M_sweep": list(Ms), "weights_rotated_MB": round(ncopy * per / 2**20)},
+                   "M": 1, "M_sweep": list(Ms), "weights_rotated_MB": round(ncopy * per / 2**20),
+                   "weights": ("MLX packed codes with a copy repacked once at load (bi_quantized_pack: the same "
+                               "codes, scales and biases in the decode GEMV's layout; M <= 16 reads it, bits equal "
+                               "to the MLX-layout call)") if packed else "MLX packed codes"},
         "roofline": {"bound": "hbm", "achieved": round(achieved / 1e9, 1), "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
                      "traffic_source": None if traffic is None else
                      "rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch x copy-kernel scale (bytes per launch)",
-                     "algorithmic_bytes": by1, "kernel": HEADLINE_KERNEL[(bits, gs)],
+                     "algorithmic_bytes": by1,
+                     "kernel": (HEADLINE_KERNEL_PACKED if packed else HEADLINE_KERNEL)[(bits, gs)],
                      "achievable": None if achievable is None else {
                          "value": round(achievable / 1e9, 1), "unit": "GB/s",
                          "frac_of_peak": round(achievable / PEAK_HBM, 4),
@@ -200,6 +230,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
                          "kernel": "bi_stream_read: a plain read of the same bytes in one launch (1 KB per wave "
                                    "instruction), graph-replayed over the same rotation"}},
         "per_m": table,
+        "mlx_layout_M1": mlx_layout,
         "bitwise_invariant_M1_vs_all": inv,
         "stock_gpu": {"dequant_plus_matmul_us": None if stock_deq is None else round(stock_deq * 1e6, 2),
                       "bf16_hipblaslt_gemv_us": None if stock_bf16 is None else round(stock_bf16 * 1e6, 2),
@@ -699,22 +730,26 @@ def bench_llama(args):
             # 4-bit also runs with every weight dequantized once next to its codes
             # (QuantizedLinear.cache_dequantized): prefill (M >= 256) then skips the
             # per-call dequantization, same bits; decode reads the codes either way.
-            runs = [("invariant", True, False)]
+            # And with every weight's codes repacked once (QuantizedLinear.cache_packed):
+            # decode (M <= 16) then reads the decode GEMV's layout, same bits.
+            runs = [("invariant", True, None)]
+            if bits:
+                runs.append(("invariant_packed", True, "packed"))
             if args.llama_stock:
-                runs.append(("stock", False, False))
+                runs.append(("stock", False, None))
                 if bits:
-                    runs.append(("invariant_dequantized_once", True, True))
+                    runs.append(("invariant_dequantized_once", True, "dequantized"))
             for label, on, cached in runs:
                 bi.reset_stats()
                 mdl = model if on else stock_model
                 qlins = [m for m in mdl.modules() if isinstance(m, QuantizedLinear)] if cached else []
                 for m in qlins:
-                    m.cache_dequantized()
+                    m.cache_packed() if cached == "packed" else m.cache_dequantized()
                 with bi.set_batch_invariant_mode(enabled=on, strict=on):
                     _llama_generate(mdl, prompt[:, :16], 2)            # warm-up
                     tp, td, lg = _llama_generate(mdl, prompt, steps)
                 for m in qlins:
-                    bi.drop_dequantized(m.weight)
+                    bi.drop_packed(m.weight) if cached == "packed" else bi.drop_dequantized(m.weight)
                 ref.setdefault(label, lg)
                 if cached:
                     entry[label + "_bits_equal_invariant"] = lg == ref["invariant"]
@@ -784,6 +819,9 @@ def main(argv=None) -> int:
     p.add_argument("--llama-stock", action=argparse.BooleanOptionalAction, default=True,
                    help="llama: also run the stock path and the dequantized-once run (off: the invariant run only)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--qmm-layout", default="packed", choices=["packed", "mlx"],
+                   help="qmm4: weights with a copy repacked once for the decode GEMV (packed, the default; the "
+                        "MLX-layout M=1 time is reported beside it) or the MLX layout alone")
     p.add_argument("--profile-m", type=int, default=1,
                    help="qmm4/qmm8: run only the graph-replayed calls at this M and print no result (for profilers)")
     p.add_argument("--headline-only", action="store_true",

@@ -150,6 +150,29 @@ size_t bi_quantized_matmul_dequantized_workspace_bytes(int64_t M, int64_t N, int
 int bi_quantized_matmul_dequantized(const void* x, int64_t ldx, const void* bq, void* out, int64_t M, int64_t N,
                                     int64_t K, int dtype, void* ws, size_t ws_bytes, void* stream);
 
+/* A repacked copy of a group-64 weight for the decode GEMV. bi_quantized_pack
+ * writes the same codes, scales and biases as w / scales / biases (bits 4 or
+ * 8, group_size 64, bf16 / fp16, K % 256 == 0) into bi_quantized_pack_bytes
+ * bytes laid out for the streaming GEMV: per 16 rows and 256-k group, the
+ * codes of each MFMA lane as the lane's 16-byte pieces of consecutive 1 KB runs,
+ * then one (scale, bias) pair per lane (pack_bytes returns 0 for an
+ * unsupported format). bi_quantized_matmul_packed is bi_quantized_matmul with
+ * that copy beside the MLX-layout operands (packed may be NULL: then it is
+ * bi_quantized_matmul): the streaming GEMV reads the copy wherever it takes
+ * the shape (M <= 16), every other launch reads w / scales / biases, and the
+ * result equals bi_quantized_matmul's bit for bit at every M. Same checks and
+ * workspace as bi_quantized_matmul; the copy must have been packed from these
+ * w / scales / biases.
+ * No counterpart in the reference (MLX reads its own layout): for callers that
+ * keep a repacked copy next to the codes, so that decode reads whole 1 KB runs
+ * per wave instruction. */
+size_t bi_quantized_pack_bytes(int64_t N, int64_t K, int bits, int group_size);
+int bi_quantized_pack(const uint32_t* w, const void* scales, const void* biases, void* packed, size_t packed_bytes,
+                      int64_t N, int64_t K, int bits, int group_size, int dtype, void* stream);
+int bi_quantized_matmul_packed(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                               const void* biases, const void* packed, void* out, int64_t M, int64_t N, int64_t K,
+                               int bits, int group_size, int dtype, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- Split-KV decode attention (one query token per sequence) -------------
  * q [B, Hq, D], k/v [B, Hkv, L, D] addressed through element strides
  *   strides[0..1] = q  (batch, head)

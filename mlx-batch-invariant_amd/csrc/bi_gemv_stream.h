@@ -45,9 +45,21 @@
 
 namespace bi {
 
-// Group size of a B source's per-group metadata; 0 for a dense B (none).
-template <class BSrc> struct StreamMeta { static constexpr int kGS = 0; };
-template <typename T, int BITS, int GS> struct StreamMeta<QuantB<T, BITS, GS>> { static constexpr int kGS = GS; };
+// Group size of a B source's per-group metadata staged in LDS; 0 for a dense B
+// (none) and for a repacked quantized B, whose metadata arrive with its codes
+// (kRegMeta: then checked for huge scales in registers).
+template <class BSrc> struct StreamMeta {
+  static constexpr int kGS = 0;
+  static constexpr bool kRegMeta = false;
+};
+template <typename T, int BITS, int GS> struct StreamMeta<QuantB<T, BITS, GS>> {
+  static constexpr int kGS = GS;
+  static constexpr bool kRegMeta = false;
+};
+template <typename T, int BITS> struct StreamMeta<QuantPacked<T, BITS>> {
+  static constexpr int kGS = 0;
+  static constexpr bool kRegMeta = true;
+};
 
 template <typename T, int GS, int W, int NB, int MR, int CT = 1, bool AG = false>
 struct GemvStreamCfg {
@@ -192,6 +204,9 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
         }
         huge |= bsrc.huge_scale(braw[j][c]);
       }
+    } else if constexpr (StreamMeta<BSrc>::kRegMeta) {
+#pragma unroll
+      for (int c = 0; c < CT; ++c) huge |= bsrc.huge_scale(braw[j][c]);
     }
     // A fragments are read from LDS one step ahead of their MFMA (not all
     // eight up front): 24 fewer live registers, which lets a CU hold every

@@ -134,31 +134,45 @@ extern "C" int bi_matmul_batched(const void* a, int64_t a_batch_stride, int64_t 
   return BI_OK;
 }
 
+namespace {
+
+// Checks shared by bi_quantized_matmul and bi_quantized_matmul_packed: BI_OK
+// to run, an error code (negative) to return, or kQmmEmpty for a call with
+// nothing to compute (M = 0), which then returns BI_OK.
+constexpr int kQmmEmpty = 1;
+int qmm_check(const char* name, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+              const void* biases, void* out, int64_t M, int64_t N, int64_t K, int bits, int group_size, int dtype,
+              void* ws, size_t ws_bytes) {
+  using namespace bi_host;
+  if ((bits != 4 && bits != 8) || (group_size != 32 && group_size != 64 && group_size != 128))
+    return fail(BI_E_UNSUPPORTED, "%s: bits=%d group_size=%d not in {4,8}x{32,64,128}", name, bits, group_size);
+  int rc = check_common(name, M, N, K, out, ws, ws_bytes, false);
+  if (rc) return rc;
+  if (K % group_size)
+    return fail(BI_E_INVALID_ARG, "%s: K=%lld not a multiple of group_size=%d", name, (long long)K, group_size);
+  if (M == 0) return kQmmEmpty;
+  if (!x || !w || !scales || !biases) return fail(BI_E_INVALID_ARG, "%s: null operand", name);
+  if (ldx % 8 || ldx < K || !aligned16(x) || !aligned16(w))
+    return fail(BI_E_INVALID_ARG, "%s: needs ldx %% 8 == 0, ldx >= K, 16-byte aligned x and w", name);
+  if (dtype != BI_F32 && bi::qmm_use_big(M, N, K, 2)) {
+    const size_t need = bi::qmm_big_ws_bytes(M, N, K);
+    if (!ws || ws_bytes < need || !aligned16(ws))
+      return fail(BI_E_WORKSPACE, "%s: 16-byte aligned workspace of %zu bytes required, got %zu", name, need,
+                  ws ? ws_bytes : (size_t)0);
+  }
+  return BI_OK;
+}
+
+}  // namespace
+
 extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w,
                                    const void* scales, const void* biases, void* out, int64_t M,
                                    int64_t N, int64_t K, int bits, int group_size, int dtype,
                                    void* ws, size_t ws_bytes, void* stream) {
   using namespace bi_host;
-  if ((bits != 4 && bits != 8) || (group_size != 32 && group_size != 64 && group_size != 128))
-    return fail(BI_E_UNSUPPORTED, "bi_quantized_matmul: bits=%d group_size=%d not in {4,8}x{32,64,128}",
-                bits, group_size);
-  int rc = check_common("bi_quantized_matmul", M, N, K, out, ws, ws_bytes, false);
-  if (rc) return rc;
-  if (K % group_size)
-    return fail(BI_E_INVALID_ARG, "bi_quantized_matmul: K=%lld not a multiple of group_size=%d",
-                (long long)K, group_size);
-  if (M == 0) return BI_OK;
-  if (!x || !w || !scales || !biases)
-    return fail(BI_E_INVALID_ARG, "bi_quantized_matmul: null operand");
-  if (ldx % 8 || ldx < K || !aligned16(x) || !aligned16(w))
-    return fail(BI_E_INVALID_ARG,
-                "bi_quantized_matmul: needs ldx %% 8 == 0, ldx >= K, 16-byte aligned x and w");
-  if (dtype != BI_F32 && bi::qmm_use_big(M, N, K, 2)) {
-    const size_t need = bi::qmm_big_ws_bytes(M, N, K);
-    if (!ws || ws_bytes < need || !aligned16(ws))
-      return fail(BI_E_WORKSPACE, "bi_quantized_matmul: 16-byte aligned workspace of %zu bytes required, got %zu",
-                  need, ws ? ws_bytes : (size_t)0);
-  }
+  const int rc = qmm_check("bi_quantized_matmul", x, ldx, w, scales, biases, out, M, N, K, bits, group_size, dtype,
+                           ws, ws_bytes);
+  if (rc) return rc == kQmmEmpty ? BI_OK : rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
   switch (dtype) {
@@ -170,6 +184,69 @@ extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w
       return bi::qmm_f32(bits, group_size, x, ldx, w, scales, biases, out, Mi, Ni, Ki, ws, st);
     default: return fail(BI_E_UNSUPPORTED, "bi_quantized_matmul: unknown dtype %d", dtype);
   }
+}
+
+// ---------------------------------------------------------------------------
+// A repacked copy of a group-64 weight for the decode GEMV (QuantPacked in
+// bi_gemm_tile.h): the same codes, scales and biases in the layout the
+// streaming GEMV reads, so bi_quantized_matmul_packed equals
+// bi_quantized_matmul bit for bit at every M.
+// ---------------------------------------------------------------------------
+extern "C" size_t bi_quantized_pack_bytes(int64_t N, int64_t K, int bits, int group_size) {
+  if ((bits != 4 && bits != 8) || group_size != 64 || N <= 0 || K <= 0 || K % bi::kGroupK || N > 0x7fffffffLL ||
+      K > 0x7fffffffLL)
+    return 0;
+  return bits == 4 ? (size_t)bi::QuantPacked<bi::bf16, 4>::bytes(N, K)
+                   : (size_t)bi::QuantPacked<bi::bf16, 8>::bytes(N, K);
+}
+
+extern "C" int bi_quantized_pack(const uint32_t* w, const void* scales, const void* biases, void* packed,
+                                 size_t packed_bytes, int64_t N, int64_t K, int bits, int group_size, int dtype,
+                                 void* stream) {
+  using namespace bi_host;
+  if ((bits != 4 && bits != 8) || group_size != 64)
+    return fail(BI_E_UNSUPPORTED, "bi_quantized_pack: bits=%d group_size=%d (4 or 8 bits, group size 64)", bits,
+                group_size);
+  if (dtype != BI_BF16 && dtype != BI_F16)
+    return fail(BI_E_UNSUPPORTED, "bi_quantized_pack: dtype %d (bf16 and fp16 only)", dtype);
+  if (N < 0 || K < 0 || N > 0x7fffffffLL || K > 0x7fffffffLL || K % bi::kGroupK)
+    return fail(BI_E_INVALID_ARG, "bi_quantized_pack: N=%lld K=%lld (K a multiple of 256)", (long long)N,
+                (long long)K);
+  if (N == 0 || K == 0) return BI_OK;
+  const size_t need = bi_quantized_pack_bytes(N, K, bits, group_size);
+  if (!w || !scales || !biases || !packed || !aligned16(packed) || !aligned16(w))
+    return fail(BI_E_INVALID_ARG, "bi_quantized_pack: null pointer, or w / packed not 16-byte aligned");
+  if (packed_bytes < need)
+    return fail(BI_E_INVALID_ARG, "bi_quantized_pack: packed holds %zu bytes, %zu required", packed_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Ni = (int)N, Ki = (int)K;
+  if (dtype == BI_BF16)
+    return bits == 4 ? bi::pack_quant<bi::bf16, 4>(w, scales, biases, packed, Ni, Ki, st)
+                     : bi::pack_quant<bi::bf16, 8>(w, scales, biases, packed, Ni, Ki, st);
+  return bits == 4 ? bi::pack_quant<bi::f16, 4>(w, scales, biases, packed, Ni, Ki, st)
+                   : bi::pack_quant<bi::f16, 8>(w, scales, biases, packed, Ni, Ki, st);
+}
+
+extern "C" int bi_quantized_matmul_packed(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                                          const void* biases, const void* packed, void* out, int64_t M,
+                                          int64_t N, int64_t K, int bits, int group_size, int dtype, void* ws,
+                                          size_t ws_bytes, void* stream) {
+  using namespace bi_host;
+  if (!packed)
+    return bi_quantized_matmul(x, ldx, w, scales, biases, out, M, N, K, bits, group_size, dtype, ws, ws_bytes,
+                               stream);
+  if (group_size != 64 || (dtype != BI_BF16 && dtype != BI_F16) || K % bi::kGroupK)
+    return fail(BI_E_UNSUPPORTED,
+                "bi_quantized_matmul_packed: a packed copy needs group_size 64, bf16 / fp16 and K %% 256 == 0 "
+                "(group_size=%d dtype=%d K=%lld)", group_size, dtype, (long long)K);
+  const int rc = qmm_check("bi_quantized_matmul_packed", x, ldx, w, scales, biases, out, M, N, K, bits, group_size,
+                           dtype, ws, ws_bytes);
+  if (rc) return rc == kQmmEmpty ? BI_OK : rc;
+  if (!aligned16(packed)) return fail(BI_E_INVALID_ARG, "bi_quantized_matmul_packed: packed not 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+  if (dtype == BI_BF16) return bi::qmm_packed_bf16(bits, x, ldx, w, scales, biases, packed, out, Mi, Ni, Ki, ws, st);
+  return bi::qmm_packed_f16(bits, x, ldx, w, scales, biases, packed, out, Mi, Ni, Ki, ws, st);
 }
 
 // ---------------------------------------------------------------------------

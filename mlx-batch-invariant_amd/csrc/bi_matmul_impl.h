@@ -864,7 +864,7 @@ static bool launch_stream1(const T* a, int64_t lda, const BSrc& b, T* out, int M
                            hipStream_t st) {
   constexpr int kCE = 16 / (int)sizeof(T);
   constexpr int GS = StreamMeta<BSrc>::kGS;
-  constexpr int kSPR = GS > 0 ? NB * kGroupK / GS : 0;
+  constexpr int kSPR = GS > 0 ? NB * kGroupK / (GS > 0 ? GS : 1) : 0;
   // 2-byte T only: the kernel's 16-byte staging pieces are whole 8-element
   // fragments only there.
   // LDS of the configuration (GemvStreamCfg::kLdsBytes, computed here so an
@@ -934,10 +934,10 @@ static bool launch_stream_ag(const T* a, int64_t lda, const BSrc& b, T* out, int
   return launch_stream1<T, BSrc, W, NB, 16, 1, 1, true>(a, lda, b, out, M, N, K, G, st);
 }
 
-template <typename T, int BITS, int GS, int W, int NB, int PD>
-static bool launch_stream_m(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b, T* out, int M, int N,
-                            int K, int G, hipStream_t st) {
-  typedef QuantB<T, BITS, GS> QB;
+template <typename T, class QB, int W, int NB, int PD>
+static bool launch_stream_m(const T* a, int64_t lda, const QB& b, T* out, int M, int N, int K, int G,
+                            hipStream_t st) {
+  constexpr int BITS = QB::kBits;
   if (M == 1) return launch_stream1<T, QB, W, NB, 1, PD>(a, lda, b, out, M, N, K, G, st);
   if (M <= 4) return launch_stream1<T, QB, W, NB, 4, PD>(a, lda, b, out, M, N, K, G, st);
   if constexpr (BITS == 4) {
@@ -977,23 +977,50 @@ static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b,
     return false;
   switch (G) {
     case 16:
-      return launch_stream_m<T, BITS, GS, 8, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
-             launch_stream_m<T, BITS, GS, 4, 4, 1>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream_m<T, QB, 8, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_m<T, QB, 4, 4, 1>(a, lda, b, out, M, N, K, G, st);
     case 8:
-      return launch_stream_m<T, BITS, GS, 4, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
-             launch_stream_m<T, BITS, GS, 2, 4, 2>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream_m<T, QB, 4, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_m<T, QB, 2, 4, 2>(a, lda, b, out, M, N, K, G, st);
     case 4:
-      return launch_stream_m<T, BITS, GS, 4, 1, 1>(a, lda, b, out, M, N, K, G, st) ||
-             launch_stream_m<T, BITS, GS, 2, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
-             launch_stream_m<T, BITS, GS, 1, 4, 2>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream_m<T, QB, 4, 1, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_m<T, QB, 2, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_m<T, QB, 1, 4, 2>(a, lda, b, out, M, N, K, G, st);
     case 32:
-      return launch_stream_m<T, BITS, GS, 8, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
+      return launch_stream_m<T, QB, 8, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
              launch_stream_ag<T, QB, 4, 8>(a, lda, b, out, M, N, K, G, st);
     case 56:
-      return launch_stream_m<T, BITS, GS, 14, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
+      return launch_stream_m<T, QB, 14, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
              launch_stream_ag<T, QB, 7, 8>(a, lda, b, out, M, N, K, G, st);
     default:
       return false;
+  }
+}
+
+// The streaming GEMV on a repacked B (QuantPacked: group size 64, the codes'
+// and metadata's layout made for it): the launch shapes of launch_stream, with
+// no staged metadata (so no scale-slice constraint). False when the shape does
+// not qualify; the caller then runs the launch the MLX-layout B would take.
+// Measured against the MLX layout (same box, bits equal), 4-bit [14336, 4096]
+// M = 1 / 4 / 8 / 16: 9.68 / 10.52 / 10.98 / 13.31 -> 9.30-9.53 / 10.10 /
+// 10.32 / 11.95 us; [4096, 14336] M = 4 / 8 / 16 11.20 / 15.59 / 20.84 ->
+// 10.84 / 14.13 / 18.99 us.
+template <typename T, int BITS>
+static bool launch_stream_packed(const T* a, int64_t lda, const QuantPacked<T, BITS>& b, T* out, int M, int N,
+                                 int K, int G, hipStream_t st) {
+  typedef QuantPacked<T, BITS> QB;
+  if (M > kStreamMMax || K % kGroupK || lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a)) return false;
+  switch (G) {
+    case 16: return launch_stream_m<T, QB, 8, 2, 1>(a, lda, b, out, M, N, K, G, st);
+    case 8: return launch_stream_m<T, QB, 4, 2, 1>(a, lda, b, out, M, N, K, G, st);
+    case 4: return M <= 2 && launch_stream_m<T, QB, 4, 1, 1>(a, lda, b, out, M, N, K, G, st);
+    case 32:
+      return launch_stream_m<T, QB, 8, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_ag<T, QB, 4, 8>(a, lda, b, out, M, N, K, G, st);
+    case 56:
+      return launch_stream_m<T, QB, 14, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_ag<T, QB, 7, 8>(a, lda, b, out, M, N, K, G, st);
+    default: return false;
   }
 }
 
@@ -1315,6 +1342,65 @@ int run_quant(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
                       static_cast<float*>(ws), st, "bi_quantized_matmul");
 }
 
+// One thread per (16-row tile, group, MFMA lane): the lane's kWords code
+// words and its (scale, bias) pair copied into the QuantPacked layout.
+template <typename T, int BITS>
+__global__ __launch_bounds__(256) void qmm_pack_rows(const uint32_t* __restrict__ w,
+                                                     const T* __restrict__ scales,
+                                                     const T* __restrict__ biases, char* __restrict__ packed,
+                                                     int N, int K) {
+  typedef QuantPacked<T, BITS> P;
+  const int G = K / kGroupK;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)((N + 15) / 16) * G * kWave) return;
+  const int l = (int)(idx % kWave);
+  const int64_t tg = idx / kWave;                  // tile * G + group
+  const int g = (int)(tg % G);
+  const int n = (int)min<int64_t>(tg / G * 16 + l % 16, N - 1);
+  const int k0 = g * kGroupK + 64 * (l / 16);
+  const uint32_t* src = w + (int64_t)n * ((int64_t)K * BITS / 32) + (int64_t)k0 * BITS / 32;
+  char* blk = packed + tg * P::kBlock;
+#pragma unroll
+  for (int i = 0; i < P::kPieces; ++i)
+    *reinterpret_cast<u32x4*>(blk + 1024 * i + 16 * l) = *reinterpret_cast<const u32x4*>(src + 4 * i);
+  const int64_t si = (int64_t)n * (K / 64) + k0 / 64;
+  const uint32_t m = (uint32_t)__builtin_bit_cast(uint16_t, scales[si]) |
+                     ((uint32_t)__builtin_bit_cast(uint16_t, biases[si]) << 16);
+  *reinterpret_cast<uint32_t*>(blk + P::kPieces * 1024 + 4 * l) = m;
+}
+
+// The quantized op with an optional repacked copy of a group-64 B: the
+// streaming GEMV reads the copy wherever it takes the shape, every other
+// launch the MLX-layout operands, so the bits equal run_quant's at every M.
+template <typename T, int BITS>
+int run_quant_packed(const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
+                     const void* packed, void* out, int M, int N, int K, void* ws, hipStream_t st) {
+  if (packed && K % kGroupK == 0 && M > 0) {
+    QuantPacked<T, BITS> b;
+    b.w = w;
+    b.scales = static_cast<const T*>(scales);
+    b.biases = static_cast<const T*>(biases);
+    b.N = N;
+    b.K = K;
+    b.words_per_row = (int64_t)K * BITS / 32;
+    b.groups_per_row = K / 64;
+    b.p = static_cast<const char*>(packed);
+    b.G = K / kGroupK;
+    if (launch_stream_packed<T, BITS>(static_cast<const T*>(x), ldx, b, static_cast<T*>(out), M, N, K, b.G, st))
+      return bi_host::launch_status("bi_quantized_matmul_packed");
+  }
+  return run_quant<T, BITS, 64>(x, ldx, w, scales, biases, out, M, N, K, ws, st);
+}
+
+template <typename T, int BITS>
+int pack_quant(const uint32_t* w, const void* scales, const void* biases, void* packed, int N, int K,
+               hipStream_t st) {
+  const int64_t n = (int64_t)ceil_div(N, 16) * (K / kGroupK) * kWave;
+  qmm_pack_rows<T, BITS><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(
+      w, static_cast<const T*>(scales), static_cast<const T*>(biases), static_cast<char*>(packed), N, K);
+  return bi_host::launch_status("bi_quantized_pack");
+}
+
 template <typename T>
 int dispatch_quant(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w,
                    const void* scales, const void* biases, void* out, int M, int N, int K,
@@ -1351,5 +1437,17 @@ int qmm8_f16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* 
              void* out, int M, int N, int K, void* ws, hipStream_t st);
 int qmm_f32(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
             const void* biases, void* out, int M, int N, int K, void* ws, hipStream_t st);
+// The op with a repacked group-64 copy (run_quant_packed; bi_qmm_<dtype>.hip,
+// the 8-bit kernels in bi_qmm8_<dtype>.hip) and the packing (pack_quant).
+int qmm_packed_bf16(int bits, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                    const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
+                    hipStream_t st);
+int qmm_packed_f16(int bits, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                   const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
+                   hipStream_t st);
+int qmm8_packed_bf16(const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
+                     const void* packed, void* out, int M, int N, int K, void* ws, hipStream_t st);
+int qmm8_packed_f16(const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
+                    const void* packed, void* out, int M, int N, int K, void* ws, hipStream_t st);
 
 }  // namespace bi

@@ -22,7 +22,8 @@ from .kernels import (
     batch_invariant_quantized_matmul,
     batch_invariant_rms_norm,
 )
-from .kernels.quantized import quantize, dequantize, pack, unpack, cache_dequantized, drop_dequantized
+from .kernels.quantized import (quantize, dequantize, pack, unpack, cache_dequantized, drop_dequantized,
+                                cache_packed, drop_packed)
 from . import library  # registers torch.ops.mlx_bi.*
 
 __all__ = [
@@ -43,6 +44,8 @@ __all__ = [
     "dequantize",
     "cache_dequantized",
     "drop_dequantized",
+    "cache_packed",
+    "drop_packed",
     "pack",
     "unpack",
 ]

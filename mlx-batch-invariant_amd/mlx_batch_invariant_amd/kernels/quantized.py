@@ -83,7 +83,17 @@ def batch_invariant_quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: t
     M = x2.shape[0]
     out = torch.empty((M, N), dtype=dt, device=x.device)
     bq = _dequantized_for(w, scales, biases, group_size, bits, dt) if M >= DEQUANTIZED_MIN_M else None
-    if bq is not None:
+    bp = _cached_for(_PACKED, w, scales, biases, group_size, bits, dt) if 0 < M <= PACKED_MAX_M else None
+    if bp is not None:
+        lib = _lib.load()
+        ws_bytes = _lib.ws_bytes("bi_quantized_matmul_workspace_bytes", M, N, K)
+        ws = _lib.workspace(ws_bytes, x.device)
+        rc = lib.bi_quantized_matmul_packed(x2.data_ptr(), x2.stride(0), w.data_ptr(), scales.data_ptr(),
+                                            biases.data_ptr(), bp.data_ptr(), out.data_ptr(), M, N, K, bits,
+                                            group_size, _lib.DTYPE_CODE[dt], _lib.ptr(ws), ws_bytes,
+                                            _lib.stream_of(x))
+        _lib.check(rc, "bi_quantized_matmul_packed")
+    elif bq is not None:
         _lib.load()
         ws_bytes = _lib.ws_bytes("bi_quantized_matmul_dequantized_workspace_bytes", M, N, K)
         ws = _lib.workspace(ws_bytes, x.device)
@@ -142,9 +152,7 @@ def cache_dequantized(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tenso
     rc = _lib.load().bi_quantized_dequantize(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), bq.data_ptr(), N, K,
                                              bits, group_size, _lib.DTYPE_CODE[dt], _lib.stream_of(w))
     _lib.check(rc, "bi_quantized_dequantize")
-    key = id(w)
-    ref = weakref.ref(w, lambda _r, k=key: _DEQUANTIZED.pop(k, None) if _DEQUANTIZED.get(k, (None,))[0] is _r else None)
-    _DEQUANTIZED[key] = (ref, w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size, bits, dt, bq)
+    _remember(_DEQUANTIZED, w, scales, biases, group_size, bits, dt, bq)
     return bq
 
 
@@ -155,16 +163,79 @@ def drop_dequantized(w: torch.Tensor) -> None:
         del _DEQUANTIZED[id(w)]
 
 
-def _dequantized_for(w, scales, biases, group_size, bits, dt):
-    """The cached copy for exactly this call (same tensor and storage, same
-    scales / biases, format and dtype), else None."""
-    e = _DEQUANTIZED.get(id(w)) if _DEQUANTIZED else None
+def _cached_for(cache, w, scales, biases, group_size, bits, dt):
+    """The copy ``cache`` keeps for exactly this call (same tensor and storage,
+    same scales / biases, format and dtype), else None."""
+    e = cache.get(id(w)) if cache else None
     if e is None or e[0]() is not w:
         return None
     if (e[1], e[2], e[3], e[4], e[5], e[6]) != (w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size,
                                                 bits, dt):
         return None
     return e[7]
+
+
+def _dequantized_for(w, scales, biases, group_size, bits, dt):
+    return _cached_for(_DEQUANTIZED, w, scales, biases, group_size, bits, dt)
+
+
+def _remember(cache, w, scales, biases, group_size, bits, dt, copy) -> None:
+    key = id(w)
+    ref = weakref.ref(w, lambda _r, k=key: cache.pop(k, None) if cache.get(k, (None,))[0] is _r else None)
+    cache[key] = (ref, w.data_ptr(), scales.data_ptr(), biases.data_ptr(), group_size, bits, dt, copy)
+
+
+# ---- weights repacked once (decode calls) -------------------------------------
+
+# Rows of x up to which a repacked copy is used (the streaming GEMV's range;
+# bi_quantized_matmul_packed reads the MLX layout for the shapes it does not take).
+PACKED_MAX_M = 16
+# id(w) -> the same record as _DEQUANTIZED's, holding the repacked copy.
+_PACKED: dict = {}
+
+
+def cache_packed(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *, group_size: int,
+                 bits: int) -> torch.Tensor:
+    """Keep a repacked copy of the packed weight ``w`` (``bi_quantized_pack``:
+    the same codes, scales and biases in the layout the decode GEMV reads, as
+    uint8 ``bi_quantized_pack_bytes`` bytes) for as long as ``w`` lives. Calls
+    of ``batch_invariant_quantized_matmul`` with at most ``PACKED_MAX_M`` rows,
+    this ``w`` (the same tensor object) and these scales / biases then run
+    ``bi_quantized_matmul_packed``: the same bits, with each wave instruction of
+    the decode GEMV reading a whole 1 KB run of codes. Group size 64, 4 or 8
+    bits, bf16 / fp16 scales, K a multiple of 256. The copy holds about the
+    codes' size plus 4 bytes per group of 64 (w's size + scales + biases). Call
+    again after changing the weight's values in place; ``drop_packed`` releases
+    it."""
+    if bits not in SUPPORTED_BITS or group_size != 64:
+        raise ValueError(f"cache_packed: bits={bits} group_size={group_size} (group size 64 only)")
+    dt = scales.dtype
+    if dt not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"cache_packed: scales dtype {dt} (bf16 or fp16)")
+    if w.dtype not in _WORD_DTYPES or w.ndim != 2 or not w.is_contiguous():
+        raise ValueError("cache_packed: w must be a contiguous 2-D uint32 tensor")
+    _lib.require_gpu("cache_packed", w, scales, biases)
+    N, K = w.shape[0], w.shape[1] * (32 // bits)
+    if K % 256:
+        raise ValueError(f"cache_packed: K={K} must be a multiple of 256")
+    if tuple(scales.shape) != (N, K // group_size) or scales.shape != biases.shape or biases.dtype != dt \
+            or not scales.is_contiguous() or not biases.is_contiguous():
+        raise ValueError("cache_packed: scales/biases must be contiguous [N, K / group_size] of one dtype")
+    lib = _lib.load()
+    nbytes = lib.bi_quantized_pack_bytes(N, K, bits, group_size)
+    bp = torch.empty((nbytes,), dtype=torch.uint8, device=w.device)
+    rc = lib.bi_quantized_pack(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), bp.data_ptr(), nbytes, N, K, bits,
+                               group_size, _lib.DTYPE_CODE[dt], _lib.stream_of(w))
+    _lib.check(rc, "bi_quantized_pack")
+    _remember(_PACKED, w, scales, biases, group_size, bits, dt, bp)
+    return bp
+
+
+def drop_packed(w: torch.Tensor) -> None:
+    """Release the repacked copy ``cache_packed`` keeps for ``w``."""
+    e = _PACKED.get(id(w))
+    if e is not None and e[0]() is w:
+        del _PACKED[id(w)]
 
 
 # ---- format helpers (host-side torch; not on the kernel path) -----------------

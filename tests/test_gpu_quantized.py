@@ -401,3 +401,122 @@ def test_quantized_linear_cache_under_the_mode():
         cached = q(x)
     assert bits(cached) == bits(plain)
     bi.drop_dequantized(q.weight)
+
+
+def _pack_reference(wq, s, b, bits_, N, K):
+    """numpy restatement of bi_quantized_pack's layout (the QuantPacked
+    source of the streaming GEMV): block (tile t, group g) of bits x 512 + 256
+    bytes holds, for MFMA lane l = r + 16 q (row min(16 t + r, N - 1), k
+    [256 g + 64 q, +64)), its 64 x bits / 32 code words as 16-byte pieces at
+    1024 i + 16 l, then its scale and bias (16-bit each, scale low) at
+    bits x 512 + 4 l."""
+    words = wq.cpu().view(torch.int32).numpy().view(np.uint32)
+    sb = s.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.uint32)
+    bb = b.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.uint32)
+    G, tiles, pieces = K // 256, (N + 15) // 16, bits_ // 2
+    wpl = 64 * bits_ // 32                                   # words per lane and group
+    blk = bits_ * 512 + 256
+    out = np.zeros(tiles * G * blk, np.uint8)
+    for t in range(tiles):
+        for g in range(G):
+            base = (t * G + g) * blk
+            for lane in range(64):
+                r, q = lane % 16, lane // 16
+                n = min(16 * t + r, N - 1)
+                k0 = 256 * g + 64 * q
+                wv = words[n, k0 * bits_ // 32:k0 * bits_ // 32 + wpl]
+                for i in range(pieces):
+                    o = base + 1024 * i + 16 * lane
+                    out[o:o + 16] = wv[4 * i:4 * i + 4].view(np.uint8)
+                m = np.uint32(sb[n, k0 // 64] | (bb[n, k0 // 64] << 16))
+                o = base + pieces * 1024 + 4 * lane
+                out[o:o + 4] = np.array([m], np.uint32).view(np.uint8)
+    return out
+
+
+@pytest.mark.parametrize("bits_", [4, 8])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_quantized_pack_layout(bits_, dt):
+    """bi_quantized_pack writes exactly the layout restated in numpy above
+    (20 rows: the second tile's rows past N repeat row N - 1; two groups)."""
+    from mlx_batch_invariant_amd import _lib
+    N, K = 20, 512
+    wq, s, b = _qweights(N, K, bits_, 64, dt, seed=bits_ + 41)
+    lib = _lib.load()
+    nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, 64)
+    got = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
+    wd, sd, bd = wq.cuda(), s.cuda(), b.cuda()      # held until the kernel has run
+    _lib.check(lib.bi_quantized_pack(wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), got.data_ptr(), nbytes, N, K,
+                                     bits_, 64, _lib.DTYPE_CODE[DT[dt]], None), "bi_quantized_pack")
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), _pack_reference(wq, s, b, bits_, N, K))
+
+
+@pytest.mark.parametrize("bits_", [4, 8])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_quantized_packed_equals_the_quantized_op(bits_, dt):
+    """bi_quantized_matmul_packed with the repacked copy equals
+    bi_quantized_matmul bit for bit at every M and group count: the streaming
+    GEMV on the copy (16 groups at 131 column tiles, the last one partial; 8
+    groups; 4 groups at M <= 2; 32 and 56 groups, A staged or read from global
+    memory at 257 and 258 tiles), and the MLX-layout launches where the stream
+    does not take the shape (12 groups; M > 16; 4 groups at M > 2). The cache
+    inside batch_invariant_quantized_matmul (up to PACKED_MAX_M rows) gives the
+    same bits, follows only the cached tensors, and is released by
+    drop_packed."""
+    from mlx_batch_invariant_amd import _lib
+    from mlx_batch_invariant_amd.kernels import quantized as kq
+    bi = _bi()
+    lib = _lib.load()
+    code = _lib.DTYPE_CODE[DT[dt]]
+    for N, K in ((2048 + 40, 4096), (1000, 2048), (100, 1024), (4096 + 8, 14336), (4096 + 24, 8192), (300, 3072)):
+        wq, s, b = _qweights(N, K, bits_, 64, dt, seed=bits_ * 17 + N % 89 + K % 97)
+        wq, s, b = wq.view(torch.int32).cuda(), s.cuda(), b.cuda()
+        nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, 64)
+        bp = torch.empty((nbytes,), dtype=torch.uint8, device="cuda")
+        _lib.check(lib.bi_quantized_pack(wq.data_ptr(), s.data_ptr(), b.data_ptr(), bp.data_ptr(), nbytes, N, K,
+                                         bits_, 64, code, None), "bi_quantized_pack")
+        x = randn((20, K), DT[dt], gen(K + N))
+        for M in (1, 2, 3, 5, 8, 12, 16, 20):
+            want = bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=64, bits=bits_)
+            need = lib.bi_quantized_matmul_workspace_bytes(M, N, K)
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+            got = torch.empty((M, N), dtype=DT[dt], device="cuda")
+            _lib.check(lib.bi_quantized_matmul_packed(x.data_ptr(), x.stride(0), wq.data_ptr(), s.data_ptr(),
+                                                      b.data_ptr(), bp.data_ptr(), got.data_ptr(), M, N, K, bits_,
+                                                      64, code, ws.data_ptr(), need, None),
+                       "bi_quantized_matmul_packed")
+            torch.cuda.synchronize()
+            assert bits(got) == bits(want), (N, K, M)
+    # the cache inside batch_invariant_quantized_matmul (last shape's operands)
+    plain = bi.batch_invariant_quantized_matmul(x, wq, s, b, group_size=64, bits=bits_)
+    cached = bi.cache_packed(wq, s, b, group_size=64, bits=bits_)
+    assert bits(cached) == bits(bp)
+    assert kq._cached_for(kq._PACKED, wq, s, b, 64, bits_, DT[dt]) is not None
+    assert kq._cached_for(kq._PACKED, wq, s.clone(), b, 64, bits_, DT[dt]) is None   # other scales: not this copy
+    for M in (1, 7, 16, 20):
+        assert bits(bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=64, bits=bits_)) == \
+            bits(plain[:M]), M
+    bi.drop_packed(wq)
+    assert kq._cached_for(kq._PACKED, wq, s, b, 64, bits_, DT[dt]) is None
+
+
+def test_quantized_linear_packed_under_the_mode():
+    """QuantizedLinear.cache_packed: decode-sized calls under the mode give the
+    same bits with and without the repacked copy, and the copy is used."""
+    bi = _bi()
+    from mlx_batch_invariant_amd.kernels import quantized as kq
+    from mlx_batch_invariant_amd.nn import QuantizedLinear
+    lin = torch.nn.Linear(4096, 1024, bias=False)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn((1024, 4096), generator=gen(37)) * 0.02)
+    q = QuantizedLinear.from_linear(lin.to(torch.bfloat16), group_size=64, bits=4).cuda()
+    x = randn((4, 3, 4096), torch.bfloat16, gen(43))
+    with bi.set_batch_invariant_mode(strict=True):
+        plain = [q(x[:, :t]) for t in (1, 2, 3)]
+        q.cache_packed()
+        assert kq._cached_for(kq._PACKED, q.weight, q.scales, q.biases, 64, 4, torch.bfloat16) is not None
+        cached = [q(x[:, :t]) for t in (1, 2, 3)]
+    for p_, c_ in zip(plain, cached):
+        assert bits(c_) == bits(p_)
+    bi.drop_packed(q.weight)
