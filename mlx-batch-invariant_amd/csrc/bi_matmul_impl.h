@@ -1011,7 +1011,16 @@ static bool launch_stream_packed(const T* a, int64_t lda, const QuantPacked<T, B
   typedef QuantPacked<T, BITS> QB;
   if (M > kStreamMMax || K % kGroupK || lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a)) return false;
   switch (G) {
-    case 16: return launch_stream_m<T, QB, 8, 2, 1>(a, lda, b, out, M, N, K, G, st);
+    case 16:
+      // 16 waves of one group (twice the waves per CU of 8 x 2 at the LDS A
+      // takes) for 9-16 rows, and for 5-8 rows with one column tile per wave:
+      // [14336, 4096] M = 12 / 16 11.2 / 11.5 -> 10.4 / 10.8 us, [4096, 4096]
+      // M = 8 / 16 5.12 / 5.52 -> 4.67 / 5.48 us; 8 x 2 stays at M <= 4 and
+      // where 5-8 rows take two column tiles (9.9 against 10.5 us at M = 8).
+      // (4-bit codes; 8-bit ones keep 8 x 2, unmeasured with 16 waves).
+      if (BITS == 4 && (M > 8 || (M > 4 && stream_ct(8, N) == 1)))
+        return launch_stream_m<T, QB, 16, 1, 1>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream_m<T, QB, 8, 2, 1>(a, lda, b, out, M, N, K, G, st);
     case 8: return launch_stream_m<T, QB, 4, 2, 1>(a, lda, b, out, M, N, K, G, st);
     case 4: return M <= 2 && launch_stream_m<T, QB, 4, 1, 1>(a, lda, b, out, M, N, K, G, st);
     case 32:

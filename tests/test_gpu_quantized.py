@@ -457,7 +457,9 @@ def test_quantized_pack_layout(bits_, dt):
 def test_quantized_packed_equals_the_quantized_op(bits_, dt):
     """bi_quantized_matmul_packed with the repacked copy equals
     bi_quantized_matmul bit for bit at every M and group count: the streaming
-    GEMV on the copy (16 groups at 131 column tiles, the last one partial; 8
+    GEMV on the copy (16 groups at 131 and 515 column tiles, the last one
+    partial: 8 waves of 2 groups, or 16 of 1 with one, two or four column
+    tiles per wave; 8
     groups; 4 groups at M <= 2; 32 and 56 groups, A staged or read from global
     memory at 257 and 258 tiles), and the MLX-layout launches where the stream
     does not take the shape (12 groups; M > 16; 4 groups at M > 2). The cache
@@ -469,7 +471,8 @@ def test_quantized_packed_equals_the_quantized_op(bits_, dt):
     bi = _bi()
     lib = _lib.load()
     code = _lib.DTYPE_CODE[DT[dt]]
-    for N, K in ((2048 + 40, 4096), (1000, 2048), (100, 1024), (4096 + 8, 14336), (4096 + 24, 8192), (300, 3072)):
+    for N, K in ((2048 + 40, 4096), (8192 + 40, 4096), (1000, 2048), (100, 1024), (4096 + 8, 14336),
+                 (4096 + 24, 8192), (300, 3072)):
         wq, s, b = _qweights(N, K, bits_, 64, dt, seed=bits_ * 17 + N % 89 + K % 97)
         wq, s, b = wq.view(torch.int32).cuda(), s.cuda(), b.cuda()
         nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, 64)
