@@ -115,9 +115,11 @@ HEADLINE_KERNEL = {
     (4, 64): "gemv_stream<bf16,4,64,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)",
     (8, 128): "gemv_stream<bf16,8,128,W=4,NB=4,MR=1,PD=1> (bi_quantized_matmul, M <= 4: one launch)",
 }
-# The same launch on the repacked copy (bi_quantized_matmul_packed; group size 64).
+# The same launch on the repacked copy (bi_quantized_matmul_packed).
 HEADLINE_KERNEL_PACKED = {
-    (4, 64): "gemv_stream<bf16,QuantPacked<4>,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul_packed, M <= 4: one launch)",
+    (4, 64): "gemv_stream<bf16,QuantPacked<4,64>,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul_packed, M <= 4: one launch)",
+    (8, 128): "gemv_stream<bf16,QuantPacked<8,128>,W=8,NB=2,MR=1,PD=1> (bi_quantized_matmul_packed, M <= 4: one "
+              "launch)",
 }
 
 
@@ -137,7 +139,7 @@ def bench_qmm(args, bits=4, gs=64, Ms=(1, 2, 4, 8, 16, 32, 64)):
     xs = (torch.randn((max(Ms), K), generator=g)).to(torch.bfloat16).cuda()
     # The decode layout: every copy repacked once (cache_packed), so calls of
     # up to PACKED_MAX_M rows read the repacked codes (same bits).
-    packed = args.qmm_layout == "packed" and gs == 64
+    packed = args.qmm_layout == "packed"
     if packed:
         for c in copies:
             bi.cache_packed(*c, group_size=gs, bits=bits)
@@ -820,8 +822,8 @@ def main(argv=None) -> int:
                    help="llama: also run the stock path and the dequantized-once run (off: the invariant run only)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--qmm-layout", default="packed", choices=["packed", "mlx"],
-                   help="qmm4: weights with a copy repacked once for the decode GEMV (packed, the default; the "
-                        "MLX-layout M=1 time is reported beside it) or the MLX layout alone")
+                   help="qmm4 / qmm8: weights with a copy repacked once for the decode GEMV (packed, the default; "
+                        "the MLX-layout M=1 time is reported beside it) or the MLX layout alone")
     p.add_argument("--profile-m", type=int, default=1,
                    help="qmm4/qmm8: run only the graph-replayed calls at this M and print no result (for profilers)")
     p.add_argument("--headline-only", action="store_true",

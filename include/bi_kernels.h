@@ -150,13 +150,13 @@ size_t bi_quantized_matmul_dequantized_workspace_bytes(int64_t M, int64_t N, int
 int bi_quantized_matmul_dequantized(const void* x, int64_t ldx, const void* bq, void* out, int64_t M, int64_t N,
                                     int64_t K, int dtype, void* ws, size_t ws_bytes, void* stream);
 
-/* A repacked copy of a group-64 weight for the decode GEMV. bi_quantized_pack
- * writes the same codes, scales and biases as w / scales / biases (bits 4 or
- * 8, group_size 64, bf16 / fp16, K % 256 == 0) into bi_quantized_pack_bytes
- * bytes laid out for the streaming GEMV: per 16 rows and 256-k group, the
- * codes of each MFMA lane as the lane's 16-byte pieces of consecutive 1 KB runs,
- * then one (scale, bias) pair per lane (pack_bytes returns 0 for an
- * unsupported format). bi_quantized_matmul_packed is bi_quantized_matmul with
+/* A repacked copy of a weight for the decode GEMV. bi_quantized_pack writes
+ * the same codes, scales and biases as w / scales / biases (bits 4 or 8,
+ * group_size 32 / 64 / 128, bf16 / fp16, K % 256 == 0) into
+ * bi_quantized_pack_bytes bytes laid out for the streaming GEMV: per 16 rows
+ * and 256-k group, the codes of each MFMA lane as the lane's 16-byte pieces of
+ * consecutive 1 KB runs, then the lane's (scale, bias) pairs (one, or two for
+ * group size 32) (pack_bytes returns 0 for an unsupported format). bi_quantized_matmul_packed is bi_quantized_matmul with
  * that copy beside the MLX-layout operands (packed may be NULL: then it is
  * bi_quantized_matmul): the streaming GEMV reads the copy wherever it takes
  * the shape (M <= 16), every other launch reads w / scales / biases, and the

@@ -291,45 +291,57 @@ struct QuantB {
 };
 
 // ---------------------------------------------------------------------------
-// An affine quantized B with group size 64 repacked once for the decode GEMV:
-// the same codes, scales and biases as QuantB<T, BITS, 64>, so the same values
-// reach the MFMA. For 16-row tile t and group g, MFMA lane l = r + 16 q holds
-// row 16 t + r, k [256 g + 64 q, +64) (the blocked map): its kWords words are
-// the l-th 16-byte pieces of kPieces consecutive 1 KB runs, followed by a
-// 256-byte run of (scale, bias) pairs, one 4-byte pair per lane. A wave's code
-// loads then read whole 1 KB runs (in the MLX layout each instruction touches
-// 16 weight rows 2 KB apart), and each lane's scale and bias arrive with its
-// codes instead of being staged per tile. Block (t, g) starts at byte
-// (t G + g) kBlock; tiles = ceil(N / 16), rows past N repeat row N - 1.
-// 2-byte T only (a pair is two 16-bit values).
+// An affine quantized B repacked once for the decode GEMV: the same codes,
+// scales and biases as QuantB<T, BITS, GS>, so the same values reach the MFMA.
+// For 16-row tile t and group g, MFMA lane l = r + 16 q holds row 16 t + r, k
+// [256 g + 64 q, +64) (the blocked map): its kWords words are the l-th 16-byte
+// pieces of kPieces consecutive 1 KB runs, followed by a run of (scale, bias)
+// pairs, kScales 4-byte pairs per lane (one for groups of 64 or 128, two for
+// 32), lane l's at 4 kScales l. A wave's code loads then read whole 1 KB runs
+// (in the MLX layout each instruction touches 16 weight rows 2 KB apart), and
+// each lane's scales and biases arrive with its codes instead of being staged
+// per tile. Block (t, g) starts at byte (t G + g) kBlock; tiles = ceil(N / 16),
+// rows past N repeat row N - 1. 2-byte T only (a pair is two 16-bit values).
 // ---------------------------------------------------------------------------
-template <typename T, int BITS>
-struct QuantPacked : QuantB<T, BITS, 64> {
-  typedef QuantB<T, BITS, 64> Base;
+template <typename T, int BITS, int GS>
+struct QuantPacked : QuantB<T, BITS, GS> {
+  typedef QuantB<T, BITS, GS> Base;
   typedef typename Base::Raw Raw;
+  static constexpr int kScales = Base::kScales;
   static constexpr int kPieces = Base::kWords / 4;               // 16-byte pieces per lane and group
-  static constexpr int kBlock = kPieces * 1024 + 256;            // bytes per (tile, group)
+  static constexpr int kBlock = kPieces * 1024 + 256 * kScales;  // bytes per (tile, group)
   static_assert(sizeof(T) == 2, "QuantPacked: 2-byte element types only");
+  static_assert(kScales == 1 || kScales == 2, "QuantPacked: one or two scales per lane");
   const char* p;
   int G;
   static constexpr int64_t bytes(int64_t N, int64_t K) { return (N + 15) / 16 * (K / kGroupK) * kBlock; }
   struct Lane {
     const char* c;   // the lane's first code piece of group 0
-    const char* m;   // the lane's (scale, bias) pair of group 0
+    const char* m;   // the lane's (scale, bias) pairs of group 0
   };
   // n must already be clamped into [0, N).
   __device__ __forceinline__ Lane lane(int n, int q) const {
     const char* b = p + (int64_t)(n / 16) * G * kBlock;
     const int l = n % 16 + 16 * q;
-    return Lane{b + 16 * l, b + kPieces * 1024 + 4 * l};
+    return Lane{b + 16 * l, b + kPieces * 1024 + 4 * kScales * l};
   }
   __device__ __forceinline__ void load_full(Raw& raw, const Lane& l, int g) const {
     const int64_t o = (int64_t)g * kBlock;
 #pragma unroll
     for (int i = 0; i < kPieces; ++i) raw.w[i] = *reinterpret_cast<const u32x4*>(l.c + o + 1024 * i);
-    const uint32_t m = *reinterpret_cast<const uint32_t*>(l.m + o);
-    raw.scale[0] = __builtin_bit_cast(T, (uint16_t)(m & 0xffffu));
-    raw.bias[0] = __builtin_bit_cast(T, (uint16_t)(m >> 16));
+    uint32_t m[kScales];
+    if constexpr (kScales == 1) {
+      m[0] = *reinterpret_cast<const uint32_t*>(l.m + o);
+    } else {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(l.m + o);
+      m[0] = v[0];
+      m[1] = v[1];
+    }
+#pragma unroll
+    for (int i = 0; i < kScales; ++i) {
+      raw.scale[i] = __builtin_bit_cast(T, (uint16_t)(m[i] & 0xffffu));
+      raw.bias[i] = __builtin_bit_cast(T, (uint16_t)(m[i] >> 16));
+    }
   }
 };
 

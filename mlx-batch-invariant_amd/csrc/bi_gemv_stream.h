@@ -56,7 +56,7 @@ template <typename T, int BITS, int GS> struct StreamMeta<QuantB<T, BITS, GS>> {
   static constexpr int kGS = GS;
   static constexpr bool kRegMeta = false;
 };
-template <typename T, int BITS> struct StreamMeta<QuantPacked<T, BITS>> {
+template <typename T, int BITS, int GS> struct StreamMeta<QuantPacked<T, BITS, GS>> {
   static constexpr int kGS = 0;
   static constexpr bool kRegMeta = true;
 };

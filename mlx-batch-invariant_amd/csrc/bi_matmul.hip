@@ -187,25 +187,46 @@ extern "C" int bi_quantized_matmul(const void* x, int64_t ldx, const uint32_t* w
 }
 
 // ---------------------------------------------------------------------------
-// A repacked copy of a group-64 weight for the decode GEMV (QuantPacked in
+// A repacked copy of a weight for the decode GEMV (QuantPacked in
 // bi_gemm_tile.h): the same codes, scales and biases in the layout the
 // streaming GEMV reads, so bi_quantized_matmul_packed equals
 // bi_quantized_matmul bit for bit at every M.
 // ---------------------------------------------------------------------------
+namespace {
+
+bool packable(int bits, int group_size) {
+  return (bits == 4 || bits == 8) && (group_size == 32 || group_size == 64 || group_size == 128);
+}
+
+template <int BITS>
+size_t pack_bytes_bits(int64_t N, int64_t K, int gs) {
+  if (gs == 32) return (size_t)bi::QuantPacked<bi::bf16, BITS, 32>::bytes(N, K);
+  if (gs == 64) return (size_t)bi::QuantPacked<bi::bf16, BITS, 64>::bytes(N, K);
+  return (size_t)bi::QuantPacked<bi::bf16, BITS, 128>::bytes(N, K);
+}
+
+template <typename T, int BITS>
+int pack_bits(int gs, const uint32_t* w, const void* scales, const void* biases, void* packed, int N, int K,
+              hipStream_t st) {
+  if (gs == 32) return bi::pack_quant<T, BITS, 32>(w, scales, biases, packed, N, K, st);
+  if (gs == 64) return bi::pack_quant<T, BITS, 64>(w, scales, biases, packed, N, K, st);
+  return bi::pack_quant<T, BITS, 128>(w, scales, biases, packed, N, K, st);
+}
+
+}  // namespace
+
 extern "C" size_t bi_quantized_pack_bytes(int64_t N, int64_t K, int bits, int group_size) {
-  if ((bits != 4 && bits != 8) || group_size != 64 || N <= 0 || K <= 0 || K % bi::kGroupK || N > 0x7fffffffLL ||
-      K > 0x7fffffffLL)
+  if (!packable(bits, group_size) || N <= 0 || K <= 0 || K % bi::kGroupK || N > 0x7fffffffLL || K > 0x7fffffffLL)
     return 0;
-  return bits == 4 ? (size_t)bi::QuantPacked<bi::bf16, 4>::bytes(N, K)
-                   : (size_t)bi::QuantPacked<bi::bf16, 8>::bytes(N, K);
+  return bits == 4 ? pack_bytes_bits<4>(N, K, group_size) : pack_bytes_bits<8>(N, K, group_size);
 }
 
 extern "C" int bi_quantized_pack(const uint32_t* w, const void* scales, const void* biases, void* packed,
                                  size_t packed_bytes, int64_t N, int64_t K, int bits, int group_size, int dtype,
                                  void* stream) {
   using namespace bi_host;
-  if ((bits != 4 && bits != 8) || group_size != 64)
-    return fail(BI_E_UNSUPPORTED, "bi_quantized_pack: bits=%d group_size=%d (4 or 8 bits, group size 64)", bits,
+  if (!packable(bits, group_size))
+    return fail(BI_E_UNSUPPORTED, "bi_quantized_pack: bits=%d group_size=%d not in {4,8}x{32,64,128}", bits,
                 group_size);
   if (dtype != BI_BF16 && dtype != BI_F16)
     return fail(BI_E_UNSUPPORTED, "bi_quantized_pack: dtype %d (bf16 and fp16 only)", dtype);
@@ -221,10 +242,10 @@ extern "C" int bi_quantized_pack(const uint32_t* w, const void* scales, const vo
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int Ni = (int)N, Ki = (int)K;
   if (dtype == BI_BF16)
-    return bits == 4 ? bi::pack_quant<bi::bf16, 4>(w, scales, biases, packed, Ni, Ki, st)
-                     : bi::pack_quant<bi::bf16, 8>(w, scales, biases, packed, Ni, Ki, st);
-  return bits == 4 ? bi::pack_quant<bi::f16, 4>(w, scales, biases, packed, Ni, Ki, st)
-                   : bi::pack_quant<bi::f16, 8>(w, scales, biases, packed, Ni, Ki, st);
+    return bits == 4 ? pack_bits<bi::bf16, 4>(group_size, w, scales, biases, packed, Ni, Ki, st)
+                     : pack_bits<bi::bf16, 8>(group_size, w, scales, biases, packed, Ni, Ki, st);
+  return bits == 4 ? pack_bits<bi::f16, 4>(group_size, w, scales, biases, packed, Ni, Ki, st)
+                   : pack_bits<bi::f16, 8>(group_size, w, scales, biases, packed, Ni, Ki, st);
 }
 
 extern "C" int bi_quantized_matmul_packed(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
@@ -235,18 +256,19 @@ extern "C" int bi_quantized_matmul_packed(const void* x, int64_t ldx, const uint
   if (!packed)
     return bi_quantized_matmul(x, ldx, w, scales, biases, out, M, N, K, bits, group_size, dtype, ws, ws_bytes,
                                stream);
-  if (group_size != 64 || (dtype != BI_BF16 && dtype != BI_F16) || K % bi::kGroupK)
+  if ((dtype != BI_BF16 && dtype != BI_F16) || K % bi::kGroupK)
     return fail(BI_E_UNSUPPORTED,
-                "bi_quantized_matmul_packed: a packed copy needs group_size 64, bf16 / fp16 and K %% 256 == 0 "
-                "(group_size=%d dtype=%d K=%lld)", group_size, dtype, (long long)K);
+                "bi_quantized_matmul_packed: a packed copy needs bf16 / fp16 and K %% 256 == 0 (dtype=%d K=%lld)",
+                dtype, (long long)K);
   const int rc = qmm_check("bi_quantized_matmul_packed", x, ldx, w, scales, biases, out, M, N, K, bits, group_size,
                            dtype, ws, ws_bytes);
   if (rc) return rc == kQmmEmpty ? BI_OK : rc;
   if (!aligned16(packed)) return fail(BI_E_INVALID_ARG, "bi_quantized_matmul_packed: packed not 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
-  if (dtype == BI_BF16) return bi::qmm_packed_bf16(bits, x, ldx, w, scales, biases, packed, out, Mi, Ni, Ki, ws, st);
-  return bi::qmm_packed_f16(bits, x, ldx, w, scales, biases, packed, out, Mi, Ni, Ki, ws, st);
+  if (dtype == BI_BF16)
+    return bi::qmm_packed_bf16(bits, group_size, x, ldx, w, scales, biases, packed, out, Mi, Ni, Ki, ws, st);
+  return bi::qmm_packed_f16(bits, group_size, x, ldx, w, scales, biases, packed, out, Mi, Ni, Ki, ws, st);
 }
 
 // ---------------------------------------------------------------------------

@@ -1005,10 +1005,10 @@ static bool launch_stream(const T* a, int64_t lda, const QuantB<T, BITS, GS>& b,
 // M = 1 / 4 / 8 / 16: 9.68 / 10.52 / 10.98 / 13.31 -> 9.30-9.53 / 10.10 /
 // 10.32 / 11.95 us; [4096, 14336] M = 4 / 8 / 16 11.20 / 15.59 / 20.84 ->
 // 10.84 / 14.13 / 18.99 us.
-template <typename T, int BITS>
-static bool launch_stream_packed(const T* a, int64_t lda, const QuantPacked<T, BITS>& b, T* out, int M, int N,
+template <typename T, int BITS, int GS>
+static bool launch_stream_packed(const T* a, int64_t lda, const QuantPacked<T, BITS, GS>& b, T* out, int M, int N,
                                  int K, int G, hipStream_t st) {
-  typedef QuantPacked<T, BITS> QB;
+  typedef QuantPacked<T, BITS, GS> QB;
   if (M > kStreamMMax || K % kGroupK || lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a)) return false;
   switch (G) {
     case 16:
@@ -1352,13 +1352,13 @@ int run_quant(const void* x, int64_t ldx, const uint32_t* w, const void* scales,
 }
 
 // One thread per (16-row tile, group, MFMA lane): the lane's kWords code
-// words and its (scale, bias) pair copied into the QuantPacked layout.
-template <typename T, int BITS>
+// words and its (scale, bias) pairs copied into the QuantPacked layout.
+template <typename T, int BITS, int GS>
 __global__ __launch_bounds__(256) void qmm_pack_rows(const uint32_t* __restrict__ w,
                                                      const T* __restrict__ scales,
                                                      const T* __restrict__ biases, char* __restrict__ packed,
                                                      int N, int K) {
-  typedef QuantPacked<T, BITS> P;
+  typedef QuantPacked<T, BITS, GS> P;
   const int G = K / kGroupK;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)((N + 15) / 16) * G * kWave) return;
@@ -1372,40 +1372,54 @@ __global__ __launch_bounds__(256) void qmm_pack_rows(const uint32_t* __restrict_
 #pragma unroll
   for (int i = 0; i < P::kPieces; ++i)
     *reinterpret_cast<u32x4*>(blk + 1024 * i + 16 * l) = *reinterpret_cast<const u32x4*>(src + 4 * i);
-  const int64_t si = (int64_t)n * (K / 64) + k0 / 64;
-  const uint32_t m = (uint32_t)__builtin_bit_cast(uint16_t, scales[si]) |
-                     ((uint32_t)__builtin_bit_cast(uint16_t, biases[si]) << 16);
-  *reinterpret_cast<uint32_t*>(blk + P::kPieces * 1024 + 4 * l) = m;
+#pragma unroll
+  for (int i = 0; i < P::kScales; ++i) {
+    const int64_t si = (int64_t)n * (K / GS) + k0 / GS + i;
+    const uint32_t m = (uint32_t)__builtin_bit_cast(uint16_t, scales[si]) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, biases[si]) << 16);
+    *reinterpret_cast<uint32_t*>(blk + P::kPieces * 1024 + 4 * (P::kScales * l + i)) = m;
+  }
 }
 
-// The quantized op with an optional repacked copy of a group-64 B: the
-// streaming GEMV reads the copy wherever it takes the shape, every other
-// launch the MLX-layout operands, so the bits equal run_quant's at every M.
-template <typename T, int BITS>
-int run_quant_packed(const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
-                     const void* packed, void* out, int M, int N, int K, void* ws, hipStream_t st) {
+// The quantized op with an optional repacked copy of B: the streaming GEMV
+// reads the copy wherever it takes the shape, every other launch the
+// MLX-layout operands, so the bits equal run_quant's at every M.
+template <typename T, int BITS, int GS>
+int run_quant_packed_gs(const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
+                        const void* packed, void* out, int M, int N, int K, void* ws, hipStream_t st) {
   if (packed && K % kGroupK == 0 && M > 0) {
-    QuantPacked<T, BITS> b;
+    QuantPacked<T, BITS, GS> b;
     b.w = w;
     b.scales = static_cast<const T*>(scales);
     b.biases = static_cast<const T*>(biases);
     b.N = N;
     b.K = K;
     b.words_per_row = (int64_t)K * BITS / 32;
-    b.groups_per_row = K / 64;
+    b.groups_per_row = K / GS;
     b.p = static_cast<const char*>(packed);
     b.G = K / kGroupK;
-    if (launch_stream_packed<T, BITS>(static_cast<const T*>(x), ldx, b, static_cast<T*>(out), M, N, K, b.G, st))
+    if (launch_stream_packed<T, BITS, GS>(static_cast<const T*>(x), ldx, b, static_cast<T*>(out), M, N, K, b.G,
+                                          st))
       return bi_host::launch_status("bi_quantized_matmul_packed");
   }
-  return run_quant<T, BITS, 64>(x, ldx, w, scales, biases, out, M, N, K, ws, st);
+  return run_quant<T, BITS, GS>(x, ldx, w, scales, biases, out, M, N, K, ws, st);
 }
 
 template <typename T, int BITS>
+int run_quant_packed(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                     const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
+                     hipStream_t st) {
+  if (gs == 32) return run_quant_packed_gs<T, BITS, 32>(x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
+  if (gs == 64) return run_quant_packed_gs<T, BITS, 64>(x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
+  if (gs == 128) return run_quant_packed_gs<T, BITS, 128>(x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
+  return bi_host::fail(BI_E_UNSUPPORTED, "bi_quantized_matmul_packed: bits=%d group_size=%d", BITS, gs);
+}
+
+template <typename T, int BITS, int GS>
 int pack_quant(const uint32_t* w, const void* scales, const void* biases, void* packed, int N, int K,
                hipStream_t st) {
   const int64_t n = (int64_t)ceil_div(N, 16) * (K / kGroupK) * kWave;
-  qmm_pack_rows<T, BITS><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(
+  qmm_pack_rows<T, BITS, GS><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(
       w, static_cast<const T*>(scales), static_cast<const T*>(biases), static_cast<char*>(packed), N, K);
   return bi_host::launch_status("bi_quantized_pack");
 }
@@ -1446,17 +1460,19 @@ int qmm8_f16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* 
              void* out, int M, int N, int K, void* ws, hipStream_t st);
 int qmm_f32(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
             const void* biases, void* out, int M, int N, int K, void* ws, hipStream_t st);
-// The op with a repacked group-64 copy (run_quant_packed; bi_qmm_<dtype>.hip,
-// the 8-bit kernels in bi_qmm8_<dtype>.hip) and the packing (pack_quant).
-int qmm_packed_bf16(int bits, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+// The op with a repacked copy (run_quant_packed; bi_qmm_<dtype>.hip, the
+// 8-bit kernels in bi_qmm8_<dtype>.hip) and the packing (pack_quant).
+int qmm_packed_bf16(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
                     const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
                     hipStream_t st);
-int qmm_packed_f16(int bits, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+int qmm_packed_f16(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
                    const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
                    hipStream_t st);
-int qmm8_packed_bf16(const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
-                     const void* packed, void* out, int M, int N, int K, void* ws, hipStream_t st);
-int qmm8_packed_f16(const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
-                    const void* packed, void* out, int M, int N, int K, void* ws, hipStream_t st);
+int qmm8_packed_bf16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                     const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
+                     hipStream_t st);
+int qmm8_packed_f16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                    const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
+                    hipStream_t st);
 
 }  // namespace bi

@@ -10,9 +10,10 @@ int qmm8_bf16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void*
   return dispatch_quant_bits<bf16, 8>(gs, x, ldx, w, scales, biases, out, M, N, K, ws, st);
 }
 
-int qmm8_packed_bf16(const void* x, int64_t ldx, const uint32_t* w, const void* scales, const void* biases,
-                     const void* packed, void* out, int M, int N, int K, void* ws, hipStream_t st) {
-  return run_quant_packed<bf16, 8>(x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
+int qmm8_packed_bf16(int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+                     const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
+                     hipStream_t st) {
+  return run_quant_packed<bf16, 8>(gs, x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
 }
 
 }  // namespace bi

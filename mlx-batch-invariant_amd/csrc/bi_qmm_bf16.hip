@@ -12,11 +12,11 @@ int qmm_bf16(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, co
   return dispatch_quant_bits<bf16, 4>(gs, x, ldx, w, scales, biases, out, M, N, K, ws, st);
 }
 
-int qmm_packed_bf16(int bits, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+int qmm_packed_bf16(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
                     const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
                     hipStream_t st) {
-  if (bits == 8) return qmm8_packed_bf16(x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
-  return run_quant_packed<bf16, 4>(x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
+  if (bits == 8) return qmm8_packed_bf16(gs, x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
+  return run_quant_packed<bf16, 4>(gs, x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
 }
 
 }  // namespace bi

@@ -12,11 +12,11 @@ int qmm_f16(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, con
   return dispatch_quant_bits<f16, 4>(gs, x, ldx, w, scales, biases, out, M, N, K, ws, st);
 }
 
-int qmm_packed_f16(int bits, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
+int qmm_packed_f16(int bits, int gs, const void* x, int64_t ldx, const uint32_t* w, const void* scales,
                    const void* biases, const void* packed, void* out, int M, int N, int K, void* ws,
                    hipStream_t st) {
-  if (bits == 8) return qmm8_packed_f16(x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
-  return run_quant_packed<f16, 4>(x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
+  if (bits == 8) return qmm8_packed_f16(gs, x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
+  return run_quant_packed<f16, 4>(gs, x, ldx, w, scales, biases, packed, out, M, N, K, ws, st);
 }
 
 }  // namespace bi

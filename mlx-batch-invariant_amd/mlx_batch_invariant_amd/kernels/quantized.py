@@ -202,13 +202,14 @@ def cache_packed(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
     of ``batch_invariant_quantized_matmul`` with at most ``PACKED_MAX_M`` rows,
     this ``w`` (the same tensor object) and these scales / biases then run
     ``bi_quantized_matmul_packed``: the same bits, with each wave instruction of
-    the decode GEMV reading a whole 1 KB run of codes. Group size 64, 4 or 8
-    bits, bf16 / fp16 scales, K a multiple of 256. The copy holds about the
-    codes' size plus 4 bytes per group of 64 (w's size + scales + biases). Call
+    the decode GEMV reading a whole 1 KB run of codes. 4 or 8 bits, group
+    size 32 / 64 / 128, bf16 / fp16 scales, K a multiple of 256. The copy holds
+    the codes, scales and biases again (4 bytes per lane and 64 k, 8 for group
+    size 32). Call
     again after changing the weight's values in place; ``drop_packed`` releases
     it."""
-    if bits not in SUPPORTED_BITS or group_size != 64:
-        raise ValueError(f"cache_packed: bits={bits} group_size={group_size} (group size 64 only)")
+    if bits not in SUPPORTED_BITS or group_size not in SUPPORTED_GROUPS:
+        raise ValueError(f"cache_packed: bits={bits} group_size={group_size}")
     dt = scales.dtype
     if dt not in (torch.bfloat16, torch.float16):
         raise ValueError(f"cache_packed: scales dtype {dt} (bf16 or fp16)")

@@ -70,8 +70,8 @@ class QuantizedLinear(torch.nn.Module):
     def cache_packed(self):
         """Keep a repacked copy of the codes (``kernels.quantized.cache_packed``):
         under the mode, calls with at most ``PACKED_MAX_M`` rows (decode) then
-        read it in the decode GEMV's layout, with the same bits. Group size 64
-        only; costs about the codes' size again in device memory."""
+        read it in the decode GEMV's layout, with the same bits. Costs about
+        the codes' size again in device memory."""
         _quant.cache_packed(self.weight, self.scales, self.biases, group_size=self.group_size, bits=self.bits)
         return self
 

@@ -220,20 +220,23 @@ def test_invalid_arguments_are_rejected_before_launch():
 
 def test_quantized_pack_sizes_and_rejections():
     """bi_quantized_pack_bytes: ceil(N / 16) tiles x K / 256 groups x (bits x
-    512 + 256) bytes (each lane's codes as 16-byte pieces of 1 KB runs, then
-    256 bytes of (scale, bias) pairs), 0 for a format without a packed form;
+    512 + 256 x pairs) bytes (each lane's codes as 16-byte pieces of 1 KB runs,
+    then its (scale, bias) pairs: one, two for group size 32), 0 for a format
+    without a packed form;
     bi_quantized_pack / bi_quantized_matmul_packed reject what they cannot take
     before launching anything (M = 0 is a no-op)."""
     lib = _lib.load()
     assert lib.bi_quantized_pack_bytes(14336, 4096, 4, 64) == 896 * 16 * 2304
     assert lib.bi_quantized_pack_bytes(4096, 14336, 4, 64) == 256 * 56 * 2304
     assert lib.bi_quantized_pack_bytes(17, 256, 8, 64) == 2 * 1 * 4352
-    for args in ((4096, 4096, 4, 32), (4096, 4096, 3, 64), (4096, 4160, 4, 64), (0, 4096, 4, 64),
+    assert lib.bi_quantized_pack_bytes(17, 256, 8, 128) == 2 * 1 * 4352
+    assert lib.bi_quantized_pack_bytes(4096, 4096, 4, 32) == 256 * 16 * 2560
+    for args in ((4096, 4096, 4, 16), (4096, 4096, 3, 64), (4096, 4160, 4, 64), (0, 4096, 4, 64),
                  (4096, 0, 4, 64)):
         assert lib.bi_quantized_pack_bytes(*args) == 0, args
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     need = lib.bi_quantized_pack_bytes(32, 512, 4, 64)
-    assert lib.bi_quantized_pack(p, p, p, p, need, 32, 512, 4, 32, 2, None) == -2           # group size 32
+    assert lib.bi_quantized_pack(p, p, p, p, need, 32, 512, 4, 16, 2, None) == -2           # group size 16
     assert lib.bi_quantized_pack(p, p, p, p, need, 32, 512, 4, 64, 0, None) == -2           # fp32
     assert lib.bi_quantized_pack(p, p, p, p, need, 32, 320, 4, 64, 2, None) == -1           # K % 256
     assert lib.bi_quantized_pack(p, p, p, p, need - 1, 32, 512, 4, 64, 2, None) == -1       # too small
@@ -242,7 +245,7 @@ def test_quantized_pack_sizes_and_rejections():
     assert lib.bi_quantized_pack(p, p, p, ctypes.c_void_p(24), need, 32, 512, 4, 64, 2, None) == -1  # misaligned
     assert lib.bi_quantized_pack(p, p, p, p, need, 0, 512, 4, 64, 2, None) == 0             # nothing to pack
     # the matmul with a packed copy: the copy's format first, then the op's own checks
-    assert lib.bi_quantized_matmul_packed(p, 512, p, p, p, p, p, 2, 32, 512, 4, 32, 2, None, 0, None) == -2
+    assert lib.bi_quantized_matmul_packed(p, 512, p, p, p, p, p, 2, 32, 512, 4, 16, 2, None, 0, None) == -2
     assert lib.bi_quantized_matmul_packed(p, 512, p, p, p, p, p, 2, 32, 512, 4, 64, 0, None, 0, None) == -2
     assert lib.bi_quantized_matmul_packed(p, 320, p, p, p, p, p, 2, 32, 320, 4, 64, 2, None, 0, None) == -2
     assert lib.bi_quantized_matmul_packed(p, 512, p, p, p, p, p, 2, 32, 512, 3, 64, 2, None, 0, None) == -2

@@ -403,19 +403,21 @@ def test_quantized_linear_cache_under_the_mode():
     bi.drop_dequantized(q.weight)
 
 
-def _pack_reference(wq, s, b, bits_, N, K):
+def _pack_reference(wq, s, b, bits_, gs, N, K):
     """numpy restatement of bi_quantized_pack's layout (the QuantPacked
     source of the streaming GEMV): block (tile t, group g) of bits x 512 + 256
-    bytes holds, for MFMA lane l = r + 16 q (row min(16 t + r, N - 1), k
-    [256 g + 64 q, +64)), its 64 x bits / 32 code words as 16-byte pieces at
-    1024 i + 16 l, then its scale and bias (16-bit each, scale low) at
-    bits x 512 + 4 l."""
+    x P bytes (P = 2 pairs per lane for group size 32, else 1) holds, for MFMA
+    lane l = r + 16 q (row min(16 t + r, N - 1), k [256 g + 64 q, +64)), its
+    64 x bits / 32 code words as 16-byte pieces at 1024 i + 16 l, then its P
+    (scale, bias) pairs (16-bit each, scale low; pair i of groups k0 / gs + i)
+    at bits x 512 + 4 (P l + i)."""
     words = wq.cpu().view(torch.int32).numpy().view(np.uint32)
     sb = s.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.uint32)
     bb = b.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.uint32)
     G, tiles, pieces = K // 256, (N + 15) // 16, bits_ // 2
+    pairs = 2 if gs == 32 else 1
     wpl = 64 * bits_ // 32                                   # words per lane and group
-    blk = bits_ * 512 + 256
+    blk = bits_ * 512 + 256 * pairs
     out = np.zeros(tiles * G * blk, np.uint8)
     for t in range(tiles):
         for g in range(G):
@@ -428,33 +430,34 @@ def _pack_reference(wq, s, b, bits_, N, K):
                 for i in range(pieces):
                     o = base + 1024 * i + 16 * lane
                     out[o:o + 16] = wv[4 * i:4 * i + 4].view(np.uint8)
-                m = np.uint32(sb[n, k0 // 64] | (bb[n, k0 // 64] << 16))
-                o = base + pieces * 1024 + 4 * lane
-                out[o:o + 4] = np.array([m], np.uint32).view(np.uint8)
+                for i in range(pairs):
+                    m = np.uint32(sb[n, k0 // gs + i] | (bb[n, k0 // gs + i] << 16))
+                    o = base + pieces * 1024 + 4 * (pairs * lane + i)
+                    out[o:o + 4] = np.array([m], np.uint32).view(np.uint8)
     return out
 
 
-@pytest.mark.parametrize("bits_", [4, 8])
+@pytest.mark.parametrize("bits_,gs", [(4, 64), (8, 64), (4, 32), (8, 32), (4, 128), (8, 128)])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_quantized_pack_layout(bits_, dt):
+def test_quantized_pack_layout(bits_, gs, dt):
     """bi_quantized_pack writes exactly the layout restated in numpy above
     (20 rows: the second tile's rows past N repeat row N - 1; two groups)."""
     from mlx_batch_invariant_amd import _lib
     N, K = 20, 512
-    wq, s, b = _qweights(N, K, bits_, 64, dt, seed=bits_ + 41)
+    wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ + gs + 41)
     lib = _lib.load()
-    nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, 64)
+    nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, gs)
     got = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
     wd, sd, bd = wq.cuda(), s.cuda(), b.cuda()      # held until the kernel has run
     _lib.check(lib.bi_quantized_pack(wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), got.data_ptr(), nbytes, N, K,
-                                     bits_, 64, _lib.DTYPE_CODE[DT[dt]], None), "bi_quantized_pack")
+                                     bits_, gs, _lib.DTYPE_CODE[DT[dt]], None), "bi_quantized_pack")
     torch.cuda.synchronize()
-    assert np.array_equal(got.cpu().numpy(), _pack_reference(wq, s, b, bits_, N, K))
+    assert np.array_equal(got.cpu().numpy(), _pack_reference(wq, s, b, bits_, gs, N, K))
 
 
-@pytest.mark.parametrize("bits_", [4, 8])
-@pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_quantized_packed_equals_the_quantized_op(bits_, dt):
+@pytest.mark.parametrize("bits_,gs,dt", [(4, 64, "bf16"), (4, 64, "f16"), (8, 64, "bf16"), (8, 64, "f16"),
+                                         (4, 32, "bf16"), (4, 128, "f16"), (8, 128, "bf16"), (8, 32, "f16")])
+def test_quantized_packed_equals_the_quantized_op(bits_, gs, dt):
     """bi_quantized_matmul_packed with the repacked copy equals
     bi_quantized_matmul bit for bit at every M and group count: the streaming
     GEMV on the copy (16 groups at 131 and 515 column tiles, the last one
@@ -473,35 +476,35 @@ def test_quantized_packed_equals_the_quantized_op(bits_, dt):
     code = _lib.DTYPE_CODE[DT[dt]]
     for N, K in ((2048 + 40, 4096), (8192 + 40, 4096), (1000, 2048), (100, 1024), (4096 + 8, 14336),
                  (4096 + 24, 8192), (300, 3072)):
-        wq, s, b = _qweights(N, K, bits_, 64, dt, seed=bits_ * 17 + N % 89 + K % 97)
+        wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 17 + gs + N % 89 + K % 97)
         wq, s, b = wq.view(torch.int32).cuda(), s.cuda(), b.cuda()
-        nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, 64)
+        nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, gs)
         bp = torch.empty((nbytes,), dtype=torch.uint8, device="cuda")
         _lib.check(lib.bi_quantized_pack(wq.data_ptr(), s.data_ptr(), b.data_ptr(), bp.data_ptr(), nbytes, N, K,
-                                         bits_, 64, code, None), "bi_quantized_pack")
+                                         bits_, gs, code, None), "bi_quantized_pack")
         x = randn((20, K), DT[dt], gen(K + N))
         for M in (1, 2, 3, 5, 8, 12, 16, 20):
-            want = bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=64, bits=bits_)
+            want = bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=gs, bits=bits_)
             need = lib.bi_quantized_matmul_workspace_bytes(M, N, K)
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
             got = torch.empty((M, N), dtype=DT[dt], device="cuda")
             _lib.check(lib.bi_quantized_matmul_packed(x.data_ptr(), x.stride(0), wq.data_ptr(), s.data_ptr(),
                                                       b.data_ptr(), bp.data_ptr(), got.data_ptr(), M, N, K, bits_,
-                                                      64, code, ws.data_ptr(), need, None),
+                                                      gs, code, ws.data_ptr(), need, None),
                        "bi_quantized_matmul_packed")
             torch.cuda.synchronize()
             assert bits(got) == bits(want), (N, K, M)
     # the cache inside batch_invariant_quantized_matmul (last shape's operands)
-    plain = bi.batch_invariant_quantized_matmul(x, wq, s, b, group_size=64, bits=bits_)
-    cached = bi.cache_packed(wq, s, b, group_size=64, bits=bits_)
+    plain = bi.batch_invariant_quantized_matmul(x, wq, s, b, group_size=gs, bits=bits_)
+    cached = bi.cache_packed(wq, s, b, group_size=gs, bits=bits_)
     assert bits(cached) == bits(bp)
-    assert kq._cached_for(kq._PACKED, wq, s, b, 64, bits_, DT[dt]) is not None
-    assert kq._cached_for(kq._PACKED, wq, s.clone(), b, 64, bits_, DT[dt]) is None   # other scales: not this copy
+    assert kq._cached_for(kq._PACKED, wq, s, b, gs, bits_, DT[dt]) is not None
+    assert kq._cached_for(kq._PACKED, wq, s.clone(), b, gs, bits_, DT[dt]) is None   # other scales: not this copy
     for M in (1, 7, 16, 20):
-        assert bits(bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=64, bits=bits_)) == \
+        assert bits(bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=gs, bits=bits_)) == \
             bits(plain[:M]), M
     bi.drop_packed(wq)
-    assert kq._cached_for(kq._PACKED, wq, s, b, 64, bits_, DT[dt]) is None
+    assert kq._cached_for(kq._PACKED, wq, s, b, gs, bits_, DT[dt]) is None
 
 
 def test_quantized_linear_packed_under_the_mode():
