@@ -709,7 +709,7 @@ def bench_llama(args):
     import torch
     import mlx_batch_invariant_amd as bi
     from mlx_batch_invariant_amd.llama import LlamaConfig, LlamaShaped
-    from mlx_batch_invariant_amd.nn import QuantizedLinear
+    from mlx_batch_invariant_amd.nn import QuantizedLinear, cache_packed_linears
     T, steps = args.llama_prompt, args.llama_steps
     batches = tuple(int(b) for b in args.llama_batches.split(","))
     weights = [w.strip() for w in args.llama_weights.split(",")]
@@ -732,11 +732,10 @@ def bench_llama(args):
             # 4-bit also runs with every weight dequantized once next to its codes
             # (QuantizedLinear.cache_dequantized): prefill (M >= 256) then skips the
             # per-call dequantization, same bits; decode reads the codes either way.
-            # And with every weight's codes repacked once (QuantizedLinear.cache_packed):
+            # And with every linear weight repacked once (nn.cache_packed_linears:
+            # QuantizedLinear.cache_packed, cache_packed_weight for nn.Linear):
             # decode (M <= 16) then reads the decode GEMV's layout, same bits.
-            runs = [("invariant", True, None)]
-            if bits:
-                runs.append(("invariant_packed", True, "packed"))
+            runs = [("invariant", True, None), ("invariant_packed", True, "packed")]
             if args.llama_stock:
                 runs.append(("stock", False, None))
                 if bits:
@@ -745,13 +744,21 @@ def bench_llama(args):
                 bi.reset_stats()
                 mdl = model if on else stock_model
                 qlins = [m for m in mdl.modules() if isinstance(m, QuantizedLinear)] if cached else []
-                for m in qlins:
-                    m.cache_packed() if cached == "packed" else m.cache_dequantized()
+                if cached == "packed":
+                    cache_packed_linears(mdl)
+                for m in qlins if cached == "dequantized" else []:
+                    m.cache_dequantized()
                 with bi.set_batch_invariant_mode(enabled=on, strict=on):
                     _llama_generate(mdl, prompt[:, :16], 2)            # warm-up
                     tp, td, lg = _llama_generate(mdl, prompt, steps)
-                for m in qlins:
-                    bi.drop_packed(m.weight) if cached == "packed" else bi.drop_dequantized(m.weight)
+                for m in qlins if cached == "dequantized" else []:
+                    bi.drop_dequantized(m.weight)
+                if cached == "packed":
+                    for m in mdl.modules():
+                        if isinstance(m, QuantizedLinear):
+                            bi.drop_packed(m.weight)
+                        elif isinstance(m, torch.nn.Linear):
+                            bi.drop_packed_weight(m.weight)
                 ref.setdefault(label, lg)
                 if cached:
                     entry[label + "_bits_equal_invariant"] = lg == ref["invariant"]

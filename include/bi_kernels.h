@@ -97,6 +97,25 @@ int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out
  * thread's next call. */
 const char* bi_matmul_launch(int64_t M, int64_t N, int64_t K);
 
+/* A repacked copy of a dense weight for the decode GEMV. bi_matmul_pack writes
+ * bt's N x K elements (bf16 / fp16, K % 256 == 0, ldb % 8 == 0) into
+ * bi_matmul_pack_bytes bytes laid out for the streaming GEMV: per 16 rows and
+ * 256-k group, each MFMA lane's 16-byte fragment of step s as the lane's piece
+ * of the s-th 1 KB run (pack_bytes returns 0 for an unsupported format).
+ * bi_matmul_packed is bi_matmul with that copy beside bt (packed may be NULL:
+ * then it is bi_matmul): the streaming GEMV reads the copy wherever it takes
+ * the shape (M <= 16), every other launch reads bt, and the result equals
+ * bi_matmul's bit for bit at every M. Same checks and workspace as bi_matmul;
+ * the copy must have been packed from this bt.
+ * No counterpart in the reference (MLX reads the weight as stored): for callers
+ * that keep a repacked copy of an nn.Linear weight, so that decode reads whole
+ * 1 KB runs per wave instruction. */
+size_t bi_matmul_pack_bytes(int64_t N, int64_t K, int dtype);
+int bi_matmul_pack(const void* bt, int64_t ldb, void* packed, size_t packed_bytes, int64_t N, int64_t K, int dtype,
+                   void* stream);
+int bi_matmul_packed(const void* a, int64_t lda, const void* bt, int64_t ldb, const void* packed, void* out,
+                     int64_t M, int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes, void* stream);
+
 /* Strided batch of dense matmuls (a [batch][M, K], bt [batch][N, K],
  * out [batch][M, N]; batch strides in elements, 0 broadcasts a or bt): slice i
  * is exactly bi_matmul on the slice's pointers, so its bits equal a 2-D call

@@ -95,6 +95,36 @@ struct DenseB {
   static __device__ __forceinline__ int stage_k(int g, int p, int kc) { return g * kGroupK + 64 * p + 8 * kc; }
 };
 
+// A dense 2-byte B repacked once for the decode GEMV: the same elements, so the
+// same values reach the MFMA. For 16-row tile t and group g, MFMA lane
+// l = r + 16 q's step-s fragment (row 16 t + r, k 256 g + 32 s + 8 q, 8
+// elements: the dense k-slot map) is the l-th 16-byte piece of the s-th 1 KB
+// run of the (tile, group)'s 8 KB block at (t G + g) 8 KB. A wave's loads then
+// read whole 1 KB runs (in the row-major layout each instruction touches 16
+// rows, 64 bytes each). tiles = ceil(N / 16), rows past N repeat row N - 1.
+template <typename T>
+struct DensePacked : DenseB<T> {
+  typedef typename DenseB<T>::Raw Raw;
+  typedef typename Frag<T>::type F;
+  static_assert(sizeof(T) == 2, "DensePacked: 2-byte element types only");
+  static constexpr int kBlock = kSteps * 1024;                  // bytes per (tile, group)
+  const char* p;
+  int G;
+  static constexpr int64_t bytes(int64_t N, int64_t K) { return (N + 15) / 16 * (K / kGroupK) * kBlock; }
+  struct Lane {
+    const char* c;   // the lane's piece of group 0, step 0
+  };
+  // n must already be clamped into [0, N).
+  __device__ __forceinline__ Lane lane(int n, int q) const {
+    return Lane{p + (int64_t)(n / 16) * G * kBlock + (n % 16 + 16 * q) * 16};
+  }
+  __device__ __forceinline__ void load_full(Raw& raw, const Lane& l, int g) const {
+    const char* b = l.c + (int64_t)g * kBlock;
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) raw.f[s] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(b + 1024 * s));
+  }
+};
+
 // ---------------------------------------------------------------------------
 // MLX affine quantized B (kernels/quantized.py:1-22, :44-67 of the reference):
 // codes packed low-to-high in uint32 (32/BITS per word), one scale and bias

@@ -109,6 +109,79 @@ extern "C" int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb
   }
 }
 
+// ---------------------------------------------------------------------------
+// A repacked copy of a dense 2-byte B for the decode GEMV (DensePacked in
+// bi_gemm_tile.h): the same elements in the layout the streaming GEMV reads,
+// so bi_matmul_packed equals bi_matmul bit for bit at every M.
+// ---------------------------------------------------------------------------
+extern "C" size_t bi_matmul_pack_bytes(int64_t N, int64_t K, int dtype) {
+  if ((dtype != BI_BF16 && dtype != BI_F16) || N <= 0 || K <= 0 || K % bi::kGroupK || N > 0x7fffffffLL ||
+      K > 0x7fffffffLL)
+    return 0;
+  return (size_t)bi::DensePacked<bi::bf16>::bytes(N, K);
+}
+
+extern "C" int bi_matmul_pack(const void* bt, int64_t ldb, void* packed, size_t packed_bytes, int64_t N, int64_t K,
+                              int dtype, void* stream) {
+  using namespace bi_host;
+  if (dtype != BI_BF16 && dtype != BI_F16)
+    return fail(BI_E_UNSUPPORTED, "bi_matmul_pack: dtype %d (bf16 and fp16 only)", dtype);
+  if (N < 0 || K < 0 || N > 0x7fffffffLL || K > 0x7fffffffLL || K % bi::kGroupK)
+    return fail(BI_E_INVALID_ARG, "bi_matmul_pack: N=%lld K=%lld (K a multiple of 256)", (long long)N,
+                (long long)K);
+  if (N == 0 || K == 0) return BI_OK;
+  if (!bt || !packed || !aligned16(bt) || !aligned16(packed) || ldb % 8 || ldb < K)
+    return fail(BI_E_INVALID_ARG,
+                "bi_matmul_pack: null pointer, bt / packed not 16-byte aligned, or ldb (%lld) not a multiple of 8 "
+                ">= K", (long long)ldb);
+  const size_t need = bi_matmul_pack_bytes(N, K, dtype);
+  if (packed_bytes < need)
+    return fail(BI_E_INVALID_ARG, "bi_matmul_pack: packed holds %zu bytes, %zu required", packed_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = (N + 15) / 16 * (K / bi::kGroupK) * bi::kWave;
+  const unsigned grid = (unsigned)((n + 255) / 256);
+  if (dtype == BI_BF16)
+    bi::dense_pack_rows<bi::bf16><<<grid, 256, 0, st>>>(static_cast<const bi::bf16*>(bt), ldb,
+                                                         static_cast<char*>(packed), (int)N, (int)K);
+  else
+    bi::dense_pack_rows<bi::f16><<<grid, 256, 0, st>>>(static_cast<const bi::f16*>(bt), ldb,
+                                                        static_cast<char*>(packed), (int)N, (int)K);
+  return launch_status("bi_matmul_pack");
+}
+
+extern "C" int bi_matmul_packed(const void* a, int64_t lda, const void* bt, int64_t ldb, const void* packed,
+                                void* out, int64_t M, int64_t N, int64_t K, int dtype, void* ws, size_t ws_bytes,
+                                void* stream) {
+  using namespace bi_host;
+  if (!packed) return bi_matmul(a, lda, bt, ldb, out, M, N, K, dtype, ws, ws_bytes, stream);
+  if ((dtype != BI_BF16 && dtype != BI_F16) || K % bi::kGroupK)
+    return fail(BI_E_UNSUPPORTED,
+                "bi_matmul_packed: a packed copy needs bf16 / fp16 and K %% 256 == 0 (dtype=%d K=%lld)", dtype,
+                (long long)K);
+  if (!aligned16(packed)) return fail(BI_E_INVALID_ARG, "bi_matmul_packed: packed not 16-byte aligned");
+  // The streaming GEMV's shapes on the copy; everything else (and any shape it
+  // does not take) is bi_matmul on the row-major operands, checks included.
+  if (M >= 1 && M <= 16 && N >= 1 && N <= 0x7fffffffLL && K <= 0x7fffffffLL && a && bt && out && lda % 8 == 0 &&
+      lda >= K && ldb % 8 == 0 && ldb >= K && aligned16(a) && aligned16(bt)) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int Mi = (int)M, Ni = (int)N, Ki = (int)K;
+    auto go = [&](auto tag) {
+      typedef decltype(tag) T;
+      bi::DensePacked<T> b;
+      b.bt = static_cast<const T*>(bt);
+      b.ldb = ldb;
+      b.N = Ni;
+      b.K = Ki;
+      b.p = static_cast<const char*>(packed);
+      b.G = Ki / bi::kGroupK;
+      return bi::launch_stream_dense_packed<T>(static_cast<const T*>(a), lda, b, static_cast<T*>(out), Mi, Ni, Ki,
+                                               b.G, st);
+    };
+    if (dtype == BI_BF16 ? go(bi::bf16{}) : go(bi::f16{})) return launch_status("bi_matmul_packed");
+  }
+  return bi_matmul(a, lda, bt, ldb, out, M, N, K, dtype, ws, ws_bytes, stream);
+}
+
 // Strided batch of independent matmuls: slice i is exactly bi_matmul on
 // a + i * a_batch_stride, bt + i * b_batch_stride, out + i * out_batch_stride
 // (element strides; 0 broadcasts an operand). The slices run one after the

@@ -1041,10 +1041,9 @@ static bool launch_stream_packed(const T* a, int64_t lda, const QuantPacked<T, B
 // [14336, 4096] M = 1 / 4 / 8 / 16 22.0 / 26.8 / 29.3 / 34.6 -> 21.5 / 22.0 /
 // 23.8 / 28.6 us; [4096, 4096] 9.1 / 9.0 / 10.0 / 11.3 -> 7.7 / 8.0 / 8.3 /
 // 9.1 us; [4096, 14336] M = 1 / 4 26.9 / 28.0 -> 21.5 / 22.4 us.
-template <typename T, int W, int NB>
-static bool launch_stream_dense_m(const T* a, int64_t lda, const DenseB<T>& b, T* out, int M, int N, int K,
-                                  int G, hipStream_t st) {
-  typedef DenseB<T> DB;
+template <typename T, int W, int NB, class DB = DenseB<T>>
+static bool launch_stream_dense_m(const T* a, int64_t lda, const DB& b, T* out, int M, int N, int K, int G,
+                                  hipStream_t st) {
   if (M == 1) return launch_stream1<T, DB, W, NB, 1, 1>(a, lda, b, out, M, N, K, G, st);
   if (M <= 4) return launch_stream1<T, DB, W, NB, 4, 1>(a, lda, b, out, M, N, K, G, st);
   if (M <= 8) return launch_stream1<T, DB, W, NB, 8, 1>(a, lda, b, out, M, N, K, G, st);
@@ -1068,6 +1067,51 @@ static bool launch_stream_dense(const T* a, int64_t lda, const DenseB<T>& b, T* 
              launch_stream_ag<T, DenseB<T>, 7, 8>(a, lda, b, out, M, N, K, G, st);
     default: return false;
   }
+}
+
+// The dense streaming GEMV on a repacked B (DensePacked): the launch shapes of
+// launch_stream_dense. False when the shape does not qualify; the caller then
+// runs the launch the row-major B would take. Measured against the row-major
+// layout (same box, bits equal), bf16 [14336, 4096] M = 1 / 8 / 16 21.50 /
+// 23.89 / 28.51 -> 20.96 / 21.86 / 27.23 us; [4096, 14336] M = 4 23.60 ->
+// 21.94; [4096, 4096] M = 1 / 8 7.99 / 8.75 -> 7.63 / 8.11; [1024, 4096]
+// M = 1 / 16 5.81 / 7.11 -> 4.57 / 5.70 us.
+template <typename T>
+static bool launch_stream_dense_packed(const T* a, int64_t lda, const DensePacked<T>& b, T* out, int M, int N,
+                                       int K, int G, hipStream_t st) {
+  typedef DensePacked<T> DB;
+  if (M > kStreamMMax || K % kGroupK || lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a)) return false;
+  switch (G) {
+    case 16: return launch_stream_dense_m<T, 8, 2, DB>(a, lda, b, out, M, N, K, G, st);
+    case 8: return launch_stream_dense_m<T, 4, 2, DB>(a, lda, b, out, M, N, K, G, st);
+    case 32:
+      return launch_stream_dense_m<T, 8, 4, DB>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_ag<T, DB, 8, 4>(a, lda, b, out, M, N, K, G, st);
+    case 56:
+      return launch_stream_dense_m<T, 14, 4, DB>(a, lda, b, out, M, N, K, G, st) ||
+             launch_stream_ag<T, DB, 7, 8>(a, lda, b, out, M, N, K, G, st);
+    default: return false;
+  }
+}
+
+// One thread per (16-row tile, group, MFMA lane): the lane's eight fragments
+// copied into the DensePacked layout.
+template <typename T>
+__global__ __launch_bounds__(256) void dense_pack_rows(const T* __restrict__ bt, int64_t ldb,
+                                                       char* __restrict__ packed, int N, int K) {
+  typedef DensePacked<T> P;
+  const int G = K / kGroupK;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)((N + 15) / 16) * G * kWave) return;
+  const int l = (int)(idx % kWave);
+  const int64_t tg = idx / kWave;                  // tile * G + group
+  const int g = (int)(tg % G);
+  const int n = (int)min<int64_t>(tg / G * 16 + l % 16, N - 1);
+  const T* src = bt + (int64_t)n * ldb + g * kGroupK + 8 * (l / 16);
+  char* blk = packed + tg * P::kBlock;
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s)
+    *reinterpret_cast<u32x4*>(blk + 1024 * s + 16 * l) = *reinterpret_cast<const u32x4*>(src + 32 * s);
 }
 
 template <typename T, class BSrc, int W>

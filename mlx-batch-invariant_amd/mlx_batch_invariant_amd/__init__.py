@@ -24,6 +24,7 @@ from .kernels import (
 )
 from .kernels.quantized import (quantize, dequantize, pack, unpack, cache_dequantized, drop_dequantized,
                                 cache_packed, drop_packed)
+from .kernels.matmul import cache_packed_weight, drop_packed_weight
 from . import library  # registers torch.ops.mlx_bi.*
 
 __all__ = [
@@ -46,6 +47,8 @@ __all__ = [
     "drop_dequantized",
     "cache_packed",
     "drop_packed",
+    "cache_packed_weight",
+    "drop_packed_weight",
     "pack",
     "unpack",
 ]

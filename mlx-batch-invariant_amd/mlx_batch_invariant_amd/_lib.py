@@ -78,6 +78,10 @@ _SIGNATURES = {
     "bi_quantized_matmul_dequantized_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, _c_i64]),
     "bi_quantized_matmul_dequantized": (ctypes.c_int, [_vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
                                                        _vp, ctypes.c_size_t, _vp]),
+    "bi_matmul_pack_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, ctypes.c_int]),
+    "bi_matmul_pack": (ctypes.c_int, [_vp, _c_i64, _vp, ctypes.c_size_t, _c_i64, _c_i64, ctypes.c_int, _vp]),
+    "bi_matmul_packed": (ctypes.c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int,
+                                        _vp, ctypes.c_size_t, _vp]),
     "bi_quantized_pack_bytes": (ctypes.c_size_t, [_c_i64, _c_i64, ctypes.c_int, ctypes.c_int]),
     "bi_quantized_pack": (ctypes.c_int, [_vp, _vp, _vp, _vp, ctypes.c_size_t, _c_i64, _c_i64, ctypes.c_int,
                                          ctypes.c_int, ctypes.c_int, _vp]),

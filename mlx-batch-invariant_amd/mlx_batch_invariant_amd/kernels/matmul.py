@@ -22,6 +22,8 @@ and odd K are copied / zero-padded first; neither changes the arithmetic.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from .. import _lib
@@ -62,11 +64,77 @@ def matmul_bt(a2: torch.Tensor, bt: torch.Tensor) -> torch.Tensor:
     _lib.load()
     ws_bytes = _lib.ws_bytes("bi_matmul_workspace_bytes", M, N, K8)
     ws = _lib.workspace(ws_bytes, a2.device)
+    bp = _packed_for(bt) if M <= PACKED_MAX_M and _PACKED else None
+    if bp is not None:
+        rc = _lib.load().bi_matmul_packed(a2.data_ptr(), a2.stride(0), bt.data_ptr(), bt.stride(0), bp.data_ptr(),
+                                          out.data_ptr(), M, N, K8, _lib.DTYPE_CODE[a2.dtype], _lib.ptr(ws),
+                                          ws_bytes, _lib.stream_of(a2))
+        _lib.check(rc, "bi_matmul_packed")
+        return out
     rc = _lib.matmul_call(a2.data_ptr(), a2.stride(0), bt.data_ptr(), bt.stride(0), out.data_ptr(),
                           M, N, K8, _lib.DTYPE_CODE[a2.dtype], _lib.ptr(ws), ws_bytes,
                           _lib.stream_of(a2))
     _lib.check(rc, "bi_matmul")
     return out
+
+
+# ---- weights repacked once (decode calls) -------------------------------------
+
+# Rows up to which a repacked copy is used (the streaming GEMV's range;
+# bi_matmul_packed reads the row-major weight for the shapes it does not take).
+PACKED_MAX_M = 16
+# weight data pointer -> (weakref to the weight, N, K, row stride, dtype,
+# version counter at packing, the copy). The weight's views (W.T, as F.linear
+# and x @ W.T pass it) share its storage and version counter, so any of them
+# finds the copy, and an in-place change of the weight makes it stale.
+_PACKED: dict = {}
+
+
+def _packed_for(bt: torch.Tensor):
+    e = _PACKED.get(bt.data_ptr())
+    if e is None:
+        return None
+    w = e[0]()
+    if w is None or w.data_ptr() != bt.data_ptr():
+        _PACKED.pop(bt.data_ptr(), None)
+        return None
+    if (e[1], e[2], e[3], e[4], e[5]) != (bt.shape[0], bt.shape[1], bt.stride(0), bt.dtype, bt._version):
+        return None
+    return e[6]
+
+
+def cache_packed_weight(weight: torch.Tensor) -> torch.Tensor:
+    """Keep a copy of a dense weight ``[N, K]`` (the ``nn.Linear`` layout; bf16 or
+    fp16, K a multiple of 256, k-contiguous 16-byte aligned rows) repacked once
+    for the decode GEMV (``bi_matmul_pack``) for as long as the weight lives.
+    Calls of ``batch_invariant_matmul(x, weight.T)`` (and ``F.linear`` under the
+    mode) with at most ``PACKED_MAX_M`` rows then run ``bi_matmul_packed``: the
+    same bits, with each wave instruction reading a whole 1 KB run. The copy
+    holds N * K * 2 bytes. An in-place change of the weight (its version
+    counter) makes the copy unused until ``cache_packed_weight`` is called
+    again; ``drop_packed_weight`` releases it."""
+    if weight.ndim != 2 or weight.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("cache_packed_weight: a 2-D bf16 / fp16 weight [N, K]")
+    _lib.require_gpu("cache_packed_weight", weight)
+    N, K = weight.shape
+    if K % 256 or not _kcontig(weight):
+        raise ValueError("cache_packed_weight: K must be a multiple of 256 and rows k-contiguous, 16-byte aligned")
+    lib = _lib.load()
+    code = _lib.DTYPE_CODE[weight.dtype]
+    nbytes = lib.bi_matmul_pack_bytes(N, K, code)
+    bp = torch.empty((nbytes,), dtype=torch.uint8, device=weight.device)
+    rc = lib.bi_matmul_pack(weight.data_ptr(), weight.stride(0), bp.data_ptr(), nbytes, N, K, code,
+                            _lib.stream_of(weight))
+    _lib.check(rc, "bi_matmul_pack")
+    _PACKED[weight.data_ptr()] = (weakref.ref(weight), N, K, weight.stride(0), weight.dtype, weight._version, bp)
+    return bp
+
+
+def drop_packed_weight(weight: torch.Tensor) -> None:
+    """Release the repacked copy ``cache_packed_weight`` keeps for ``weight``."""
+    e = _PACKED.get(weight.data_ptr())
+    if e is not None and e[0]() is weight:
+        del _PACKED[weight.data_ptr()]
 
 
 def batch_invariant_matmul(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:

@@ -79,3 +79,21 @@ class QuantizedLinear(torch.nn.Module):
         y = _this.quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
                                    group_size=self.group_size, bits=self.bits)
         return y if self.bias is None else y + self.bias
+
+
+def cache_packed_linears(module: torch.nn.Module) -> torch.nn.Module:
+    """Repack every linear weight of ``module`` once for the decode GEMV:
+    ``QuantizedLinear.cache_packed()`` for the quantized ones and
+    ``cache_packed_weight`` for each ``nn.Linear`` whose weight qualifies (bf16 /
+    fp16, in_features a multiple of 256). Decode calls (at most 16 rows) under
+    the mode then read the copies, with the same bits."""
+    from .kernels.matmul import cache_packed_weight
+    for m in module.modules():
+        if isinstance(m, QuantizedLinear):
+            if m.in_features % 256 == 0 and m.scales.dtype in (torch.bfloat16, torch.float16):
+                m.cache_packed()
+        elif isinstance(m, torch.nn.Linear):
+            w = m.weight
+            if w.is_cuda and w.dtype in (torch.bfloat16, torch.float16) and w.shape[1] % 256 == 0:
+                cache_packed_weight(w)     # the parameter itself: the cache holds a weak reference to it
+    return module

@@ -367,3 +367,117 @@ def test_matmul_tall_configurations(dt, M, N, K, launch):
     assert_bits_equal(to_np(full)[rows], ora.matmul(to_np(x[rows]), to_np(W), dt), f"{dt} {launch}")
     for lo, hi in ((0, 1), (M - 1, M), (3, 19)):
         assert bits(_mm(x[lo:hi], W.t())) == bits(full[lo:hi]), (lo, hi)
+
+
+def _dense_pack_reference(bt, N, K):
+    """numpy restatement of bi_matmul_pack's layout (the DensePacked source of
+    the streaming GEMV): block (tile t, group g) of 8 KB holds, for MFMA lane
+    l = r + 16 q (row min(16 t + r, N - 1)) and step s, the 8 elements k
+    [256 g + 32 s + 8 q, +8) as the 16-byte piece at 1024 s + 16 l."""
+    w = bt.cpu().view(torch.int16).numpy()
+    G, tiles = K // 256, (N + 15) // 16
+    out = np.zeros(tiles * G * 8192, np.uint8)
+    for t in range(tiles):
+        for g in range(G):
+            base = (t * G + g) * 8192
+            for lane in range(64):
+                n = min(16 * t + lane % 16, N - 1)
+                for s in range(8):
+                    k0 = 256 * g + 32 * s + 8 * (lane // 16)
+                    o = base + 1024 * s + 16 * lane
+                    out[o:o + 16] = w[n, k0:k0 + 8].view(np.uint8)
+    return out
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_matmul_pack_layout(dt):
+    """bi_matmul_pack writes exactly the layout restated in numpy above (20
+    rows: the second tile's rows past N repeat row N - 1; two groups; a row
+    stride past K)."""
+    from mlx_batch_invariant_amd import _lib
+    N, K = 20, 512
+    wide = randn((N, K + 64), DT[dt], gen(53))
+    bt = wide[:, :K]
+    lib = _lib.load()
+    code = _lib.DTYPE_CODE[DT[dt]]
+    nbytes = lib.bi_matmul_pack_bytes(N, K, code)
+    got = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device="cuda")
+    _lib.check(lib.bi_matmul_pack(bt.data_ptr(), bt.stride(0), got.data_ptr(), nbytes, N, K, code, None),
+               "bi_matmul_pack")
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), _dense_pack_reference(bt, N, K))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_matmul_packed_equals_bi_matmul(dt):
+    """bi_matmul_packed with the repacked copy equals bi_matmul bit for bit at
+    every M and group count: the streaming GEMV on the copy (16 groups at 131
+    column tiles, the last one partial; 8 groups; 32 and 56 groups, A staged or
+    read from global memory at 257 and 258 tiles; one partial tile) and the
+    row-major launches where the stream does not take the shape (12 groups;
+    M > 16). The cache behind batch_invariant_matmul(x, W.T) (up to
+    PACKED_MAX_M rows) gives the same bits, is found through W's views, goes
+    stale on an in-place change of W and is released by drop_packed_weight."""
+    from mlx_batch_invariant_amd import _lib
+    from mlx_batch_invariant_amd.kernels import matmul as km
+    bi = _bi()
+    lib = _lib.load()
+    code = _lib.DTYPE_CODE[DT[dt]]
+    for N, K in ((2048 + 40, 4096), (1000, 2048), (4096 + 8, 14336), (4096 + 24, 8192), (300, 3072), (5, 4096)):
+        g = gen(N + 7 * K)
+        bt = randn((N, K), DT[dt], g)
+        x = randn((20, K), DT[dt], g)
+        nbytes = lib.bi_matmul_pack_bytes(N, K, code)
+        bp = torch.empty((nbytes,), dtype=torch.uint8, device="cuda")
+        _lib.check(lib.bi_matmul_pack(bt.data_ptr(), bt.stride(0), bp.data_ptr(), nbytes, N, K, code, None),
+                   "bi_matmul_pack")
+        for M in (1, 3, 5, 8, 12, 16, 20):
+            want = _mm(x[:M], bt.t())
+            need = lib.bi_matmul_workspace_bytes(M, N, K)
+            ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+            got = torch.empty((M, N), dtype=DT[dt], device="cuda")
+            _lib.check(lib.bi_matmul_packed(x.data_ptr(), x.stride(0), bt.data_ptr(), bt.stride(0), bp.data_ptr(),
+                                            got.data_ptr(), M, N, K, code, ws.data_ptr(), need, None),
+                       "bi_matmul_packed")
+            torch.cuda.synchronize()
+            assert bits(got) == bits(want), (N, K, M)
+    # the cache behind batch_invariant_matmul (last shape's operands)
+    W = randn((4096, 4096), DT[dt], gen(59))
+    xs = randn((20, 4096), DT[dt], gen(61))
+    plain = _mm(xs, W.t())
+    bi.cache_packed_weight(W)
+    assert km._packed_for(W.t().t()) is not None                # found through a view
+    for M in (1, 7, 16, 20):
+        assert bits(_mm(xs[:M], W.t())) == bits(plain[:M]), M
+    W.add_(0)                                                   # in place: the copy goes stale
+    assert km._packed_for(W) is None
+    bi.cache_packed_weight(W)
+    assert km._packed_for(W) is not None
+    bi.drop_packed_weight(W)
+    assert km._packed_for(W) is None
+
+
+def test_linear_packed_under_the_mode():
+    """nn.cache_packed_linears on a small model (nn.Linear weights and a
+    QuantizedLinear): decode-sized calls under the mode give the same bits with
+    and without the repacked copies."""
+    bi = _bi()
+    from mlx_batch_invariant_amd.kernels import matmul as km
+    from mlx_batch_invariant_amd.nn import QuantizedLinear, cache_packed_linears
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(1024, 512, bias=True).to(torch.bfloat16)
+    model = torch.nn.Sequential(torch.nn.Linear(4096, 1024, bias=False), torch.nn.SiLU(), lin).to(
+        device="cuda", dtype=torch.bfloat16)
+    q = QuantizedLinear.from_linear(torch.nn.Linear(512, 2048, bias=False).to(torch.bfloat16), 64, 4).cuda()
+    x = randn((4, 2, 4096), torch.bfloat16, gen(67))
+    with torch.no_grad(), bi.set_batch_invariant_mode(strict=True):
+        plain = [q(model(x[:, :t])) for t in (1, 2)]
+        cache_packed_linears(model)
+        cache_packed_linears(q)
+        assert km._packed_for(model[0].weight) is not None
+        cached = [q(model(x[:, :t])) for t in (1, 2)]
+    for p_, c_ in zip(plain, cached):
+        assert bits(c_) == bits(p_)
+    bi.drop_packed_weight(model[0].weight)
+    bi.drop_packed_weight(lin.weight)
+    bi.drop_packed(q.weight)
