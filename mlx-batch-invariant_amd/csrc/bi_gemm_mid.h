@@ -54,6 +54,10 @@ template <typename T> struct MidLoads<DenseB<T>> { static constexpr int kMin = k
 template <typename T, int BITS, int GS> struct MidLoads<QuantB<T, BITS, GS>> {
   static constexpr int kMin = QuantB<T, BITS, GS>::kWords / 4 + 2;
 };
+// The repacked B: its code pieces and one load of the lane's (scale, bias) pairs.
+template <typename T, int BITS, int GS> struct MidLoads<QuantPacked<T, BITS, GS>> {
+  static constexpr int kMin = QuantPacked<T, BITS, GS>::kPieces + 1;
+};
 
 // The A ring lives in one __shared__ array per slot, and every access names
 // its slot by a compile-time index: a DS read of one slot then provably does

@@ -1442,9 +1442,21 @@ int run_quant_packed_gs(const void* x, int64_t ldx, const uint32_t* w, const voi
     b.groups_per_row = K / GS;
     b.p = static_cast<const char*>(packed);
     b.G = K / kGroupK;
-    if (launch_stream_packed<T, BITS, GS>(static_cast<const T*>(x), ldx, b, static_cast<T*>(out), M, N, K, b.G,
-                                          st))
+    const T* a = static_cast<const T*>(x);
+    if (launch_stream_packed<T, BITS, GS>(a, ldx, b, static_cast<T*>(out), M, N, K, b.G, st))
       return bi_host::launch_status("bi_quantized_matmul_packed");
+    // The mid-M launches read B through the same per-lane interface, so they
+    // take the copy too: Llama MLP up [14336, 4096] M = 17 / 32 / 64 17.9-19.2
+    // / 18.8-19.8 / 22.2 -> 13.6-14.6 / 14.2-14.9 / 17.8 us, down [4096,
+    // 14336] M = 32 / 64 30.4-31.1 / 43.1 -> 24.1-24.3 / 36.1 us, [4096,
+    // 4096] M = 32 / 64 15.8-16.1 / 17.8 -> 14.0-14.2 / 16.7 us (same box,
+    // bits equal): their per-CU load rate, not the arithmetic, bounds them.
+    const MidPlan mp = mid_plan(M, N, K);
+    if (use_mid<T, QuantPacked<T, BITS, GS>>(mp, ldx, a)) {
+      launch_mid<T, QuantPacked<T, BITS, GS>>(a, ldx, b, static_cast<T*>(out), static_cast<float*>(ws), M, N, K,
+                                              b.G, mp, st);
+      return bi_host::launch_status("bi_quantized_matmul_packed");
+    }
   }
   return run_quant<T, BITS, GS>(x, ldx, w, scales, biases, out, M, N, K, ws, st);
 }

@@ -187,9 +187,11 @@ def _remember(cache, w, scales, biases, group_size, bits, dt, copy) -> None:
 
 # ---- weights repacked once (decode calls) -------------------------------------
 
-# Rows of x up to which a repacked copy is used (the streaming GEMV's range;
-# bi_quantized_matmul_packed reads the MLX layout for the shapes it does not take).
-PACKED_MAX_M = 16
+# Rows of x up to which a repacked copy is used (the streaming GEMV's and the
+# mid-M launches' range, below the large-M launch, which dequantizes B once per
+# call; bi_quantized_matmul_packed reads the MLX layout for the shapes those
+# do not take).
+PACKED_MAX_M = DEQUANTIZED_MIN_M - 1
 # id(w) -> the same record as _DEQUANTIZED's, holding the repacked copy.
 _PACKED: dict = {}
 

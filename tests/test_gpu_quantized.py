@@ -462,10 +462,11 @@ def test_quantized_packed_equals_the_quantized_op(bits_, gs, dt):
     bi_quantized_matmul bit for bit at every M and group count: the streaming
     GEMV on the copy (16 groups at 131 and 515 column tiles, the last one
     partial: 8 waves of 2 groups, or 16 of 1 with one, two or four column
-    tiles per wave; 8
-    groups; 4 groups at M <= 2; 32 and 56 groups, A staged or read from global
-    memory at 257 and 258 tiles), and the MLX-layout launches where the stream
-    does not take the shape (12 groups; M > 16; 4 groups at M > 2). The cache
+    tiles per wave; 8 groups; 4 groups at M <= 2; 32 and 56 groups, A staged
+    or read from global memory at 257 and 258 tiles), the mid-M launches on
+    the copy (M = 20 .. 100, and 5 .. 16 rows split over K with 1000 columns
+    and 56 groups), and the MLX-layout launches where neither takes the shape
+    (12 groups at M <= 16; 4 groups at M > 2). The cache
     inside batch_invariant_quantized_matmul (up to PACKED_MAX_M rows) gives the
     same bits, follows only the cached tensors, and is released by
     drop_packed."""
@@ -475,15 +476,15 @@ def test_quantized_packed_equals_the_quantized_op(bits_, gs, dt):
     lib = _lib.load()
     code = _lib.DTYPE_CODE[DT[dt]]
     for N, K in ((2048 + 40, 4096), (8192 + 40, 4096), (1000, 2048), (100, 1024), (4096 + 8, 14336),
-                 (4096 + 24, 8192), (300, 3072)):
+                 (4096 + 24, 8192), (300, 3072), (1000, 14336)):
         wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 17 + gs + N % 89 + K % 97)
         wq, s, b = wq.view(torch.int32).cuda(), s.cuda(), b.cuda()
         nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, gs)
         bp = torch.empty((nbytes,), dtype=torch.uint8, device="cuda")
         _lib.check(lib.bi_quantized_pack(wq.data_ptr(), s.data_ptr(), b.data_ptr(), bp.data_ptr(), nbytes, N, K,
                                          bits_, gs, code, None), "bi_quantized_pack")
-        x = randn((20, K), DT[dt], gen(K + N))
-        for M in (1, 2, 3, 5, 8, 12, 16, 20):
+        x = randn((100, K), DT[dt], gen(K + N))
+        for M in (1, 2, 3, 5, 8, 12, 16, 20, 33, 64, 100):
             want = bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=gs, bits=bits_)
             need = lib.bi_quantized_matmul_workspace_bytes(M, N, K)
             ws = torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
@@ -500,7 +501,7 @@ def test_quantized_packed_equals_the_quantized_op(bits_, gs, dt):
     assert bits(cached) == bits(bp)
     assert kq._cached_for(kq._PACKED, wq, s, b, gs, bits_, DT[dt]) is not None
     assert kq._cached_for(kq._PACKED, wq, s.clone(), b, gs, bits_, DT[dt]) is None   # other scales: not this copy
-    for M in (1, 7, 16, 20):
+    for M in (1, 7, 16, 20, 64, 100):
         assert bits(bi.batch_invariant_quantized_matmul(x[:M], wq, s, b, group_size=gs, bits=bits_)) == \
             bits(plain[:M]), M
     bi.drop_packed(wq)
