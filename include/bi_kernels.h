@@ -174,11 +174,12 @@ int bi_quantized_matmul_dequantized(const void* x, int64_t ldx, const void* bq, 
  * group_size 32 / 64 / 128, bf16 / fp16, K % 256 == 0) into
  * bi_quantized_pack_bytes bytes laid out for the streaming GEMV: per 16 rows
  * and 256-k group, the codes of each MFMA lane as the lane's 16-byte pieces of
- * consecutive 1 KB runs, then the lane's (scale, bias) pairs (one, or two for
- * group size 32) (pack_bytes returns 0 for an unsupported format). bi_quantized_matmul_packed is bi_quantized_matmul with
+ * consecutive 1 KB runs, then the block's (scale, bias) pairs, each once
+ * (pack_bytes returns 0 for an unsupported format). bi_quantized_matmul_packed is bi_quantized_matmul with
  * that copy beside the MLX-layout operands (packed may be NULL: then it is
- * bi_quantized_matmul): the streaming GEMV reads the copy wherever it takes
- * the shape (M <= 16), every other launch reads w / scales / biases, and the
+ * bi_quantized_matmul): the streaming GEMV (M <= 16) and the mid-M launches
+ * (M < 256) read the copy wherever they take the shape, every other launch
+ * reads w / scales / biases, and the
  * result equals bi_quantized_matmul's bit for bit at every M. Same checks and
  * workspace as bi_quantized_matmul; the copy must have been packed from these
  * w / scales / biases.

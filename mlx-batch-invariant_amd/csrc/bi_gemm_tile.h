@@ -325,9 +325,10 @@ struct QuantB {
 // scales and biases as QuantB<T, BITS, GS>, so the same values reach the MFMA.
 // For 16-row tile t and group g, MFMA lane l = r + 16 q holds row 16 t + r, k
 // [256 g + 64 q, +64) (the blocked map): its kWords words are the l-th 16-byte
-// pieces of kPieces consecutive 1 KB runs, followed by a run of (scale, bias)
-// pairs, kScales 4-byte pairs per lane (one for groups of 64 or 128, two for
-// 32), lane l's at 4 kScales l. A wave's code loads then read whole 1 KB runs
+// pieces of kPieces consecutive 1 KB runs, followed by a run of the block's
+// (scale, bias) pairs, 4 bytes each, every pair once: for groups of 32 and 64
+// lane l's kScales pairs at 4 kScales l; for groups of 128 (two lanes of a row
+// share a pair) row r's pair of half h at 4 (16 h + r). A wave's code loads then read whole 1 KB runs
 // (in the MLX layout each instruction touches 16 weight rows 2 KB apart), and
 // each lane's scales and biases arrive with its codes instead of being staged
 // per tile. Block (t, g) starts at byte (t G + g) kBlock; tiles = ceil(N / 16),
@@ -339,7 +340,12 @@ struct QuantPacked : QuantB<T, BITS, GS> {
   typedef typename Base::Raw Raw;
   static constexpr int kScales = Base::kScales;
   static constexpr int kPieces = Base::kWords / 4;               // 16-byte pieces per lane and group
-  static constexpr int kBlock = kPieces * 1024 + 256 * kScales;  // bytes per (tile, group)
+  static constexpr int kMetaBytes = 16 * (kGroupK / GS) * 4;     // the block's pairs, each once
+  static constexpr int kBlock = kPieces * 1024 + kMetaBytes;     // bytes per (tile, group)
+  // Byte offset of lane (r, q)'s first pair within the metadata run.
+  static __host__ __device__ constexpr int meta_off(int r, int q) {
+    return GS >= 128 ? 4 * (16 * (q * 64 / GS) + r) : 4 * kScales * (r + 16 * q);
+  }
   static_assert(sizeof(T) == 2, "QuantPacked: 2-byte element types only");
   static_assert(kScales == 1 || kScales == 2, "QuantPacked: one or two scales per lane");
   const char* p;
@@ -353,7 +359,7 @@ struct QuantPacked : QuantB<T, BITS, GS> {
   __device__ __forceinline__ Lane lane(int n, int q) const {
     const char* b = p + (int64_t)(n / 16) * G * kBlock;
     const int l = n % 16 + 16 * q;
-    return Lane{b + 16 * l, b + kPieces * 1024 + 4 * kScales * l};
+    return Lane{b + 16 * l, b + kPieces * 1024 + meta_off(n % 16, q)};
   }
   __device__ __forceinline__ void load_full(Raw& raw, const Lane& l, int g) const {
     const int64_t o = (int64_t)g * kBlock;

@@ -1416,12 +1416,14 @@ __global__ __launch_bounds__(256) void qmm_pack_rows(const uint32_t* __restrict_
 #pragma unroll
   for (int i = 0; i < P::kPieces; ++i)
     *reinterpret_cast<u32x4*>(blk + 1024 * i + 16 * l) = *reinterpret_cast<const u32x4*>(src + 4 * i);
+  // Groups of 128: the two lanes of a row that share a pair both write it
+  // (the same value).
 #pragma unroll
   for (int i = 0; i < P::kScales; ++i) {
     const int64_t si = (int64_t)n * (K / GS) + k0 / GS + i;
     const uint32_t m = (uint32_t)__builtin_bit_cast(uint16_t, scales[si]) |
                        ((uint32_t)__builtin_bit_cast(uint16_t, biases[si]) << 16);
-    *reinterpret_cast<uint32_t*>(blk + P::kPieces * 1024 + 4 * (P::kScales * l + i)) = m;
+    *reinterpret_cast<uint32_t*>(blk + P::kPieces * 1024 + P::meta_off(l % 16, l / 16) + 4 * i) = m;
   }
 }
 

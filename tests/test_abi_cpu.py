@@ -220,16 +220,16 @@ def test_invalid_arguments_are_rejected_before_launch():
 
 def test_quantized_pack_sizes_and_rejections():
     """bi_quantized_pack_bytes: ceil(N / 16) tiles x K / 256 groups x (bits x
-    512 + 256 x pairs) bytes (each lane's codes as 16-byte pieces of 1 KB runs,
-    then its (scale, bias) pairs: one, two for group size 32), 0 for a format
-    without a packed form;
+    512 + 16 x 256 / group_size x 4) bytes (each lane's codes as 16-byte pieces
+    of 1 KB runs, then the block's (scale, bias) pairs, each once), 0 for a
+    format without a packed form;
     bi_quantized_pack / bi_quantized_matmul_packed reject what they cannot take
     before launching anything (M = 0 is a no-op)."""
     lib = _lib.load()
     assert lib.bi_quantized_pack_bytes(14336, 4096, 4, 64) == 896 * 16 * 2304
     assert lib.bi_quantized_pack_bytes(4096, 14336, 4, 64) == 256 * 56 * 2304
     assert lib.bi_quantized_pack_bytes(17, 256, 8, 64) == 2 * 1 * 4352
-    assert lib.bi_quantized_pack_bytes(17, 256, 8, 128) == 2 * 1 * 4352
+    assert lib.bi_quantized_pack_bytes(17, 256, 8, 128) == 2 * 1 * 4224
     assert lib.bi_quantized_pack_bytes(4096, 4096, 4, 32) == 256 * 16 * 2560
     for args in ((4096, 4096, 4, 16), (4096, 4096, 3, 64), (4096, 4160, 4, 64), (0, 4096, 4, 64),
                  (4096, 0, 4, 64)):

@@ -405,19 +405,21 @@ def test_quantized_linear_cache_under_the_mode():
 
 def _pack_reference(wq, s, b, bits_, gs, N, K):
     """numpy restatement of bi_quantized_pack's layout (the QuantPacked
-    source of the streaming GEMV): block (tile t, group g) of bits x 512 + 256
-    x P bytes (P = 2 pairs per lane for group size 32, else 1) holds, for MFMA
-    lane l = r + 16 q (row min(16 t + r, N - 1), k [256 g + 64 q, +64)), its
-    64 x bits / 32 code words as 16-byte pieces at 1024 i + 16 l, then its P
-    (scale, bias) pairs (16-bit each, scale low; pair i of groups k0 / gs + i)
-    at bits x 512 + 4 (P l + i)."""
+    source of the streaming GEMV): block (tile t, group g) of bits x 512 +
+    16 x (256 / gs) x 4 bytes holds, for MFMA lane l = r + 16 q (row
+    min(16 t + r, N - 1), k [256 g + 64 q, +64)), its 64 x bits / 32 code
+    words as 16-byte pieces at 1024 i + 16 l, then the block's (scale, bias)
+    pairs (16-bit each, scale low), each once: lane l's P pairs (P = 2 for
+    group size 32, else 1; pair i of group k0 / gs + i) at bits x 512 +
+    4 (P l + i) for groups of 32 and 64, row r's pair of 128-k half h at
+    bits x 512 + 4 (16 h + r) for groups of 128."""
     words = wq.cpu().view(torch.int32).numpy().view(np.uint32)
     sb = s.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.uint32)
     bb = b.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.uint32)
     G, tiles, pieces = K // 256, (N + 15) // 16, bits_ // 2
     pairs = 2 if gs == 32 else 1
     wpl = 64 * bits_ // 32                                   # words per lane and group
-    blk = bits_ * 512 + 256 * pairs
+    blk = bits_ * 512 + 16 * (256 // gs) * 4
     out = np.zeros(tiles * G * blk, np.uint8)
     for t in range(tiles):
         for g in range(G):
@@ -432,7 +434,8 @@ def _pack_reference(wq, s, b, bits_, gs, N, K):
                     out[o:o + 16] = wv[4 * i:4 * i + 4].view(np.uint8)
                 for i in range(pairs):
                     m = np.uint32(sb[n, k0 // gs + i] | (bb[n, k0 // gs + i] << 16))
-                    o = base + pieces * 1024 + 4 * (pairs * lane + i)
+                    slot = 16 * (q * 64 // gs) + r if gs == 128 else pairs * lane + i
+                    o = base + pieces * 1024 + 4 * slot
                     out[o:o + 4] = np.array([m], np.uint32).view(np.uint8)
     return out
 
