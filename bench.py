@@ -396,6 +396,25 @@ def bench_linear(args):
         out[M] = {"rmsnorm_us": round(tn * 1e6, 2), "rmsnorm_GBps": round(by_n / tn / 1e9, 1),
                   "linear_us": round(tl * 1e6, 2), "linear_GBps": round(by_l / tl / 1e9, 1),
                   "linear_frac_hbm": round(by_l / tl / PEAK_HBM, 4), "stock_linear_us": round(ts * 1e6, 2)}
+    # The same linear with every weight copy repacked once (cache_packed_weight,
+    # zero-filled to K = 1024): calls of up to 16 rows take the streaming GEMV,
+    # with the bits of the row-major call.
+    xs_h = {M: bi.batch_invariant_rms_norm(torch.randn((M, K), generator=g).to(torch.bfloat16).cuda(), gam, 1e-6)
+            for M in (1, 4, 16)}
+    plain = {M: bi.batch_invariant_matmul(xs_h[M], Ws[0].t()) for M in xs_h}
+    for W in Ws:
+        bi.cache_packed_weight(W)
+    for M in (1, 4, 16):
+        h = xs_h[M]
+        tp = statistics.median(_time_calls(lambda i: bi.batch_invariant_matmul(h, Ws[i].t()), args.steps, args.warmup,
+                                           ncopy))
+        by_l = per + 2 * M * (K + N)
+        out[M]["linear_packed_us"] = round(tp * 1e6, 2)
+        out[M]["linear_packed_frac_hbm"] = round(by_l / tp / PEAK_HBM, 4)
+        out[M]["linear_packed_bits_equal"] = bool(
+            bi.batch_invariant_matmul(h, Ws[0].t()).view(torch.int16).equal(plain[M].view(torch.int16)))
+    for W in Ws:
+        bi.drop_packed_weight(W)
     cpu = None
     if not args.no_cpu:
         with _CpuThreads() as nth:

@@ -98,10 +98,11 @@ int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb, void* out
 const char* bi_matmul_launch(int64_t M, int64_t N, int64_t K);
 
 /* A repacked copy of a dense weight for the decode GEMV. bi_matmul_pack writes
- * bt's N x K elements (bf16 / fp16, K % 256 == 0, ldb % 8 == 0) into
+ * bt's N x K elements (bf16 / fp16, K % 8 == 0, ldb % 8 == 0) into
  * bi_matmul_pack_bytes bytes laid out for the streaming GEMV: per 16 rows and
- * 256-k group, each MFMA lane's 16-byte fragment of step s as the lane's piece
- * of the s-th 1 KB run (pack_bytes returns 0 for an unsupported format).
+ * 256-k group (ceil(K / 256) groups, zero past K), each MFMA lane's 16-byte
+ * fragment of step s as the lane's piece of the s-th 1 KB run (pack_bytes
+ * returns 0 for an unsupported format).
  * bi_matmul_packed is bi_matmul with that copy beside bt (packed may be NULL:
  * then it is bi_matmul): the streaming GEMV reads the copy wherever it takes
  * the shape (M <= 16), every other launch reads bt, and the result equals

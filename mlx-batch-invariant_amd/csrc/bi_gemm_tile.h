@@ -101,7 +101,8 @@ struct DenseB {
 // elements: the dense k-slot map) is the l-th 16-byte piece of the s-th 1 KB
 // run of the (tile, group)'s 8 KB block at (t G + g) 8 KB. A wave's loads then
 // read whole 1 KB runs (in the row-major layout each instruction touches 16
-// rows, 64 bytes each). tiles = ceil(N / 16), rows past N repeat row N - 1.
+// rows, 64 bytes each). tiles = ceil(N / 16), rows past N repeat row N - 1;
+// G = ceil(K / 256), elements past K are zero (K % 8 == 0).
 template <typename T>
 struct DensePacked : DenseB<T> {
   typedef typename DenseB<T>::Raw Raw;
@@ -110,7 +111,9 @@ struct DensePacked : DenseB<T> {
   static constexpr int kBlock = kSteps * 1024;                  // bytes per (tile, group)
   const char* p;
   int G;
-  static constexpr int64_t bytes(int64_t N, int64_t K) { return (N + 15) / 16 * (K / kGroupK) * kBlock; }
+  static constexpr int64_t bytes(int64_t N, int64_t K) {
+    return (N + 15) / 16 * ((K + kGroupK - 1) / kGroupK) * kBlock;
+  }
   struct Lane {
     const char* c;   // the lane's piece of group 0, step 0
   };

@@ -47,18 +47,29 @@ namespace bi {
 
 // Group size of a B source's per-group metadata staged in LDS; 0 for a dense B
 // (none) and for a repacked quantized B, whose metadata arrive with its codes
-// (kRegMeta: then checked for huge scales in registers).
+// (kRegMeta: then checked for huge scales in registers). kPadK: B is zero past
+// K within its last group (a repacked dense B, zero-filled to whole groups), so
+// K need not be a multiple of 256; A's elements past K are then loaded as zero,
+// as every other launch's partial last group has them.
 template <class BSrc> struct StreamMeta {
   static constexpr int kGS = 0;
   static constexpr bool kRegMeta = false;
+  static constexpr bool kPadK = false;
 };
 template <typename T, int BITS, int GS> struct StreamMeta<QuantB<T, BITS, GS>> {
   static constexpr int kGS = GS;
   static constexpr bool kRegMeta = false;
+  static constexpr bool kPadK = false;
 };
 template <typename T, int BITS, int GS> struct StreamMeta<QuantPacked<T, BITS, GS>> {
   static constexpr int kGS = 0;
   static constexpr bool kRegMeta = true;
+  static constexpr bool kPadK = false;
+};
+template <typename T> struct StreamMeta<DensePacked<T>> {
+  static constexpr int kGS = 0;
+  static constexpr bool kRegMeta = false;
+  static constexpr bool kPadK = true;
 };
 
 template <typename T, int GS, int W, int NB, int MR, int CT = 1, bool AG = false>
@@ -110,7 +121,14 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   for (int i = 0; i < C::kALoads; ++i) {
     const int c = lane + kWave * i;
     const int ar = c / (NB * kGroupK / C::kCE), ac = (c % (NB * kGroupK / C::kCE)) * C::kCE;
-    av[i] = frag_load(a + (int64_t)min(ar, M - 1) * lda + g0 * kGroupK + ac);
+    const int kk = g0 * kGroupK + ac;
+    if constexpr (StreamMeta<BSrc>::kPadK) {
+      const bool ok = kk < K;                      // K % 8 == 0: a chunk lies wholly before or past K
+      const F v = frag_load(a + (ok ? (int64_t)min(ar, M - 1) * lda + kk : 0));
+      av[i] = ok ? v : frag_zero<F>();
+    } else {
+      av[i] = frag_load(a + (int64_t)min(ar, M - 1) * lda + kk);
+    }
   }
   // 2. Scales then biases of rows n_base .. n_base + kRows - 1 for the wave's
   // groups (a quantized B; a dense one has none).
@@ -148,7 +166,16 @@ __global__ __launch_bounds__(kWave* W) void gemv_stream(const T* a, int64_t lda,
   auto load_a = [&](int j) {
     if constexpr (AG) {
 #pragma unroll
-      for (int s = 0; s < kSteps; ++s) areg[j % kAR][s] = frag_load(arowp + QB::a_k(g0 + j, q, s));
+      for (int s = 0; s < kSteps; ++s) {
+        const int kk = QB::a_k(g0 + j, q, s);
+        if constexpr (StreamMeta<BSrc>::kPadK) {
+          const bool ok = kk < K;
+          const F v = frag_load(ok ? arowp + kk : a);
+          areg[j % kAR][s] = ok ? v : frag_zero<F>();
+        } else {
+          areg[j % kAR][s] = frag_load(arowp + kk);
+        }
+      }
     }
   };
   typename QB::Raw braw[NB][CT];

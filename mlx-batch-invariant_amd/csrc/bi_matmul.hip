@@ -115,8 +115,7 @@ extern "C" int bi_matmul(const void* a, int64_t lda, const void* bt, int64_t ldb
 // so bi_matmul_packed equals bi_matmul bit for bit at every M.
 // ---------------------------------------------------------------------------
 extern "C" size_t bi_matmul_pack_bytes(int64_t N, int64_t K, int dtype) {
-  if ((dtype != BI_BF16 && dtype != BI_F16) || N <= 0 || K <= 0 || K % bi::kGroupK || N > 0x7fffffffLL ||
-      K > 0x7fffffffLL)
+  if ((dtype != BI_BF16 && dtype != BI_F16) || N <= 0 || K <= 0 || K % 8 || N > 0x7fffffffLL || K > 0x7fffffffLL)
     return 0;
   return (size_t)bi::DensePacked<bi::bf16>::bytes(N, K);
 }
@@ -126,9 +125,8 @@ extern "C" int bi_matmul_pack(const void* bt, int64_t ldb, void* packed, size_t 
   using namespace bi_host;
   if (dtype != BI_BF16 && dtype != BI_F16)
     return fail(BI_E_UNSUPPORTED, "bi_matmul_pack: dtype %d (bf16 and fp16 only)", dtype);
-  if (N < 0 || K < 0 || N > 0x7fffffffLL || K > 0x7fffffffLL || K % bi::kGroupK)
-    return fail(BI_E_INVALID_ARG, "bi_matmul_pack: N=%lld K=%lld (K a multiple of 256)", (long long)N,
-                (long long)K);
+  if (N < 0 || K < 0 || N > 0x7fffffffLL || K > 0x7fffffffLL || K % 8)
+    return fail(BI_E_INVALID_ARG, "bi_matmul_pack: N=%lld K=%lld (K a multiple of 8)", (long long)N, (long long)K);
   if (N == 0 || K == 0) return BI_OK;
   if (!bt || !packed || !aligned16(bt) || !aligned16(packed) || ldb % 8 || ldb < K)
     return fail(BI_E_INVALID_ARG,
@@ -138,7 +136,7 @@ extern "C" int bi_matmul_pack(const void* bt, int64_t ldb, void* packed, size_t 
   if (packed_bytes < need)
     return fail(BI_E_INVALID_ARG, "bi_matmul_pack: packed holds %zu bytes, %zu required", packed_bytes, need);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t n = (N + 15) / 16 * (K / bi::kGroupK) * bi::kWave;
+  const int64_t n = (N + 15) / 16 * ((K + bi::kGroupK - 1) / bi::kGroupK) * bi::kWave;
   const unsigned grid = (unsigned)((n + 255) / 256);
   if (dtype == BI_BF16)
     bi::dense_pack_rows<bi::bf16><<<grid, 256, 0, st>>>(static_cast<const bi::bf16*>(bt), ldb,
@@ -154,10 +152,9 @@ extern "C" int bi_matmul_packed(const void* a, int64_t lda, const void* bt, int6
                                 void* stream) {
   using namespace bi_host;
   if (!packed) return bi_matmul(a, lda, bt, ldb, out, M, N, K, dtype, ws, ws_bytes, stream);
-  if ((dtype != BI_BF16 && dtype != BI_F16) || K % bi::kGroupK)
-    return fail(BI_E_UNSUPPORTED,
-                "bi_matmul_packed: a packed copy needs bf16 / fp16 and K %% 256 == 0 (dtype=%d K=%lld)", dtype,
-                (long long)K);
+  if ((dtype != BI_BF16 && dtype != BI_F16) || K % 8)
+    return fail(BI_E_UNSUPPORTED, "bi_matmul_packed: a packed copy needs bf16 / fp16 and K %% 8 == 0 (dtype=%d K=%lld)",
+                dtype, (long long)K);
   if (!aligned16(packed)) return fail(BI_E_INVALID_ARG, "bi_matmul_packed: packed not 16-byte aligned");
   // The streaming GEMV's shapes on the copy; everything else (and any shape it
   // does not take) is bi_matmul on the row-major operands, checks included.
@@ -173,7 +170,7 @@ extern "C" int bi_matmul_packed(const void* a, int64_t lda, const void* bt, int6
       b.N = Ni;
       b.K = Ki;
       b.p = static_cast<const char*>(packed);
-      b.G = Ki / bi::kGroupK;
+      b.G = (Ki + bi::kGroupK - 1) / bi::kGroupK;
       return bi::launch_stream_dense_packed<T>(static_cast<const T*>(a), lda, b, static_cast<T*>(out), Mi, Ni, Ki,
                                                b.G, st);
     };

@@ -1076,12 +1076,21 @@ static bool launch_stream_dense(const T* a, int64_t lda, const DenseB<T>& b, T* 
 // 23.89 / 28.51 -> 20.96 / 21.86 / 27.23 us; [4096, 14336] M = 4 23.60 ->
 // 21.94; [4096, 4096] M = 1 / 8 7.99 / 8.75 -> 7.63 / 8.11; [1024, 4096]
 // M = 1 / 16 5.81 / 7.11 -> 4.57 / 5.70 us.
+// G = ceil(K / 256): the copy is zero past K, so K need only be a multiple of
+// 8; 4 groups (K = 769 .. 1024, the Qwen2-0.5B projections' K = 896) run 4
+// waves of one group, A's rows staged in LDS (config-1 linear [4864, 896]
+// M = 1 / 4 / 16: 4.86 / 5.13 / 5.84 -> 4.12 / 4.15 / 4.70 us against the
+// workgroup-fold GEMV on the row-major weight).
 template <typename T>
 static bool launch_stream_dense_packed(const T* a, int64_t lda, const DensePacked<T>& b, T* out, int M, int N,
                                        int K, int G, hipStream_t st) {
   typedef DensePacked<T> DB;
-  if (M > kStreamMMax || K % kGroupK || lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a)) return false;
+  if (M > kStreamMMax || K % 8 || lda % (16 / (int)sizeof(T)) || !bi_host::aligned16(a)) return false;
   switch (G) {
+    case 4:
+      if (M <= 4) return launch_stream1<T, DB, 4, 1, 4, 1>(a, lda, b, out, M, N, K, G, st);
+      if (M <= 8) return launch_stream1<T, DB, 4, 1, 8, 1>(a, lda, b, out, M, N, K, G, st);
+      return launch_stream1<T, DB, 4, 1, 16, 1>(a, lda, b, out, M, N, K, G, st);
     case 16: return launch_stream_dense_m<T, 8, 2, DB>(a, lda, b, out, M, N, K, G, st);
     case 8: return launch_stream_dense_m<T, 4, 2, DB>(a, lda, b, out, M, N, K, G, st);
     case 32:
@@ -1095,23 +1104,26 @@ static bool launch_stream_dense_packed(const T* a, int64_t lda, const DensePacke
 }
 
 // One thread per (16-row tile, group, MFMA lane): the lane's eight fragments
-// copied into the DensePacked layout.
+// copied into the DensePacked layout, zero past K (K % 8 == 0).
 template <typename T>
 __global__ __launch_bounds__(256) void dense_pack_rows(const T* __restrict__ bt, int64_t ldb,
                                                        char* __restrict__ packed, int N, int K) {
   typedef DensePacked<T> P;
-  const int G = K / kGroupK;
+  const int G = (K + kGroupK - 1) / kGroupK;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)((N + 15) / 16) * G * kWave) return;
   const int l = (int)(idx % kWave);
   const int64_t tg = idx / kWave;                  // tile * G + group
   const int g = (int)(tg % G);
   const int n = (int)min<int64_t>(tg / G * 16 + l % 16, N - 1);
-  const T* src = bt + (int64_t)n * ldb + g * kGroupK + 8 * (l / 16);
+  const int k0 = g * kGroupK + 8 * (l / 16);
+  const T* src = bt + (int64_t)n * ldb + k0;
   char* blk = packed + tg * P::kBlock;
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s)
-    *reinterpret_cast<u32x4*>(blk + 1024 * s + 16 * l) = *reinterpret_cast<const u32x4*>(src + 32 * s);
+  for (int s = 0; s < kSteps; ++s) {
+    const u32x4 v = k0 + 32 * s < K ? *reinterpret_cast<const u32x4*>(src + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<u32x4*>(blk + 1024 * s + 16 * l) = v;
+  }
 }
 
 template <typename T, class BSrc, int W>

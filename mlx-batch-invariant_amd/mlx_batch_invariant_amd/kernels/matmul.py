@@ -105,20 +105,20 @@ def _packed_for(bt: torch.Tensor):
 
 def cache_packed_weight(weight: torch.Tensor) -> torch.Tensor:
     """Keep a copy of a dense weight ``[N, K]`` (the ``nn.Linear`` layout; bf16 or
-    fp16, K a multiple of 256, k-contiguous 16-byte aligned rows) repacked once
+    fp16, K a multiple of 8, k-contiguous 16-byte aligned rows) repacked once
     for the decode GEMV (``bi_matmul_pack``) for as long as the weight lives.
     Calls of ``batch_invariant_matmul(x, weight.T)`` (and ``F.linear`` under the
     mode) with at most ``PACKED_MAX_M`` rows then run ``bi_matmul_packed``: the
     same bits, with each wave instruction reading a whole 1 KB run. The copy
-    holds N * K * 2 bytes. An in-place change of the weight (its version
+    holds N * K * 2 bytes, K rounded up to a multiple of 256 (zero-filled). An in-place change of the weight (its version
     counter) makes the copy unused until ``cache_packed_weight`` is called
     again; ``drop_packed_weight`` releases it."""
     if weight.ndim != 2 or weight.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("cache_packed_weight: a 2-D bf16 / fp16 weight [N, K]")
     _lib.require_gpu("cache_packed_weight", weight)
     N, K = weight.shape
-    if K % 256 or not _kcontig(weight):
-        raise ValueError("cache_packed_weight: K must be a multiple of 256 and rows k-contiguous, 16-byte aligned")
+    if K % 8 or not _kcontig(weight):
+        raise ValueError("cache_packed_weight: K must be a multiple of 8 and rows k-contiguous, 16-byte aligned")
     lib = _lib.load()
     code = _lib.DTYPE_CODE[weight.dtype]
     nbytes = lib.bi_matmul_pack_bytes(N, K, code)

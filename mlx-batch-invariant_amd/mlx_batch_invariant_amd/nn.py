@@ -83,10 +83,10 @@ class QuantizedLinear(torch.nn.Module):
 
 def cache_packed_linears(module: torch.nn.Module) -> torch.nn.Module:
     """Repack every linear weight of ``module`` once for the decode GEMV:
-    ``QuantizedLinear.cache_packed()`` for the quantized ones and
-    ``cache_packed_weight`` for each ``nn.Linear`` whose weight qualifies (bf16 /
-    fp16, in_features a multiple of 256). Decode calls (at most 16 rows) under
-    the mode then read the copies, with the same bits."""
+    ``QuantizedLinear.cache_packed()`` for the quantized ones (in_features a
+    multiple of 256) and ``cache_packed_weight`` for each ``nn.Linear`` whose
+    weight qualifies (bf16 / fp16, in_features a multiple of 8). Decode calls
+    (at most 16 rows) under the mode then read the copies, with the same bits."""
     from .kernels.matmul import cache_packed_weight
     for m in module.modules():
         if isinstance(m, QuantizedLinear):
@@ -94,6 +94,6 @@ def cache_packed_linears(module: torch.nn.Module) -> torch.nn.Module:
                 m.cache_packed()
         elif isinstance(m, torch.nn.Linear):
             w = m.weight
-            if w.is_cuda and w.dtype in (torch.bfloat16, torch.float16) and w.shape[1] % 256 == 0:
+            if w.is_cuda and w.dtype in (torch.bfloat16, torch.float16) and w.shape[1] % 8 == 0:
                 cache_packed_weight(w)     # the parameter itself: the cache holds a weak reference to it
     return module

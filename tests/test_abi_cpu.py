@@ -258,26 +258,27 @@ def test_quantized_pack_sizes_and_rejections():
 
 
 def test_dense_pack_sizes_and_rejections():
-    """bi_matmul_pack_bytes: ceil(N / 16) tiles x K / 256 groups x 8 KB (each
-    lane's eight 16-byte fragments as pieces of 1 KB runs), 0 for fp32 or K not
-    a multiple of 256; bi_matmul_pack / bi_matmul_packed reject what they cannot
-    take before launching anything."""
+    """bi_matmul_pack_bytes: ceil(N / 16) tiles x ceil(K / 256) groups x 8 KB
+    (each lane's eight 16-byte fragments as pieces of 1 KB runs, zero past K),
+    0 for fp32 or K not a multiple of 8; bi_matmul_pack / bi_matmul_packed
+    reject what they cannot take before launching anything."""
     lib = _lib.load()
     assert lib.bi_matmul_pack_bytes(14336, 4096, 2) == 896 * 16 * 8192
     assert lib.bi_matmul_pack_bytes(1000, 256, 1) == 63 * 1 * 8192
-    for args in ((4096, 4096, 0), (4096, 4160, 2), (0, 4096, 2), (4096, 0, 2)):
+    assert lib.bi_matmul_pack_bytes(4864, 896, 2) == 304 * 4 * 8192
+    for args in ((4096, 4096, 0), (4096, 4100, 2), (0, 4096, 2), (4096, 0, 2)):
         assert lib.bi_matmul_pack_bytes(*args) == 0, args
     p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
     need = lib.bi_matmul_pack_bytes(32, 512, 2)
     assert lib.bi_matmul_pack(p, 512, p, need, 32, 512, 0, None) == -2          # fp32
-    assert lib.bi_matmul_pack(p, 320, p, need, 32, 320, 2, None) == -1          # K % 256
+    assert lib.bi_matmul_pack(p, 328, p, need, 32, 324, 2, None) == -1          # K % 8
     assert lib.bi_matmul_pack(p, 512, p, need - 1, 32, 512, 2, None) == -1      # too small
     assert "required" in _err(lib)
     assert lib.bi_matmul_pack(p, 500, p, need, 32, 512, 2, None) == -1          # ldb < K
     assert lib.bi_matmul_pack(p, 512, ctypes.c_void_p(24), need, 32, 512, 2, None) == -1   # misaligned copy
     assert lib.bi_matmul_pack(p, 512, p, need, 0, 512, 2, None) == 0            # nothing to pack
     assert lib.bi_matmul_packed(p, 512, p, 512, p, p, 2, 32, 512, 0, None, 0, None) == -2      # fp32 copy
-    assert lib.bi_matmul_packed(p, 320, p, 320, p, p, 2, 32, 320, 2, None, 0, None) == -2      # K % 256
+    assert lib.bi_matmul_packed(p, 328, p, 328, p, p, 2, 32, 324, 2, None, 0, None) == -2      # K % 8
     assert lib.bi_matmul_packed(p, 512, p, 512, ctypes.c_void_p(24), p, 2, 32, 512, 2, None, 0, None) == -1
     assert lib.bi_matmul_packed(p, 512, p, 512, p, p, 0, 32, 512, 2, None, 0, None) == 0       # M = 0
     # without a copy it is bi_matmul, checks included

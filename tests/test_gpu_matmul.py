@@ -371,11 +371,12 @@ def test_matmul_tall_configurations(dt, M, N, K, launch):
 
 def _dense_pack_reference(bt, N, K):
     """numpy restatement of bi_matmul_pack's layout (the DensePacked source of
-    the streaming GEMV): block (tile t, group g) of 8 KB holds, for MFMA lane
-    l = r + 16 q (row min(16 t + r, N - 1)) and step s, the 8 elements k
-    [256 g + 32 s + 8 q, +8) as the 16-byte piece at 1024 s + 16 l."""
+    the streaming GEMV): block (tile t, group g < ceil(K / 256)) of 8 KB holds,
+    for MFMA lane l = r + 16 q (row min(16 t + r, N - 1)) and step s, the 8
+    elements k [256 g + 32 s + 8 q, +8) as the 16-byte piece at 1024 s + 16 l,
+    zero past K."""
     w = bt.cpu().view(torch.int16).numpy()
-    G, tiles = K // 256, (N + 15) // 16
+    G, tiles = (K + 255) // 256, (N + 15) // 16
     out = np.zeros(tiles * G * 8192, np.uint8)
     for t in range(tiles):
         for g in range(G):
@@ -385,17 +386,19 @@ def _dense_pack_reference(bt, N, K):
                 for s in range(8):
                     k0 = 256 * g + 32 * s + 8 * (lane // 16)
                     o = base + 1024 * s + 16 * lane
-                    out[o:o + 16] = w[n, k0:k0 + 8].view(np.uint8)
+                    if k0 < K:
+                        out[o:o + 16] = w[n, k0:k0 + 8].view(np.uint8)
     return out
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_matmul_pack_layout(dt):
+@pytest.mark.parametrize("K", [512, 896])
+def test_matmul_pack_layout(dt, K):
     """bi_matmul_pack writes exactly the layout restated in numpy above (20
-    rows: the second tile's rows past N repeat row N - 1; two groups; a row
-    stride past K)."""
+    rows: the second tile's rows past N repeat row N - 1; two groups, or four
+    with the last one zero-filled past K = 896; a row stride past K)."""
     from mlx_batch_invariant_amd import _lib
-    N, K = 20, 512
+    N = 20
     wide = randn((N, K + 64), DT[dt], gen(53))
     bt = wide[:, :K]
     lib = _lib.load()
@@ -413,9 +416,10 @@ def test_matmul_packed_equals_bi_matmul(dt):
     """bi_matmul_packed with the repacked copy equals bi_matmul bit for bit at
     every M and group count: the streaming GEMV on the copy (16 groups at 131
     column tiles, the last one partial; 8 groups; 32 and 56 groups, A staged or
-    read from global memory at 257 and 258 tiles; one partial tile) and the
-    row-major launches where the stream does not take the shape (12 groups;
-    M > 16). The cache behind batch_invariant_matmul(x, W.T) (up to
+    read from global memory at 257 and 258 tiles; one partial tile; 4 groups
+    with the last one partial, K = 896 (the Qwen2-0.5B linear) and 1000) and
+    the row-major launches where the stream does not take the shape (12
+    groups; M > 16). The cache behind batch_invariant_matmul(x, W.T) (up to
     PACKED_MAX_M rows) gives the same bits, is found through W's views, goes
     stale on an in-place change of W and is released by drop_packed_weight."""
     from mlx_batch_invariant_amd import _lib
@@ -423,7 +427,8 @@ def test_matmul_packed_equals_bi_matmul(dt):
     bi = _bi()
     lib = _lib.load()
     code = _lib.DTYPE_CODE[DT[dt]]
-    for N, K in ((2048 + 40, 4096), (1000, 2048), (4096 + 8, 14336), (4096 + 24, 8192), (300, 3072), (5, 4096)):
+    for N, K in ((2048 + 40, 4096), (1000, 2048), (4096 + 8, 14336), (4096 + 24, 8192), (300, 3072), (5, 4096),
+                 (4864, 896), (100, 1000)):
         g = gen(N + 7 * K)
         bt = randn((N, K), DT[dt], g)
         x = randn((20, K), DT[dt], g)
