@@ -1465,7 +1465,20 @@ int run_quant_packed_gs(const void* x, int64_t ldx, const uint32_t* w, const voi
     // 14336] M = 32 / 64 30.4-31.1 / 43.1 -> 24.1-24.3 / 36.1 us, [4096,
     // 4096] M = 32 / 64 15.8-16.1 / 17.8 -> 14.0-14.2 / 16.7 us (same box,
     // bits equal): their per-CU load rate, not the arithmetic, bounds them.
-    const MidPlan mp = mid_plan(M, N, K);
+    MidPlan mp = mid_plan(M, N, K);
+    // 33-64 rows that the plan splits over K (64-row blocks, fewer than
+    // kMidMinTiles of them) run unsplit on the copy as 32-row blocks when that
+    // gives at least 128 workgroups: [4096, 4096] / [4096, 8192] / [4096,
+    // 14336] M = 64 17.1 / 22.5 / 37.0 -> 12.5 / 19.8 / 31.0 us, M = 48 14.7
+    // / 20.0 / 33.0 -> 12.8 / 20.5 / 32.2 us (same box, bits equal: the same
+    // group partials, folded in the same order).
+    if (mp.use && mp.mt == 4 && mp.chunks > 1 && (int64_t)ceil_div(N, 64) * ceil_div(M, 32) >= 128 &&
+        (int64_t)ceil_div(N, 64) * ceil_div(M, 32) <= kMidInterleaveMaxTiles) {
+      mp.mt = 2;
+      mp.mtiles = ceil_div(M, 32);
+      mp.cg = b.G;
+      mp.chunks = 1;
+    }
     if (use_mid<T, QuantPacked<T, BITS, GS>>(mp, ldx, a)) {
       launch_mid<T, QuantPacked<T, BITS, GS>>(a, ldx, b, static_cast<T*>(out), static_cast<float*>(ws), M, N, K,
                                               b.G, mp, st);

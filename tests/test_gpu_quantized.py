@@ -467,8 +467,9 @@ def test_quantized_packed_equals_the_quantized_op(bits_, gs, dt):
     partial: 8 waves of 2 groups, or 16 of 1 with one, two or four column
     tiles per wave; 8 groups; 4 groups at M <= 2; 32 and 56 groups, A staged
     or read from global memory at 257 and 258 tiles), the mid-M launches on
-    the copy (M = 20 .. 100, and 5 .. 16 rows split over K with 1000 columns
-    and 56 groups), and the MLX-layout launches where neither takes the shape
+    the copy (M = 20 .. 100; 33 .. 64 rows on 65 and 129 column blocks as
+    unsplit 32-row blocks; 5 .. 16 rows split over K with 1000 columns and 56
+    groups), and the MLX-layout launches where neither takes the shape
     (12 groups at M <= 16; 4 groups at M > 2). The cache
     inside batch_invariant_quantized_matmul (up to PACKED_MAX_M rows) gives the
     same bits, follows only the cached tensors, and is released by
