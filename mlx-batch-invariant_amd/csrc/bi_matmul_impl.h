@@ -1022,7 +1022,10 @@ static bool launch_stream_packed(const T* a, int64_t lda, const QuantPacked<T, B
         return launch_stream_m<T, QB, 16, 1, 1>(a, lda, b, out, M, N, K, G, st);
       return launch_stream_m<T, QB, 8, 2, 1>(a, lda, b, out, M, N, K, G, st);
     case 8: return launch_stream_m<T, QB, 4, 2, 1>(a, lda, b, out, M, N, K, G, st);
-    case 4: return M <= 2 && launch_stream_m<T, QB, 4, 1, 1>(a, lda, b, out, M, N, K, G, st);
+    case 4:
+      return M <= 2 && (launch_stream_m<T, QB, 4, 1, 1>(a, lda, b, out, M, N, K, G, st) ||
+                        launch_stream_m<T, QB, 2, 2, 1>(a, lda, b, out, M, N, K, G, st) ||
+                        launch_stream_m<T, QB, 1, 4, 2>(a, lda, b, out, M, N, K, G, st));
     case 32:
       return launch_stream_m<T, QB, 8, 4, 1>(a, lda, b, out, M, N, K, G, st) ||
              launch_stream_ag<T, QB, 4, 8>(a, lda, b, out, M, N, K, G, st);
