@@ -204,12 +204,11 @@ def cache_packed(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, *,
     of ``batch_invariant_quantized_matmul`` with at most ``PACKED_MAX_M`` rows,
     this ``w`` (the same tensor object) and these scales / biases then run
     ``bi_quantized_matmul_packed``: the same bits, with each wave instruction of
-    the decode GEMV reading a whole 1 KB run of codes. 4 or 8 bits, group
-    size 32 / 64 / 128, bf16 / fp16 scales, K a multiple of 256. The copy holds
-    the codes, scales and biases again (4 bytes per lane and 64 k, 8 for group
-    size 32). Call
-    again after changing the weight's values in place; ``drop_packed`` releases
-    it."""
+    the decode GEMV reading a whole 1 KB run of codes; the mid-M launches read
+    it too. 4 or 8 bits, group size 32 / 64 / 128, bf16 / fp16 scales, K a
+    multiple of 256. The copy holds the codes, scales and biases again (each
+    byte once, in another order). Call again after changing the weight's
+    values in place; ``drop_packed`` releases it."""
     if bits not in SUPPORTED_BITS or group_size not in SUPPORTED_GROUPS:
         raise ValueError(f"cache_packed: bits={bits} group_size={group_size}")
     dt = scales.dtype
