@@ -463,9 +463,9 @@ def test_quantized_pack_layout(bits_, gs, dt):
 def test_quantized_packed_equals_the_quantized_op(bits_, gs, dt):
     """bi_quantized_matmul_packed with the repacked copy equals
     bi_quantized_matmul bit for bit at every M and group count: the streaming
-    GEMV on the copy (16 groups at 131 and 515 column tiles, the last one
+    GEMV on the copy (16 groups at 131, 257 and 515 column tiles, the last one
     partial: 8 waves of 2 groups, or 16 of 1 with one, two or four column
-    tiles per wave; 8 groups; 4 groups at M <= 2; 32 and 56 groups, A staged
+    tiles per wave, at 257 tiles from one row; 8 groups; 4 groups at M <= 2; 32 and 56 groups, A staged
     or read from global memory at 257 and 258 tiles), the mid-M launches on
     the copy (M = 20 .. 100; 33 .. 64 rows on 65 and 129 column blocks as
     unsplit 32-row blocks; 5 .. 16 rows split over K with 1000 columns and 56
@@ -479,8 +479,8 @@ def test_quantized_packed_equals_the_quantized_op(bits_, gs, dt):
     bi = _bi()
     lib = _lib.load()
     code = _lib.DTYPE_CODE[DT[dt]]
-    for N, K in ((2048 + 40, 4096), (8192 + 40, 4096), (1000, 2048), (100, 1024), (4096 + 8, 14336),
-                 (4096 + 24, 8192), (300, 3072), (1000, 14336)):
+    for N, K in ((2048 + 40, 4096), (4096 + 8, 4096), (8192 + 40, 4096), (1000, 2048), (100, 1024),
+                 (4096 + 8, 14336), (4096 + 24, 8192), (300, 3072), (1000, 14336)):
         wq, s, b = _qweights(N, K, bits_, gs, dt, seed=bits_ * 17 + gs + N % 89 + K % 97)
         wq, s, b = wq.view(torch.int32).cuda(), s.cuda(), b.cuda()
         nbytes = lib.bi_quantized_pack_bytes(N, K, bits_, gs)
