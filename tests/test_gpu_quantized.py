@@ -144,7 +144,7 @@ def test_quantized_stream_launch_up_to_16_rows(bits_, gs, dt):
     W = ora.dequantize(wq.cpu().view(torch.int32).numpy().view(np.uint32), to_np(s.cpu()), to_np(b.cpu()),
                        gs, bits_, dt)
     cols = np.r_[0:24, 4100:4124, N - 24:N]
-    for M in (1, 4, 5, 8, 9, 12, 16):
+    for M in (1, 2, 4, 5, 8, 9, 12, 16):
         got = run(x[:M])
         rows = sorted({0, M // 2, M - 1})
         want = ora.matmul(to_np(x[rows]), W[cols], dt, kmap="blocked")
@@ -173,7 +173,7 @@ def test_quantized_stream_launch_fewer_tiles_and_longer_k(bits_, gs, N, K):
     wq, s, b = wq.cuda(), s.cuda(), b.cuda()
     x = randn((16, K), DT[dt], gen(19))
     run = lambda xx: _bi().batch_invariant_quantized_matmul(xx, wq, s, b, group_size=gs, bits=bits_)
-    for M in (1, 3, 5, 8, 12, 16):
+    for M in (1, 2, 3, 5, 8, 12, 16):
         got = run(x[:M])
         rows = sorted({0, M // 2, M - 1})
         want = ora.matmul(to_np(x[rows]), W, dt, kmap="blocked")
