@@ -1017,13 +1017,13 @@ static bool launch_stream_packed(const T* a, int64_t lda, const QuantPacked<T, B
       // 16 waves of one group (twice the waves per CU of 8 x 2 at the LDS A
       // takes) for 9-16 rows, and for 5-8 rows with one column tile per wave:
       // [14336, 4096] M = 12 / 16 11.2 / 11.5 -> 10.4 / 10.8 us, [4096, 4096]
-      // M = 8 / 16 5.12 / 5.52 -> 4.67 / 5.48 us; 8 x 2 stays at M <= 4 and
-      // where 5-8 rows take two column tiles (9.9 against 10.5 us at M = 8).
-      // (4-bit codes; 8-bit ones keep 8 x 2, unmeasured with 16 waves). With
-      // 256 to 512 column tiles 16 x 1 also takes 1-4 rows (as a 4-row A
-      // slice): [4096, 4096] M = 1 / 2 / 4 4.36-4.44 / 4.55-4.68 / 4.62-4.70
-      // -> 4.15-4.33 / 4.20-4.40 / 4.26-4.34 us; at 896 tiles 8 x 2 stays
-      // (M = 1 9.3-9.7 against 10.1-10.7 us).
+      // M = 8 / 16 5.12 / 5.52 -> 4.67 / 5.48 us; 8 x 2 stays where 5-8 rows
+      // take two column tiles (9.9 against 10.5 us at M = 8). For 1-4 rows
+      // 16 x 1 (a 4-row A slice) wins only at 256 to 512 column tiles:
+      // [4096, 4096] M = 1 / 2 / 4 4.36-4.44 / 4.55-4.68 / 4.62-4.70 ->
+      // 4.15-4.33 / 4.20-4.40 / 4.26-4.34 us; with more tiles 8 x 2 stays
+      // (896 tiles, M = 1: 9.3-9.7 against 10.1-10.7 us). (4-bit codes; 8-bit
+      // ones keep 8 x 2, unmeasured with 16 waves.)
       if (BITS == 4 && M <= 4 && ceil_div(N, 16) >= 256 && ceil_div(N, 16) <= 512)
         return launch_stream1<T, QB, 16, 1, 4, 1>(a, lda, b, out, M, N, K, G, st);
       if (BITS == 4 && (M > 8 || (M > 4 && stream_ct(8, N) == 1)))
