@@ -1022,8 +1022,10 @@ static bool launch_stream_packed(const T* a, int64_t lda, const QuantPacked<T, B
       // 16 x 1 (a 4-row A slice) wins only at 256 to 512 column tiles:
       // [4096, 4096] M = 1 / 2 / 4 4.36-4.44 / 4.55-4.68 / 4.62-4.70 ->
       // 4.15-4.33 / 4.20-4.40 / 4.26-4.34 us; with more tiles 8 x 2 stays
-      // (896 tiles, M = 1: 9.3-9.7 against 10.1-10.7 us). (4-bit codes; 8-bit
-      // ones keep 8 x 2, unmeasured with 16 waves.)
+      // (896 tiles, M = 1: 9.3-9.7 against 10.1-10.7 us). 4-bit codes only:
+      // 8-bit ones keep 8 x 2 (g128 [14336, 4096] M = 1 / 4 12.6-12.7 /
+      // 13.4-13.7 against 16.6-17.0 / 17.2 us for 16 x 1, [4096, 4096] 5.3-5.6
+      // / 5.7-5.9 against 5.6-5.8 / 5.9-6.0 us).
       if (BITS == 4 && M <= 4 && ceil_div(N, 16) >= 256 && ceil_div(N, 16) <= 512)
         return launch_stream1<T, QB, 16, 1, 4, 1>(a, lda, b, out, M, N, K, G, st);
       if (BITS == 4 && (M > 8 || (M > 4 && stream_ct(8, N) == 1)))
